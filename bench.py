@@ -1,0 +1,330 @@
+#!/usr/bin/env python3
+"""MLA latent-cache decode benchmark on one MI355X.
+
+Workload: one MLA layer geometry (n_embd 1024, 16
+heads, kv_lora_rank 256, rope 64, nope 128, v 128), bf16, batch 32, every
+sequence pre-filled to 4096 cached tokens by the append path on N(0,1)
+hidden states, then K decode steps of append + attention through the drop-in
+``swamla_amd.MLA.forward`` (GEMMs in ATen, append / attention / merge in the
+HIP kernels), captured as one HIP graph per step.
+
+One layer's cache (86.5 MB) fits MI355X's 256 MB Infinity Cache, so a single
+layer decoded back to back would be served from there, not from HBM.  The
+bench therefore rotates ``--layers`` independent layers (own weights, own
+cache: 4 x 86.5 MB by default), like a decoder stack, and counts each token
+once per layer it passes: value = batch * steps * layers / seconds
+("layer-token decodes per second"); ms_per_step is per layer-step.
+
+roofline: the decode-attention kernel (mla_decode_mfma), timed with HIP
+events recorded on its own stream immediately around each of its launches;
+achieved = algorithmic bytes per launch / average launch duration, with
+bytes = sum_b L_b*(R+P)*2 (latent + rope cache) + B*H*(R+P)*2 (queries) +
+B*H*R*2 (latent outputs).
+
+cpu_baseline: the oracle's op-for-op CPU restatement of the reference MLA
+(oracle/mla_ref.py, which re-projects the cache and runs SDPA exactly as
+models/mla.py does) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+R, P, H = 256, 64, 16
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=128)
+    p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--layers", type=int, default=4, help="independent layers rotated per step")
+    p.add_argument("--batch", type=int, default=32)
+    p.add_argument("--ctx", type=int, default=4096)
+    p.add_argument("--dim", type=int, default=1024)
+    p.add_argument("--cache", choices=["bf16", "fp8"], default="bf16")
+    p.add_argument("--kernel-reps", type=int, default=50, help="roofline launches per layer")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--cpu-batch", type=int, default=4)
+    return p.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def attention_bytes(B: int, L: int, fp8: bool) -> int:
+    per_tok = R * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0)
+    return B * L * per_tok + B * H * (R + P) * 2 + B * H * R * 2
+
+
+def build_layers(args, dev, torch):
+    from oracle.mla_ref import MLAConfig, init_weights  # weight init recipe only
+    from swamla_amd import MLA
+
+    max_seq = (args.ctx + args.steps + args.warmup + 63) // 64 * 64
+    cfg = MLAConfig(n_embd=args.dim, max_batch_size=args.batch, max_seq_len=max_seq)
+    layers = []
+    g = torch.Generator(device=dev).manual_seed(1234)
+    for i in range(args.layers):
+        m = MLA(cfg, cache_dtype="fp8_e4m3" if args.cache == "fp8" else None)
+        init_weights(m, 100 + i)
+        m.eval().to(torch.bfloat16).to(dev)
+        m.set_inference_mode(True)
+        with torch.no_grad():
+            x = torch.randn(args.batch, args.ctx, args.dim, generator=g, device=dev, dtype=torch.bfloat16)
+            m.prefill_cache(x, 0)  # append path over the whole prompt (RoPE positions 0..ctx-1)
+            del x
+        layers.append(m)
+    torch.cuda.synchronize()
+    return layers
+
+
+def time_decode_kernel(layers, xs, args, dev, torch):
+    """Average duration of the decode-attention kernel from HIP events
+    recorded on its stream right before and after each launch."""
+    from swamla_amd import _abi, kernels
+
+    lib = _abi.lib()
+    stream = torch.cuda.current_stream(dev)
+    preps = []
+    with torch.no_grad():
+        for m, x in zip(layers, xs):
+            B = x.shape[0]
+            q = m.wq(x).view(B, H, -1)
+            w_uk, _ = m.absorbed_weights()
+            q_abs = torch.bmm(q[:, :, :128].transpose(0, 1).contiguous(), w_uk)  # [H, B, R]
+            cache = m.latent_cache()
+            L = int(args.ctx + args.steps)
+            kv_len = torch.full((B,), L, dtype=torch.int32, device=dev)
+            n_splits, min_chunk = m._split_plan(B, L, dev)
+            ws = kernels.DecodeWorkspace.allocate(B, n_splits, dev)
+            o_lat = torch.empty(H, B, R, dtype=torch.bfloat16, device=dev)
+            cos, sin = m.rope.half_tables()
+            zeros = torch.zeros(B, dtype=torch.int32, device=dev)
+            seq = torch.arange(B, dtype=torch.int32, device=dev)
+            qa = q_abs.transpose(0, 1)
+            qp = q[:, :, 128:]
+            ol = o_lat.transpose(0, 1)
+            dargs = (
+                qa.data_ptr(), qa.stride(0), qa.stride(1), qp.data_ptr(), qp.stride(0), qp.stride(1),
+                zeros.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
+                cache.ckv.shape[0], cache.ckv.shape[1], seq.data_ptr(), kv_len.data_ptr(), B, H, R, P,
+                float(m.softmax_scale), n_splits, min_chunk, ws.o_part.data_ptr(), ws.lse_part.data_ptr(),
+                ol.data_ptr(), ol.stride(0), ol.stride(1), _abi.DTYPE_BF16, cache.cache_code,
+            )
+            margs = (ws.o_part.data_ptr(), ws.lse_part.data_ptr(), kv_len.data_ptr(), B, H, R, n_splits,
+                     min_chunk, ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16)
+            preps.append((dargs, margs, (q, q_abs, kv_len, ws, o_lat, cos, sin, zeros, seq), L, B, n_splits))
+    h = stream.cuda_stream
+
+    def run(indices, reps):
+        evs = []
+        for _ in range(reps):
+            for i in indices:
+                dargs, margs = preps[i][0], preps[i][1]
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                _abi.check(lib.mla_decode_attn(*dargs, h))
+                e1.record(stream)
+                _abi.check(lib.mla_merge(*margs, h))
+                evs.append((e0, e1))
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in evs) / len(evs) * 1e3  # us
+
+    run(range(len(preps)), 3)  # warm
+    cold_us = run(range(len(preps)), args.kernel_reps)
+    warm_us = run([0], args.kernel_reps * len(preps))
+    L, B, n_splits = preps[0][3], preps[0][4], preps[0][5]
+    return cold_us, warm_us, L, B, n_splits
+
+
+def cpu_baseline(args, torch):
+    """Op-for-op restatement of the reference on the host: a bounded sample
+    of decode steps over a bf16 cache of length ctx."""
+    from oracle.mla_ref import MLAConfig, RefMLA, enable_cache, init_weights
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    B = args.cpu_batch
+    cfg = MLAConfig(n_embd=args.dim, max_batch_size=B, max_seq_len=args.ctx + 64)
+    m = RefMLA(cfg)
+    init_weights(m, 7)
+    m.eval()
+    enable_cache(m)
+    m.to(torch.bfloat16)
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        m.kv_cache[:, : args.ctx] = torch.randn(B, args.ctx, R, generator=g).to(torch.bfloat16)
+        m.pe_cache[:, : args.ctx] = torch.randn(B, args.ctx, P, generator=g).to(torch.bfloat16)
+        x = torch.randn(B, 1, args.dim, generator=g).to(torch.bfloat16)
+        m(x, args.ctx)  # untimed warm-up step
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            m(x, args.ctx + 1 + steps)
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds or steps >= 40:
+                break
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": B * steps / el,
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"{B} sequences x {steps} decode steps at ctx {args.ctx + 1}-{args.ctx + steps}, bf16, "
+            f"oracle/mla_ref.RefMLA (op-for-op restatement of models/mla.py absorb branch: cache "
+            f"re-projection einsums + SDPA) on {el:.1f} s of CPU time; per-token cost is independent "
+            f"of batch, so the rate stands for batch {args.batch}"
+        ),
+        "cpu": cpu_model,
+        "nproc": os.cpu_count(),
+        "capability": torch.backends.cpu.get_cpu_capability(),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(
+            f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the decode "
+            "path shards by sequence with no exchange, so the one-GPU figure is per-GPU throughput",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    fp8 = args.cache == "fp8"
+    log(f"building {args.layers} layers, batch {args.batch}, prefill {args.ctx} ({args.cache} cache)")
+    layers = build_layers(args, dev, torch)
+    g = torch.Generator(device=dev).manual_seed(99)
+    xs = [torch.randn(args.batch, 1, args.dim, generator=g, device=dev, dtype=torch.bfloat16) for _ in layers]
+    sps = [torch.full((args.batch,), args.ctx, dtype=torch.int32, device=dev) for _ in layers]
+    outs = [None] * len(layers)
+
+    def stack_step():
+        for i, m in enumerate(layers):
+            outs[i] = m(xs[i], sps[i])
+            sps[i].add_(1)
+
+    # eager warm-up (allocates workspaces), then capture one stack step
+    with torch.no_grad():
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            stack_step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            stack_step()
+        for sp in sps:
+            sp.fill_(args.ctx)
+        for _ in range(args.warmup):
+            graph.replay()
+        for sp in sps:  # timed steps decode positions ctx .. ctx+K-1
+            sp.fill_(args.ctx)
+        log("timing")
+        if torch.distributed.is_available() and torch.distributed.is_initialized():
+            torch.distributed.barrier()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        if torch.distributed.is_available() and torch.distributed.is_initialized():
+            torch.distributed.barrier()
+        ok = all(bool(torch.isfinite(o).all()) for o in outs)
+
+    layer_steps = args.steps * len(layers)
+    value = args.batch * layer_steps / elapsed
+    ms_per_step = elapsed / layer_steps * 1e3
+    log(f"decode: {value:.0f} layer-token/s, {ms_per_step * 1e3:.1f} us per layer-step, finite={ok}")
+
+    cold_us, warm_us, L, B, n_splits = time_decode_kernel(layers, xs, args, dev, torch)
+    abytes = attention_bytes(B, L, fp8)
+    achieved = abytes / (cold_us * 1e-6) / 1e9
+    warm = abytes / (warm_us * 1e-6) / 1e9
+    log(f"decode kernel: {cold_us:.2f} us cold ({achieved:.0f} GB/s), {warm_us:.2f} us warm ({warm:.0f} GB/s)")
+    # algorithmic bytes of one full layer-step (attention + append + weights), mean context
+    mean_L = args.ctx + (args.steps + 1) / 2
+    w_bytes = sum(p.numel() * p.element_size() for p in layers[0].parameters())
+    step_bytes = attention_bytes(args.batch, int(mean_L), fp8) + w_bytes + args.batch * (R + P) * 2 * 2
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(args, torch)
+        log(f"cpu: {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": "MLA decode tok/s + achieved HBM GB/s (% peak), bs=32 ctx=4096 bf16",
+        "value": value,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if not fp8 else "bf16+e4m3-cache",
+        "data": "synthetic: N(0,1) hidden states, N(0,0.02) random-init weights (no checkpoint)",
+        "config": {
+            "workload": "BASELINE config 2: MLA decode, batch 32, prefill 4096 then append+attention steps",
+            "batch": args.batch, "ctx": args.ctx, "decode_steps": args.steps, "n_embd": args.dim,
+            "heads": H, "kv_lora_rank": R, "rope_dim": P, "cache": args.cache,
+            "layers_rotated": len(layers),
+            "value_counts": "tokens x layers per second (each token counted once per MLA layer)",
+            "step": "full drop-in MLA.forward (wq, wkv_a, append, absorption bmm, decode, merge, "
+                    "W_uv bmm, wo) as one HIP graph per layer-step",
+        },
+        "hbm_gbs_step": step_bytes / (ms_per_step * 1e-3) / 1e9,
+        "roofline": {
+            "kernel": "mla_decode_mfma (split-KV decode attention)",
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "bytes_per_launch": abytes,
+            "avg_launch_us": cold_us,
+            "launch": f"B={B} L={L} splits<={n_splits}, caches rotated over {len(layers)} layers",
+            "warm_mall_achieved": warm,
+            "warm_mall_avg_launch_us": warm_us,
+        },
+        "cpu_baseline": cpu,
+        "host": platform.node(),
+        "gpu": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if ok else 3
+
+
+if __name__ == "__main__":
+    sys.exit(main())

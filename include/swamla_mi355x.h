@@ -1,0 +1,141 @@
+/*
+ * swamla_mi355x.h — C-ABI of the MI355X (gfx950) MLA latent-KV-cache kernels.
+ *
+ * Every entry point replaces one piece of the absorb branch of the reference
+ * `MLA.forward` (Orolol/swamla, models/mla.py).  The library allocates no
+ * memory, keeps no pointer after it returns and holds no device state: the
+ * caller owns caches, partial buffers and outputs.  Work is enqueued on the
+ * caller's HIP stream (`stream` is a hipStream_t; NULL = default stream) and
+ * nothing synchronises the host.  All entry points are graph-capturable.
+ *
+ * Return value: SWAMLA_OK (0) or a negative SWAMLA_ERR_* code; the message of
+ * the last failure on the calling thread is returned by mla_last_error().
+ *
+ * Element types (the `*_dtype` arguments):
+ *   SWAMLA_DTYPE_F32   IEEE binary32
+ *   SWAMLA_DTYPE_BF16  bfloat16 (raw 16-bit storage)
+ *   SWAMLA_DTYPE_FP8   OCP float8 e4m3fn with one fp32 scale per cached token
+ *                      (latent c_kv only; k_pe stays in the model dtype)
+ *
+ * Fixed geometry of this build: kv_lora_rank R = 256, qk_rope_head_dim P = 64,
+ * heads H = 16 (the BASELINE configurations).  Other values return
+ * SWAMLA_ERR_UNSUPPORTED.
+ */
+#ifndef SWAMLA_MI355X_H
+#define SWAMLA_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SWAMLA_ABI_VERSION 1
+
+enum {
+  SWAMLA_OK = 0,
+  SWAMLA_ERR_INVALID_ARG = -1,  /* null pointer, negative size, bad stride  */
+  SWAMLA_ERR_UNSUPPORTED = -2,  /* geometry / dtype combination not built   */
+  SWAMLA_ERR_MISALIGNED = -3,   /* pointer or stride breaks 16-byte loads   */
+  SWAMLA_ERR_OUT_OF_RANGE = -4, /* position beyond the cache / rope table   */
+  SWAMLA_ERR_HIP = -5           /* the HIP runtime rejected a launch        */
+};
+
+enum { SWAMLA_DTYPE_F32 = 0, SWAMLA_DTYPE_BF16 = 1, SWAMLA_DTYPE_FP8 = 2 };
+
+/* ABI revision of the loaded library; callers compare it with
+ * SWAMLA_ABI_VERSION.  No reference counterpart (the reference has no FFI). */
+int mla_abi_version(void);
+
+/* Message describing the last non-zero return on this thread ("" if none).
+ * No reference counterpart: the reference raises Python exceptions. */
+const char* mla_last_error(void);
+
+/*
+ * mla_append — fused cache append (one call per forward, any T).
+ * Replaces models/mla.py:307-323 (split of wkv_a(x) into c / k_pe and RoPE on
+ * k_pe), :409 (kv_norm LayerNorm) and :413-414 (scatter into kv_cache /
+ * pe_cache at [:bsz, start_pos:end_pos]).
+ *
+ * kv_in        [n_tok, in_row_stride] rows in in_dtype; columns 0..R-1 are the
+ *              latent c, R..R+P-1 are k_pe (the wkv_a output, no copy needed).
+ * seq_idx      [n_tok] int32, cache row (batch slot) of each token.
+ * dst_pos      [n_tok] int32, cache position of each token.
+ * rope_pos     [n_tok] int32, RoPE table row of each token (the reference uses
+ *              the chunk-local index t, positional_encoding.py:49-50).
+ * ln_w, ln_b   [R] LayerNorm affine parameters in in_dtype; eps as in torch.
+ * cos_tab,     [rope_len, P/2] in in_dtype: the first P/2 columns of the
+ * sin_tab      reference cos_cached / sin_cached (positional_encoding.py:21-28).
+ * ckv_cache    [cache_batch, cache_seq, R] in cache_dtype (u8 codes for FP8).
+ * kpe_cache    [cache_batch, cache_seq, P] in in_dtype.
+ * ckv_scale    [cache_batch, cache_seq] fp32, written only for FP8 (else NULL).
+ * err_flag     optional device int32; a token whose seq_idx / dst_pos /
+ *              rope_pos lies outside the buffers is skipped and sets it to 1.
+ *
+ * Numerics: LayerNorm statistics are reduced in fp64 in a fixed order and the
+ * result is rounded once to the cache dtype (exactly-rounded LayerNorm).
+ * RoPE rounds after every multiply and add in in_dtype, as eager PyTorch does.
+ * FP8: scale = max(amax, 1e-12) / 448 in fp32, code = RNE(y / scale).
+ */
+int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok,
+               const int32_t* seq_idx, const int32_t* dst_pos,
+               const int32_t* rope_pos, const void* ln_w, const void* ln_b,
+               float eps, const void* cos_tab, const void* sin_tab,
+               int64_t rope_len, void* ckv_cache, void* kpe_cache,
+               float* ckv_scale, int64_t cache_batch, int64_t cache_seq,
+               int32_t* err_flag, int32_t in_dtype, int32_t cache_dtype,
+               int32_t R, int32_t P, void* stream);
+
+/*
+ * mla_decode_attn — absorbed attention of query rows over the latent cache.
+ * Replaces models/mla.py:417-487 (cache gather, wkv_b up-projection of the
+ * whole cache, cat with k_pe, SDPA with scale softmax_scale) by the
+ * re-associated form  s_t = scale * (q_abs . c_t + rope(q_pe) . k_pe_t),
+ * o_lat = sum_t softmax(s)_t c_t.
+ *
+ * Query row r attends to cache row row_seq[r], positions [0, kv_len[r]) (a
+ * prefill token t at start_pos passes kv_len = start_pos + t + 1: causal).
+ * q_abs        row r, head h at q_abs + r*q_abs_rs + h*q_abs_hs, R values.
+ * q_pe         row r, head h at q_pe + r*q_pe_rs + h*q_pe_hs, P values before
+ *              RoPE; rotated in-kernel with table row q_rope_pos[r].
+ * Split-KV: each row is cut into ns = ceil(L / chunk) splits of
+ *   chunk = round_up(max(min_chunk, ceil(L / n_splits)), 64) tokens.
+ * Rows with ns == 1 are written straight to o_lat; others write normalised
+ * partials o_part [n_rows, n_splits, H, R] fp32 and log-sum-exp lse_part
+ * [n_rows, n_splits, H] (natural log of sum exp(s)) for mla_merge.
+ * o_lat        row r, head h at o_lat + r*o_rs + h*o_hs, R values, in dtype.
+ */
+int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
+                    const void* q_pe, int64_t q_pe_rs, int64_t q_pe_hs,
+                    const int32_t* q_rope_pos, const void* cos_tab,
+                    const void* sin_tab, int64_t rope_len,
+                    const void* ckv_cache, const void* kpe_cache,
+                    const float* ckv_scale, int64_t cache_batch,
+                    int64_t cache_seq, const int32_t* row_seq,
+                    const int32_t* kv_len, int32_t n_rows, int32_t H,
+                    int32_t R, int32_t P, float sm_scale, int32_t n_splits,
+                    int32_t min_chunk, float* o_part, float* lse_part,
+                    void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
+                    int32_t cache_dtype, void* stream);
+
+/*
+ * mla_merge — log-sum-exp merge of split-KV partials (no reference
+ * counterpart: the reference attends in one SDPA call, mla.py:581-595).
+ * o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M), M = max_s lse_s, for
+ * every row whose split count (same formula as mla_decode_attn) exceeds 1.
+ * lse_out [n_rows, H] fp32 is optional (NULL = not written).
+ */
+int mla_merge(const float* o_part, const float* lse_part,
+              const int32_t* kv_len, int32_t n_rows, int32_t H, int32_t R,
+              int32_t n_splits, int32_t min_chunk, void* o_lat, int64_t o_rs,
+              int64_t o_hs, float* lse_out, int32_t dtype, void* stream);
+
+/* Split plan used by both kernels, exported so hosts and tests can size the
+ * partial buffers: number of splits of a row of length L (0 for L <= 0). */
+int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SWAMLA_MI355X_H */

@@ -1,0 +1,217 @@
+// mla_abi.cpp — the extern "C" boundary: argument validation, error
+// reporting and dispatch to the gfx950 launchers.  Validation never touches
+// the GPU, so every error path is testable on a machine without one.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/swamla_mi355x.h"
+#include "../../include/swamla_mi355x_testing.h"
+#include "mla_args.h"
+#include "numerics.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return SWAMLA_OK;
+}
+
+bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+int check_geometry(int32_t H, int32_t R, int32_t P) {
+  if (H != 16 || R != 256 || P != 64)
+    return fail(SWAMLA_ERR_UNSUPPORTED,
+                "unsupported geometry H=%d R=%d P=%d (this build: H=16, R=256, P=64)", H, R, P);
+  return SWAMLA_OK;
+}
+
+// Element size of the model (query/output/k_pe) dtype; 0 if not a model dtype.
+int model_elem(int32_t dt) { return dt == SWAMLA_DTYPE_F32 ? 4 : (dt == SWAMLA_DTYPE_BF16 ? 2 : 0); }
+
+int check_pair(int32_t dt, int32_t cdt) {
+  const bool okp = (dt == SWAMLA_DTYPE_BF16 && (cdt == SWAMLA_DTYPE_BF16 || cdt == SWAMLA_DTYPE_FP8)) ||
+                   (dt == SWAMLA_DTYPE_F32 && cdt == SWAMLA_DTYPE_F32);
+  if (!okp)
+    return fail(SWAMLA_ERR_UNSUPPORTED,
+                "unsupported dtype pair model=%d cache=%d (built: bf16/bf16, bf16/fp8, f32/f32)", dt,
+                cdt);
+  return SWAMLA_OK;
+}
+
+int hip_fail(const char* what) {
+  const hipError_t e = hipGetLastError();
+  return fail(SWAMLA_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mla_abi_version(void) { return SWAMLA_ABI_VERSION; }
+
+const char* mla_last_error(void) { return g_err; }
+
+int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk) {
+  if (n_splits < 1 || min_chunk < 1) return 0;
+  int c = (L + n_splits - 1) / n_splits;
+  if (c < min_chunk) c = min_chunk;
+  c = (c + 63) & ~63;
+  return L <= 0 ? 0 : (L + c - 1) / c;
+}
+
+int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const int32_t* seq_idx,
+               const int32_t* dst_pos, const int32_t* rope_pos, const void* ln_w,
+               const void* ln_b, float eps, const void* cos_tab, const void* sin_tab,
+               int64_t rope_len, void* ckv_cache, void* kpe_cache, float* ckv_scale,
+               int64_t cache_batch, int64_t cache_seq, int32_t* err_flag, int32_t in_dtype,
+               int32_t cache_dtype, int32_t R, int32_t P, void* stream) {
+  if (int e = check_geometry(16, R, P)) return e;
+  if (int e = check_pair(in_dtype, cache_dtype)) return e;
+  if (n_tok < 0) return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: n_tok=%d < 0", n_tok);
+  if (n_tok > (1 << 30)) return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: n_tok=%d too large", n_tok);
+  if (!ckv_cache || !kpe_cache || !ln_w || !ln_b || !cos_tab || !sin_tab)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: null cache / LayerNorm / RoPE pointer");
+  if (n_tok > 0 && (!kv_in || !seq_idx || !dst_pos || !rope_pos))
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: null input or index pointer");
+  if (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: fp8 cache needs ckv_scale");
+  if (in_row_stride < R + P)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: in_row_stride=%lld < R+P=%d",
+                (long long)in_row_stride, R + P);
+  if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: bad cache shape [%lld, %lld]",
+                (long long)cache_batch, (long long)cache_seq);
+  if (rope_len < 1) return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: rope_len=%lld < 1", (long long)rope_len);
+  const int es = model_elem(in_dtype);
+  if (!aligned(ckv_cache, 16) || !aligned(kpe_cache, es) || (kv_in && !aligned(kv_in, es)) ||
+      !aligned(ln_w, es) || !aligned(ln_b, es) || !aligned(cos_tab, es) || !aligned(sin_tab, es) ||
+      (ckv_scale && !aligned(ckv_scale, 4)))
+    return fail(SWAMLA_ERR_MISALIGNED, "mla_append: ckv_cache must be 16-byte aligned, others element-aligned");
+  swamla::AppendArgs a{kv_in,   in_row_stride, n_tok,     seq_idx,   dst_pos,     rope_pos,
+                       ln_w,    ln_b,          eps,       cos_tab,   sin_tab,     rope_len,
+                       ckv_cache, kpe_cache,   ckv_scale, cache_batch, cache_seq, err_flag};
+  const int rc = swamla::launch_append(a, in_dtype, cache_dtype, static_cast<hipStream_t>(stream));
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_append: no kernel for this dtype pair");
+  if (rc != 0) return hip_fail("mla_append");
+  return ok();
+}
+
+int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const void* q_pe,
+                    int64_t q_pe_rs, int64_t q_pe_hs, const int32_t* q_rope_pos,
+                    const void* cos_tab, const void* sin_tab, int64_t rope_len,
+                    const void* ckv_cache, const void* kpe_cache, const float* ckv_scale,
+                    int64_t cache_batch, int64_t cache_seq, const int32_t* row_seq,
+                    const int32_t* kv_len, int32_t n_rows, int32_t H, int32_t R, int32_t P,
+                    float sm_scale, int32_t n_splits, int32_t min_chunk, float* o_part,
+                    float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
+                    int32_t cache_dtype, void* stream) {
+  if (int e = check_geometry(H, R, P)) return e;
+  if (int e = check_pair(dtype, cache_dtype)) return e;
+  if (n_rows < 0 || n_rows > 65535)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: n_rows=%d outside [0, 65535]", n_rows);
+  if (n_splits < 1 || n_splits > 1024)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: n_splits=%d outside [1, 1024]", n_splits);
+  if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: min_chunk=%d < 1", min_chunk);
+  if (!(sm_scale > 0.f)) return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: sm_scale must be > 0");
+  if (!ckv_cache || !kpe_cache || !cos_tab || !sin_tab || !o_lat)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: null cache / RoPE / output pointer");
+  if (n_rows > 0 && (!q_abs || !q_pe || !q_rope_pos || !row_seq || !kv_len))
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: null query / index pointer");
+  if (n_splits > 1 && (!o_part || !lse_part))
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: n_splits > 1 needs o_part and lse_part");
+  if (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: fp8 cache needs ckv_scale");
+  if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1 || rope_len < 1)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: bad cache / rope table shape");
+  if (q_abs_hs < R || q_pe_hs < P || o_hs < R || q_abs_rs < 0 || q_pe_rs < 0 || o_rs < 0)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: head strides must cover R / P values");
+  if (dtype == SWAMLA_DTYPE_BF16) {
+    // 16-byte vector loads / stores of 8 bf16.
+    if (!aligned(q_abs, 16) || !aligned(q_pe, 16) || !aligned(o_lat, 16) || !aligned(ckv_cache, 16) ||
+        !aligned(kpe_cache, 16) || (q_abs_rs | q_abs_hs | q_pe_rs | q_pe_hs | o_rs | o_hs) % 8 != 0)
+      return fail(SWAMLA_ERR_MISALIGNED,
+                  "mla_decode_attn: bf16 operands need 16-byte aligned bases and strides that are "
+                  "multiples of 8 elements");
+  } else {
+    if (!aligned(q_abs, 4) || !aligned(q_pe, 4) || !aligned(o_lat, 16) || !aligned(ckv_cache, 4) ||
+        !aligned(kpe_cache, 4) || (o_rs | o_hs) % 4 != 0)
+      return fail(SWAMLA_ERR_MISALIGNED,
+                  "mla_decode_attn: fp32 output needs a 16-byte aligned base and strides that are "
+                  "multiples of 4");
+  }
+  if ((o_part && !aligned(o_part, 16)) || (lse_part && !aligned(lse_part, 4)) ||
+      (ckv_scale && !aligned(ckv_scale, 4)))
+    return fail(SWAMLA_ERR_MISALIGNED, "mla_decode_attn: o_part must be 16-byte aligned");
+  const float log2e = 1.4426950408889634f;
+  swamla::DecodeArgs a{q_abs,    q_abs_rs,  q_abs_hs,    q_pe,     q_pe_rs,   q_pe_hs,
+                       q_rope_pos, cos_tab, sin_tab,     rope_len, ckv_cache, kpe_cache,
+                       ckv_scale, cache_batch, cache_seq, row_seq, kv_len,    n_rows,
+                       sm_scale * log2e, n_splits, min_chunk, o_part, lse_part, o_lat,
+                       o_rs,      o_hs};
+  const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_attn: no kernel for this dtype pair");
+  if (rc != 0) return hip_fail("mla_decode_attn");
+  return ok();
+}
+
+int mla_merge(const float* o_part, const float* lse_part, const int32_t* kv_len, int32_t n_rows,
+              int32_t H, int32_t R, int32_t n_splits, int32_t min_chunk, void* o_lat, int64_t o_rs,
+              int64_t o_hs, float* lse_out, int32_t dtype, void* stream) {
+  if (int e = check_geometry(H, R, 64)) return e;
+  if (!model_elem(dtype)) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: dtype %d not built", dtype);
+  if (n_rows < 0 || n_rows > 65535)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: n_rows=%d outside [0, 65535]", n_rows);
+  if (n_splits < 1 || n_splits > 1024)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: n_splits=%d outside [1, 1024]", n_splits);
+  if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: min_chunk=%d < 1", min_chunk);
+  if (n_splits == 1 || n_rows == 0) return ok();  // nothing to merge
+  if (!o_part || !lse_part || !kv_len || !o_lat)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: null pointer");
+  if (o_hs < R || o_rs < 0) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: bad output strides");
+  const int vec = dtype == SWAMLA_DTYPE_F32 ? 4 : 4;  // 4 channels per lane
+  if (!aligned(o_part, 16) || !aligned(o_lat, dtype == SWAMLA_DTYPE_F32 ? 16 : 8) || (o_rs | o_hs) % vec != 0)
+    return fail(SWAMLA_ERR_MISALIGNED, "mla_merge: misaligned partials or output");
+  swamla::MergeArgs a{o_part, lse_part, kv_len, n_rows, n_splits, min_chunk, o_lat, o_rs, o_hs, lse_out};
+  const int rc = swamla::launch_merge(a, dtype, static_cast<hipStream_t>(stream));
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: no kernel for dtype %d", dtype);
+  if (rc != 0) return hip_fail("mla_merge");
+  return ok();
+}
+
+// ---- host-side test hooks: the kernels' bit-level conversions run on the CPU.
+void mla_host_f32_to_e4m3(const float* x, uint8_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = swamla::f32_to_e4m3(x[i]);
+}
+void mla_host_e4m3_to_f32(const uint8_t* c, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = swamla::e4m3_to_f32(c[i]);
+}
+void mla_host_e4m3x4_to_bf16(const uint32_t* w, uint16_t* out, int64_t n_words) {
+  for (int64_t i = 0; i < n_words; ++i) {
+    uint32_t lo, hi;
+    swamla::e4m3x4_to_bf16x4(w[i], lo, hi);
+    out[4 * i + 0] = lo & 0xFFFF;
+    out[4 * i + 1] = lo >> 16;
+    out[4 * i + 2] = hi & 0xFFFF;
+    out[4 * i + 3] = hi >> 16;
+  }
+}
+void mla_host_f64_to_bf16(const double* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = swamla::f64_to_bf16(x[i]);
+}
+void mla_host_f32_to_bf16(const float* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = swamla::f32_to_bf16(x[i]);
+}
+
+}  // extern "C"

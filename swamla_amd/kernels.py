@@ -1,0 +1,251 @@
+"""Tensor-level wrappers of the three C-ABI kernels.
+
+Each wrapper checks shapes, dtypes and devices of torch tensors, then passes
+raw pointers, strides and torch's current HIP stream to the library.  They
+allocate only the outputs they return (callers that cannot allocate pass
+``out=`` / workspace tensors).  There is no CPU or eager fallback: a tensor
+that is not on a ROCm device is an error.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _abi
+
+R, P, H = 256, 64, 16
+
+
+def _need_gpu(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"swamla_amd kernels run on the GPU only; got a tensor on {t.device}"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    assert dev is not None
+    return dev
+
+
+def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.int32 or not t.is_contiguous() or t.dim() != 1:
+        raise TypeError(f"{name} must be a contiguous 1-D int32 tensor")
+    return t
+
+
+@dataclass
+class LatentCache:
+    """Latent KV cache of one MLA layer.
+
+    ckv   [B, S, R]  model dtype (bf16 / fp32) or uint8 e4m3fn codes
+    kpe   [B, S, P]  model dtype
+    scale [B, S]     fp32 per-token scale (e4m3 caches only)
+    """
+
+    ckv: torch.Tensor
+    kpe: torch.Tensor
+    scale: Optional[torch.Tensor] = None
+
+    @property
+    def is_fp8(self) -> bool:
+        return self.ckv.dtype == torch.uint8
+
+    @property
+    def model_dtype(self) -> torch.dtype:
+        return self.kpe.dtype
+
+    @property
+    def cache_code(self) -> int:
+        return _abi.DTYPE_FP8 if self.is_fp8 else _abi.dtype_code(self.ckv.dtype)
+
+    def validate(self) -> None:
+        c, p = self.ckv, self.kpe
+        if c.dim() != 3 or p.dim() != 3 or c.shape[:2] != p.shape[:2]:
+            raise ValueError(f"cache shapes {tuple(c.shape)} / {tuple(p.shape)} disagree")
+        if c.shape[2] != R or p.shape[2] != P:
+            raise ValueError(f"cache last dims must be R={R}, P={P}")
+        if not (c.is_contiguous() and p.is_contiguous()):
+            raise ValueError("cache buffers must be contiguous")
+        if self.is_fp8:
+            s = self.scale
+            if s is None or s.dtype != torch.float32 or tuple(s.shape) != tuple(c.shape[:2]):
+                raise ValueError("e4m3 cache needs a float32 scale of shape [B, S]")
+            if not s.is_contiguous():
+                raise ValueError("scale must be contiguous")
+        elif c.dtype != p.dtype:
+            raise ValueError(f"latent cache dtype {c.dtype} != k_pe dtype {p.dtype}")
+
+    @staticmethod
+    def allocate(batch: int, seq: int, dtype: torch.dtype, device, fp8: bool = False) -> "LatentCache":
+        if fp8:
+            return LatentCache(
+                torch.zeros(batch, seq, R, dtype=torch.uint8, device=device),
+                torch.zeros(batch, seq, P, dtype=dtype, device=device),
+                torch.zeros(batch, seq, dtype=torch.float32, device=device),
+            )
+        return LatentCache(
+            torch.zeros(batch, seq, R, dtype=dtype, device=device),
+            torch.zeros(batch, seq, P, dtype=dtype, device=device),
+        )
+
+
+def append(
+    kv: torch.Tensor,
+    seq_idx: torch.Tensor,
+    dst_pos: torch.Tensor,
+    rope_pos: torch.Tensor,
+    ln_w: torch.Tensor,
+    ln_b: torch.Tensor,
+    eps: float,
+    cos_tab: torch.Tensor,
+    sin_tab: torch.Tensor,
+    cache: LatentCache,
+    err_flag: Optional[torch.Tensor] = None,
+) -> None:
+    """Fused kv_norm + RoPE(k_pe) + (e4m3) + scatter of ``kv`` rows.
+
+    kv: [N, >=R+P] with unit stride in the last dim (the wkv_a output, or a
+    view of it).  Reference: models/mla.py:307-323, :409-414.
+    """
+    cache.validate()
+    dev = _need_gpu(kv, seq_idx, dst_pos, rope_pos, ln_w, ln_b, cos_tab, sin_tab, cache.ckv)
+    if kv.dim() != 2 or kv.stride(1) != 1 or kv.shape[1] < R + P:
+        raise ValueError("kv must be [N, R+P] with unit last-dim stride")
+    dt = cache.model_dtype
+    if kv.dtype != dt or ln_w.dtype != dt or ln_b.dtype != dt or cos_tab.dtype != dt or sin_tab.dtype != dt:
+        raise TypeError(f"kv / LayerNorm / RoPE tensors must all be {dt}")
+    n = kv.shape[0]
+    for name, t in (("seq_idx", seq_idx), ("dst_pos", dst_pos), ("rope_pos", rope_pos)):
+        _i32(t, name)
+        if t.numel() != n:
+            raise ValueError(f"{name} has {t.numel()} entries, expected {n}")
+    if not (ln_w.is_contiguous() and ln_b.is_contiguous() and ln_w.numel() == R and ln_b.numel() == R):
+        raise ValueError("LayerNorm weight / bias must be contiguous [R]")
+    if cos_tab.dim() != 2 or cos_tab.shape[1] != P // 2 or cos_tab.shape != sin_tab.shape:
+        raise ValueError("RoPE tables must be [S, P/2]")
+    if not (cos_tab.is_contiguous() and sin_tab.is_contiguous()):
+        raise ValueError("RoPE tables must be contiguous")
+    lib = _abi.lib()
+    _abi.check(
+        lib.mla_append(
+            kv.data_ptr(), kv.stride(0), n, seq_idx.data_ptr(), dst_pos.data_ptr(),
+            rope_pos.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), float(eps),
+            cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+            cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
+            cache.ckv.shape[0], cache.ckv.shape[1], _abi.ptr(err_flag),
+            _abi.dtype_code(dt), cache.cache_code, R, P, _abi.stream_handle(dev),
+        )
+    )
+
+
+def plan_splits(n_rows: int, max_len: int, num_cus: int = 256, waves: int = 2,
+                min_chunk: int = 256) -> tuple[int, int]:
+    """Host heuristic for the split-KV plan: about ``waves`` blocks per CU.
+
+    Returns (n_splits, min_chunk).  The kernels derive each row's own split
+    count from its length on the device, so ``max_len`` may be an upper bound.
+    """
+    if n_rows <= 0:
+        return 1, min_chunk
+    target = max(1, (num_cus * waves + n_rows - 1) // n_rows)
+    by_len = max(1, (max_len + min_chunk - 1) // min_chunk)
+    return int(max(1, min(target, by_len, 1024))), int(min_chunk)
+
+
+@dataclass
+class DecodeWorkspace:
+    """Split-KV partial buffers: o_part [rows, splits, H, R], lse [rows, splits, H]."""
+
+    o_part: torch.Tensor
+    lse_part: torch.Tensor
+
+    @staticmethod
+    def allocate(n_rows: int, n_splits: int, device) -> "DecodeWorkspace":
+        return DecodeWorkspace(
+            torch.empty(max(n_rows, 1), n_splits, H, R, dtype=torch.float32, device=device),
+            torch.empty(max(n_rows, 1), n_splits, H, dtype=torch.float32, device=device),
+        )
+
+    def fits(self, n_rows: int, n_splits: int) -> bool:
+        return self.o_part.shape[0] >= n_rows and self.o_part.shape[1] == n_splits
+
+
+def decode_attention(
+    q_abs: torch.Tensor,
+    q_pe: torch.Tensor,
+    q_rope_pos: torch.Tensor,
+    cos_tab: torch.Tensor,
+    sin_tab: torch.Tensor,
+    cache: LatentCache,
+    row_seq: torch.Tensor,
+    kv_len: torch.Tensor,
+    sm_scale: float,
+    n_splits: int = 1,
+    min_chunk: int = 256,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[DecodeWorkspace] = None,
+    lse_out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Absorbed attention of query rows over the latent cache (+ merge).
+
+    q_abs [rows, H, R] and q_pe [rows, H, P] may be strided views (unit last
+    stride).  Returns o_lat [rows, H, R] (``out`` may be a strided view, e.g.
+    a transpose of a [H, rows, R] buffer).  Reference: models/mla.py:417-487.
+    """
+    cache.validate()
+    dev = _need_gpu(q_abs, q_pe, q_rope_pos, cos_tab, sin_tab, cache.ckv, row_seq, kv_len)
+    dt = cache.model_dtype
+    rows = q_abs.shape[0]
+    if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (H, R) or q_abs.stride(2) != 1:
+        raise ValueError(f"q_abs must be [rows, {H}, {R}] with unit last stride")
+    if q_pe.dim() != 3 or tuple(q_pe.shape) != (rows, H, P) or q_pe.stride(2) != 1:
+        raise ValueError(f"q_pe must be [rows, {H}, {P}] with unit last stride")
+    if q_abs.dtype != dt or q_pe.dtype != dt or cos_tab.dtype != dt:
+        raise TypeError(f"query and RoPE tensors must be {dt}")
+    for name, t in (("q_rope_pos", q_rope_pos), ("row_seq", row_seq), ("kv_len", kv_len)):
+        _i32(t, name)
+        if t.numel() != rows:
+            raise ValueError(f"{name} has {t.numel()} entries, expected {rows}")
+    if out is None:
+        out = torch.empty(rows, H, R, dtype=dt, device=dev)
+    if tuple(out.shape) != (rows, H, R) or out.stride(2) != 1 or out.dtype != dt:
+        raise ValueError("out must be [rows, H, R] in the model dtype with unit last stride")
+    if n_splits > 1:
+        if workspace is None:
+            workspace = DecodeWorkspace.allocate(rows, n_splits, dev)
+        if not workspace.fits(rows, n_splits):
+            raise ValueError("workspace too small for (rows, n_splits)")
+    lib = _abi.lib()
+    stream = _abi.stream_handle(dev)
+    _abi.check(
+        lib.mla_decode_attn(
+            q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1),
+            q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
+            q_rope_pos.data_ptr(), cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+            cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
+            cache.ckv.shape[0], cache.ckv.shape[1],
+            row_seq.data_ptr(), kv_len.data_ptr(), rows, H, R, P, float(sm_scale),
+            n_splits, min_chunk,
+            _abi.ptr(workspace.o_part if workspace else None),
+            _abi.ptr(workspace.lse_part if workspace else None),
+            out.data_ptr(), out.stride(0), out.stride(1),
+            _abi.dtype_code(dt), cache.cache_code, stream,
+        )
+    )
+    if n_splits > 1:
+        _abi.check(
+            lib.mla_merge(
+                workspace.o_part.data_ptr(), workspace.lse_part.data_ptr(), kv_len.data_ptr(),
+                rows, H, R, n_splits, min_chunk, out.data_ptr(), out.stride(0), out.stride(1),
+                _abi.ptr(lse_out), _abi.dtype_code(dt), stream,
+            )
+        )
+    return out

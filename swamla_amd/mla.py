@@ -1,0 +1,343 @@
+"""Drop-in ``MLA`` module whose inference path runs on the MI355X kernels.
+
+Reference: models/mla.py:53-693 (Orolol/swamla).  Constructor, attribute and
+parameter names (``wq`` | ``wq_a``/``q_norm``/``wq_b``, ``wkv_a``,
+``kv_norm``, ``wkv_b``, ``wo``), ``forward(x, start_pos, ...)``,
+``set_inference_mode`` and ``clear_cache`` follow the reference so state
+dicts load unchanged and callers need no edits.
+
+What runs where (per forward):
+  ATen GEMMs   wq / wkv_a / wo and the two per-head absorption products
+               q_abs = q_nope . W_uk   and   o = o_lat . W_uv^T
+  HIP kernels  mla_append (kv_norm + RoPE(k_pe) + e4m3 + scatter) and
+               mla_decode_attn + mla_merge (attention over the latent cache)
+
+Differences from the reference, all deliberate:
+  * attention is absorbed: the reference re-projects the whole cache through
+    wkv_b every step (mla.py:427-437); here the query is projected into the
+    latent space instead (same maths, re-associated, bf16 tolerance);
+  * ``start_pos`` may also be an int tensor [B] (per-sequence positions,
+    ragged batches); the reference takes one int for the whole batch;
+  * chunked prefill (T > 1 at start_pos > 0) is causal bottom-right; the
+    reference's SDPA ``is_causal`` is top-left there (mla.py:483);
+  * caches are allocated in the module's dtype and device (the reference
+    allocates fp32 on the default device, mla.py:207-215);
+  * ``cache_dtype="fp8_e4m3"`` stores the latent as e4m3fn codes with one
+    fp32 scale per token (``kv_scale``);
+  * ``clear_cache()`` also leaves inference mode, so the next
+    ``set_inference_mode(True)`` reallocates (the reference leaves None
+    caches behind and its next forward fails);
+  * the training / autograd path, ``mask``, ``position_ids`` and
+    ``cu_seqlens`` backends and ``attn_impl="naive"`` are not part of this
+    path and raise ``NotImplementedError``.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Union
+
+import torch
+import torch.nn as nn
+
+from . import kernels
+from .kernels import DecodeWorkspace, LatentCache
+from .rope import RoPE
+
+RopeMode = str  # "chunk" (reference: positions 0..T-1 of the call) or "absolute"
+
+
+class MLA(nn.Module):
+    def __init__(self, config, cache_dtype: Optional[str] = None, rope_positions: Optional[str] = None):
+        super().__init__()
+        # --- mla.py:73-118: dimensions, projections, scale
+        self.dim = config.n_embd if hasattr(config, "n_embd") else config.dim
+        self.n_heads = config.n_head if hasattr(config, "n_head") else config.n_heads
+        self.world_size = getattr(config, "world_size", 1)
+        self.n_local_heads = self.n_heads // self.world_size
+        self.q_lora_rank = getattr(config, "q_lora_rank", 0)
+        self.kv_lora_rank = getattr(config, "kv_lora_rank", 512)
+        self.qk_nope_head_dim = getattr(config, "qk_nope_head_dim", 128)
+        self.qk_rope_head_dim = getattr(config, "qk_rope_head_dim", 64)
+        self.qk_head_dim = self.qk_nope_head_dim + self.qk_rope_head_dim
+        self.v_head_dim = getattr(config, "v_head_dim", 128)
+        self.dropout = getattr(config, "dropout", 0.0)
+        bias = config.bias if hasattr(config, "bias") else False
+
+        if self.q_lora_rank == 0:
+            self.wq = nn.Linear(self.dim, self.n_heads * self.qk_head_dim, bias=bias)
+        else:
+            self.wq_a = nn.Linear(self.dim, self.q_lora_rank, bias=bias)
+            self.q_norm = nn.LayerNorm(self.q_lora_rank)
+            self.wq_b = nn.Linear(self.q_lora_rank, self.n_heads * self.qk_head_dim, bias=bias)
+        self.wkv_a = nn.Linear(self.dim, self.kv_lora_rank + self.qk_rope_head_dim, bias=bias)
+        self.kv_norm = nn.LayerNorm(self.kv_lora_rank)
+        self.wkv_b = nn.Linear(
+            self.kv_lora_rank, self.n_heads * (self.qk_nope_head_dim + self.v_head_dim), bias=bias
+        )
+        self.wo = nn.Linear(self.n_heads * self.v_head_dim, self.dim, bias=bias)
+        self.attn_dropout = nn.Dropout(self.dropout)
+        self.resid_dropout = nn.Dropout(self.dropout)
+
+        self.softmax_scale = self.qk_head_dim ** -0.5
+        rope_factor = getattr(config, "rope_factor", 1.0)
+        if rope_factor > 1.0 and hasattr(config, "original_seq_len") and hasattr(config, "max_seq_len"):
+            if config.max_seq_len > config.original_seq_len:  # mla.py:121-126
+                mscale = getattr(config, "mscale", 1.0)
+                mscale = 0.1 * mscale * math.log(rope_factor) + 1.0
+                self.softmax_scale = self.softmax_scale * mscale * mscale
+
+        # --- mla.py:130-132, :172: cache geometry and RoPE (base 10000)
+        self.max_batch_size = getattr(config, "max_batch_size", 8)
+        self.max_seq_len = getattr(config, "max_seq_len", 4096)
+        self.attn_impl = getattr(config, "attn_impl", "absorb")
+        self.rope = RoPE(self.qk_rope_head_dim, self.max_seq_len)
+
+        self.cache_dtype = cache_dtype if cache_dtype is not None else getattr(config, "kv_cache_dtype", None)
+        if self.cache_dtype not in (None, "model", "fp8_e4m3"):
+            raise ValueError(f"cache_dtype must be None/'model' or 'fp8_e4m3', got {self.cache_dtype!r}")
+        self.rope_positions: RopeMode = rope_positions or getattr(config, "rope_positions", "chunk")
+        if self.rope_positions not in ("chunk", "absolute"):
+            raise ValueError("rope_positions must be 'chunk' or 'absolute'")
+
+        self.inference_mode = False
+        self.k_cache = None
+        self.v_cache = None
+        self.kv_cache = None
+        self.pe_cache = None
+        self.kv_scale = None
+        self._absorbed = None  # (key, W_uk [H,nope,R], W_uv^T [H,R,v])
+        self._workspace: Optional[DecodeWorkspace] = None
+        self._num_cus: Optional[int] = None
+
+    # ------------------------------------------------------------------ cache
+    @property
+    def fp8_cache(self) -> bool:
+        return self.cache_dtype == "fp8_e4m3"
+
+    def _param_like(self) -> torch.Tensor:
+        return self.wkv_a.weight
+
+    def set_inference_mode(self, mode: bool = True) -> None:
+        """mla.py:184-225: allocate (True) or delete (False) the latent cache."""
+        if mode == self.inference_mode:
+            return
+        self.inference_mode = mode
+        if mode:
+            # __init__ assigns plain None attributes; register_buffer refuses to
+            # replace those (the reference's set_inference_mode raises KeyError
+            # here, mla.py:180-182 vs :209), so drop them first.
+            for name in ("kv_cache", "pe_cache", "kv_scale"):
+                if name in self.__dict__ and self.__dict__[name] is None:
+                    del self.__dict__[name]
+            if self.attn_impl == "naive":
+                raise NotImplementedError("attn_impl='naive' (full K/V cache) is not built")
+            p = self._param_like()
+            if getattr(self, "kv_cache", None) is None:
+                shape = (self.max_batch_size, self.max_seq_len)
+                if self.fp8_cache:
+                    self.register_buffer(
+                        "kv_cache",
+                        torch.zeros(*shape, self.kv_lora_rank, dtype=torch.uint8, device=p.device),
+                        persistent=False,
+                    )
+                    self.register_buffer(
+                        "kv_scale", torch.zeros(*shape, dtype=torch.float32, device=p.device), persistent=False
+                    )
+                else:
+                    self.register_buffer(
+                        "kv_cache",
+                        torch.zeros(*shape, self.kv_lora_rank, dtype=p.dtype, device=p.device),
+                        persistent=False,
+                    )
+            if getattr(self, "pe_cache", None) is None:
+                self.register_buffer(
+                    "pe_cache",
+                    torch.zeros(
+                        self.max_batch_size, self.max_seq_len, self.qk_rope_head_dim, dtype=p.dtype, device=p.device
+                    ),
+                    persistent=False,
+                )
+        else:
+            for name in ("k_cache", "v_cache", "kv_cache", "pe_cache", "kv_scale"):
+                if hasattr(self, name):
+                    delattr(self, name)
+
+    def clear_cache(self) -> None:
+        """mla.py:685-693, and leave inference mode so caches are reallocated."""
+        for name in ("k_cache", "v_cache", "kv_cache", "pe_cache", "kv_scale"):
+            if name in self._buffers:
+                del self._buffers[name]
+            setattr(self, name, None)
+        self.inference_mode = False
+        self._workspace = None
+
+    def _apply(self, fn, recurse=True):
+        # The e4m3 scale stays fp32 whatever dtype the module is cast to; it
+        # only follows the module's device.
+        scale = self._buffers.pop("kv_scale", None)
+        try:
+            out = super()._apply(fn, recurse)
+        finally:
+            if scale is not None:
+                moved = fn(scale)
+                self._buffers["kv_scale"] = scale.to(device=moved.device)
+        return out
+
+    def latent_cache(self) -> LatentCache:
+        """The module's cache buffers as a kernel-level ``LatentCache``."""
+        if self.kv_cache is None or self.pe_cache is None:
+            raise RuntimeError("no latent cache: call set_inference_mode(True) first")
+        dt = self._param_like().dtype
+        if self.pe_cache.dtype != dt or (not self.fp8_cache and self.kv_cache.dtype != dt):
+            raise RuntimeError(
+                f"cache dtype ({self.kv_cache.dtype}/{self.pe_cache.dtype}) does not match the "
+                f"parameters ({dt}); convert the module before set_inference_mode(True)"
+            )
+        return LatentCache(self.kv_cache, self.pe_cache, self.kv_scale if self.fp8_cache else None)
+
+    # ------------------------------------------------------------- weights
+    def absorbed_weights(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """W_uk [H, nope, R] and W_uv^T [H, R, v] from wkv_b (mla.py:404-406, :427, :433)."""
+        w = self.wkv_b.weight
+        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        if self._absorbed is None or self._absorbed[0] != key:
+            wv = w.detach().view(self.n_heads, -1, self.kv_lora_rank)
+            w_uk = wv[:, : self.qk_nope_head_dim].contiguous()
+            w_uv_t = wv[:, -self.v_head_dim:].transpose(1, 2).contiguous()
+            self._absorbed = (key, w_uk, w_uv_t)
+        return self._absorbed[1], self._absorbed[2]
+
+    def _check_geometry(self) -> None:
+        if (self.n_heads, self.kv_lora_rank, self.qk_rope_head_dim) != (kernels.H, kernels.R, kernels.P):
+            raise NotImplementedError(
+                f"kernels are built for n_heads={kernels.H}, kv_lora_rank={kernels.R}, "
+                f"qk_rope_head_dim={kernels.P}; got {self.n_heads}, {self.kv_lora_rank}, "
+                f"{self.qk_rope_head_dim}"
+            )
+
+    def _split_plan(self, n_rows: int, max_len: int, device) -> tuple[int, int]:
+        if self._num_cus is None:
+            self._num_cus = torch.cuda.get_device_properties(device).multi_processor_count
+        return kernels.plan_splits(n_rows, max_len, num_cus=self._num_cus)
+
+    def _workspace_for(self, n_rows: int, n_splits: int, device) -> Optional[DecodeWorkspace]:
+        if n_splits <= 1:
+            return None
+        ws = self._workspace
+        if ws is None or not ws.fits(n_rows, n_splits) or ws.o_part.device != device:
+            ws = DecodeWorkspace.allocate(n_rows, n_splits, device)
+            self._workspace = ws
+        return ws
+
+    # ------------------------------------------------------------- forward
+    def forward(
+        self,
+        x: torch.Tensor,
+        start_pos: Union[int, torch.Tensor],
+        freqs_cis: Optional[torch.Tensor] = None,
+        mask: Optional[torch.Tensor] = None,
+        position_ids: Optional[torch.Tensor] = None,
+        cu_seqlens: Optional[torch.Tensor] = None,
+        max_seqlen: Optional[int] = None,
+    ) -> torch.Tensor:
+        """mla.py:232-495 (absorb branch).  ``freqs_cis`` is ignored exactly as
+        in the reference's RoPE call (positional_encoding.py:30-34)."""
+        if self.training and self.inference_mode:  # mla.py:274-275
+            self.set_inference_mode(False)
+        if mask is not None or position_ids is not None or cu_seqlens is not None:
+            raise NotImplementedError("mask / position_ids / cu_seqlens backends are not part of this path")
+        if self.attn_impl != "absorb":
+            raise NotImplementedError(f"attn_impl={self.attn_impl!r} is not built")
+        if torch.is_grad_enabled() and x.requires_grad:
+            raise NotImplementedError("the training / autograd path is not part of this build")
+        if x.device.type != "cuda":
+            raise RuntimeError("swamla_amd.MLA runs on the GPU only (no CPU fallback)")
+        self._check_geometry()
+        with torch.no_grad():
+            return self._forward_kernels(x, start_pos)
+
+    def prefill_cache(self, x: torch.Tensor, start_pos: Union[int, torch.Tensor] = 0) -> None:
+        """Append path only (wkv_a GEMM + fused append kernel), no attention:
+        writes the latent / k_pe rows of the T tokens of ``x`` into the cache,
+        exactly as ``forward`` would (mla.py:307-323, :409-414)."""
+        if not self.inference_mode:
+            raise RuntimeError("prefill_cache needs set_inference_mode(True)")
+        if x.device.type != "cuda":
+            raise RuntimeError("swamla_amd.MLA runs on the GPU only (no CPU fallback)")
+        self._check_geometry()
+        B, T, _ = x.size()
+        cache = self.latent_cache()
+        if not isinstance(start_pos, torch.Tensor) and (start_pos < 0 or start_pos + T > cache.ckv.shape[1]):
+            raise ValueError(f"start_pos {start_pos} + seqlen {T} exceeds max_seq_len {cache.ckv.shape[1]}")
+        with torch.no_grad():
+            b_idx, dst, rope_pos, _, _ = self._positions(B, T, start_pos, x.device)
+            kv = self.wkv_a(x).view(B * T, -1)
+            cos, sin = self.rope.half_tables()
+            kernels.append(kv, b_idx, dst, rope_pos, self.kv_norm.weight, self.kv_norm.bias,
+                           self.kv_norm.eps, cos, sin, cache)
+
+    def _positions(self, B: int, T: int, start_pos, device):
+        """int32 index vectors of the B*T new tokens (token i = b*T + t)."""
+        t_idx = torch.arange(T, dtype=torch.int32, device=device).repeat(B)
+        b_idx = torch.arange(B, dtype=torch.int32, device=device).repeat_interleave(T)
+        if isinstance(start_pos, torch.Tensor):
+            sp = start_pos.to(device=device, dtype=torch.int32).reshape(-1)
+            if sp.numel() != B:
+                raise ValueError(f"start_pos tensor has {sp.numel()} entries for batch {B}")
+            dst = sp.repeat_interleave(T) + t_idx if T > 1 else sp.clone()
+            max_len = self.max_seq_len
+        else:
+            sp = int(start_pos)
+            dst = t_idx + sp
+            max_len = sp + T
+        rope = t_idx if self.rope_positions == "chunk" else dst
+        return b_idx, dst, rope, dst + 1, max_len
+
+    def _forward_kernels(self, x: torch.Tensor, start_pos) -> torch.Tensor:
+        B, T, _ = x.size()
+        dev = x.device
+        H, R, Dn, Dv = self.n_heads, self.kv_lora_rank, self.qk_nope_head_dim, self.v_head_dim
+        n = B * T
+
+        if self.inference_mode:
+            cache = self.latent_cache()
+            if B > cache.ckv.shape[0]:
+                raise ValueError(f"batch {B} exceeds max_batch_size {cache.ckv.shape[0]}")
+            if not isinstance(start_pos, torch.Tensor) and (start_pos < 0 or start_pos + T > cache.ckv.shape[1]):
+                raise ValueError(
+                    f"start_pos {start_pos} + seqlen {T} exceeds max_seq_len {cache.ckv.shape[1]}"
+                )
+            b_idx, dst, rope_pos, kv_len, max_len = self._positions(B, T, start_pos, dev)
+        else:
+            # No cache (mla.py:419-423): attend over this call's tokens only.
+            cache = LatentCache.allocate(B, T, x.dtype, dev, fp8=self.fp8_cache)
+            b_idx, dst, rope_pos, kv_len, max_len = self._positions(B, T, 0, dev)
+            if self.rope_positions == "absolute" and isinstance(start_pos, int):
+                rope_pos = rope_pos + start_pos
+
+        if self.q_lora_rank == 0:  # mla.py:281-288
+            q = self.wq(x)
+        else:
+            q = self.wq_b(self.q_norm(self.wq_a(x)))
+        q = q.view(n, H, self.qk_head_dim)
+        kv = self.wkv_a(x).view(n, -1)  # mla.py:307-308
+
+        cos, sin = self.rope.half_tables()
+        kernels.append(
+            kv, b_idx, dst, rope_pos, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps,
+            cos, sin, cache,
+        )
+
+        w_uk, w_uv_t = self.absorbed_weights()
+        q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]
+        q_abs = torch.bmm(q_nope, w_uk)  # [H, n, R]
+        o_lat = torch.empty(H, n, R, dtype=x.dtype, device=dev)
+        n_splits, min_chunk = self._split_plan(n, max_len, dev)
+        kernels.decode_attention(
+            q_abs.transpose(0, 1), q[:, :, Dn:], rope_pos, cos, sin, cache, b_idx, kv_len,
+            self.softmax_scale, n_splits=n_splits, min_chunk=min_chunk,
+            out=o_lat.transpose(0, 1), workspace=self._workspace_for(n, n_splits, dev),
+        )
+        o = torch.bmm(o_lat, w_uv_t)  # [H, n, Dv]
+        out = o.transpose(0, 1).reshape(B, T, H * Dv)
+        return self.resid_dropout(self.wo(out))  # mla.py:490-495

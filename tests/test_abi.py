@@ -1,0 +1,194 @@
+"""C-ABI and host-side checks that need no GPU: the library loads, exports
+every symbol the headers declare, and rejects bad arguments before any HIP
+call; the drop-in module mirrors the reference's interface."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+import torch
+
+from swamla_amd import _abi
+from swamla_amd.mla import MLA
+from oracle.mla_ref import MLAConfig, RefMLA, init_weights
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE = 0x10000  # a 16-byte aligned non-null address; never dereferenced
+
+
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[\w]+\s*\*?\s*(mla_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert {"mla_append", "mla_decode_attn", "mla_merge", "mla_abi_version", "mla_last_error"} <= names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(_abi.EXPORTED_SYMBOLS) == names
+
+
+def test_abi_version(lib):
+    assert lib.mla_abi_version() == _abi.ABI_VERSION == 1
+
+
+def _append(lib, **kw):
+    args = dict(kv_in=FAKE, in_rs=320, n_tok=4, seq=FAKE, dst=FAKE, rope=FAKE, w=FAKE, b=FAKE, eps=1e-5,
+                cos=FAKE, sin=FAKE, rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, err=None,
+                in_dt=1, c_dt=1, R=256, P=64, stream=None)
+    args.update(kw)
+    return lib.mla_append(*args.values())
+
+
+def _decode(lib, **kw):
+    args = dict(qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, qrp=FAKE, cos=FAKE, sin=FAKE,
+                rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, row_seq=FAKE, kv_len=FAKE, n_rows=2,
+                H=16, R=256, P=64, sm=0.07, ns=1, mc=64, o_part=None, lse=None, o=FAKE, o_rs=4096, o_hs=256,
+                dt=1, c_dt=1, stream=None)
+    args.update(kw)
+    return lib.mla_decode_attn(*args.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(R=128), -2),
+        (dict(P=32), -2),
+        (dict(in_dt=0, c_dt=1), -2),
+        (dict(in_dt=2, c_dt=2), -2),
+        (dict(n_tok=-1), -1),
+        (dict(ckv=None), -1),
+        (dict(seq=None), -1),
+        (dict(c_dt=2), -1),  # fp8 without a scale buffer
+        (dict(in_rs=100), -1),
+        (dict(cs=0), -1),
+        (dict(rope_len=0), -1),
+        (dict(ckv=FAKE + 8), -3),
+    ],
+)
+def test_append_rejects(lib, kw, code):
+    assert _append(lib, **kw) == code
+    assert lib.mla_last_error().decode()
+
+
+def test_append_zero_tokens_is_a_noop(lib):
+    # n_tok = 0 returns before any launch (no GPU needed)
+    assert _append(lib, n_tok=0, kv_in=None, seq=None, dst=None, rope=None) == 0
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(H=8), -2),
+        (dict(R=512), -2),
+        (dict(dt=1, c_dt=0), -2),
+        (dict(n_rows=70000), -1),
+        (dict(ns=0), -1),
+        (dict(ns=2000), -1),
+        (dict(ns=4), -1),  # no partial buffers
+        (dict(mc=0), -1),
+        (dict(sm=0.0), -1),
+        (dict(sm=float("nan")), -1),
+        (dict(o=None), -1),
+        (dict(qa_hs=100), -1),
+        (dict(c_dt=2), -1),
+        (dict(qa=FAKE + 4), -3),
+        (dict(o_rs=4100), -3),
+        (dict(qp_hs=196), -3),
+    ],
+)
+def test_decode_rejects(lib, kw, code):
+    assert _decode(lib, **kw) == code
+    assert lib.mla_last_error().decode()
+
+
+def test_merge_rejects_and_noop(lib):
+    assert lib.mla_merge(FAKE, FAKE, FAKE, 2, 16, 256, 1, 64, FAKE, 4096, 256, None, 1, None) == 0
+    assert lib.mla_merge(FAKE, FAKE, FAKE, 2, 16, 128, 4, 64, FAKE, 4096, 256, None, 1, None) == -2
+    assert lib.mla_merge(None, FAKE, FAKE, 2, 16, 256, 4, 64, FAKE, 4096, 256, None, 1, None) == -1
+    assert lib.mla_merge(FAKE, FAKE, FAKE, 2, 16, 256, 4, 64, FAKE, 4096, 256, None, 2, None) == -2
+    assert lib.mla_merge(FAKE + 4, FAKE, FAKE, 2, 16, 256, 4, 64, FAKE, 4096, 256, None, 1, None) == -3
+
+
+def test_python_check_raises_with_message(lib):
+    rc = _append(lib, R=128)
+    with pytest.raises(_abi.SwamlaError, match="UNSUPPORTED.*R=128"):
+        _abi.check(rc)
+    with pytest.raises(RuntimeError):
+        _abi.check(rc)
+
+
+# ---------------------------------------------------------------- module
+def small_cfg(**kw):
+    d = dict(n_embd=128, max_batch_size=2, max_seq_len=32)
+    d.update(kw)
+    return MLAConfig(**d)
+
+
+def test_state_dict_interchanges_with_reference():
+    ref = RefMLA(small_cfg())
+    init_weights(ref, 0, ln_random=True)
+    ours = MLA(small_cfg())
+    ours.load_state_dict(ref.state_dict())
+    assert list(ours.state_dict().keys()) == list(ref.state_dict().keys())
+    for k, v in ref.state_dict().items():
+        assert torch.equal(ours.state_dict()[k], v)
+    assert ours.softmax_scale == ref.softmax_scale == 192 ** -0.5
+
+
+def test_rope_table_bitwise_equal_to_reference():
+    ref = RefMLA(small_cfg(max_seq_len=300)).to(torch.bfloat16)
+    ours = MLA(small_cfg(max_seq_len=300)).to(torch.bfloat16)
+    assert torch.equal(ours.rope.cos_cached, ref.rope.cos_cached)
+    assert torch.equal(ours.rope.sin_cached, ref.rope.sin_cached)
+    cos, sin = ours.rope.half_tables()
+    assert cos.shape == (300, 32) and torch.equal(cos, ref.rope.cos_cached[0, 0, :, :32])
+
+
+def test_inference_mode_allocation_and_clear():
+    m = MLA(small_cfg()).to(torch.bfloat16)
+    m.set_inference_mode(True)  # works directly (the reference's raises KeyError)
+    assert m.kv_cache.shape == (2, 32, 256) and m.kv_cache.dtype == torch.bfloat16
+    assert m.pe_cache.shape == (2, 32, 64) and m.pe_cache.dtype == torch.bfloat16
+    assert "kv_cache" not in m.state_dict()  # persistent=False as in mla.py:207-215
+    m.set_inference_mode(False)
+    assert not hasattr(m, "kv_cache")
+    m.set_inference_mode(True)
+    m.clear_cache()
+    assert m.kv_cache is None and m.inference_mode is False
+    m.set_inference_mode(True)
+    assert m.kv_cache is not None
+
+
+def test_fp8_cache_scale_stays_fp32():
+    m = MLA(small_cfg(), cache_dtype="fp8_e4m3")
+    m.set_inference_mode(True)
+    assert m.kv_cache.dtype == torch.uint8 and m.kv_scale.dtype == torch.float32
+    m.to(torch.bfloat16)
+    assert m.kv_cache.dtype == torch.uint8 and m.kv_scale.dtype == torch.float32
+    assert m.pe_cache.dtype == torch.bfloat16
+
+
+def test_no_cpu_fallback():
+    m = MLA(small_cfg()).eval()
+    m.set_inference_mode(True)
+    with torch.no_grad(), pytest.raises(RuntimeError, match="GPU only"):
+        m(torch.randn(1, 1, 128), 0)
+
+
+def test_unsupported_paths_raise():
+    m = MLA(small_cfg()).eval()
+    x = torch.randn(1, 2, 128)
+    with pytest.raises(NotImplementedError):
+        m(x, 0, mask=torch.zeros(2, 2))
+    with pytest.raises(NotImplementedError):
+        m(x, 0, position_ids=torch.zeros(1, 2, dtype=torch.long))
+    with pytest.raises(NotImplementedError):
+        m(x.requires_grad_(), 0)

@@ -1,0 +1,227 @@
+"""GPU parity of the three kernels against the oracle (oracle/latent_ops.py).
+
+Bars: cache contents bit-exact (exactly-rounded LayerNorm, per-op-rounded
+RoPE, torch's e4m3 cast, scatter); attention outputs within 2e-2 relative /
+1e-2 absolute in bf16 (the north_star tolerance), 1e-4 in fp32.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import latent_ops as lo
+from swamla_amd import kernels
+from swamla_amd.kernels import DecodeWorkspace, LatentCache
+from swamla_amd.rope import rope_tables
+
+pytestmark = pytest.mark.gpu
+
+R, P, H = 256, 64, 16
+SCALE = 192 ** -0.5
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def tables(dtype, S, device):
+    cos, sin = rope_tables(64, S)
+    return (cos.to(dtype)[0, 0, :, :32].contiguous().to(device), sin.to(dtype)[0, 0, :, :32].contiguous().to(device))
+
+
+def close(out, ref, rtol, atol):
+    out, ref = out.double().cpu(), ref.double().cpu()
+    err = (out - ref).abs()
+    lim = atol + rtol * ref.abs()
+    bad = err > lim
+    assert not bool(bad.any()), f"{int(bad.sum())} / {bad.numel()} outside tol; max err {float(err.max()):.3e}"
+
+
+# ------------------------------------------------------------------ append
+def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0):
+    say(f"append case dtype={dtype} fp8={fp8} n_tok={n_tok}")
+    g = torch.Generator().manual_seed(seed)
+    kv = torch.randn(n_tok, 336, generator=g) * 2 + 0.3  # row stride 336 > 320
+    kv = kv.to(dtype)
+    w = (1 + 0.1 * torch.randn(R, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(R, generator=g)).to(dtype)
+    seq = torch.randint(0, B, (n_tok,), generator=g, dtype=torch.int32)
+    # distinct destination per token: a random permutation of the (b, pos) grid
+    flat = torch.randperm(B * S, generator=g)[:n_tok]
+    seq = (flat // S).to(torch.int32)
+    dst = (flat % S).to(torch.int32)
+    rp = torch.randint(0, S, (n_tok,), generator=g, dtype=torch.int32)
+    cache = LatentCache.allocate(B, S, dtype, gpu, fp8=fp8)
+    canary_c = torch.randint(0, 255, cache.ckv.shape, generator=g).to(torch.uint8) if fp8 else \
+        torch.randn(cache.ckv.shape, generator=g).to(dtype)
+    canary_p = torch.randn(cache.kpe.shape, generator=g).to(dtype)
+    cache.ckv.copy_(canary_c)
+    cache.kpe.copy_(canary_p)
+    if fp8:
+        cache.scale.fill_(-1.0)
+    cos, sin = tables(dtype, S, gpu)
+    kvg = kv.to(gpu)
+    kernels.append(kvg[:, :], seq.to(gpu), dst.to(gpu), rp.to(gpu), w.to(gpu), b.to(gpu), 1e-5, cos, sin, cache)
+    torch.cuda.synchronize()
+
+    # expected rows
+    y = lo.layernorm_exact(kv[:, :R].float().numpy(), w.float().numpy(), b.float().numpy(), 1e-5,
+                           torch.bfloat16 if fp8 else dtype)
+    cos_c, sin_c = cos.cpu(), sin.cpu()
+    kpe = lo.rope_interleaved(kv[:, R:R + P], cos_c[rp.long()], sin_c[rp.long()])
+    exp_c = canary_c.clone()
+    exp_p = canary_p.clone()
+    if fp8:
+        codes, scale = lo.fp8_quantize(y)
+        exp_c[seq.long(), dst.long()] = codes
+        exp_s = torch.full((B, S), -1.0)
+        exp_s[seq.long(), dst.long()] = scale
+        assert torch.equal(cache.scale.cpu(), exp_s), "fp8 scales differ"
+    else:
+        exp_c[seq.long(), dst.long()] = y
+    exp_p[seq.long(), dst.long()] = kpe
+    got_c, got_p = cache.ckv.cpu(), cache.kpe.cpu()
+    if dtype == torch.float32 or fp8:
+        assert torch.equal(got_c, exp_c), "latent rows differ"
+    else:
+        assert torch.equal(got_c.view(torch.int16), exp_c.view(torch.int16)), "latent rows differ"
+    assert torch.equal(got_p.view(torch.int16) if dtype == torch.bfloat16 else got_p,
+                       exp_p.view(torch.int16) if dtype == torch.bfloat16 else exp_p), "k_pe rows differ"
+
+
+@pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.float32, False), (torch.bfloat16, True)])
+def test_append_bit_exact(gpu, dtype, fp8):
+    _append_case(gpu, dtype, fp8)
+
+
+def test_append_many_tokens_bit_exact(gpu):
+    _append_case(gpu, torch.bfloat16, False, n_tok=4093, B=8, S=1024, seed=3)
+    _append_case(gpu, torch.bfloat16, True, n_tok=4093, B=8, S=1024, seed=4)
+
+
+def test_append_out_of_range_is_skipped_and_flagged(gpu):
+    say("append out-of-range")
+    dtype = torch.bfloat16
+    cache = LatentCache.allocate(2, 8, dtype, gpu)
+    cos, sin = tables(dtype, 8, gpu)
+    kv = torch.randn(3, 320, dtype=dtype, device=gpu)
+    seq = torch.tensor([0, 1, 2], dtype=torch.int32, device=gpu)  # 2 >= batch
+    dst = torch.tensor([0, 9, 1], dtype=torch.int32, device=gpu)  # 9 >= seq
+    rp = torch.zeros(3, dtype=torch.int32, device=gpu)
+    flag = torch.zeros(1, dtype=torch.int32, device=gpu)
+    w = torch.ones(R, dtype=dtype, device=gpu)
+    b = torch.zeros(R, dtype=dtype, device=gpu)
+    kernels.append(kv, seq, dst, rp, w, b, 1e-5, cos, sin, cache, err_flag=flag)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+    assert bool((cache.ckv[0, 0] != 0).any())  # the valid token landed
+    assert int((cache.ckv != 0).sum()) == int((cache.ckv[0, 0] != 0).sum())
+
+
+# ------------------------------------------------------------------ decode
+def _decode_case(gpu, dtype, fp8, lens, n_splits, min_chunk, row_seq=None, B=None, S=None, seed=0,
+                 q_scale=1.0, rope_pos=None, rtol=2e-2, atol=1e-2):
+    rows = len(lens)
+    B = B or rows
+    S = S or max(max(lens), 1)
+    say(f"decode case dtype={dtype} fp8={fp8} rows={rows} lens={lens[:6]}... splits={n_splits} chunk={min_chunk}")
+    g = torch.Generator().manual_seed(seed)
+    cdt = torch.bfloat16 if fp8 else dtype
+    ckv = (torch.randn(B, S, R, generator=g)).to(cdt)
+    kpe = (torch.randn(B, S, P, generator=g)).to(dtype)
+    if fp8:
+        codes, scale = lo.fp8_quantize(ckv.reshape(-1, R))
+        cache = LatentCache(codes.view(B, S, R).to(gpu), kpe.to(gpu), scale.view(B, S).to(gpu))
+    else:
+        cache = LatentCache(ckv.to(gpu), kpe.to(gpu))
+    q_abs = (torch.randn(rows, H, R, generator=g) * q_scale).to(dtype)
+    q_pe = (torch.randn(rows, H, P, generator=g) * q_scale).to(dtype)
+    rs = torch.arange(rows, dtype=torch.int32) if row_seq is None else torch.tensor(row_seq, dtype=torch.int32)
+    kl = torch.tensor(lens, dtype=torch.int32)
+    rp = torch.zeros(rows, dtype=torch.int32) if rope_pos is None else torch.tensor(rope_pos, dtype=torch.int32)
+    cos, sin = tables(dtype, max(S, 64), gpu)
+    out = kernels.decode_attention(
+        q_abs.to(gpu), q_pe.to(gpu), rp.to(gpu), cos, sin, cache, rs.to(gpu), kl.to(gpu), SCALE,
+        n_splits=n_splits, min_chunk=min_chunk,
+    )
+    torch.cuda.synchronize()
+    q_pe_rot = lo.rope_interleaved(q_pe, cos.cpu()[rp.long()][:, None], sin.cpu()[rp.long()][:, None])
+    ref, _ = lo.absorbed_attention_f64(
+        q_abs, q_pe_rot, cache.ckv.cpu(), kpe, kl, rs, SCALE, cache.scale.cpu() if fp8 else None
+    )
+    close(out, ref, rtol, atol)
+    return out
+
+
+@pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.bfloat16, True), (torch.float32, False)])
+def test_decode_short_rows(gpu, dtype, fp8):
+    tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else {}
+    _decode_case(gpu, dtype, fp8, [1], 1, 256, **tol)
+    _decode_case(gpu, dtype, fp8, [15, 64, 100, 17], 1, 256, seed=1, **tol)
+    _decode_case(gpu, dtype, fp8, [130, 1, 63, 65], 4, 64, seed=2, **tol)
+
+
+@pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.bfloat16, True), (torch.float32, False)])
+def test_decode_split_kv_merge(gpu, dtype, fp8):
+    tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else {}
+    _decode_case(gpu, dtype, fp8, [1000, 1, 513, 4096], 8, 64, seed=3, **tol)
+    _decode_case(gpu, dtype, fp8, [4096, 4096], 64, 64, seed=4, **tol)
+
+
+def test_decode_ragged_row_mapping_and_rope(gpu):
+    """Rows map to arbitrary cache rows (prefill semantics: several query rows
+    per sequence with causal lengths) and rotate q_pe at their own position."""
+    row_seq = [2, 2, 2, 0, 1, 1, 3, 0]
+    lens = [5, 6, 7, 300, 1, 2, 2000, 301]
+    _decode_case(gpu, torch.bfloat16, False, lens, 8, 64, row_seq=row_seq, B=4, S=2048, seed=5,
+                 rope_pos=[0, 1, 2, 3, 0, 1, 77, 9])
+
+
+def test_decode_random_ragged_batch(gpu):
+    rng = np.random.default_rng(6)
+    lens = [int(x) for x in rng.integers(1, 3000, 24)]
+    _decode_case(gpu, torch.bfloat16, False, lens, 16, 128, seed=6)
+    _decode_case(gpu, torch.bfloat16, True, lens, 16, 128, seed=7)
+
+
+def test_decode_peaked_and_flat_softmax(gpu):
+    _decode_case(gpu, torch.bfloat16, False, [700, 1500], 4, 64, seed=8, q_scale=4.0)
+    _decode_case(gpu, torch.bfloat16, False, [700, 1500], 4, 64, seed=9, q_scale=0.01)
+
+
+def test_decode_split_invariance(gpu):
+    """The merged result does not depend on the split plan (within fp32 ulps
+    before the final bf16 rounding, so at most 1 bf16 ulp apart)."""
+    outs = [
+        _decode_case(gpu, torch.bfloat16, False, [3000, 2500, 64], ns, mc, seed=10)
+        for ns, mc in ((1, 64), (8, 64), (47, 64))
+    ]
+    for o in outs[1:]:
+        assert float((o.float() - outs[0].float()).abs().max()) <= 2 ** -7 * float(outs[0].float().abs().max())
+
+
+def test_decode_constant_latent_rows(gpu):
+    """All cached latent rows equal -> o_lat equals that row exactly (the
+    weights sum to 1 in the kernel's own arithmetic)."""
+    dtype = torch.bfloat16
+    B, S = 2, 777
+    row = torch.randn(R).to(dtype)
+    cache = LatentCache(row.expand(B, S, R).contiguous().to(gpu), torch.randn(B, S, P).to(dtype).to(gpu))
+    q_abs = torch.randn(B, H, R).to(dtype).to(gpu)
+    q_pe = torch.randn(B, H, P).to(dtype).to(gpu)
+    cos, sin = tables(dtype, S, gpu)
+    z = torch.zeros(B, dtype=torch.int32, device=gpu)
+    out = kernels.decode_attention(q_abs, q_pe, z, cos, sin, cache, torch.arange(B, dtype=torch.int32, device=gpu),
+                                   torch.tensor([S, 300], dtype=torch.int32, device=gpu), SCALE, n_splits=1)
+    torch.cuda.synchronize()
+    err = (out.float().cpu() - row.float()).abs().max()
+    assert float(err) <= 2 ** -8 * float(row.float().abs().max())
+
+
+def test_decode_headline_shape(gpu):
+    """Config-2 shape: 32 rows over 4097 cached tokens, graph-style split plan."""
+    lens = [4097] * 32
+    n_splits, mc = kernels.plan_splits(32, 4097)
+    _decode_case(gpu, torch.bfloat16, False, lens, n_splits, mc, seed=11, q_scale=0.5)
+    _decode_case(gpu, torch.bfloat16, True, lens, n_splits, mc, seed=12, q_scale=0.5)
