@@ -47,10 +47,21 @@ struct Elem<0> {  // fp32
   static __device__ __forceinline__ float ld(const T* p, int64_t i) { return p[i]; }
   static __device__ __forceinline__ T from_f32(float f) { return f; }
   static __device__ __forceinline__ T from_f64(double d) { return static_cast<float>(d); }
-  // op-by-op rounding of eager fp32 math (no fused multiply-add)
-  static __device__ __forceinline__ float mul(float a, float b) { return __fmul_rn(a, b); }
-  static __device__ __forceinline__ float add(float a, float b) { return __fadd_rn(a, b); }
-  static __device__ __forceinline__ float sub(float a, float b) { return __fsub_rn(a, b); }
+  // op-by-op rounding of eager fp32 math: contraction into a fused
+  // multiply-add is switched off (HIP's __fmul_rn is a plain multiply that
+  // the compiler may otherwise fuse with the following add).
+  static __device__ __forceinline__ float mul(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+  }
+  static __device__ __forceinline__ float add(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+  }
+  static __device__ __forceinline__ float sub(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+  }
 };
 template <>
 struct Elem<1> {  // bf16
@@ -59,9 +70,18 @@ struct Elem<1> {  // bf16
   static __device__ __forceinline__ T from_f32(float f) { return f32_to_bf16(f); }
   static __device__ __forceinline__ T from_f64(double d) { return f64_to_bf16(d); }
   // eager bf16 math: compute in fp32, round to bf16 after every op
-  static __device__ __forceinline__ float mul(float a, float b) { return round_bf16(__fmul_rn(a, b)); }
-  static __device__ __forceinline__ float add(float a, float b) { return round_bf16(__fadd_rn(a, b)); }
-  static __device__ __forceinline__ float sub(float a, float b) { return round_bf16(__fsub_rn(a, b)); }
+  static __device__ __forceinline__ float mul(float a, float b) {
+#pragma clang fp contract(off)
+    return round_bf16(a * b);
+  }
+  static __device__ __forceinline__ float add(float a, float b) {
+#pragma clang fp contract(off)
+    return round_bf16(a + b);
+  }
+  static __device__ __forceinline__ float sub(float a, float b) {
+#pragma clang fp contract(off)
+    return round_bf16(a - b);
+  }
 };
 
 // Interleaved-pair RoPE of one pair (positional_encoding.py:37-41, :57-60):
@@ -85,6 +105,9 @@ __device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xo
 // C_DT : 0 fp32 / 1 bf16 / 2 e4m3 (latent cache dtype).
 template <int IN_DT, int C_DT>
 __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
+  // Every multiply / add below is rounded on its own: the LayerNorm must
+  // reproduce the fixed-order fp64 statement exactly.
+#pragma clang fp contract(off)
   using E = Elem<IN_DT>;
   using T = typename E::T;
   const int lane = threadIdx.x & 63;
@@ -105,26 +128,25 @@ __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
   double x[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) x[i] = static_cast<double>(E::ld(row, 4 * lane + i));
-  double s = __dadd_rn(__dadd_rn(__dadd_rn(x[0], x[1]), x[2]), x[3]);
+  double s = ((x[0] + x[1]) + x[2]) + x[3];
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) s = __dadd_rn(s, shfl_xor_f64(s, m));
+  for (int m = 1; m < 64; m <<= 1) s = s + shfl_xor_f64(s, m);
   const double mean = s * (1.0 / 256.0);
-  double d[4], q = 0.0;
+  double d[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) d[i] = __dsub_rn(x[i], mean);
-  q = __dadd_rn(__dadd_rn(__dadd_rn(__dmul_rn(d[0], d[0]), __dmul_rn(d[1], d[1])),
-                          __dmul_rn(d[2], d[2])),
-                __dmul_rn(d[3], d[3]));
+  for (int i = 0; i < 4; ++i) d[i] = x[i] - mean;
+  double q = ((d[0] * d[0] + d[1] * d[1]) + d[2] * d[2]) + d[3] * d[3];
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) q = __dadd_rn(q, shfl_xor_f64(q, m));
+  for (int m = 1; m < 64; m <<= 1) q = q + shfl_xor_f64(q, m);
   const double var = q * (1.0 / 256.0);
-  const double rstd = __drcp_rn(__dsqrt_rn(__dadd_rn(var, static_cast<double>(a.eps))));
+  // correctly rounded square root and IEEE division
+  const double rstd = 1.0 / __dsqrt_rn(var + static_cast<double>(a.eps));
   double y[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const double wi = static_cast<double>(E::ld(w, 4 * lane + i));
     const double bi = static_cast<double>(E::ld(bb, 4 * lane + i));
-    y[i] = __dadd_rn(__dmul_rn(__dmul_rn(d[i], rstd), wi), bi);
+    y[i] = (d[i] * rstd) * wi + bi;
   }
 
   const int64_t crow = static_cast<int64_t>(b) * a.cache_s + pos;
