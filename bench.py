@@ -11,12 +11,14 @@ HIP kernels), captured as one HIP graph per step.
 One layer's cache (86.5 MB) fits MI355X's 256 MB Infinity Cache, so a single
 layer decoded back to back would be served from there, not from HBM.  The
 bench therefore rotates ``--layers`` independent layers (own weights, own
-cache: 4 x 86.5 MB by default), like a decoder stack, and counts each token
+cache: 8 x 86.5 MB by default), like a decoder stack, and counts each token
 once per layer it passes: value = batch * steps * layers / seconds
 ("layer-token decodes per second"); ms_per_step is per layer-step.
 
-roofline: the decode-attention kernel (mla_decode_mfma), timed with HIP
-events recorded on its own stream immediately around each of its launches;
+roofline: the decode-attention kernel (mla_decode_mfma, split-KV), timed with
+HIP events on its stream around back-to-back launches rotating over the
+layers' caches (each launch does its full work; the split merge, a separate
+small kernel, is timed the same way and reported beside it);
 achieved = algorithmic bytes per launch / average launch duration, with
 bytes = sum_b L_b*(R+P)*2 (latent + rope cache) + B*H*(R+P)*2 (queries) +
 B*H*R*2 (latent outputs).
@@ -46,7 +48,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=128)
     p.add_argument("--warmup", type=int, default=8)
-    p.add_argument("--layers", type=int, default=4, help="independent layers rotated per step")
+    p.add_argument("--layers", type=int, default=8, help="independent layers rotated per step")
     p.add_argument("--batch", type=int, default=32)
     p.add_argument("--ctx", type=int, default=4096)
     p.add_argument("--dim", type=int, default=1024)
@@ -90,12 +92,16 @@ def build_layers(args, dev, torch):
 
 
 def time_decode_kernel(layers, xs, args, dev, torch):
-    """Average duration of the decode-attention kernel from HIP events
-    recorded on its stream right before and after each launch."""
+    """Average duration of one decode-attention launch from HIP events
+    recorded on its stream around back-to-back launches that rotate over the
+    layers' caches ("cold": the working set exceeds the MALL) or repeat on one
+    layer ("warm": served from the MALL); the merge kernel is timed the same
+    way."""
     from swamla_amd import _abi, kernels
 
     lib = _abi.lib()
     stream = torch.cuda.current_stream(dev)
+    h = stream.cuda_stream
     preps = []
     with torch.no_grad():
         for m, x in zip(layers, xs):
@@ -105,49 +111,45 @@ def time_decode_kernel(layers, xs, args, dev, torch):
             q_abs = torch.bmm(q[:, :, :128].transpose(0, 1).contiguous(), w_uk)  # [H, B, R]
             cache = m.latent_cache()
             L = int(args.ctx + args.steps)
-            kv_len = torch.full((B,), L, dtype=torch.int32, device=dev)
+            sp = torch.full((B,), L - 1, dtype=torch.int32, device=dev)  # attend [0, L)
             n_splits, min_chunk = m._split_plan(B, L, dev)
             ws = kernels.DecodeWorkspace.allocate(B, n_splits, dev)
             o_lat = torch.empty(H, B, R, dtype=torch.bfloat16, device=dev)
             cos, sin = m.rope.half_tables()
-            zeros = torch.zeros(B, dtype=torch.int32, device=dev)
-            seq = torch.arange(B, dtype=torch.int32, device=dev)
-            qa = q_abs.transpose(0, 1)
-            qp = q[:, :, 128:]
-            ol = o_lat.transpose(0, 1)
+            qa, qp, ol = q_abs.transpose(0, 1), q[:, :, 128:], o_lat.transpose(0, 1)
             dargs = (
                 qa.data_ptr(), qa.stride(0), qa.stride(1), qp.data_ptr(), qp.stride(0), qp.stride(1),
-                zeros.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
-                cache.ckv.shape[0], cache.ckv.shape[1], seq.data_ptr(), kv_len.data_ptr(), B, H, R, P,
-                float(m.softmax_scale), n_splits, min_chunk, ws.o_part.data_ptr(), ws.lse_part.data_ptr(),
-                ol.data_ptr(), ol.stride(0), ol.stride(1), _abi.DTYPE_BF16, cache.cache_code,
+                cache.ckv.shape[0], cache.ckv.shape[1], None, None, None, sp.data_ptr(), 1, 0,
+                B, H, R, P, float(m.softmax_scale), n_splits, min_chunk,
+                ws.o_part.data_ptr(), ws.lse_part.data_ptr(),
+                ol.data_ptr(), ol.stride(0), ol.stride(1), _abi.DTYPE_BF16, cache.cache_code, h,
             )
-            margs = (ws.o_part.data_ptr(), ws.lse_part.data_ptr(), kv_len.data_ptr(), B, H, R, n_splits,
-                     min_chunk, ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16)
-            preps.append((dargs, margs, (q, q_abs, kv_len, ws, o_lat, cos, sin, zeros, seq), L, B, n_splits))
-    h = stream.cuda_stream
+            margs = (ws.o_part.data_ptr(), ws.lse_part.data_ptr(), None, sp.data_ptr(), 1, B, H, R, n_splits,
+                     min_chunk, ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16, h)
+            preps.append((dargs, (q, q_abs, sp, ws, o_lat, cos, sin), L, B, n_splits, margs))
 
-    def run(indices, reps):
-        evs = []
+    def run(indices, reps, which=0):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
         for _ in range(reps):
             for i in indices:
-                dargs, margs = preps[i][0], preps[i][1]
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                _abi.check(lib.mla_decode_attn(*dargs, h))
-                e1.record(stream)
-                _abi.check(lib.mla_merge(*margs, h))
-                evs.append((e0, e1))
+                if which == 0:
+                    _abi.check(lib.mla_decode_attn(*preps[i][0]))
+                else:
+                    _abi.check(lib.mla_merge(*preps[i][5]))
+        e1.record(stream)
         torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in evs) / len(evs) * 1e3  # us
+        return e0.elapsed_time(e1) * 1e3 / (reps * len(indices))  # us
 
-    run(range(len(preps)), 3)  # warm
+    run(range(len(preps)), 3)  # warm-up
     cold_us = run(range(len(preps)), args.kernel_reps)
     warm_us = run([0], args.kernel_reps * len(preps))
-    L, B, n_splits = preps[0][3], preps[0][4], preps[0][5]
-    return cold_us, warm_us, L, B, n_splits
+    merge_us = run(range(len(preps)), args.kernel_reps, which=1)
+    L, B, n_splits = preps[0][2], preps[0][3], preps[0][4]
+    return cold_us, warm_us, merge_us, L, B, n_splits
 
 
 def cpu_baseline(args, torch):
@@ -158,7 +160,7 @@ def cpu_baseline(args, torch):
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
     B = args.cpu_batch
-    cfg = MLAConfig(n_embd=args.dim, max_batch_size=B, max_seq_len=args.ctx + 64)
+    cfg = MLAConfig(n_embd=args.dim, max_batch_size=B, max_seq_len=args.ctx + 1024)
     m = RefMLA(cfg)
     init_weights(m, 7)
     m.eval()
@@ -175,7 +177,7 @@ def cpu_baseline(args, torch):
             m(x, args.ctx + 1 + steps)
             steps += 1
             el = time.perf_counter() - t0
-            if el >= args.cpu_seconds or steps >= 40:
+            if el >= args.cpu_seconds or steps >= 1000:
                 break
     cpu_model = ""
     try:
@@ -265,11 +267,12 @@ def main() -> int:
     ms_per_step = elapsed / layer_steps * 1e3
     log(f"decode: {value:.0f} layer-token/s, {ms_per_step * 1e3:.1f} us per layer-step, finite={ok}")
 
-    cold_us, warm_us, L, B, n_splits = time_decode_kernel(layers, xs, args, dev, torch)
+    cold_us, warm_us, merge_us, L, B, n_splits = time_decode_kernel(layers, xs, args, dev, torch)
     abytes = attention_bytes(B, L, fp8)
     achieved = abytes / (cold_us * 1e-6) / 1e9
     warm = abytes / (warm_us * 1e-6) / 1e9
-    log(f"decode kernel: {cold_us:.2f} us cold ({achieved:.0f} GB/s), {warm_us:.2f} us warm ({warm:.0f} GB/s)")
+    log(f"decode kernel: {cold_us:.2f} us cold ({achieved:.0f} GB/s), {warm_us:.2f} us warm ({warm:.0f} GB/s); "
+        f"merge {merge_us:.2f} us")
     # algorithmic bytes of one full layer-step (attention + append + weights), mean context
     mean_L = args.ctx + (args.steps + 1) / 2
     w_bytes = sum(p.numel() * p.element_size() for p in layers[0].parameters())
@@ -317,6 +320,8 @@ def main() -> int:
             "launch": f"B={B} L={L} splits<={n_splits}, caches rotated over {len(layers)} layers",
             "warm_mall_achieved": warm,
             "warm_mall_avg_launch_us": warm_us,
+            "merge_avg_launch_us": merge_us,
+            "attention_achieved_with_merge": abytes / ((cold_us + merge_us) * 1e-6) / 1e9,
         },
         "cpu_baseline": cpu,
         "host": platform.node(),

@@ -52,6 +52,20 @@ int mla_abi_version(void);
 const char* mla_last_error(void);
 
 /*
+ * Addressing of tokens (mla_append) and query rows (mla_decode_attn,
+ * mla_merge) — exactly one of two modes per call:
+ *   explicit  per-entry int32 device arrays (cache row, position, RoPE row);
+ *             start_pos must be NULL.
+ *   dense     start_pos = int32 device array [n / T]: entry i belongs to cache
+ *             row i / T at position start_pos[i / T] + i % T — the layout of
+ *             the reference's forward(x[B, T, dim], start_pos) with one start
+ *             position per sequence (mla.py:277-278, :413-418).  RoPE row is
+ *             i % T when rope_abs = 0 (the reference's chunk-local positions,
+ *             positional_encoding.py:49-50) or the absolute position when 1.
+ *             The per-entry arrays must be NULL.
+ */
+
+/*
  * mla_append — fused cache append (one call per forward, any T).
  * Replaces models/mla.py:307-323 (split of wkv_a(x) into c / k_pe and RoPE on
  * k_pe), :409 (kv_norm LayerNorm) and :413-414 (scatter into kv_cache /
@@ -59,18 +73,17 @@ const char* mla_last_error(void);
  *
  * kv_in        [n_tok, in_row_stride] rows in in_dtype; columns 0..R-1 are the
  *              latent c, R..R+P-1 are k_pe (the wkv_a output, no copy needed).
- * seq_idx      [n_tok] int32, cache row (batch slot) of each token.
- * dst_pos      [n_tok] int32, cache position of each token.
- * rope_pos     [n_tok] int32, RoPE table row of each token (the reference uses
- *              the chunk-local index t, positional_encoding.py:49-50).
+ * seq_idx, dst_pos, rope_pos   explicit addressing: cache row, cache position
+ *              and RoPE table row of each token.
+ * start_pos, tokens_per_seq, rope_abs   dense addressing (see above).
  * ln_w, ln_b   [R] LayerNorm affine parameters in in_dtype; eps as in torch.
  * cos_tab,     [rope_len, P/2] in in_dtype: the first P/2 columns of the
  * sin_tab      reference cos_cached / sin_cached (positional_encoding.py:21-28).
  * ckv_cache    [cache_batch, cache_seq, R] in cache_dtype (u8 codes for FP8).
  * kpe_cache    [cache_batch, cache_seq, P] in in_dtype.
  * ckv_scale    [cache_batch, cache_seq] fp32, written only for FP8 (else NULL).
- * err_flag     optional device int32; a token whose seq_idx / dst_pos /
- *              rope_pos lies outside the buffers is skipped and sets it to 1.
+ * err_flag     optional device int32; a token whose cache row / position /
+ *              RoPE row lies outside the buffers is skipped and sets it to 1.
  *
  * Numerics: LayerNorm statistics are reduced in fp64 in a fixed order and the
  * result is rounded once to the cache dtype (exactly-rounded LayerNorm).
@@ -79,12 +92,13 @@ const char* mla_last_error(void);
  */
 int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok,
                const int32_t* seq_idx, const int32_t* dst_pos,
-               const int32_t* rope_pos, const void* ln_w, const void* ln_b,
-               float eps, const void* cos_tab, const void* sin_tab,
-               int64_t rope_len, void* ckv_cache, void* kpe_cache,
-               float* ckv_scale, int64_t cache_batch, int64_t cache_seq,
-               int32_t* err_flag, int32_t in_dtype, int32_t cache_dtype,
-               int32_t R, int32_t P, void* stream);
+               const int32_t* rope_pos, const int32_t* start_pos,
+               int32_t tokens_per_seq, int32_t rope_abs, const void* ln_w,
+               const void* ln_b, float eps, const void* cos_tab,
+               const void* sin_tab, int64_t rope_len, void* ckv_cache,
+               void* kpe_cache, float* ckv_scale, int64_t cache_batch,
+               int64_t cache_seq, int32_t* err_flag, int32_t in_dtype,
+               int32_t cache_dtype, int32_t R, int32_t P, void* stream);
 
 /*
  * mla_decode_attn — absorbed attention of query rows over the latent cache.
@@ -93,27 +107,29 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok,
  * re-associated form  s_t = scale * (q_abs . c_t + rope(q_pe) . k_pe_t),
  * o_lat = sum_t softmax(s)_t c_t.
  *
- * Query row r attends to cache row row_seq[r], positions [0, kv_len[r]) (a
- * prefill token t at start_pos passes kv_len = start_pos + t + 1: causal).
+ * Query row r attends to its cache row over positions [0, L): explicit mode
+ * row_seq[r], L = kv_len[r], RoPE row q_rope_pos[r]; dense mode L = start +
+ * r % T + 1 (causal, bottom-right for a prefill chunk).
  * q_abs        row r, head h at q_abs + r*q_abs_rs + h*q_abs_hs, R values.
  * q_pe         row r, head h at q_pe + r*q_pe_rs + h*q_pe_hs, P values before
- *              RoPE; rotated in-kernel with table row q_rope_pos[r].
+ *              RoPE; rotated in-kernel.
  * Split-KV: each row is cut into ns = ceil(L / chunk) splits of
- *   chunk = round_up(max(min_chunk, ceil(L / n_splits)), 64) tokens.
- * Rows with ns == 1 are written straight to o_lat; others write normalised
+ *   chunk = round_up(max(min_chunk, ceil(L / n_splits)), 16) tokens.
+ * Rows with ns == 1 are written straight to o_lat.  Others write normalised
  * partials o_part [n_rows, n_splits, H, R] fp32 and log-sum-exp lse_part
- * [n_rows, n_splits, H] (natural log of sum exp(s)) for mla_merge.
+ * [n_rows, n_splits, H] (natural log of sum exp(s)) that mla_merge combines.
  * o_lat        row r, head h at o_lat + r*o_rs + h*o_hs, R values, in dtype.
  */
 int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
                     const void* q_pe, int64_t q_pe_rs, int64_t q_pe_hs,
-                    const int32_t* q_rope_pos, const void* cos_tab,
-                    const void* sin_tab, int64_t rope_len,
+                    const void* cos_tab, const void* sin_tab, int64_t rope_len,
                     const void* ckv_cache, const void* kpe_cache,
                     const float* ckv_scale, int64_t cache_batch,
                     int64_t cache_seq, const int32_t* row_seq,
-                    const int32_t* kv_len, int32_t n_rows, int32_t H,
-                    int32_t R, int32_t P, float sm_scale, int32_t n_splits,
+                    const int32_t* kv_len, const int32_t* q_rope_pos,
+                    const int32_t* start_pos, int32_t rows_per_seq,
+                    int32_t rope_abs, int32_t n_rows, int32_t H, int32_t R,
+                    int32_t P, float sm_scale, int32_t n_splits,
                     int32_t min_chunk, float* o_part, float* lse_part,
                     void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
                     int32_t cache_dtype, void* stream);
@@ -123,10 +139,12 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
  * counterpart: the reference attends in one SDPA call, mla.py:581-595).
  * o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M), M = max_s lse_s, for
  * every row whose split count (same formula as mla_decode_attn) exceeds 1.
+ * Row lengths: kv_len (explicit) or start_pos / rows_per_seq (dense).
  * lse_out [n_rows, H] fp32 is optional (NULL = not written).
  */
 int mla_merge(const float* o_part, const float* lse_part,
-              const int32_t* kv_len, int32_t n_rows, int32_t H, int32_t R,
+              const int32_t* kv_len, const int32_t* start_pos,
+              int32_t rows_per_seq, int32_t n_rows, int32_t H, int32_t R,
               int32_t n_splits, int32_t min_chunk, void* o_lat, int64_t o_rs,
               int64_t o_hs, float* lse_out, int32_t dtype, void* stream);
 

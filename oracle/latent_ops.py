@@ -117,7 +117,7 @@ def rope_interleaved(x: torch.Tensor, cos_half: torch.Tensor, sin_half: torch.Te
 # ---------------------------------------------------------------- attention
 def split_chunk(L: int, n_splits: int, min_chunk: int) -> int:
     c = max(min_chunk, -(-L // n_splits))
-    return (c + 63) // 64 * 64
+    return (c + 15) // 16 * 16
 
 
 def split_count(L: int, n_splits: int, min_chunk: int) -> int:

@@ -66,18 +66,18 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_split_count.argtypes = [_I32, _I32, _I32]
     lib.mla_append.restype = ctypes.c_int
     lib.mla_append.argtypes = [
-        _P, _I64, _I32, _P, _P, _P, _P, _P, _F, _P, _P, _I64,
+        _P, _I64, _I32, _P, _P, _P, _P, _I32, _I32, _P, _P, _F, _P, _P, _I64,
         _P, _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _I32, _P,
     ]
     lib.mla_decode_attn.restype = ctypes.c_int
     lib.mla_decode_attn.argtypes = [
-        _P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _I64,
-        _P, _P, _P, _I64, _I64, _P, _P, _I32, _I32, _I32, _I32,
+        _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
+        _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
         _F, _I32, _I32, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
     ]
     lib.mla_merge.restype = ctypes.c_int
     lib.mla_merge.argtypes = [
-        _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I32, _P,
+        _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I32, _P,
     ]
     lib.mla_host_f32_to_e4m3.restype = None
     lib.mla_host_f32_to_e4m3.argtypes = [_P, _P, _I64]

@@ -55,36 +55,66 @@ int hip_fail(const char* what) {
   return fail(SWAMLA_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
 }
 
+
+int mla_abi_version_impl() { return SWAMLA_ABI_VERSION; }
+
+const char* last_error_impl() { return g_err; }
+
+int32_t split_count_impl(int32_t L, int32_t n_splits, int32_t min_chunk) {
+  if (n_splits < 1 || min_chunk < 1) return 0;
+  int c = (L + n_splits - 1) / n_splits;
+  if (c < min_chunk) c = min_chunk;
+  c = (c + 15) & ~15;
+  return L <= 0 ? 0 : (L + c - 1) / c;
+}
+
+// Addressing: explicit per-entry arrays, or dense (start_pos[n / T]).
+int check_addressing(const char* fn, int32_t n, const int32_t* a0, const int32_t* a1, const int32_t* a2,
+                     const int32_t* start_pos, int32_t T, bool need_a0, bool need_a2,
+                     swamla::Addressing* ad, int32_t rope_abs) {
+  if (start_pos) {
+    if (a0 || a1 || a2)
+      return fail(SWAMLA_ERR_INVALID_ARG, "%s: pass either start_pos or the per-entry arrays, not both", fn);
+    if (T < 1) return fail(SWAMLA_ERR_INVALID_ARG, "%s: entries per sequence %d < 1", fn, T);
+    if (n % T != 0) return fail(SWAMLA_ERR_INVALID_ARG, "%s: %d entries is not a multiple of %d", fn, n, T);
+    if (rope_abs != 0 && rope_abs != 1) return fail(SWAMLA_ERR_INVALID_ARG, "%s: rope_abs must be 0 or 1", fn);
+  } else if (n > 0 && ((need_a0 && !a0) || !a1 || (need_a2 && !a2))) {
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: null per-entry index array", fn);
+  }
+  *ad = swamla::Addressing{a0, a1, a2, start_pos, start_pos ? T : 1, rope_abs};
+  return SWAMLA_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int mla_abi_version(void) { return SWAMLA_ABI_VERSION; }
+int mla_abi_version(void) { return mla_abi_version_impl(); }
 
-const char* mla_last_error(void) { return g_err; }
+const char* mla_last_error(void) { return last_error_impl(); }
 
 int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk) {
-  if (n_splits < 1 || min_chunk < 1) return 0;
-  int c = (L + n_splits - 1) / n_splits;
-  if (c < min_chunk) c = min_chunk;
-  c = (c + 63) & ~63;
-  return L <= 0 ? 0 : (L + c - 1) / c;
+  return split_count_impl(L, n_splits, min_chunk);
 }
 
 int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const int32_t* seq_idx,
-               const int32_t* dst_pos, const int32_t* rope_pos, const void* ln_w,
-               const void* ln_b, float eps, const void* cos_tab, const void* sin_tab,
-               int64_t rope_len, void* ckv_cache, void* kpe_cache, float* ckv_scale,
-               int64_t cache_batch, int64_t cache_seq, int32_t* err_flag, int32_t in_dtype,
-               int32_t cache_dtype, int32_t R, int32_t P, void* stream) {
+               const int32_t* dst_pos, const int32_t* rope_pos, const int32_t* start_pos,
+               int32_t tokens_per_seq, int32_t rope_abs, const void* ln_w, const void* ln_b, float eps,
+               const void* cos_tab, const void* sin_tab, int64_t rope_len, void* ckv_cache,
+               void* kpe_cache, float* ckv_scale, int64_t cache_batch, int64_t cache_seq,
+               int32_t* err_flag, int32_t in_dtype, int32_t cache_dtype, int32_t R, int32_t P,
+               void* stream) {
   if (int e = check_geometry(16, R, P)) return e;
   if (int e = check_pair(in_dtype, cache_dtype)) return e;
   if (n_tok < 0) return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: n_tok=%d < 0", n_tok);
   if (n_tok > (1 << 30)) return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: n_tok=%d too large", n_tok);
   if (!ckv_cache || !kpe_cache || !ln_w || !ln_b || !cos_tab || !sin_tab)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: null cache / LayerNorm / RoPE pointer");
-  if (n_tok > 0 && (!kv_in || !seq_idx || !dst_pos || !rope_pos))
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: null input or index pointer");
+  if (n_tok > 0 && !kv_in) return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: null input rows");
+  swamla::Addressing ad;
+  if (int e = check_addressing("mla_append", n_tok, seq_idx, dst_pos, rope_pos, start_pos, tokens_per_seq,
+                               true, true, &ad, rope_abs))
+    return e;
   if (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: fp8 cache needs ckv_scale");
   if (in_row_stride < R + P)
@@ -99,9 +129,9 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const in
       !aligned(ln_w, es) || !aligned(ln_b, es) || !aligned(cos_tab, es) || !aligned(sin_tab, es) ||
       (ckv_scale && !aligned(ckv_scale, 4)))
     return fail(SWAMLA_ERR_MISALIGNED, "mla_append: ckv_cache must be 16-byte aligned, others element-aligned");
-  swamla::AppendArgs a{kv_in,   in_row_stride, n_tok,     seq_idx,   dst_pos,     rope_pos,
-                       ln_w,    ln_b,          eps,       cos_tab,   sin_tab,     rope_len,
-                       ckv_cache, kpe_cache,   ckv_scale, cache_batch, cache_seq, err_flag};
+  swamla::AppendArgs a{kv_in,    in_row_stride, n_tok,     ad,          ln_w,      ln_b,    eps,
+                       cos_tab,  sin_tab,       rope_len,  ckv_cache,   kpe_cache, ckv_scale,
+                       cache_batch, cache_seq,  err_flag};
   const int rc = swamla::launch_append(a, in_dtype, cache_dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_append: no kernel for this dtype pair");
   if (rc != 0) return hip_fail("mla_append");
@@ -109,14 +139,14 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const in
 }
 
 int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const void* q_pe,
-                    int64_t q_pe_rs, int64_t q_pe_hs, const int32_t* q_rope_pos,
-                    const void* cos_tab, const void* sin_tab, int64_t rope_len,
-                    const void* ckv_cache, const void* kpe_cache, const float* ckv_scale,
-                    int64_t cache_batch, int64_t cache_seq, const int32_t* row_seq,
-                    const int32_t* kv_len, int32_t n_rows, int32_t H, int32_t R, int32_t P,
-                    float sm_scale, int32_t n_splits, int32_t min_chunk, float* o_part,
-                    float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
-                    int32_t cache_dtype, void* stream) {
+                    int64_t q_pe_rs, int64_t q_pe_hs, const void* cos_tab, const void* sin_tab,
+                    int64_t rope_len, const void* ckv_cache, const void* kpe_cache,
+                    const float* ckv_scale, int64_t cache_batch, int64_t cache_seq,
+                    const int32_t* row_seq, const int32_t* kv_len, const int32_t* q_rope_pos,
+                    const int32_t* start_pos, int32_t rows_per_seq, int32_t rope_abs, int32_t n_rows,
+                    int32_t H, int32_t R, int32_t P, float sm_scale, int32_t n_splits,
+                    int32_t min_chunk, float* o_part, float* lse_part, void* o_lat,
+                    int64_t o_rs, int64_t o_hs, int32_t dtype, int32_t cache_dtype, void* stream) {
   if (int e = check_geometry(H, R, P)) return e;
   if (int e = check_pair(dtype, cache_dtype)) return e;
   if (n_rows < 0 || n_rows > 65535)
@@ -127,8 +157,11 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const
   if (!(sm_scale > 0.f)) return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: sm_scale must be > 0");
   if (!ckv_cache || !kpe_cache || !cos_tab || !sin_tab || !o_lat)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: null cache / RoPE / output pointer");
-  if (n_rows > 0 && (!q_abs || !q_pe || !q_rope_pos || !row_seq || !kv_len))
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: null query / index pointer");
+  if (n_rows > 0 && (!q_abs || !q_pe)) return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: null query pointer");
+  swamla::Addressing ad;
+  if (int e = check_addressing("mla_decode_attn", n_rows, row_seq, kv_len, q_rope_pos, start_pos, rows_per_seq,
+                               true, true, &ad, rope_abs))
+    return e;
   if (n_splits > 1 && (!o_part || !lse_part))
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: n_splits > 1 needs o_part and lse_part");
   if (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale)
@@ -155,20 +188,20 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const
       (ckv_scale && !aligned(ckv_scale, 4)))
     return fail(SWAMLA_ERR_MISALIGNED, "mla_decode_attn: o_part must be 16-byte aligned");
   const float log2e = 1.4426950408889634f;
-  swamla::DecodeArgs a{q_abs,    q_abs_rs,  q_abs_hs,    q_pe,     q_pe_rs,   q_pe_hs,
-                       q_rope_pos, cos_tab, sin_tab,     rope_len, ckv_cache, kpe_cache,
-                       ckv_scale, cache_batch, cache_seq, row_seq, kv_len,    n_rows,
-                       sm_scale * log2e, n_splits, min_chunk, o_part, lse_part, o_lat,
-                       o_rs,      o_hs};
+  swamla::DecodeArgs a{q_abs,     q_abs_rs,  q_abs_hs,  q_pe,      q_pe_rs,     q_pe_hs,
+                       cos_tab,   sin_tab,   rope_len,  ckv_cache, kpe_cache,   ckv_scale,
+                       cache_batch, cache_seq, ad,      n_rows,    sm_scale * log2e, n_splits,
+                       min_chunk, o_part,    lse_part,  o_lat,     o_rs,      o_hs};
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_attn: no kernel for this dtype pair");
   if (rc != 0) return hip_fail("mla_decode_attn");
   return ok();
 }
 
-int mla_merge(const float* o_part, const float* lse_part, const int32_t* kv_len, int32_t n_rows,
-              int32_t H, int32_t R, int32_t n_splits, int32_t min_chunk, void* o_lat, int64_t o_rs,
-              int64_t o_hs, float* lse_out, int32_t dtype, void* stream) {
+int mla_merge(const float* o_part, const float* lse_part, const int32_t* kv_len,
+              const int32_t* start_pos, int32_t rows_per_seq, int32_t n_rows, int32_t H, int32_t R,
+              int32_t n_splits, int32_t min_chunk, void* o_lat, int64_t o_rs, int64_t o_hs,
+              float* lse_out, int32_t dtype, void* stream) {
   if (int e = check_geometry(H, R, 64)) return e;
   if (!model_elem(dtype)) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: dtype %d not built", dtype);
   if (n_rows < 0 || n_rows > 65535)
@@ -177,13 +210,16 @@ int mla_merge(const float* o_part, const float* lse_part, const int32_t* kv_len,
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: n_splits=%d outside [1, 1024]", n_splits);
   if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: min_chunk=%d < 1", min_chunk);
   if (n_splits == 1 || n_rows == 0) return ok();  // nothing to merge
-  if (!o_part || !lse_part || !kv_len || !o_lat)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: null pointer");
+  swamla::Addressing ad;
+  if (int e = check_addressing("mla_merge", n_rows, nullptr, kv_len, nullptr, start_pos, rows_per_seq, false,
+                               false, &ad, 0))
+    return e;
+  if (!o_part || !lse_part || !o_lat) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: null pointer");
   if (o_hs < R || o_rs < 0) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: bad output strides");
-  const int vec = dtype == SWAMLA_DTYPE_F32 ? 4 : 4;  // 4 channels per lane
-  if (!aligned(o_part, 16) || !aligned(o_lat, dtype == SWAMLA_DTYPE_F32 ? 16 : 8) || (o_rs | o_hs) % vec != 0)
+  // a lane writes 4 channels: 16 B (fp32) or 8 B (bf16)
+  if (!aligned(o_part, 16) || !aligned(o_lat, dtype == SWAMLA_DTYPE_F32 ? 16 : 8) || (o_rs | o_hs) % 4 != 0)
     return fail(SWAMLA_ERR_MISALIGNED, "mla_merge: misaligned partials or output");
-  swamla::MergeArgs a{o_part, lse_part, kv_len, n_rows, n_splits, min_chunk, o_lat, o_rs, o_hs, lse_out};
+  swamla::MergeArgs a{o_part, lse_part, ad, n_rows, n_splits, min_chunk, o_lat, o_rs, o_hs, lse_out};
   const int rc = swamla::launch_merge(a, dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: no kernel for dtype %d", dtype);
   if (rc != 0) return hip_fail("mla_merge");

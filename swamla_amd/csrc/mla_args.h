@@ -7,13 +7,24 @@
 
 namespace swamla {
 
+// Where token / query-row positions come from.  Explicit mode: per-entry
+// arrays.  Dense mode (start_pos != nullptr): entry i belongs to sequence
+// i / T at position start_pos[i / T] + i % T, the layout of the reference's
+// forward (x[B, T, dim] at one start position per sequence).
+struct Addressing {
+  const int32_t* seq;        // explicit: cache row of each entry
+  const int32_t* pos;        // explicit append: destination position; decode: kv_len
+  const int32_t* rope;       // explicit: RoPE table row
+  const int32_t* start_pos;  // dense: [n / T] first position of each sequence
+  int32_t T;                 // dense: entries per sequence
+  int32_t rope_abs;          // dense: RoPE row = position (1) or t = i % T (0)
+};
+
 struct AppendArgs {
   const void* kv_in;
   int64_t in_rs;
   int n_tok;
-  const int32_t* seq_idx;
-  const int32_t* dst_pos;
-  const int32_t* rope_pos;
+  Addressing ad;
   const void* ln_w;
   const void* ln_b;
   float eps;
@@ -33,7 +44,6 @@ struct DecodeArgs {
   int64_t qa_rs, qa_hs;
   const void* q_pe;
   int64_t qp_rs, qp_hs;
-  const int32_t* q_rope_pos;
   const void* cos_tab;
   const void* sin_tab;
   int64_t rope_len;
@@ -41,8 +51,7 @@ struct DecodeArgs {
   const void* kpe;
   const float* ckv_scale;
   int64_t cache_b, cache_s;
-  const int32_t* row_seq;
-  const int32_t* kv_len;
+  Addressing ad;  // pos = kv_len in explicit mode
   int n_rows;
   float scale_log2;  // softmax_scale * log2(e)
   int n_splits, min_chunk;
@@ -55,7 +64,7 @@ struct DecodeArgs {
 struct MergeArgs {
   const float* o_part;
   const float* lse_part;
-  const int32_t* kv_len;
+  Addressing ad;  // only the row lengths are used
   int n_rows, n_splits, min_chunk;
   void* o_lat;
   int64_t o_rs, o_hs;

@@ -97,36 +97,61 @@ class LatentCache:
         )
 
 
+def _addressing(n, arrays, start_pos, per_seq, names):
+    """Validate one of the two addressing modes; returns the ctypes pointers."""
+    if start_pos is not None:
+        if any(a is not None for a in arrays):
+            raise ValueError("pass either start_pos or the per-entry index arrays, not both")
+        _i32(start_pos, "start_pos")
+        if per_seq < 1 or n % per_seq != 0 or start_pos.numel() != n // per_seq:
+            raise ValueError(f"start_pos has {start_pos.numel()} entries for {n} entries of {per_seq} per sequence")
+        return [None] * len(arrays), start_pos.data_ptr()
+    out = []
+    for name, t in zip(names, arrays):
+        if t is None:
+            out.append(None)
+            continue
+        _i32(t, name)
+        if t.numel() != n:
+            raise ValueError(f"{name} has {t.numel()} entries, expected {n}")
+        out.append(t.data_ptr())
+    return out, None
+
+
 def append(
     kv: torch.Tensor,
-    seq_idx: torch.Tensor,
-    dst_pos: torch.Tensor,
-    rope_pos: torch.Tensor,
+    cache: LatentCache,
     ln_w: torch.Tensor,
     ln_b: torch.Tensor,
     eps: float,
     cos_tab: torch.Tensor,
     sin_tab: torch.Tensor,
-    cache: LatentCache,
+    *,
+    seq_idx: Optional[torch.Tensor] = None,
+    dst_pos: Optional[torch.Tensor] = None,
+    rope_pos: Optional[torch.Tensor] = None,
+    start_pos: Optional[torch.Tensor] = None,
+    tokens_per_seq: int = 1,
+    rope_abs: bool = False,
     err_flag: Optional[torch.Tensor] = None,
 ) -> None:
     """Fused kv_norm + RoPE(k_pe) + (e4m3) + scatter of ``kv`` rows.
 
     kv: [N, >=R+P] with unit stride in the last dim (the wkv_a output, or a
-    view of it).  Reference: models/mla.py:307-323, :409-414.
+    view of it).  Addressing: explicit (seq_idx, dst_pos, rope_pos) or dense
+    (start_pos [N / tokens_per_seq]).  Reference: models/mla.py:307-323,
+    :409-414.
     """
     cache.validate()
-    dev = _need_gpu(kv, seq_idx, dst_pos, rope_pos, ln_w, ln_b, cos_tab, sin_tab, cache.ckv)
+    dev = _need_gpu(kv, ln_w, ln_b, cos_tab, sin_tab, cache.ckv, seq_idx, dst_pos, rope_pos, start_pos)
     if kv.dim() != 2 or kv.stride(1) != 1 or kv.shape[1] < R + P:
         raise ValueError("kv must be [N, R+P] with unit last-dim stride")
     dt = cache.model_dtype
     if kv.dtype != dt or ln_w.dtype != dt or ln_b.dtype != dt or cos_tab.dtype != dt or sin_tab.dtype != dt:
         raise TypeError(f"kv / LayerNorm / RoPE tensors must all be {dt}")
     n = kv.shape[0]
-    for name, t in (("seq_idx", seq_idx), ("dst_pos", dst_pos), ("rope_pos", rope_pos)):
-        _i32(t, name)
-        if t.numel() != n:
-            raise ValueError(f"{name} has {t.numel()} entries, expected {n}")
+    (p_seq, p_dst, p_rope), p_sp = _addressing(
+        n, (seq_idx, dst_pos, rope_pos), start_pos, tokens_per_seq, ("seq_idx", "dst_pos", "rope_pos"))
     if not (ln_w.is_contiguous() and ln_b.is_contiguous() and ln_w.numel() == R and ln_b.numel() == R):
         raise ValueError("LayerNorm weight / bias must be contiguous [R]")
     if cos_tab.dim() != 2 or cos_tab.shape[1] != P // 2 or cos_tab.shape != sin_tab.shape:
@@ -136,26 +161,26 @@ def append(
     lib = _abi.lib()
     _abi.check(
         lib.mla_append(
-            kv.data_ptr(), kv.stride(0), n, seq_idx.data_ptr(), dst_pos.data_ptr(),
-            rope_pos.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), float(eps),
-            cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
-            cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
+            kv.data_ptr(), kv.stride(0), n, p_seq, p_dst, p_rope, p_sp, int(tokens_per_seq), int(bool(rope_abs)),
+            ln_w.data_ptr(), ln_b.data_ptr(), float(eps), cos_tab.data_ptr(), sin_tab.data_ptr(),
+            cos_tab.shape[0], cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
             cache.ckv.shape[0], cache.ckv.shape[1], _abi.ptr(err_flag),
             _abi.dtype_code(dt), cache.cache_code, R, P, _abi.stream_handle(dev),
         )
     )
 
 
-def plan_splits(n_rows: int, max_len: int, num_cus: int = 256, waves: int = 2,
+def plan_splits(n_rows: int, max_len: int, num_cus: int = 256, blocks_per_cu: int = 1,
                 min_chunk: int = 256) -> tuple[int, int]:
-    """Host heuristic for the split-KV plan: about ``waves`` blocks per CU.
+    """Host heuristic for the split-KV plan: about ``blocks_per_cu`` blocks
+    per CU (fewer, longer blocks amortise each block's fixed cost).
 
     Returns (n_splits, min_chunk).  The kernels derive each row's own split
     count from its length on the device, so ``max_len`` may be an upper bound.
     """
     if n_rows <= 0:
         return 1, min_chunk
-    target = max(1, (num_cus * waves + n_rows - 1) // n_rows)
+    target = max(1, (num_cus * blocks_per_cu + n_rows - 1) // n_rows)
     by_len = max(1, (max_len + min_chunk - 1) // min_chunk)
     return int(max(1, min(target, by_len, 1024))), int(min_chunk)
 
@@ -169,9 +194,10 @@ class DecodeWorkspace:
 
     @staticmethod
     def allocate(n_rows: int, n_splits: int, device) -> "DecodeWorkspace":
+        rows = max(n_rows, 1)
         return DecodeWorkspace(
-            torch.empty(max(n_rows, 1), n_splits, H, R, dtype=torch.float32, device=device),
-            torch.empty(max(n_rows, 1), n_splits, H, dtype=torch.float32, device=device),
+            torch.empty(rows, n_splits, H, R, dtype=torch.float32, device=device),
+            torch.empty(rows, n_splits, H, dtype=torch.float32, device=device),
         )
 
     def fits(self, n_rows: int, n_splits: int) -> bool:
@@ -181,13 +207,17 @@ class DecodeWorkspace:
 def decode_attention(
     q_abs: torch.Tensor,
     q_pe: torch.Tensor,
-    q_rope_pos: torch.Tensor,
     cos_tab: torch.Tensor,
     sin_tab: torch.Tensor,
     cache: LatentCache,
-    row_seq: torch.Tensor,
-    kv_len: torch.Tensor,
     sm_scale: float,
+    *,
+    row_seq: Optional[torch.Tensor] = None,
+    kv_len: Optional[torch.Tensor] = None,
+    q_rope_pos: Optional[torch.Tensor] = None,
+    start_pos: Optional[torch.Tensor] = None,
+    rows_per_seq: int = 1,
+    rope_abs: bool = False,
     n_splits: int = 1,
     min_chunk: int = 256,
     out: Optional[torch.Tensor] = None,
@@ -197,11 +227,15 @@ def decode_attention(
     """Absorbed attention of query rows over the latent cache (+ merge).
 
     q_abs [rows, H, R] and q_pe [rows, H, P] may be strided views (unit last
-    stride).  Returns o_lat [rows, H, R] (``out`` may be a strided view, e.g.
-    a transpose of a [H, rows, R] buffer).  Reference: models/mla.py:417-487.
+    stride).  Addressing: explicit (row_seq, kv_len, q_rope_pos) or dense
+    (start_pos [rows / rows_per_seq], causal).  Returns o_lat [rows, H, R]
+    (``out`` may be a strided view, e.g. a transpose of a [H, rows, R]
+    buffer).  With more than one split, mla_merge runs after the decode
+    kernel (and writes the log-sum-exp to ``lse_out`` if given).
+    Reference: models/mla.py:417-487.
     """
     cache.validate()
-    dev = _need_gpu(q_abs, q_pe, q_rope_pos, cos_tab, sin_tab, cache.ckv, row_seq, kv_len)
+    dev = _need_gpu(q_abs, q_pe, cos_tab, sin_tab, cache.ckv, row_seq, kv_len, q_rope_pos, start_pos)
     dt = cache.model_dtype
     rows = q_abs.shape[0]
     if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (H, R) or q_abs.stride(2) != 1:
@@ -210,10 +244,8 @@ def decode_attention(
         raise ValueError(f"q_pe must be [rows, {H}, {P}] with unit last stride")
     if q_abs.dtype != dt or q_pe.dtype != dt or cos_tab.dtype != dt:
         raise TypeError(f"query and RoPE tensors must be {dt}")
-    for name, t in (("q_rope_pos", q_rope_pos), ("row_seq", row_seq), ("kv_len", kv_len)):
-        _i32(t, name)
-        if t.numel() != rows:
-            raise ValueError(f"{name} has {t.numel()} entries, expected {rows}")
+    (p_seq, p_len, p_rope), p_sp = _addressing(
+        rows, (row_seq, kv_len, q_rope_pos), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
     if out is None:
         out = torch.empty(rows, H, R, dtype=dt, device=dev)
     if tuple(out.shape) != (rows, H, R) or out.stride(2) != 1 or out.dtype != dt:
@@ -229,11 +261,11 @@ def decode_attention(
         lib.mla_decode_attn(
             q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1),
             q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
-            q_rope_pos.data_ptr(), cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+            cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
             cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
             cache.ckv.shape[0], cache.ckv.shape[1],
-            row_seq.data_ptr(), kv_len.data_ptr(), rows, H, R, P, float(sm_scale),
-            n_splits, min_chunk,
+            p_seq, p_len, p_rope, p_sp, int(rows_per_seq), int(bool(rope_abs)),
+            rows, H, R, P, float(sm_scale), n_splits, min_chunk,
             _abi.ptr(workspace.o_part if workspace else None),
             _abi.ptr(workspace.lse_part if workspace else None),
             out.data_ptr(), out.stride(0), out.stride(1),
@@ -243,7 +275,7 @@ def decode_attention(
     if n_splits > 1:
         _abi.check(
             lib.mla_merge(
-                workspace.o_part.data_ptr(), workspace.lse_part.data_ptr(), kv_len.data_ptr(),
+                workspace.o_part.data_ptr(), workspace.lse_part.data_ptr(), p_len, p_sp, int(rows_per_seq),
                 rows, H, R, n_splits, min_chunk, out.data_ptr(), out.stride(0), out.stride(1),
                 _abi.ptr(lse_out), _abi.dtype_code(dt), stream,
             )

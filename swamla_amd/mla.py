@@ -267,53 +267,44 @@ class MLA(nn.Module):
         self._check_geometry()
         B, T, _ = x.size()
         cache = self.latent_cache()
-        if not isinstance(start_pos, torch.Tensor) and (start_pos < 0 or start_pos + T > cache.ckv.shape[1]):
-            raise ValueError(f"start_pos {start_pos} + seqlen {T} exceeds max_seq_len {cache.ckv.shape[1]}")
+        sp = self._start_positions(B, T, start_pos, cache, x.device)
         with torch.no_grad():
-            b_idx, dst, rope_pos, _, _ = self._positions(B, T, start_pos, x.device)
             kv = self.wkv_a(x).view(B * T, -1)
             cos, sin = self.rope.half_tables()
-            kernels.append(kv, b_idx, dst, rope_pos, self.kv_norm.weight, self.kv_norm.bias,
-                           self.kv_norm.eps, cos, sin, cache)
+            kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
+                           start_pos=sp, tokens_per_seq=T, rope_abs=self.rope_positions == "absolute")
 
-    def _positions(self, B: int, T: int, start_pos, device):
-        """int32 index vectors of the B*T new tokens (token i = b*T + t)."""
-        t_idx = torch.arange(T, dtype=torch.int32, device=device).repeat(B)
-        b_idx = torch.arange(B, dtype=torch.int32, device=device).repeat_interleave(T)
+    def _start_positions(self, B: int, T: int, start_pos, cache: LatentCache, device) -> torch.Tensor:
+        """int32 [B] device tensor of per-sequence start positions (checked
+        against the cache when given as an int, as mla.py:413 would raise)."""
+        if B > cache.ckv.shape[0]:
+            raise ValueError(f"batch {B} exceeds max_batch_size {cache.ckv.shape[0]}")
         if isinstance(start_pos, torch.Tensor):
             sp = start_pos.to(device=device, dtype=torch.int32).reshape(-1)
             if sp.numel() != B:
                 raise ValueError(f"start_pos tensor has {sp.numel()} entries for batch {B}")
-            dst = sp.repeat_interleave(T) + t_idx if T > 1 else sp.clone()
-            max_len = self.max_seq_len
-        else:
-            sp = int(start_pos)
-            dst = t_idx + sp
-            max_len = sp + T
-        rope = t_idx if self.rope_positions == "chunk" else dst
-        return b_idx, dst, rope, dst + 1, max_len
+            return sp if sp.is_contiguous() else sp.contiguous()
+        start_pos = int(start_pos)
+        if start_pos < 0 or start_pos + T > cache.ckv.shape[1]:
+            raise ValueError(f"start_pos {start_pos} + seqlen {T} exceeds max_seq_len {cache.ckv.shape[1]}")
+        return torch.full((B,), start_pos, dtype=torch.int32, device=device)
 
     def _forward_kernels(self, x: torch.Tensor, start_pos) -> torch.Tensor:
         B, T, _ = x.size()
         dev = x.device
         H, R, Dn, Dv = self.n_heads, self.kv_lora_rank, self.qk_nope_head_dim, self.v_head_dim
         n = B * T
+        rope_abs = self.rope_positions == "absolute"
 
         if self.inference_mode:
             cache = self.latent_cache()
-            if B > cache.ckv.shape[0]:
-                raise ValueError(f"batch {B} exceeds max_batch_size {cache.ckv.shape[0]}")
-            if not isinstance(start_pos, torch.Tensor) and (start_pos < 0 or start_pos + T > cache.ckv.shape[1]):
-                raise ValueError(
-                    f"start_pos {start_pos} + seqlen {T} exceeds max_seq_len {cache.ckv.shape[1]}"
-                )
-            b_idx, dst, rope_pos, kv_len, max_len = self._positions(B, T, start_pos, dev)
+            sp = self._start_positions(B, T, start_pos, cache, dev)
+            max_len = (int(start_pos) + T) if not isinstance(start_pos, torch.Tensor) else cache.ckv.shape[1]
         else:
             # No cache (mla.py:419-423): attend over this call's tokens only.
             cache = LatentCache.allocate(B, T, x.dtype, dev, fp8=self.fp8_cache)
-            b_idx, dst, rope_pos, kv_len, max_len = self._positions(B, T, 0, dev)
-            if self.rope_positions == "absolute" and isinstance(start_pos, int):
-                rope_pos = rope_pos + start_pos
+            sp = torch.zeros(B, dtype=torch.int32, device=dev)
+            max_len = T
 
         if self.q_lora_rank == 0:  # mla.py:281-288
             q = self.wq(x)
@@ -323,10 +314,8 @@ class MLA(nn.Module):
         kv = self.wkv_a(x).view(n, -1)  # mla.py:307-308
 
         cos, sin = self.rope.half_tables()
-        kernels.append(
-            kv, b_idx, dst, rope_pos, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps,
-            cos, sin, cache,
-        )
+        kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
+                       start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
 
         w_uk, w_uv_t = self.absorbed_weights()
         q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]
@@ -334,8 +323,8 @@ class MLA(nn.Module):
         o_lat = torch.empty(H, n, R, dtype=x.dtype, device=dev)
         n_splits, min_chunk = self._split_plan(n, max_len, dev)
         kernels.decode_attention(
-            q_abs.transpose(0, 1), q[:, :, Dn:], rope_pos, cos, sin, cache, b_idx, kv_len,
-            self.softmax_scale, n_splits=n_splits, min_chunk=min_chunk,
+            q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
+            start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
             out=o_lat.transpose(0, 1), workspace=self._workspace_for(n, n_splits, dev),
         )
         o = torch.bmm(o_lat, w_uv_t)  # [H, n, Dv]

@@ -40,18 +40,18 @@ def test_abi_version(lib):
 
 
 def _append(lib, **kw):
-    args = dict(kv_in=FAKE, in_rs=320, n_tok=4, seq=FAKE, dst=FAKE, rope=FAKE, w=FAKE, b=FAKE, eps=1e-5,
-                cos=FAKE, sin=FAKE, rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, err=None,
-                in_dt=1, c_dt=1, R=256, P=64, stream=None)
+    args = dict(kv_in=FAKE, in_rs=320, n_tok=4, seq=FAKE, dst=FAKE, rope=FAKE, sp=None, T=1, rope_abs=0,
+                w=FAKE, b=FAKE, eps=1e-5, cos=FAKE, sin=FAKE, rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2,
+                cs=16, err=None, in_dt=1, c_dt=1, R=256, P=64, stream=None)
     args.update(kw)
     return lib.mla_append(*args.values())
 
 
 def _decode(lib, **kw):
-    args = dict(qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, qrp=FAKE, cos=FAKE, sin=FAKE,
-                rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, row_seq=FAKE, kv_len=FAKE, n_rows=2,
-                H=16, R=256, P=64, sm=0.07, ns=1, mc=64, o_part=None, lse=None, o=FAKE, o_rs=4096, o_hs=256,
-                dt=1, c_dt=1, stream=None)
+    args = dict(qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, cos=FAKE, sin=FAKE,
+                rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, row_seq=FAKE, kv_len=FAKE, qrp=FAKE,
+                sp=None, T=1, rope_abs=0, n_rows=2, H=16, R=256, P=64, sm=0.07, ns=1, mc=64, o_part=None,
+                lse=None, o=FAKE, o_rs=4096, o_hs=256, dt=1, c_dt=1, stream=None)
     args.update(kw)
     return lib.mla_decode_attn(*args.values())
 
@@ -71,6 +71,10 @@ def _decode(lib, **kw):
         (dict(cs=0), -1),
         (dict(rope_len=0), -1),
         (dict(ckv=FAKE + 8), -3),
+        (dict(sp=FAKE), -1),  # both addressing modes
+        (dict(seq=None, dst=None, rope=None, sp=FAKE, T=3), -1),  # 4 tokens, 3 per sequence
+        (dict(seq=None, dst=None, rope=None, sp=FAKE, T=0), -1),
+        (dict(seq=None, dst=None, rope=None, sp=FAKE, T=2, rope_abs=2), -1),
     ],
 )
 def test_append_rejects(lib, kw, code):
@@ -81,6 +85,7 @@ def test_append_rejects(lib, kw, code):
 def test_append_zero_tokens_is_a_noop(lib):
     # n_tok = 0 returns before any launch (no GPU needed)
     assert _append(lib, n_tok=0, kv_in=None, seq=None, dst=None, rope=None) == 0
+    assert _append(lib, n_tok=0, kv_in=None, seq=None, dst=None, rope=None, sp=FAKE, T=4) == 0
 
 
 @pytest.mark.parametrize(
@@ -102,6 +107,9 @@ def test_append_zero_tokens_is_a_noop(lib):
         (dict(qa=FAKE + 4), -3),
         (dict(o_rs=4100), -3),
         (dict(qp_hs=196), -3),
+        (dict(sp=FAKE), -1),
+        (dict(row_seq=None, kv_len=None, qrp=None, sp=FAKE, T=3), -1),
+        (dict(row_seq=None), -1),
     ],
 )
 def test_decode_rejects(lib, kw, code):
@@ -109,12 +117,21 @@ def test_decode_rejects(lib, kw, code):
     assert lib.mla_last_error().decode()
 
 
+def _merge(lib, **kw):
+    args = dict(o_part=FAKE, lse=FAKE, kv_len=FAKE, sp=None, T=1, n_rows=2, H=16, R=256, ns=4, mc=64, o=FAKE,
+                o_rs=4096, o_hs=256, lse_out=None, dt=1, stream=None)
+    args.update(kw)
+    return lib.mla_merge(*args.values())
+
+
 def test_merge_rejects_and_noop(lib):
-    assert lib.mla_merge(FAKE, FAKE, FAKE, 2, 16, 256, 1, 64, FAKE, 4096, 256, None, 1, None) == 0
-    assert lib.mla_merge(FAKE, FAKE, FAKE, 2, 16, 128, 4, 64, FAKE, 4096, 256, None, 1, None) == -2
-    assert lib.mla_merge(None, FAKE, FAKE, 2, 16, 256, 4, 64, FAKE, 4096, 256, None, 1, None) == -1
-    assert lib.mla_merge(FAKE, FAKE, FAKE, 2, 16, 256, 4, 64, FAKE, 4096, 256, None, 2, None) == -2
-    assert lib.mla_merge(FAKE + 4, FAKE, FAKE, 2, 16, 256, 4, 64, FAKE, 4096, 256, None, 1, None) == -3
+    assert _merge(lib, ns=1) == 0
+    assert _merge(lib, R=128) == -2
+    assert _merge(lib, o_part=None) == -1
+    assert _merge(lib, dt=2) == -2
+    assert _merge(lib, o_part=FAKE + 4) == -3
+    assert _merge(lib, kv_len=None) == -1
+    assert _merge(lib, sp=FAKE) == -1
 
 
 def test_python_check_raises_with_message(lib):

@@ -62,7 +62,8 @@ def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0):
         cache.scale.fill_(-1.0)
     cos, sin = tables(dtype, S, gpu)
     kvg = kv.to(gpu)
-    kernels.append(kvg[:, :], seq.to(gpu), dst.to(gpu), rp.to(gpu), w.to(gpu), b.to(gpu), 1e-5, cos, sin, cache)
+    kernels.append(kvg, cache, w.to(gpu), b.to(gpu), 1e-5, cos, sin,
+                   seq_idx=seq.to(gpu), dst_pos=dst.to(gpu), rope_pos=rp.to(gpu))
     torch.cuda.synchronize()
 
     # expected rows
@@ -112,7 +113,7 @@ def test_append_out_of_range_is_skipped_and_flagged(gpu):
     flag = torch.zeros(1, dtype=torch.int32, device=gpu)
     w = torch.ones(R, dtype=dtype, device=gpu)
     b = torch.zeros(R, dtype=dtype, device=gpu)
-    kernels.append(kv, seq, dst, rp, w, b, 1e-5, cos, sin, cache, err_flag=flag)
+    kernels.append(kv, cache, w, b, 1e-5, cos, sin, seq_idx=seq, dst_pos=dst, rope_pos=rp, err_flag=flag)
     torch.cuda.synchronize()
     assert int(flag.item()) == 1
     assert bool((cache.ckv[0, 0] != 0).any())  # the valid token landed
@@ -125,7 +126,8 @@ def _decode_case(gpu, dtype, fp8, lens, n_splits, min_chunk, row_seq=None, B=Non
     rows = len(lens)
     B = B or rows
     S = S or max(max(lens), 1)
-    say(f"decode case dtype={dtype} fp8={fp8} rows={rows} lens={lens[:6]}... splits={n_splits} chunk={min_chunk}")
+    say(f"decode case dtype={dtype} fp8={fp8} rows={rows} lens={lens[:6]}... splits={n_splits} "
+        f"chunk={min_chunk}")
     g = torch.Generator().manual_seed(seed)
     cdt = torch.bfloat16 if fp8 else dtype
     ckv = (torch.randn(B, S, R, generator=g)).to(cdt)
@@ -142,8 +144,8 @@ def _decode_case(gpu, dtype, fp8, lens, n_splits, min_chunk, row_seq=None, B=Non
     rp = torch.zeros(rows, dtype=torch.int32) if rope_pos is None else torch.tensor(rope_pos, dtype=torch.int32)
     cos, sin = tables(dtype, max(S, 64), gpu)
     out = kernels.decode_attention(
-        q_abs.to(gpu), q_pe.to(gpu), rp.to(gpu), cos, sin, cache, rs.to(gpu), kl.to(gpu), SCALE,
-        n_splits=n_splits, min_chunk=min_chunk,
+        q_abs.to(gpu), q_pe.to(gpu), cos, sin, cache, SCALE, row_seq=rs.to(gpu), kv_len=kl.to(gpu),
+        q_rope_pos=rp.to(gpu), n_splits=n_splits, min_chunk=min_chunk,
     )
     torch.cuda.synchronize()
     q_pe_rot = lo.rope_interleaved(q_pe, cos.cpu()[rp.long()][:, None], sin.cpu()[rp.long()][:, None])
@@ -212,8 +214,10 @@ def test_decode_constant_latent_rows(gpu):
     q_pe = torch.randn(B, H, P).to(dtype).to(gpu)
     cos, sin = tables(dtype, S, gpu)
     z = torch.zeros(B, dtype=torch.int32, device=gpu)
-    out = kernels.decode_attention(q_abs, q_pe, z, cos, sin, cache, torch.arange(B, dtype=torch.int32, device=gpu),
-                                   torch.tensor([S, 300], dtype=torch.int32, device=gpu), SCALE, n_splits=1)
+    out = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE,
+                                   row_seq=torch.arange(B, dtype=torch.int32, device=gpu),
+                                   kv_len=torch.tensor([S, 300], dtype=torch.int32, device=gpu),
+                                   q_rope_pos=z, n_splits=1)
     torch.cuda.synchronize()
     err = (out.float().cpu() - row.float()).abs().max()
     assert float(err) <= 2 ** -8 * float(row.float().abs().max())
@@ -225,3 +229,63 @@ def test_decode_headline_shape(gpu):
     n_splits, mc = kernels.plan_splits(32, 4097)
     _decode_case(gpu, torch.bfloat16, False, lens, n_splits, mc, seed=11, q_scale=0.5)
     _decode_case(gpu, torch.bfloat16, True, lens, n_splits, mc, seed=12, q_scale=0.5)
+
+
+def test_workspace_reuse_repeated_calls(gpu):
+    """Back-to-back calls that reuse one partial workspace (as a replayed
+    graph does) keep giving the single-pass result."""
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(13)
+    B, S = 6, 3000
+    cache = LatentCache(torch.randn(B, S, R, generator=g).to(dtype).to(gpu),
+                        torch.randn(B, S, P, generator=g).to(dtype).to(gpu))
+    cos, sin = tables(dtype, S, gpu)
+    q_abs = torch.randn(B, H, R, generator=g).to(dtype).to(gpu)
+    q_pe = torch.randn(B, H, P, generator=g).to(dtype).to(gpu)
+    seq = torch.arange(B, dtype=torch.int32, device=gpu)
+    z = torch.zeros(B, dtype=torch.int32, device=gpu)
+    ws = kernels.DecodeWorkspace.allocate(B, 16, gpu)
+    outs = []
+    for i in range(5):
+        kl = torch.tensor([S - 7 * i, 64 + i, 1, 2000, 700 + i, S], dtype=torch.int32, device=gpu)
+        ref = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE, row_seq=seq, kv_len=kl,
+                                       q_rope_pos=z, n_splits=1)
+        got = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE, row_seq=seq, kv_len=kl,
+                                       q_rope_pos=z, n_splits=16, min_chunk=64, workspace=ws)
+        outs.append((got.float().cpu(), ref.float().cpu()))
+    torch.cuda.synchronize()
+    for got, ref in outs:
+        assert float((got - ref).abs().max()) <= 2 ** -7 * float(ref.abs().max())
+
+
+def test_dense_addressing_equals_explicit(gpu):
+    """start_pos addressing (entry i -> sequence i // T at start + i % T) gives
+    the same cache bits and attention outputs as the explicit arrays."""
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(14)
+    B, T, S = 3, 5, 256
+    start = torch.tensor([0, 17, 200], dtype=torch.int32)
+    kv = (torch.randn(B * T, 320, generator=g) * 2).to(dtype).to(gpu)
+    w = (1 + 0.1 * torch.randn(R, generator=g)).to(dtype).to(gpu)
+    b = (0.1 * torch.randn(R, generator=g)).to(dtype).to(gpu)
+    cos, sin = tables(dtype, S, gpu)
+    seq = torch.arange(B, dtype=torch.int32).repeat_interleave(T)
+    t = torch.arange(T, dtype=torch.int32).repeat(B)
+    dst = start.repeat_interleave(T) + t
+    for rope_abs in (False, True):
+        rp = dst if rope_abs else t
+        c1 = LatentCache.allocate(B, S, dtype, gpu)
+        c2 = LatentCache.allocate(B, S, dtype, gpu)
+        kernels.append(kv, c1, w, b, 1e-5, cos, sin, seq_idx=seq.to(gpu), dst_pos=dst.to(gpu), rope_pos=rp.to(gpu))
+        kernels.append(kv, c2, w, b, 1e-5, cos, sin, start_pos=start.to(gpu), tokens_per_seq=T, rope_abs=rope_abs)
+        torch.cuda.synchronize()
+        assert torch.equal(c1.ckv.view(torch.int16), c2.ckv.view(torch.int16))
+        assert torch.equal(c1.kpe.view(torch.int16), c2.kpe.view(torch.int16))
+        q_abs = torch.randn(B * T, H, R, generator=g).to(dtype).to(gpu)
+        q_pe = torch.randn(B * T, H, P, generator=g).to(dtype).to(gpu)
+        o1 = kernels.decode_attention(q_abs, q_pe, cos, sin, c1, SCALE, row_seq=seq.to(gpu),
+                                      kv_len=(dst + 1).to(gpu), q_rope_pos=rp.to(gpu), n_splits=4, min_chunk=64)
+        o2 = kernels.decode_attention(q_abs, q_pe, cos, sin, c2, SCALE, start_pos=start.to(gpu), rows_per_seq=T,
+                                      rope_abs=rope_abs, n_splits=4, min_chunk=64)
+        torch.cuda.synchronize()
+        assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))

@@ -255,7 +255,7 @@ def test_split_plan_matches_library(lib):
         assert lib.mla_split_count(L, ns, mc) == ours
         if L > 0:
             ch = lo.split_chunk(L, ns, mc)
-            assert 1 <= ours <= ns and (ours - 1) * ch < L <= ours * ch and ch % 64 == 0
+            assert 1 <= ours <= ns and (ours - 1) * ch < L <= ours * ch and ch % 16 == 0
 
 
 # --------------------------------------------------------- whole-path oracle
