@@ -57,6 +57,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--cpu-batch", type=int, default=4)
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run plain device copies of known size (calibrates FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -64,14 +66,55 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+KERNEL_SOURCE = os.path.join(ROOT, "swamla_amd", "csrc", "mla_kernels.hip")
+
+
+def measured_traffic(B: int, L: int, cache: str):
+    """HBM bytes per decode launch from a committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/*_traffic.md) taken on this kernel source at
+    this launch shape, else None (counters cannot be read from inside this
+    process).  Returns (bytes, summary file name)."""
+    import glob
+    import hashlib
+
+    try:
+        src = hashlib.sha256(open(KERNEL_SOURCE, "rb").read()).hexdigest()[:16]
+    except OSError:
+        return None, None
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_traffic.md"))):
+        fields = {}
+        for line in open(path).read().splitlines():
+            key, sep, val = line.partition(": ")
+            if sep and key.isidentifier():
+                fields[key] = val.strip()
+        if fields.get("kernel_source_sha256_16") == src and fields.get("launch") == f"B={B} L={L} cache={cache}":
+            try:
+                return int(fields["traffic_bytes_per_launch"]), os.path.relpath(path, ROOT)
+            except (KeyError, ValueError):
+                pass
+    return None, None
+
+
 def attention_bytes(B: int, L: int, fp8: bool) -> int:
     per_tok = R * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0)
     return B * L * per_tok + B * H * (R + P) * 2 + B * H * R * 2
 
 
+def init_linear_weights(module, seed: int, torch) -> None:
+    """N(0, 0.02) Linear weights in parameter order from a CPU generator and
+    zero biases; LayerNorm stays at weight 1 / bias 0, as the reference model
+    initialises it (models/swa_mla_model.py:314-320)."""
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in module.named_parameters():
+            if name.startswith(("wq", "wkv_a", "wkv_b", "wo")) and name.endswith("weight"):
+                p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+            elif name.endswith("bias") and not name.startswith(("kv_norm", "q_norm")):
+                p.zero_()
+
+
 def build_layers(args, dev, torch):
-    from oracle.mla_ref import MLAConfig, init_weights  # weight init recipe only
-    from swamla_amd import MLA
+    from swamla_amd import MLA, MLAConfig
 
     max_seq = (args.ctx + args.steps + args.warmup + 63) // 64 * 64
     cfg = MLAConfig(n_embd=args.dim, max_batch_size=args.batch, max_seq_len=max_seq)
@@ -79,7 +122,7 @@ def build_layers(args, dev, torch):
     g = torch.Generator(device=dev).manual_seed(1234)
     for i in range(args.layers):
         m = MLA(cfg, cache_dtype="fp8_e4m3" if args.cache == "fp8" else None)
-        init_weights(m, 100 + i)
+        init_linear_weights(m, 100 + i, torch)
         m.eval().to(torch.bfloat16).to(dev)
         m.set_inference_mode(True)
         with torch.no_grad():
@@ -220,6 +263,15 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        # 256 MiB bf16 -> 256 MiB: each copy reads and writes exactly 268435456 B.
+        src = torch.randn(128 << 20, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2, "copies": 5}))
+        return 0
     fp8 = args.cache == "fp8"
     log(f"building {args.layers} layers, batch {args.batch}, prefill {args.ctx} ({args.cache} cache)")
     layers = build_layers(args, dev, torch)
@@ -269,6 +321,7 @@ def main() -> int:
 
     cold_us, warm_us, merge_us, L, B, n_splits = time_decode_kernel(layers, xs, args, dev, torch)
     abytes = attention_bytes(B, L, fp8)
+    traffic, traffic_src = measured_traffic(B, L, args.cache)
     achieved = abytes / (cold_us * 1e-6) / 1e9
     warm = abytes / (warm_us * 1e-6) / 1e9
     log(f"decode kernel: {cold_us:.2f} us cold ({achieved:.0f} GB/s), {warm_us:.2f} us warm ({warm:.0f} GB/s); "
@@ -314,7 +367,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": (f"rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated: {traffic_src}" if traffic
+                               else "no committed PMC summary for this kernel source and launch shape"),
             "bytes_per_launch": abytes,
             "avg_launch_us": cold_us,
             "launch": f"B={B} L={L} splits<={n_splits}, caches rotated over {len(layers)} layers",

@@ -5,12 +5,14 @@ A drop-in for the absorb branch of Orolol/swamla's ``MLA`` module
 log-sum-exp merge as hand-written HIP kernels behind a C-ABI
 (include/swamla_mi355x.h), driven from PyTorch-ROCm host code.
 """
+from .config import MLAConfig
 from .kernels import DecodeWorkspace, LatentCache, append, decode_attention, plan_splits
 from .mla import MLA
 from .rope import RoPE, rope_tables
 
 __all__ = [
     "MLA",
+    "MLAConfig",
     "RoPE",
     "rope_tables",
     "LatentCache",
