@@ -296,36 +296,60 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ o_part, con
 // ---------------------------------------------------------------------------
 // Kernel 2: absorbed decode attention, bf16 MFMA (cache bf16 or e4m3).
 //
-// Block = NW wavefronts, one block per (query row, split).  Wave w streams
-// the 16-token sub-tiles base = t0 + 16*(w + NW*i), keeping DEPTH sub-tiles
-// of global loads in flight.  Per sub-tile:
+// One block of four wavefronts per (query row, split).  The waves walk the
+// split's tokens in lockstep, 64-token tiles, wave w owning tokens
+// 16w..16w+15 of each tile, with DEPTH tiles of its global loads in flight
+// in registers.  The loads read whole 128-byte lines: one instruction
+// covers 8 tokens x 128 B (lane l: token l%8, bytes 16*(l/8) of a segment);
+// loading in the MFMA operand layout instead (16 tokens x 64 B per
+// instruction) touches twice the lines per instruction and streams ~25 %
+// slower.  Per tile:
+//   the wave stores its 16 latent rows (as bf16; e4m3 codes are decoded
+//       exactly) and rope rows into the block's LDS tile and reads them back
+//       in the MFMA operand layout (lane = token, 8 channels)
 //   S^T[16 tok x 16 heads] = K[16 tok x 320] . Q^T[320 x 16 heads]
-//       10 x mfma_f32_16x16x32_bf16; K comes straight from 16 B global loads
-//       (lane = token, 8 channels), Q^T stays in registers
-//   online softmax per head, lane-local (lane owns head l%16, tokens 4g..4g+3)
-//   O^T[256 ch x 16 heads] += C^T[256 x 16 tok] . P^T[16 tok x 16 heads]
-//       16 x mfma_f32_16x16x16_bf16; the latent rows go to a wave-private
-//       LDS tile (row-major, 544 B rows) and come back transposed through
-//       ds_read_b64_tr_b16: in each 16-lane group, lane i element k is element
-//       i%4 of the 8 bytes addressed by lane i/4 + 4k, so lane s points at
-//       C[4g + s/4][16mb + 4(s%4)].
-// The NW waves' (m, l, O) are merged through LDS at the end; rows with more
-// than one split write normalised partials for mla_merge.  (Merging inside
-// the decode kernel — the last block of a row combining the others' partials
-// — needs device-scope release fences, which write back the whole L2 of an
-// XCD per block on gfx950 and serialised the kernel; it is not done.)
+//       10 x mfma_f32_16x16x32_bf16 on its own tokens; Q^T stays in
+//       registers for the whole split
+//   the four waves' per-head maxima meet in LDS, so every wave applies the
+//       same softmax reference (moved lazily, see kLazy), and each wave writes
+//       its bf16 weights P into a shared [16 heads x 64 tokens] LDS array
+//   O^T[64 ch x 16 heads] += C^T[64 ch x 64 tok] . P^T[64 tok x 16 heads]
+//       8 x mfma_f32_16x16x32_bf16 per wave over ITS 64 of the 256 latent
+//       channels (channels 64w..64w+63) and all 64 tokens of the tile.  C^T
+//       comes from the tile through ds_read_b64_tr_b16: in each 16-lane
+//       group, lane i element k is element i%4 of the 8 bytes addressed by
+//       lane i/4 + 4k, so lane s points at C[4g + s/4][c + 4(s%4)].
+// Each wave thus ends with the final O of its own channels and nothing is
+// combined across waves except the per-head sums of the weights.  Rows with
+// more than one split write normalised fp32 partials and their log-sum-exp
+// for mla_merge.  (Merging inside this kernel — the last block of a row
+// combining the others' partials — needs device-scope release fences, which
+// write back the whole L2 of an XCD per block on gfx950 and serialised the
+// kernel; it is not done.)
+//
+// LDS rows are padded so that every access pattern above is free of bank
+// conflicts beyond its minimum: latent rows 528 B (16 tokens x 16 B at one
+// column hit 16 distinct 16-byte slots), rope rows 144 B.
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kSub = 16;                 // tokens per wave sub-tile
-constexpr int kCRow = 544;               // bytes per LDS row of a latent sub-tile (512 + 32 pad)
-constexpr int kCTile = kSub * kCRow;     // 8704 B per wave
-constexpr int kOStride = kR + 4;         // fp32 row stride of the cross-wave merge buffer
+constexpr int kSub = 16;                   // tokens per wave in a tile
+constexpr int kWaves = 4;                  // waves per block
+constexpr int kTileTok = kSub * kWaves;    // 64 tokens per lockstep tile
+constexpr int kCRow = 2 * kR + 16;         // 528 B per LDS latent row
+constexpr int kPeRow = 2 * kP + 16;        // 144 B per LDS rope row
+constexpr int kCBytes = kTileTok * kCRow;  // 33792 B
+constexpr int kPeBytes = kTileTok * kPeRow;  // 9216 B
+constexpr int kPRow = 2 * kTileTok + 16;   // bytes per head row of P (128 + 16 pad)
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+__device__ __forceinline__ bf16x8_t cat_bf16x8(s16x4_t lo, s16x4_t hi) {
+  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+  return as_bf16x8(make_uint4(a.x, a.y, b.x, b.y));
+}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -349,18 +373,20 @@ __device__ __forceinline__ float wave_max_rows(float v) {
 
 constexpr float kLazy = 8.0f;  // log2 headroom before the softmax reference moves
 
-// Channel order of the K dimension for MFMA step s (0..7) and lane group g:
-// the 8 channels [chan(s,g), +8).  bf16 cache: plain order.  e4m3 cache: a
-// 16 B load of 16 codes feeds steps 2j and 2j+1, so channels interleave.
-template <int C_DT>
-__device__ __forceinline__ int chan_of(int s, int g) {
-  if constexpr (C_DT == 2) return 64 * (s >> 1) + 16 * g + 8 * (s & 1);
-  return 32 * s + 8 * g;
+// Workgroup barrier that orders LDS only: global loads stay in flight across
+// it (a full fence would also wait for them).  The release half completes
+// this wave's earlier LDS reads and writes before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Registers of one in-flight sub-tile.  bf16: 8 x 16 B latent + 2 x 16 B
-// rope.  e4m3: 4 x 16 B codes + 2 x 16 B rope + the 4 scales this lane's
-// scores need.
+// Registers of one in-flight tile (this wave's 16 tokens), loaded as whole
+// lines: element s of c covers tokens 8(s&1)..+8, bytes 128(s>>1)..+128 of
+// the latent rows (lane: token l%8, 16 B at 16(l/8)); p[j] the same for
+// rope rows, tokens 8j..+8.  e4m3: 4 segments of codes plus the 4 scales this
+// lane's scores need.
 template <int C_DT>
 struct KTile;
 template <>
@@ -385,12 +411,22 @@ __device__ __forceinline__ uint2 e4m3x4_to_bf16x4_hw(uint32_t w) {
   return make_uint2(a, b);
 }
 
-template <int C_DT, int NW, int DEPTH>
-__global__ __launch_bounds__(NW * 64, 2) void mla_decode_mfma(DecodeArgs a) {
-  constexpr int kLdsBytes = (NW * kCTile > NW * kH * kOStride * 4) ? NW * kCTile : NW * kH * kOStride * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t c_lds[kLdsBytes];
-  __shared__ float m_lds[NW][kH];
-  __shared__ float l_lds[NW][kH];
+// 16-byte global load marked non-temporal: the cache is streamed once, and
+// the non-temporal hint keeps it from thrashing the vector L1 (measured
+// ~10 % more read bandwidth for this kernel on MI355X).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+template <int C_DT, int DEPTH>
+__global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t c_lds[kCBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t pe_lds[kPeBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t p_lds[kH * kPRow];
+  __shared__ float mx_lds[kWaves][kH];
+  __shared__ float l_lds[kWaves][kH];
 
   const int r = blockIdx.y;
   const int split = blockIdx.x;
@@ -400,6 +436,7 @@ __global__ __launch_bounds__(NW * 64, 2) void mla_decode_mfma(DecodeArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
+  const int lt = lane & 7, lc = lane >> 3;  // whole-line loads: token, 16-byte column
 
   const TokAddr ra = row_addr(a.ad, r);
   const int b = ra.b;
@@ -411,139 +448,153 @@ __global__ __launch_bounds__(NW * 64, 2) void mla_decode_mfma(DecodeArgs a) {
   const int chunk = ns ? split_chunk(L, a.n_splits, a.min_chunk) : 0;
   const int t0 = split * chunk;
   const int t1 = min(L, t0 + chunk);
+  const int n_tiles = t1 > t0 ? (t1 - t0 + kTileTok - 1) / kTileTok : 0;  // block-uniform
 
-  // Loads below are issued unconditionally, so every address is clamped to a
-  // valid cache element: an invalid or empty row reads row 0, token 0.
+  // Loads are issued unconditionally, so every address is clamped to a valid
+  // cache element: an invalid or empty row reads row 0, token 0.
   const int64_t cache_row0 = static_cast<int64_t>((b < 0 || b >= a.cache_b) ? 0 : b) * a.cache_s;
   const int t_last = t1 > 0 ? t1 - 1 : 0;
-  const uint16_t* kpe = static_cast<const uint16_t*>(a.kpe);
 
-  // Global loads of the sub-tile at `base`: lane's token = base + n (clamped
-  // into range; masked in the softmax).
-  auto load_tile = [&](int base, KTile<C_DT>& kt) {
-    int tok = base + n;
-    tok = tok < t_last ? tok : t_last;
-    const int64_t crow = cache_row0 + tok;
+  // Global loads of this wave's 16 tokens of tile j (tokens clamped into
+  // range; the surplus ones are masked in the softmax).
+  auto load_tile = [&](int j, KTile<C_DT>& kt) {
+    const int wbase = t0 + j * kTileTok + kSub * w;
+    const int64_t row_a = cache_row0 + min(wbase + lt, t_last);
+    const int64_t row_b = cache_row0 + min(wbase + 8 + lt, t_last);
     if constexpr (C_DT == 2) {
-      const uint8_t* cp = static_cast<const uint8_t*>(a.ckv) + crow * kR;
+      const uint8_t* ca = static_cast<const uint8_t*>(a.ckv) + row_a * kR + 16 * lc;
+      const uint8_t* cb = static_cast<const uint8_t*>(a.ckv) + row_b * kR + 16 * lc;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) kt.c[j] = *reinterpret_cast<const uint4*>(cp + 64 * j + 16 * g);
-      const int tb = base + 4 * g;  // scales of the 4 tokens this lane scores
+      for (int q = 0; q < 2; ++q) {
+        kt.c[2 * q] = ld_stream16(ca + 128 * q);
+        kt.c[2 * q + 1] = ld_stream16(cb + 128 * q);
+      }
+      const int tb = wbase + 4 * g;  // scales of the 4 tokens this lane scores
       const float* sp = a.ckv_scale + cache_row0;
       kt.sc.x = sp[min(tb + 0, t_last)];
       kt.sc.y = sp[min(tb + 1, t_last)];
       kt.sc.z = sp[min(tb + 2, t_last)];
       kt.sc.w = sp[min(tb + 3, t_last)];
     } else {
-      const uint16_t* cp = static_cast<const uint16_t*>(a.ckv) + crow * kR;
+      const uint8_t* ca = static_cast<const uint8_t*>(a.ckv) + row_a * (2 * kR) + 16 * lc;
+      const uint8_t* cb = static_cast<const uint8_t*>(a.ckv) + row_b * (2 * kR) + 16 * lc;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) kt.c[s] = *reinterpret_cast<const uint4*>(cp + 32 * s + 8 * g);
+      for (int q = 0; q < 4; ++q) {
+        kt.c[2 * q] = ld_stream16(ca + 128 * q);
+        kt.c[2 * q + 1] = ld_stream16(cb + 128 * q);
+      }
     }
-    const uint16_t* pp = kpe + crow * kP;
-    kt.p[0] = *reinterpret_cast<const uint4*>(pp + 8 * g);
-    kt.p[1] = *reinterpret_cast<const uint4*>(pp + 32 + 8 * g);
+    const uint8_t* kpe = static_cast<const uint8_t*>(a.kpe);
+    kt.p[0] = ld_stream16(kpe + row_a * (2 * kP) + 16 * lc);
+    kt.p[1] = ld_stream16(kpe + row_b * (2 * kP) + 16 * lc);
   };
 
-  // ---- Q^T operand (B of S^T): lane holds head n, channels chan(s,g)..+8.
+  // ---- Q^T operand (B of S^T): lane holds head n, channels 32s + 8g..+8.
+  KTile<C_DT> kt[DEPTH];
   bf16x8_t qb[10];
   {
     const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + r * a.qa_rs + n * a.qa_hs;
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      qb[s] = as_bf16x8(*reinterpret_cast<const uint4*>(qa + chan_of<C_DT>(s, g)));
+    for (int s = 0; s < 8; ++s) qb[s] = as_bf16x8(*reinterpret_cast<const uint4*>(qa + 32 * s + 8 * g));
     // q_pe with interleaved RoPE at the row's table position
     const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + r * a.qp_rs + n * a.qp_hs;
     int rp = ra.rope;
     rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
     const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
     const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
+    uint4 raw[2];
+    uint2 cr[2], sr[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int c0 = 32 * s + 8 * g;
-      uint4 raw = *reinterpret_cast<const uint4*>(qp + c0);
-      uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+      raw[s] = *reinterpret_cast<const uint4*>(qp + c0);
+      cr[s] = *reinterpret_cast<const uint2*>(ct + c0 / 2);
+      sr[s] = *reinterpret_cast<const uint2*>(st + c0 / 2);
+    }
+    // Q's loads are issued first, the tiles' right behind them: waiting for
+    // Q leaves every tile load in flight.
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load_tile(d, kt[d]);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t wv_in[4] = {raw[s].x, raw[s].y, raw[s].z, raw[s].w};
+      const uint32_t cw2[2] = {cr[s].x, cr[s].y}, sw2[2] = {sr[s].x, sr[s].y};
+      uint32_t wv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int pi = c0 / 2 + j;
+        const uint32_t cj = (j & 1) ? (cw2[j >> 1] >> 16) : (cw2[j >> 1] & 0xFFFF);
+        const uint32_t sj = (j & 1) ? (sw2[j >> 1] >> 16) : (sw2[j >> 1] & 0xFFFF);
         float o1, o2;
-        rope_pair<1>(bf16_to_f32(wv[j] & 0xFFFF), bf16_to_f32(wv[j] >> 16), bf16_to_f32(ct[pi]),
-                     bf16_to_f32(st[pi]), o1, o2);
+        rope_pair<1>(bf16_to_f32(wv_in[j] & 0xFFFF), bf16_to_f32(wv_in[j] >> 16), bf16_to_f32(cj),
+                     bf16_to_f32(sj), o1, o2);
         wv[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
       }
       qb[8 + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
     }
   }
 
-  // Start the stream.  Every tile load is issued unconditionally (addresses
-  // are clamped into the row, surplus tiles are never consumed): the wave
-  // then always has exactly DEPTH tiles of loads in flight and the compiler
-  // can wait on the oldest tile alone.  A conditional load would force it to
-  // wait for every outstanding load, since the counter drains in order.
-  // Q's loads were issued first, so waiting for them leaves the tiles in flight.
-  constexpr int kStep = kSub * NW;
-  const int base0 = t0 + kSub * w;
-  const bool has_work = t1 > t0;  // block-uniform; false only for an empty row
-  KTile<C_DT> kt[DEPTH];
+  f32x4_t oacc[4];
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) load_tile(base0 + d * kStep, kt[d]);
-
-  f32x4_t oacc[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_part = 0.f;
 
-  uint8_t* cw = c_lds + w * kCTile;
-  // tr16 source address of this lane: row 4g + s/4, channel 4(s%4) (+16 mb)
-  const uint8_t* tr_src = cw + (4 * g + (n >> 2)) * kCRow + 8 * (n & 3);
+  // LDS addresses of this lane.  Stores (whole-line layout): token
+  // 16w + lt (+8), column 16*lc of a 128-byte segment.  Operand reads: token
+  // 16w + n, 8 channels at 32s + 8g.  C^T reads: token row 4g + n/4 of each
+  // 16-token block, channel 64w + 4(n%4) (+16 mb).
+  uint8_t* const c_st = c_lds + (kSub * w + lt) * kCRow + 16 * lc;
+  uint8_t* const pe_st = pe_lds + (kSub * w + lt) * kPeRow + 16 * lc;
+  const uint8_t* const c_op = c_lds + (kSub * w + n) * kCRow + 2 * (8 * g);
+  const uint8_t* const pe_op = pe_lds + (kSub * w + n) * kPeRow + 2 * (8 * g);
+  const uint8_t* const c_tr = c_lds + (4 * g + (n >> 2)) * kCRow + 2 * (64 * w) + 8 * (n & 3);
+  uint8_t* const p_mine = p_lds + n * kPRow + 2 * (kSub * w + 4 * g);
+  const uint8_t* const p_row = p_lds + n * kPRow + 2 * (4 * g);
 
-  auto process = [&](int base, KTile<C_DT>& kt) {
-    const bool full = base + kSub <= t1;  // wave-uniform
-    // MFMA operands of the latent part (e4m3 -> bf16 exactly).
-    uint4 cv[8];
-    float4 scv = make_float4(1.f, 1.f, 1.f, 1.f);
+  auto process = [&](int j, KTile<C_DT>& kt) {
+    const int wbase = t0 + j * kTileTok + kSub * w;
+    const bool full = t0 + (j + 1) * kTileTok <= t1;  // block-uniform
+
+    // This wave's latent and rope rows into the tile (e4m3 decoded to bf16).
     if constexpr (C_DT == 2) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint2 a0 = e4m3x4_to_bf16x4_hw(kt.c[j].x), a1 = e4m3x4_to_bf16x4_hw(kt.c[j].y);
-        const uint2 a2 = e4m3x4_to_bf16x4_hw(kt.c[j].z), a3 = e4m3x4_to_bf16x4_hw(kt.c[j].w);
-        cv[2 * j] = make_uint4(a0.x, a0.y, a1.x, a1.y);
-        cv[2 * j + 1] = make_uint4(a2.x, a2.y, a3.x, a3.y);
+      for (int q = 0; q < 4; ++q) {
+        const uint2 a0 = e4m3x4_to_bf16x4_hw(kt.c[q].x), a1 = e4m3x4_to_bf16x4_hw(kt.c[q].y);
+        const uint2 a2 = e4m3x4_to_bf16x4_hw(kt.c[q].z), a3 = e4m3x4_to_bf16x4_hw(kt.c[q].w);
+        // 16 codes: token 16w + 8(q&1) + lt, channels 128(q>>1) + 16lc..+16
+        uint8_t* dst = c_lds + (kSub * w + 8 * (q & 1) + lt) * kCRow + 2 * (128 * (q >> 1) + 16 * lc);
+        *reinterpret_cast<uint4*>(dst) = make_uint4(a0.x, a0.y, a1.x, a1.y);
+        *reinterpret_cast<uint4*>(dst + 16) = make_uint4(a2.x, a2.y, a3.x, a3.y);
       }
-      scv = kt.sc;
     } else {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) cv[s] = kt.c[s];
+      for (int s = 0; s < 8; ++s) {
+        // element-wise: a whole-struct copy becomes a memcpy that keeps kt
+        // out of registers
+        const uint4 v = kt.c[s];
+        *reinterpret_cast<uint4*>(c_st + 8 * (s & 1) * kCRow + 128 * (s >> 1)) = make_uint4(v.x, v.y, v.z, v.w);
+      }
     }
-    const uint4 pv0 = kt.p[0], pv1 = kt.p[1];
+    *reinterpret_cast<uint4*>(pe_st) = kt.p[0];
+    *reinterpret_cast<uint4*>(pe_st + 8 * kPeRow) = kt.p[1];
+    float4 scv = make_float4(1.f, 1.f, 1.f, 1.f);
+    if constexpr (C_DT == 2) scv = kt.sc;
 
-    // Latent rows into the wave's LDS tile (row-major, padded rows), then
-    // issue all transposed reads at once so their latency hides under the
-    // score MFMAs and the softmax.
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-      *reinterpret_cast<uint4*>(cw + n * kCRow + 2 * chan_of<C_DT>(s, g)) = cv[s];
-    s16x4_t ct[16];
-#pragma unroll
-    for (int mb = 0; mb < 16; ++mb)
-      ct[mb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4_t*)(tr_src + 32 * mb));
+    // The registers of kt are free: refill them with the tile DEPTH ahead
+    // (unconditionally, see above).
+    load_tile(j + DEPTH, kt);
 
-    // S^T = K . Q^T : lane gets head n, tokens base+4g+i.
+    // S^T = K . Q^T from the wave's own rows (LDS operations of one wave
+    // complete in order, so no wait beyond the operand reads is needed).
     f32x4_t s_c = {0.f, 0.f, 0.f, 0.f}, s_p = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 8; ++s)
-      s_c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cv[s]), qb[s], s_c, 0, 0, 0);
-    s_p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pv0), qb[8], s_p, 0, 0, 0);
-    s_p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pv1), qb[9], s_p, 0, 0, 0);
+      s_c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          as_bf16x8(*reinterpret_cast<const uint4*>(c_op + 2 * (32 * s))), qb[s], s_c, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      s_p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          as_bf16x8(*reinterpret_cast<const uint4*>(pe_op + 2 * (32 * s))), qb[8 + s], s_p, 0, 0, 0);
 
-    // The registers of kt are free: refill them with the sub-tile DEPTH ahead
-    // (unconditionally, see above).
-    load_tile(base + DEPTH * kStep, kt);
-
-    // Online softmax in the log2 domain with a lazily moved reference: the
-    // running reference m_run only moves when a head's tile maximum exceeds
-    // it by more than kLazy, so weights stay <= 2^kLazy and O is rescaled
-    // rarely (the normalisation by l is exact either way).
     float x[4];
     const float sc4[4] = {scv.x, scv.y, scv.z, scv.w};
 #pragma unroll
@@ -554,17 +605,38 @@ __global__ __launch_bounds__(NW * 64, 2) void mla_decode_mfma(DecodeArgs a) {
     if (!full) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (base + 4 * g + i >= t1) x[i] = -INFINITY;
+        if (wbase + 4 * g + i >= t1) x[i] = -INFINITY;
     }
     float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    mt = wave_max_rows(mt);  // max over lanes n, n+16, n+32, n+48 (one head)
-    if (__any(mt > m_run + kLazy)) {
-      const float m_new = fmaxf(m_run, mt);  // finite: token `base` is valid
+    mt = wave_max_rows(mt);  // max over this wave's 16 tokens of head n
+    if (g == 0) mx_lds[w][n] = mt;
+    lds_barrier();  // latent rows and maxima of all waves are visible
+
+    // C^T of this wave's channels for the whole tile; the reads' latency
+    // hides under the softmax below.
+    s16x4_t ct[2][4][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          ct[kb][mb][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4_t*)(c_tr + (32 * kb + 16 * h) * kCRow + 32 * mb));
+
+    // Online softmax in the log2 domain with a lazily moved reference shared
+    // by the four waves: m_run only moves when a head's tile maximum exceeds
+    // it by more than kLazy, so weights stay <= 2^kLazy and O is rescaled
+    // rarely (the normalisation by l is exact either way).  Every wave sees
+    // the same maxima, so the branch is taken alike in all four.
+    const float mtile = fmaxf(fmaxf(mx_lds[0][n], mx_lds[1][n]), fmaxf(mx_lds[2][n], mx_lds[3][n]));
+    if (__any(mtile > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, mtile);  // finite: the tile's first token is valid
       const float alpha = exp2f(m_run - m_new);
       m_run = m_new;
       l_part *= alpha;
 #pragma unroll
-      for (int mb = 0; mb < 16; ++mb) oacc[mb] = oacc[mb] * alpha;
+      for (int mb = 0; mb < 4; ++mb) oacc[mb] = oacc[mb] * alpha;
     }
     float p[4];
 #pragma unroll
@@ -580,104 +652,67 @@ __global__ __launch_bounds__(NW * 64, 2) void mla_decode_mfma(DecodeArgs a) {
     } else {
       pw = make_uint2(w01, w23);
     }
-    const s16x4_t pb = __builtin_bit_cast(s16x4_t, pw);
+    *reinterpret_cast<uint2*>(p_mine) = pw;
+    // P of all waves is visible; every wave's reads of this tile's rows have
+    // completed, so the next tile may overwrite them.
+    lds_barrier();
 
-    // O^T += C^T . P^T over 16 channel blocks.
+    // O^T[64w + 16mb + ., head] += C^T . P^T over the tile's two 32-token
+    // halves; the 8 K slots of lane group g are tokens 32kb + 4g + {0..3}
+    // and 32kb + 16 + 4g + {0..3} in both operands.
 #pragma unroll
-    for (int mb = 0; mb < 16; ++mb)
-      oacc[mb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ct[mb], pb, oacc[mb], 0, 0, 0);
+    for (int kb = 0; kb < 2; ++kb) {
+      const uint2 plo = *reinterpret_cast<const uint2*>(p_row + 2 * (32 * kb));
+      const uint2 phi = *reinterpret_cast<const uint2*>(p_row + 2 * (32 * kb + 16));
+      const bf16x8_t pb = as_bf16x8(make_uint4(plo.x, plo.y, phi.x, phi.y));
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        oacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat_bf16x8(ct[kb][mb][0], ct[kb][mb][1]), pb,
+                                                           oacc[mb], 0, 0, 0);
+    }
   };
 
-  // Sub-tiles of this wave: full groups of DEPTH in the loop, the remainder
-  // after it; every branch is uniform.  Surplus refills at the end of the
-  // stream re-read the wave's last row (cache hits) and drain in order right
+  // Full groups of DEPTH tiles in the loop, the remainder after it; every
+  // branch is block-uniform.  Surplus refills at the end of the stream
+  // re-read the split's last row (cache hits) and drain in order right
   // behind the real tiles.
-  const int n_sub = (has_work && base0 < t1) ? (t1 - base0 + kStep - 1) / kStep : 0;
   int it = 0;
-  for (; it + DEPTH <= n_sub; it += DEPTH) {
+  for (; it + DEPTH <= n_tiles; it += DEPTH) {
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) process(base0 + (it + d) * kStep, kt[d]);
+    for (int d = 0; d < DEPTH; ++d) process(it + d, kt[d]);
   }
 #pragma unroll
   for (int d = 0; d < DEPTH - 1; ++d)
-    if (it + d < n_sub) process(base0 + (it + d) * kStep, kt[d]);
+    if (it + d < n_tiles) process(it + d, kt[d]);
 
-  // ---- Merge the NW waves.  l: reduce the lane partials of each head.
-  float l_tot = l_part + shfl_xor_f32(l_part, 16);
-  l_tot += shfl_xor_f32(l_tot, 32);
-  if (g == 0) {
-    m_lds[w][n] = m_run;
-    l_lds[w][n] = l_tot;
-  }
-  __syncthreads();
-  float M = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < NW; ++k) M = fmaxf(M, m_lds[k][n]);
-  float Ltot = 0.f, my_a = 0.f;
-#pragma unroll
-  for (int k = 0; k < NW; ++k) {
-    const float mk = m_lds[k][n];
-    const float ak = (mk == -INFINITY) ? 0.f : exp2f(mk - M);
-    Ltot += ak * l_lds[k][n];
-    if (k == w) my_a = ak;
-  }
-  // Each wave stores its rescaled O into its own fp32 LDS region
-  // [16][kOStride] (reusing the tiles); after one barrier every thread sums
-  // the NW regions for its channels.  A lane stores 4 consecutive channels
-  // (16 B); the padded rows keep 8-lane groups on distinct banks.
-  float* o_lds = reinterpret_cast<float*>(c_lds);
-  {
-    float* mine = o_lds + w * (kH * kOStride);
-#pragma unroll
-    for (int mb = 0; mb < 16; ++mb)
-      *reinterpret_cast<float4*>(mine + n * kOStride + 16 * mb + 4 * g) =
-          make_float4(oacc[mb][0] * my_a, oacc[mb][1] * my_a, oacc[mb][2] * my_a, oacc[mb][3] * my_a);
-  }
-  __syncthreads();
+  // ---- Sum of the weights per head over the four waves.
+  float l_w = l_part + shfl_xor_f32(l_part, 16);
+  l_w += shfl_xor_f32(l_w, 32);
+  if (g == 0) l_lds[w][n] = l_w;
+  lds_barrier();
+  const float Ltot = (l_lds[0][n] + l_lds[1][n]) + (l_lds[2][n] + l_lds[3][n]);
+  const float inv = Ltot > 0.f ? 1.f / Ltot : 0.f;
 
-  // Thread t writes head h, CPT channels.
-  constexpr int TPH = NW * 64 / kH, CPT = kR / TPH;
-  const int h = threadIdx.x / TPH, c0 = (threadIdx.x % TPH) * CPT;
-  const float Lh = __shfl(Ltot, h, 64);  // lanes 0..15 of every wave hold head = lane
-  const float Mh = __shfl(M, h, 64);
-  const float inv = Lh > 0.f ? 1.f / Lh : 0.f;
-  float orow[CPT];
-#pragma unroll
-  for (int j = 0; j < CPT / 4; ++j) {
-    float4 acc = *reinterpret_cast<const float4*>(o_lds + h * kOStride + c0 + 4 * j);
-#pragma unroll
-    for (int k = 1; k < NW; ++k) {
-      const float4 v = *reinterpret_cast<const float4*>(o_lds + k * (kH * kOStride) + h * kOStride + c0 + 4 * j);
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
-    }
-    orow[4 * j] = acc.x;
-    orow[4 * j + 1] = acc.y;
-    orow[4 * j + 2] = acc.z;
-    orow[4 * j + 3] = acc.w;
-  }
+  // Lane (n, g) holds head n, channels 64w + 16mb + 4g + {0..3}.
+  const int ch0 = 64 * w + 4 * g;
   if (ns <= 1) {
-    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + h * a.o_hs + c0;
+    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + n * a.o_hs + ch0;
 #pragma unroll
-    for (int j = 0; j < CPT / 8; ++j) {
-      uint32_t pk[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        pk[k] = f32_to_bf16(orow[8 * j + 2 * k] * inv) |
-                (static_cast<uint32_t>(f32_to_bf16(orow[8 * j + 2 * k + 1] * inv)) << 16);
-      reinterpret_cast<uint4*>(op)[j] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    for (int mb = 0; mb < 4; ++mb) {
+      uint2 pk;
+      pk.x = f32_to_bf16(oacc[mb][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(oacc[mb][1] * inv)) << 16);
+      pk.y = f32_to_bf16(oacc[mb][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(oacc[mb][3] * inv)) << 16);
+      *reinterpret_cast<uint2*>(op + 16 * mb) = pk;
     }
     return;
   }
-  const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * kH + h;
-  float* op = a.o_part + pidx * kR + c0;
+  const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * kH + n;
+  float* op = a.o_part + pidx * kR + ch0;
 #pragma unroll
-  for (int j = 0; j < CPT / 4; ++j)
-    reinterpret_cast<float4*>(op)[j] = make_float4(orow[4 * j] * inv, orow[4 * j + 1] * inv,
-                                                   orow[4 * j + 2] * inv, orow[4 * j + 3] * inv);
-  if ((threadIdx.x % TPH) == 0) a.lse_part[pidx] = (Lh > 0.f) ? (Mh + __log2f(Lh)) * kLn2 : -INFINITY;
+  for (int mb = 0; mb < 4; ++mb)
+    *reinterpret_cast<float4*>(op + 16 * mb) =
+        make_float4(oacc[mb][0] * inv, oacc[mb][1] * inv, oacc[mb][2] * inv, oacc[mb][3] * inv);
+  if (w == 0 && g == 0) a.lse_part[pidx] = (Ltot > 0.f) ? (m_run + __log2f(Ltot)) * kLn2 : -INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -816,11 +851,16 @@ int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+#ifndef SWAMLA_DECODE_DEPTH
+#define SWAMLA_DECODE_DEPTH 2
+#endif
+constexpr int kDecodeDepth = SWAMLA_DECODE_DEPTH;  // tiles of loads in flight per wave
+
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
   const dim3 grid(a.n_splits, a.n_rows);
-  if (dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_decode_mfma<1, 4, 2>), grid, dim3(256), 0, s, a);
-  else if (dt == 1 && c_dt == 2) hipLaunchKernelGGL((mla_decode_mfma<2, 4, 2>), grid, dim3(256), 0, s, a);
+  if (dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth>), grid, dim3(256), 0, s, a);
+  else if (dt == 1 && c_dt == 2) hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth>), grid, dim3(256), 0, s, a);
   else if (dt == 0 && c_dt == 0) hipLaunchKernelGGL(mla_decode_f32, grid, dim3(256), 0, s, a);
   else return -1;
   return hipGetLastError() == hipSuccess ? 0 : -2;
