@@ -277,13 +277,15 @@ def main() -> int:
     layers = build_layers(args, dev, torch)
     g = torch.Generator(device=dev).manual_seed(99)
     xs = [torch.randn(args.batch, 1, args.dim, generator=g, device=dev, dtype=torch.bfloat16) for _ in layers]
-    sps = [torch.full((args.batch,), args.ctx, dtype=torch.int32, device=dev) for _ in layers]
+    # one start-position tensor for the whole stack, advanced once per step
+    # (every layer of a decoder sees the same positions)
+    sp = torch.full((args.batch,), args.ctx, dtype=torch.int32, device=dev)
     outs = [None] * len(layers)
 
     def stack_step():
         for i, m in enumerate(layers):
-            outs[i] = m(xs[i], sps[i])
-            sps[i].add_(1)
+            outs[i] = m(xs[i], sp)
+        sp.add_(1)
 
     # eager warm-up (allocates workspaces), then capture one stack step
     with torch.no_grad():
@@ -295,12 +297,10 @@ def main() -> int:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             stack_step()
-        for sp in sps:
-            sp.fill_(args.ctx)
+        sp.fill_(args.ctx)
         for _ in range(args.warmup):
             graph.replay()
-        for sp in sps:  # timed steps decode positions ctx .. ctx+K-1
-            sp.fill_(args.ctx)
+        sp.fill_(args.ctx)  # timed steps decode positions ctx .. ctx+K-1
         log("timing")
         if torch.distributed.is_available() and torch.distributed.is_initialized():
             torch.distributed.barrier()

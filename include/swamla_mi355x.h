@@ -148,6 +148,26 @@ int mla_merge(const float* o_part, const float* lse_part,
               int32_t n_splits, int32_t min_chunk, void* o_lat, int64_t o_rs,
               int64_t o_hs, float* lse_out, int32_t dtype, void* stream);
 
+/*
+ * mla_linear — batched linear layer for the few query rows of a decode step:
+ *   y[b][m][n] = sum_k x[b][m][k] * w[b][n][k] (+ bias[b][n]),  b < batch,
+ * bf16 inputs and output, fp32 accumulation, one rounding per output (what
+ * a bf16 nn.Linear returns).  Replaces, for decode-sized inputs, the
+ * step's GEMMs: wq (models/mla.py:281-288) and wkv_a (:307) as one product
+ * over their stacked weights, the per-head absorbed products q_nope . W_uk
+ * and o_lat . W_uv^T that re-associate the einsums of mla.py:427 and :433,
+ * and wo (mla.py:490-495).
+ * Element strides: x row x_rs / batch x_bs, w row w_rs / batch w_bs, y row
+ * y_rs / batch y_bs, bias batch bias_bs; the k and n dimensions are
+ * contiguous.  bias may be NULL.
+ * Limits: 1 <= M <= 64, N a multiple of 16, K a multiple of 128, x and w
+ * 16-byte aligned with row / batch strides that are multiples of 8.
+ */
+int mla_linear(const void* x, int64_t x_rs, int64_t x_bs, const void* w,
+               int64_t w_rs, int64_t w_bs, const void* bias, int64_t bias_bs,
+               void* y, int64_t y_rs, int64_t y_bs, int32_t M, int32_t N,
+               int32_t K, int32_t batch, int32_t dtype, void* stream);
+
 /* Split plan used by both kernels, exported so hosts and tests can size the
  * partial buffers: number of splits of a row of length L (0 for L <= 0). */
 int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk);

@@ -11,7 +11,11 @@ import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SOURCES = [os.path.join(HERE, "csrc", "mla_kernels.hip"), os.path.join(HERE, "csrc", "mla_abi.cpp")]
+SOURCES = [
+    os.path.join(HERE, "csrc", "mla_kernels.hip"),
+    os.path.join(HERE, "csrc", "mla_linear.hip"),
+    os.path.join(HERE, "csrc", "mla_abi.cpp"),
+]
 OUTPUT = os.path.join(HERE, "libswamla_mi355x.so")
 ARCH = os.environ.get("SWAMLA_OFFLOAD_ARCH", "gfx950")
 

@@ -226,6 +226,30 @@ int mla_merge(const float* o_part, const float* lse_part, const int32_t* kv_len,
   return ok();
 }
 
+int mla_linear(const void* x, int64_t x_rs, int64_t x_bs, const void* w, int64_t w_rs, int64_t w_bs,
+               const void* bias, int64_t bias_bs, void* y, int64_t y_rs, int64_t y_bs, int32_t M,
+               int32_t N, int32_t K, int32_t batch, int32_t dtype, void* stream) {
+  if (dtype != SWAMLA_DTYPE_BF16) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: dtype %d not built (bf16 only)", dtype);
+  if (M < 0 || M > 64) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: M=%d outside [0, 64]", M);
+  if (N < 0 || N % 16 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: N=%d is not a multiple of 16", N);
+  if (K < 128 || K % 128 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: K=%d is not a positive multiple of 128", K);
+  if (batch < 0 || batch > 65535) return fail(SWAMLA_ERR_INVALID_ARG, "mla_linear: batch=%d outside [0, 65535]", batch);
+  if (N / 16 > 65535) return fail(SWAMLA_ERR_INVALID_ARG, "mla_linear: N=%d too large", N);
+  if (M == 0 || N == 0 || batch == 0) return ok();
+  if (!x || !w || !y) return fail(SWAMLA_ERR_INVALID_ARG, "mla_linear: null x / w / y");
+  if (x_rs < K || w_rs < K || y_rs < N || x_rs < 0 || x_bs < 0 || w_bs < 0 || y_bs < 0 || bias_bs < 0)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_linear: row strides must cover K (x, w) and N (y)");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 2) || (bias && !aligned(bias, 2)) ||
+      (x_rs | x_bs | w_rs | w_bs) % 8 != 0)
+    return fail(SWAMLA_ERR_MISALIGNED,
+                "mla_linear: x and w need 16-byte aligned bases and strides that are multiples of 8");
+  swamla::LinearArgs a{x, x_rs, x_bs, w, w_rs, w_bs, bias, bias_bs, y, y_rs, y_bs, M, N, K};
+  const int rc = swamla::launch_linear(a, batch, static_cast<hipStream_t>(stream));
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: no kernel for M=%d", M);
+  if (rc != 0) return hip_fail("mla_linear");
+  return ok();
+}
+
 // ---- host-side test hooks: the kernels' bit-level conversions run on the CPU.
 void mla_host_f32_to_e4m3(const float* x, uint8_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = swamla::f32_to_e4m3(x[i]);

@@ -71,8 +71,23 @@ struct MergeArgs {
   float* lse_out;
 };
 
+// Batched small-row linear layer: Y[b] = X[b] W[b]^T (+ bias[b]), bf16.
+// Element strides: rows (_rs) and batch entries (_bs); columns are unit-stride.
+struct LinearArgs {
+  const void* x;
+  int64_t x_rs, x_bs;
+  const void* w;
+  int64_t w_rs, w_bs;
+  const void* bias;
+  int64_t bias_bs;
+  void* y;
+  int64_t y_rs, y_bs;
+  int M, N, K;
+};
+
 int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s);
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s);
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s);
+int launch_linear(const LinearArgs& a, int batch, hipStream_t s);
 
 }  // namespace swamla

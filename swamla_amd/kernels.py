@@ -281,3 +281,52 @@ def decode_attention(
             )
         )
     return out
+
+
+LINEAR_MAX_ROWS = 64
+
+
+def linear(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    bias: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """out[b, m, n] = x[b, m, :] . w[b, n, :] (+ bias[b, n]) in bf16 with fp32
+    accumulation (mla_linear).  x [batch, M, K], w [batch, N, K], out
+    [batch, M, N] and bias [batch, N] may be strided views with a unit last
+    stride; 2-D x / w / out (and 1-D bias) are one batch entry.  For the
+    decode step's products (M <= 64): wq / wkv_a (models/mla.py:281-288,
+    :307), the absorbed W_uk / W_uv products (re-associating :427, :433) and
+    wo (:490-495)."""
+    squeeze = x.dim() == 2
+    if squeeze:
+        x, w = x.unsqueeze(0), w.unsqueeze(0)
+        out = None if out is None else out.unsqueeze(0)
+        bias = None if bias is None else bias.unsqueeze(0)
+    dev = _need_gpu(x, w, out, bias)
+    if x.dim() != 3 or w.dim() != 3 or x.shape[0] != w.shape[0] or x.shape[2] != w.shape[2]:
+        raise ValueError(f"x {tuple(x.shape)} and w {tuple(w.shape)} must be [batch, M, K] / [batch, N, K]")
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError("linear: bf16 inputs only")
+    batch, M, K = x.shape
+    N = w.shape[1]
+    if out is None:
+        out = torch.empty(batch, M, N, dtype=x.dtype, device=dev)
+    if tuple(out.shape) != (batch, M, N) or out.dtype != x.dtype:
+        raise ValueError(f"out must be [{batch}, {M}, {N}] bf16")
+    for t, name in ((x, "x"), (w, "w"), (out, "out")):
+        if t.stride(2) != 1:
+            raise ValueError(f"{name} needs a unit last stride")
+    if bias is not None and (bias.dim() != 2 or tuple(bias.shape) != (batch, N) or bias.stride(1) != 1
+                             or bias.dtype != x.dtype):
+        raise ValueError(f"bias must be [{batch}, {N}] bf16 with a unit last stride")
+    _abi.check(
+        _abi.lib().mla_linear(
+            x.data_ptr(), x.stride(1), x.stride(0), w.data_ptr(), w.stride(1), w.stride(0),
+            _abi.ptr(bias), 0 if bias is None else bias.stride(0),
+            out.data_ptr(), out.stride(1), out.stride(0), M, N, K, batch,
+            _abi.DTYPE_BF16, _abi.stream_handle(dev),
+        )
+    )
+    return out[0] if squeeze else out

@@ -106,6 +106,7 @@ class MLA(nn.Module):
         self.pe_cache = None
         self.kv_scale = None
         self._absorbed = None  # (key, W_uk [H,nope,R], W_uv^T [H,R,v])
+        self._decode_w = None  # (key, stacked wq/wkv_a, stacked bias, W_uk^T [H,R,nope])
         self._workspace: Optional[DecodeWorkspace] = None
         self._num_cus: Optional[int] = None
 
@@ -207,6 +208,37 @@ class MLA(nn.Module):
             self._absorbed = (key, w_uk, w_uv_t)
         return self._absorbed[1], self._absorbed[2]
 
+    def decode_weights(self) -> tuple[torch.Tensor, Optional[torch.Tensor], torch.Tensor]:
+        """Weights of the fused decode-step projections: wq and wkv_a stacked
+        ([H*192 + R + P, dim], one product for both, mla.py:281-288, :307),
+        their stacked bias (or None), and W_uk transposed per head
+        ([H, R, nope]) so that q_abs = q_nope . W_uk is a row-major product.
+        Rebuilt when any source weight changes."""
+        ws = (self.wq.weight, self.wkv_a.weight, self.wkv_b.weight)
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in ws)
+        if self._decode_w is None or self._decode_w[0] != key:
+            w_in = torch.cat([self.wq.weight.detach(), self.wkv_a.weight.detach()], 0).contiguous()
+            b_in = None
+            if self.wq.bias is not None and self.wkv_a.bias is not None:
+                b_in = torch.cat([self.wq.bias.detach(), self.wkv_a.bias.detach()], 0).contiguous()
+            wv = self.wkv_b.weight.detach().view(self.n_heads, -1, self.kv_lora_rank)
+            w_uk_t = wv[:, : self.qk_nope_head_dim].transpose(1, 2).contiguous()
+            self._decode_w = (key, w_in, b_in, w_uk_t)
+        return self._decode_w[1], self._decode_w[2], self._decode_w[3]
+
+    def _fused_step_ok(self, x: torch.Tensor, n: int) -> bool:
+        """The decode-step kernels cover bf16 modules with at most 64 query
+        rows, no q low-rank path and 128-aligned model widths."""
+        return (
+            x.dtype == torch.bfloat16
+            and self.wq.weight.dtype == torch.bfloat16
+            and 0 < n <= kernels.LINEAR_MAX_ROWS
+            and self.q_lora_rank == 0
+            and self.dim % 128 == 0
+            and (self.n_heads * self.v_head_dim) % 128 == 0
+            and (self.wq.bias is None) == (self.wkv_a.bias is None)
+        )
+
     def _check_geometry(self) -> None:
         if (self.n_heads, self.kv_lora_rank, self.qk_rope_head_dim) != (kernels.H, kernels.R, kernels.P):
             raise NotImplementedError(
@@ -269,10 +301,33 @@ class MLA(nn.Module):
         cache = self.latent_cache()
         sp = self._start_positions(B, T, start_pos, cache, x.device)
         with torch.no_grad():
-            kv = self.wkv_a(x).view(B * T, -1)
+            _, kv = self.input_projections(x, need_q=False)
             cos, sin = self.rope.half_tables()
             kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
                            start_pos=sp, tokens_per_seq=T, rope_abs=self.rope_positions == "absolute")
+
+    def input_projections(self, x: torch.Tensor, need_q: bool = True) -> tuple[Optional[torch.Tensor], torch.Tensor]:
+        """q [B*T, H, 192] and the wkv_a rows kv [B*T, R + P] that forward
+        feeds the kernels (mla.py:281-288, :307-308).  Decode-sized bf16
+        inputs use one mla_linear product over the stacked wq / wkv_a weights
+        (q and kv are column views of it); other inputs use the ATen
+        projections (q is skipped when not needed)."""
+        B, T, _ = x.size()
+        n, H = B * T, self.n_heads
+        with torch.no_grad():
+            if self._fused_step_ok(x, n):
+                w_in, b_in, _ = self.decode_weights()
+                y = kernels.linear(x.reshape(n, self.dim), w_in, bias=b_in)
+                q = y[:, : H * self.qk_head_dim].view(n, H, self.qk_head_dim)
+                return q, y[:, H * self.qk_head_dim:]
+            kv = self.wkv_a(x).view(n, -1)
+            if not need_q:
+                return None, kv
+            if self.q_lora_rank == 0:
+                q = self.wq(x)
+            else:
+                q = self.wq_b(self.q_norm(self.wq_a(x)))
+            return q.view(n, H, self.qk_head_dim), kv
 
     def _start_positions(self, B: int, T: int, start_pos, cache: LatentCache, device) -> torch.Tensor:
         """int32 [B] device tensor of per-sequence start positions (checked
@@ -306,22 +361,37 @@ class MLA(nn.Module):
             sp = torch.zeros(B, dtype=torch.int32, device=dev)
             max_len = T
 
-        if self.q_lora_rank == 0:  # mla.py:281-288
-            q = self.wq(x)
-        else:
-            q = self.wq_b(self.q_norm(self.wq_a(x)))
-        q = q.view(n, H, self.qk_head_dim)
-        kv = self.wkv_a(x).view(n, -1)  # mla.py:307-308
+        fused = self._fused_step_ok(x, n)
+        q, kv = self.input_projections(x)
 
         cos, sin = self.rope.half_tables()
         kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
                        start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
 
+        n_splits, min_chunk = self._split_plan(n, max_len, dev)
+        if fused:
+            _, _, w_uk_t = self.decode_weights()
+            # q_abs[r, h] = q_nope[r, h] . W_uk[h]  (batched over heads)
+            q_abs = torch.empty(n, H, R, dtype=x.dtype, device=dev)
+            kernels.linear(q[:, :, :Dn].transpose(0, 1), w_uk_t, out=q_abs.transpose(0, 1))
+            o_lat = torch.empty(n, H, R, dtype=x.dtype, device=dev)
+            kernels.decode_attention(
+                q_abs, q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
+                start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
+                out=o_lat, workspace=self._workspace_for(n, n_splits, dev),
+            )
+            # o[r, h*Dv + d] = W_uv[h][d] . o_lat[r, h]: written straight in wo's input layout
+            w_uv = self.wkv_b.weight.detach().view(H, Dn + Dv, R)[:, Dn:, :]
+            o = torch.empty(n, H * Dv, dtype=x.dtype, device=dev)
+            kernels.linear(o_lat.transpose(0, 1), w_uv, out=o.view(n, H, Dv).transpose(0, 1))
+            wo_b = None if self.wo.bias is None else self.wo.bias.detach()
+            out = kernels.linear(o, self.wo.weight.detach(), bias=wo_b).view(B, T, self.dim)
+            return self.resid_dropout(out)  # mla.py:490-495
+
         w_uk, w_uv_t = self.absorbed_weights()
         q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]
         q_abs = torch.bmm(q_nope, w_uk)  # [H, n, R]
         o_lat = torch.empty(H, n, R, dtype=x.dtype, device=dev)
-        n_splits, min_chunk = self._split_plan(n, max_len, dev)
         kernels.decode_attention(
             q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
             start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,

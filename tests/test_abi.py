@@ -134,6 +134,40 @@ def test_merge_rejects_and_noop(lib):
     assert _merge(lib, sp=FAKE) == -1
 
 
+def _linear(lib, **kw):
+    args = dict(x=FAKE, x_rs=1024, x_bs=0, w=FAKE, w_rs=1024, w_bs=0, bias=None, bias_bs=0, y=FAKE,
+                y_rs=64, y_bs=0, M=32, N=64, K=1024, batch=1, dt=1, stream=None)
+    args.update(kw)
+    return lib.mla_linear(*args.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(dt=0), -2),
+        (dict(M=65), -2),
+        (dict(N=40), -2),
+        (dict(K=100), -2),
+        (dict(K=0), -2),
+        (dict(batch=-1), -1),
+        (dict(x=None), -1),
+        (dict(x_rs=512), -1),
+        (dict(y_rs=32), -1),
+        (dict(x=FAKE + 8), -3),
+        (dict(w_rs=1028), -3),
+        (dict(x_bs=4), -3),
+    ],
+)
+def test_linear_rejects(lib, kw, code):
+    assert _linear(lib, **kw) == code
+    assert lib.mla_last_error().decode()
+
+
+def test_linear_empty_is_a_noop(lib):
+    assert _linear(lib, M=0, x=None, w=None, y=None) == 0
+    assert _linear(lib, batch=0, x=None, w=None, y=None) == 0
+
+
 def test_python_check_raises_with_message(lib):
     rc = _append(lib, R=128)
     with pytest.raises(_abi.SwamlaError, match="UNSUPPORTED.*R=128"):

@@ -47,7 +47,7 @@ def expected_cache(m, xs, dtype, fp8=False):
     with torch.no_grad():
         for x in xs:
             B, T, _ = x.shape
-            kv = m.wkv_a(x).reshape(B * T, -1).cpu()
+            kv = m.input_projections(x)[1].cpu()  # the rows forward fed the append kernel
             y = lo.layernorm_exact(kv[:, :256].float().numpy(), w, b, m.kv_norm.eps,
                                    torch.bfloat16 if fp8 else dtype)
             rp = torch.arange(T).repeat(B)
