@@ -168,6 +168,33 @@ int mla_linear(const void* x, int64_t x_rs, int64_t x_bs, const void* w,
                void* y, int64_t y_rs, int64_t y_bs, int32_t M, int32_t N,
                int32_t K, int32_t batch, int32_t dtype, void* stream);
 
+/*
+ * mla_merge_project — split-KV merge fused with the W_uv read-out:
+ *   y[r][h][d] = sum_c W_uv[h][d][c] * o_lat[r][h][c],
+ * where o_lat is the log-sum-exp merge of the mla_decode_attn partials
+ * (rows with more than one split, merged as mla_merge does and rounded to
+ * bf16) or the o_lat row mla_decode_attn wrote itself (one split).
+ * Replaces mla_merge followed by the per-head product with the value half of
+ * wkv_b, i.e. the re-associated einsum of models/mla.py:433 and the reshape
+ * to wo's input layout at :490-491.
+ * Row lengths and splits are derived exactly as mla_decode_attn does (same
+ * addressing arguments, same cache_batch / cache_seq clamping).
+ * w            head h, output d at w + h*w_hs + d*w_rs, R values (a view of
+ *              wkv_b.weight: w_hs = (nope + Dv)*R, w_rs = R, base + nope*R).
+ * y            row r, head h at y + r*y_rs + h*y_hs, Dv values (wo's input
+ *              [rows, H*Dv]: y_rs = H*Dv, y_hs = Dv).
+ * o_part / lse_part may be NULL when n_splits == 1.  bf16 only, Dv = 128.
+ */
+int mla_merge_project(const float* o_part, const float* lse_part,
+                      const void* o_lat, int64_t o_rs, int64_t o_hs,
+                      const int32_t* kv_len, const int32_t* row_seq,
+                      const int32_t* start_pos, int32_t rows_per_seq,
+                      int64_t cache_batch, int64_t cache_seq, int32_t n_rows,
+                      int32_t H, int32_t R, int32_t n_splits,
+                      int32_t min_chunk, const void* w, int64_t w_rs,
+                      int64_t w_hs, int32_t Dv, void* y, int64_t y_rs,
+                      int64_t y_hs, int32_t dtype, void* stream);
+
 /* Split plan used by both kernels, exported so hosts and tests can size the
  * partial buffers: number of splits of a row of length L (0 for L <= 0). */
 int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk);

@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "mla_merge",
     "mla_split_count",
     "mla_linear",
+    "mla_merge_project",
     "mla_host_f32_to_e4m3",
     "mla_host_e4m3_to_f32",
     "mla_host_e4m3x4_to_bf16",
@@ -83,6 +84,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_linear.restype = ctypes.c_int
     lib.mla_linear.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P,
+    ]
+    lib.mla_merge_project.restype = ctypes.c_int
+    lib.mla_merge_project.argtypes = [
+        _P, _P, _P, _I64, _I64, _P, _P, _P, _I32, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
+        _P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P,
     ]
     lib.mla_host_f32_to_e4m3.restype = None
     lib.mla_host_f32_to_e4m3.argtypes = [_P, _P, _I64]

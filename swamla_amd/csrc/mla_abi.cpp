@@ -250,6 +250,44 @@ int mla_linear(const void* x, int64_t x_rs, int64_t x_bs, const void* w, int64_t
   return ok();
 }
 
+int mla_merge_project(const float* o_part, const float* lse_part, const void* o_lat, int64_t o_rs,
+                      int64_t o_hs, const int32_t* kv_len, const int32_t* row_seq,
+                      const int32_t* start_pos, int32_t rows_per_seq, int64_t cache_batch,
+                      int64_t cache_seq, int32_t n_rows, int32_t H, int32_t R, int32_t n_splits,
+                      int32_t min_chunk, const void* w, int64_t w_rs, int64_t w_hs, int32_t Dv,
+                      void* y, int64_t y_rs, int64_t y_hs, int32_t dtype, void* stream) {
+  if (int e = check_geometry(H, R, 64)) return e;
+  if (dtype != SWAMLA_DTYPE_BF16)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge_project: dtype %d not built (bf16 only)", dtype);
+  if (Dv != 128) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge_project: Dv=%d (this build: 128)", Dv);
+  if (n_rows < 0 || n_rows > 65535 * 8)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: n_rows=%d out of range", n_rows);
+  if (n_splits < 1 || n_splits > 1024)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: n_splits=%d outside [1, 1024]", n_splits);
+  if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: min_chunk=%d < 1", min_chunk);
+  if (n_rows == 0) return ok();
+  swamla::Addressing ad;
+  if (int e = check_addressing("mla_merge_project", n_rows, row_seq, kv_len, nullptr, start_pos, rows_per_seq,
+                               true, false, &ad, 0))
+    return e;
+  if (!o_lat || !w || !y) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: null o_lat / w / y");
+  if (n_splits > 1 && (!o_part || !lse_part))
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: n_splits > 1 needs o_part and lse_part");
+  if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: bad cache shape");
+  if (o_hs < R || w_rs < R || y_hs < Dv || o_rs < 0 || w_hs < 0 || y_rs < 0)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: strides must cover R / Dv values");
+  if (!aligned(o_lat, 16) || !aligned(w, 16) || !aligned(y, 2) || (o_part && !aligned(o_part, 16)) ||
+      (lse_part && !aligned(lse_part, 4)) || (o_rs | o_hs | w_rs | w_hs) % 8 != 0)
+    return fail(SWAMLA_ERR_MISALIGNED,
+                "mla_merge_project: o_lat and w need 16-byte aligned bases and strides that are multiples of 8");
+  swamla::MergeProjectArgs a{o_part, lse_part, o_lat, o_rs, o_hs, ad, cache_batch, cache_seq, n_rows,
+                             n_splits, min_chunk, w, w_rs, w_hs, y, y_rs, y_hs};
+  const int rc = swamla::launch_merge_project(a, static_cast<hipStream_t>(stream));
+  if (rc != 0) return hip_fail("mla_merge_project");
+  return ok();
+}
+
 // ---- host-side test hooks: the kernels' bit-level conversions run on the CPU.
 void mla_host_f32_to_e4m3(const float* x, uint8_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = swamla::f32_to_e4m3(x[i]);

@@ -85,9 +85,26 @@ struct LinearArgs {
   int M, N, K;
 };
 
+// Split merge fused with the per-head W_uv product: y[r, h, :] =
+// W_uv[h] . merge_s(o_part[r, s, h, :]) (or o_lat[r, h, :] for one split).
+struct MergeProjectArgs {
+  const float* o_part;
+  const float* lse_part;
+  const void* o_lat;
+  int64_t ol_rs, ol_hs;
+  Addressing ad;  // row lengths, clamped to the cache as the decode kernel does
+  int64_t cache_b, cache_s;
+  int n_rows, n_splits, min_chunk;
+  const void* w;
+  int64_t w_rs, w_hs;
+  void* y;
+  int64_t y_rs, y_hs;
+};
+
 int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s);
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s);
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s);
 int launch_linear(const LinearArgs& a, int batch, hipStream_t s);
+int launch_merge_project(const MergeProjectArgs& a, hipStream_t s);
 
 }  // namespace swamla

@@ -13,6 +13,7 @@
 #include <stdint.h>
 
 #include "mla_args.h"
+#include "mla_plan.h"
 #include "numerics.h"
 
 namespace swamla {
@@ -21,20 +22,6 @@ constexpr int kR = 256;
 constexpr int kP = 64;
 constexpr int kH = 16;
 constexpr int kKC = kR + kP;  // 320 channels scored per cached token
-
-// ---------------------------------------------------------------------------
-// Split plan (shared by decode and merge; mirrored by mla_split_count).
-// ---------------------------------------------------------------------------
-SW_HD int split_chunk(int L, int n_splits, int min_chunk) {
-  int c = (L + n_splits - 1) / n_splits;
-  if (c < min_chunk) c = min_chunk;
-  return (c + 15) & ~15;
-}
-SW_HD int split_count(int L, int n_splits, int min_chunk) {
-  if (L <= 0) return 0;
-  int c = split_chunk(L, n_splits, min_chunk);
-  return (L + c - 1) / c;
-}
 
 // ---------------------------------------------------------------------------
 // Small helpers
@@ -96,41 +83,6 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
 
 __device__ __forceinline__ double shfl_xor_f64(double v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xor(v, m, 64); }
-
-// ---------------------------------------------------------------------------
-// Addressing of tokens (append) and query rows (decode / merge).
-// ---------------------------------------------------------------------------
-struct TokAddr {
-  int b, pos, rope;
-};
-
-// Append: cache row, destination position, RoPE table row of token i.
-__device__ __forceinline__ TokAddr tok_addr(const Addressing& ad, int i) {
-  if (ad.start_pos) {
-    const int b = i / ad.T, t = i - b * ad.T;
-    const int p = ad.start_pos[b] + t;
-    return {b, p, ad.rope_abs ? p : t};
-  }
-  return {ad.seq[i], ad.pos[i], ad.rope[i]};
-}
-
-// Decode: cache row, attended length (causal: position + 1), RoPE row of row r.
-__device__ __forceinline__ TokAddr row_addr(const Addressing& ad, int r) {
-  if (ad.start_pos) {
-    const int b = r / ad.T, t = r - b * ad.T;
-    const int p = ad.start_pos[b] + t;
-    return {b, p + 1, ad.rope_abs ? p : t};
-  }
-  return {ad.seq[r], ad.pos[r], ad.rope[r]};
-}
-
-__device__ __forceinline__ int row_len(const Addressing& ad, int r) {
-  if (ad.start_pos) {
-    const int b = r / ad.T;
-    return ad.start_pos[b] + (r - b * ad.T) + 1;
-  }
-  return ad.pos[r];
-}
 
 // ---------------------------------------------------------------------------
 // Kernel 1: fused append.  One wavefront per token, 4 tokens per block.

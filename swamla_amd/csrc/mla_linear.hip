@@ -11,12 +11,13 @@
 // (mla.py:490-495).  These products have M = 32 rows and read 0.6-6.6 MB of
 // weights, so they are bound by launch latency and weight streaming, not by
 // MFMA throughput: a block owns a 16-column tile of Y for all M rows, its
-// four waves split K, and each wave keeps up to eight 32-wide K steps of
-// loads in flight before its MFMAs.
+// waves (four, or eight for long K) split K, and each wave keeps up to eight
+// 32-wide K steps of loads in flight before its MFMAs.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "mla_args.h"
+#include "mla_plan.h"
 #include "numerics.h"
 
 namespace swamla {
@@ -28,24 +29,25 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-constexpr int kLinWaves = 4;
 constexpr int kLinBatch = 8;  // K steps of 32 whose loads are issued together
 
 // Block: 16 output columns [16*blockIdx.x, +16) of batch entry blockIdx.y
-// for all M rows (MT tiles of 16 rows).  Wave w reduces K range
-// [w*K/4, (w+1)*K/4).  MFMA operands: A = X rows (lane: row l%16, k
+// for all M rows (MT tiles of 16 rows).  Wave w of NW reduces K range
+// [w*K/NW, (w+1)*K/NW).  MFMA operands: A = X rows (lane: row l%16, k
 // 8(l/16)..+8), B = W rows (lane: column l%16, same k); the result lane holds
-// rows 4(l/16)+i of column l%16.
-template <int MT>
-__global__ __launch_bounds__(kLinWaves * 64) void mla_linear_kernel(LinearArgs a) {
-  __shared__ float red[kLinWaves][MT][16][17];
+// rows 4(l/16)+i of column l%16.  Eight waves serve the long products (K >=
+// 1024): each wave's loads then fit in one batch and the weight stream of
+// a block is twice as wide.
+template <int MT, int NW>
+__global__ __launch_bounds__(NW * 64) void mla_linear_kernel(LinearArgs a) {
+  __shared__ float red[NW][MT][16][17];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int bt = blockIdx.y;
   const int col0 = blockIdx.x * 16;
 
-  const int kw = a.K / kLinWaves;  // multiple of 32 (checked by the caller)
+  const int kw = a.K / NW;  // multiple of 32 (checked by the caller)
   const int kbeg = w * kw;
   const uint16_t* X = static_cast<const uint16_t*>(a.x) + bt * a.x_bs;
   const uint16_t* wr =
@@ -83,38 +85,171 @@ __global__ __launch_bounds__(kLinWaves * 64) void mla_linear_kernel(LinearArgs a
     }
   }
 
-  // Sum the four waves' K ranges in a fixed order, add the bias, round once.
+  // Sum the waves' K ranges in a fixed order, add the bias, round once.
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[w][mt][4 * g + i][n] = acc[mt][i];
   __syncthreads();
-  const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
+  const int c = threadIdx.x & 15;
   float bias = 0.f;
   if (a.bias) bias = bf16_to_f32(static_cast<const uint16_t*>(a.bias)[bt * a.bias_bs + col0 + c]);
   uint16_t* Y = static_cast<uint16_t*>(a.y) + bt * a.y_bs + col0 + c;
+  for (int e = threadIdx.x >> 4; e < MT * 16; e += NW * 4) {  // e = output row
+    const int mt = e >> 4, r = e & 15;
+    if (e < a.M) {
+      float v = red[0][mt][r][c];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int row = 16 * mt + r;
-    if (row < a.M) {
-      float v = ((red[0][mt][r][c] + red[1][mt][r][c]) + red[2][mt][r][c]) + red[3][mt][r][c];
+      for (int k = 1; k < NW; ++k) v += red[k][mt][r][c];
       if (a.bias) v += bias;
-      Y[static_cast<int64_t>(row) * a.y_rs] = f32_to_bf16(v);
+      Y[static_cast<int64_t>(e) * a.y_rs] = f32_to_bf16(v);
+    }
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Split merge + W_uv read-out.  Block = (8 query rows, head h), 4 waves.
+// The block first issues its W_uv[h] loads (wave w: output tiles w and w+4,
+// all 256 K), then merges its rows' split partials into bf16 rows in LDS
+// (thread t: row t/32, channels 8(t%32)..+8; one split: the decode kernel's
+// o_lat row), then multiplies: y[r, h, d] = sum_c W_uv[h][d][c] x[r][c].
+// The merge is o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M) with
+// M = max_s lse_s, accumulated over groups of 8 splits in order.
+// ---------------------------------------------------------------------------
+constexpr int kMpRows = 8;              // query rows per block
+constexpr int kMpXRow = 2 * 256 + 16;   // LDS bytes per merged row (padded)
+
+template <int DV>
+__global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs a) {
+  constexpr int R = 256, H = 16;
+  constexpr int kTilesPerWave = DV / 16 / 4;
+  __shared__ __attribute__((aligned(16))) uint8_t x_lds[kMpRows * kMpXRow];
+  const int h = blockIdx.y, r0 = blockIdx.x * kMpRows;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+
+  // W_uv[h] rows of this wave's output tiles (B operand: lane = output d).
+  uint4 wb[kTilesPerWave][8];
+#pragma unroll
+  for (int j = 0; j < kTilesPerWave; ++j) {
+    const int d = 16 * (w + 4 * j) + n;
+    const uint16_t* wp = static_cast<const uint16_t*>(a.w) + h * a.w_hs + static_cast<int64_t>(d) * a.w_rs + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) wb[j][s] = *reinterpret_cast<const uint4*>(wp + 32 * s);
+  }
+
+  // Merge: thread -> (row rr, 8 channels cc).
+  {
+    const int rr = threadIdx.x >> 5, cc = 8 * (threadIdx.x & 31);
+    const int r = r0 + rr;
+    uint4 xv = make_uint4(0, 0, 0, 0);
+    if (r < a.n_rows) {
+      const int L = clamped_row_len(a.ad, r, a.cache_b, a.cache_s);
+      const int ns = split_count(L, a.n_splits, a.min_chunk);
+      if (ns <= 1) {
+        xv = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.o_lat) + r * a.ol_rs + h * a.ol_hs + cc);
+      } else {
+        const float* lp = a.lse_part + static_cast<int64_t>(r) * a.n_splits * H + h;
+        const float* op0 = a.o_part + (static_cast<int64_t>(r) * a.n_splits * H + h) * R + cc;
+        // Splits in groups of 8 with every load of a group issued before it is
+        // used; the running maximum moves per group (online log-sum-exp).
+        float M = -INFINITY, tot = 0.f;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < ns; s0 += 8) {
+          float ls[8];
+          float4 v[8][2];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const int s = min(s0 + k, ns - 1);  // surplus slots re-read the last split and get weight 0
+            ls[k] = lp[s * H];
+            const float* op = op0 + static_cast<int64_t>(s) * H * R;
+            v[k][0] = *reinterpret_cast<const float4*>(op);
+            v[k][1] = *reinterpret_cast<const float4*>(op + 4);
+          }
+          float mg = M;
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (s0 + k < ns) mg = fmaxf(mg, ls[k]);
+          const float alpha = (M == -INFINITY) ? 0.f : __expf(M - mg);
+          tot *= alpha;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+          M = mg;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float ws = (s0 + k < ns && ls[k] != -INFINITY) ? __expf(ls[k] - M) : 0.f;
+            tot += ws;
+            acc[0] += ws * v[k][0].x; acc[1] += ws * v[k][0].y; acc[2] += ws * v[k][0].z; acc[3] += ws * v[k][0].w;
+            acc[4] += ws * v[k][1].x; acc[5] += ws * v[k][1].y; acc[6] += ws * v[k][1].z; acc[7] += ws * v[k][1].w;
+          }
+        }
+        const float inv = tot > 0.f ? 1.f / tot : 0.f;
+        uint32_t pk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pk[i] = f32_to_bf16(acc[2 * i] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[2 * i + 1] * inv)) << 16);
+        xv = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      }
+    }
+    *reinterpret_cast<uint4*>(x_lds + rr * kMpXRow + 2 * cc) = xv;
+  }
+  __syncthreads();
+
+  // y = X . W_uv[h]^T: A = merged rows (lanes of rows 8..15 repeat rows 0..7;
+  // their results are dropped), B = W_uv rows.
+  f32x4_t acc[kTilesPerWave];
+#pragma unroll
+  for (int j = 0; j < kTilesPerWave; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint8_t* xa = x_lds + (n & (kMpRows - 1)) * kMpXRow + 2 * (8 * g);
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const bf16x8_t av = as_bf16x8(*reinterpret_cast<const uint4*>(xa + 2 * (32 * s)));
+#pragma unroll
+    for (int j = 0; j < kTilesPerWave; ++j)
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, as_bf16x8(wb[j][s]), acc[j], 0, 0, 0);
+  }
+  // lane (n, g) holds rows 4g+i of output column 16*tile + n
+  if (g < 2) {
+#pragma unroll
+    for (int j = 0; j < kTilesPerWave; ++j) {
+      const int d = 16 * (w + 4 * j) + n;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = r0 + 4 * g + i;
+        if (r < a.n_rows) static_cast<uint16_t*>(a.y)[r * a.y_rs + h * a.y_hs + d] = f32_to_bf16(acc[j][i]);
+      }
     }
   }
 }
 
 }  // namespace
 
+template <int NW>
+void launch_linear_nw(const LinearArgs& a, dim3 grid, int mt, hipStream_t s) {
+  const dim3 block(NW * 64);
+  if (mt == 1) hipLaunchKernelGGL((mla_linear_kernel<1, NW>), grid, block, 0, s, a);
+  else if (mt == 2) hipLaunchKernelGGL((mla_linear_kernel<2, NW>), grid, block, 0, s, a);
+  else if (mt == 3) hipLaunchKernelGGL((mla_linear_kernel<3, NW>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((mla_linear_kernel<4, NW>), grid, block, 0, s, a);
+}
+
 int launch_linear(const LinearArgs& a, int batch, hipStream_t s) {
   if (a.M == 0 || a.N == 0 || batch == 0) return 0;
-  const dim3 grid(a.N / 16, batch), block(kLinWaves * 64);
   const int mt = (a.M + 15) / 16;
-  if (mt == 1) hipLaunchKernelGGL((mla_linear_kernel<1>), grid, block, 0, s, a);
-  else if (mt == 2) hipLaunchKernelGGL((mla_linear_kernel<2>), grid, block, 0, s, a);
-  else if (mt == 3) hipLaunchKernelGGL((mla_linear_kernel<3>), grid, block, 0, s, a);
-  else if (mt == 4) hipLaunchKernelGGL((mla_linear_kernel<4>), grid, block, 0, s, a);
-  else return -1;
+  if (mt < 1 || mt > 4) return -1;
+  const dim3 grid(a.N / 16, batch);
+  // each wave's K range must be a whole number of 32-wide steps
+  if (a.K >= 1024 && a.K % 256 == 0) launch_linear_nw<8>(a, grid, mt, s);
+  else launch_linear_nw<4>(a, grid, mt, s);  // K is a multiple of 128 (checked by the caller)
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_merge_project(const MergeProjectArgs& a, hipStream_t s) {
+  if (a.n_rows == 0) return 0;
+  const dim3 grid((a.n_rows + kMpRows - 1) / kMpRows, 16), block(256);
+  hipLaunchKernelGGL((mla_merge_project_kernel<128>), grid, block, 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -223,6 +223,7 @@ def decode_attention(
     out: Optional[torch.Tensor] = None,
     workspace: Optional[DecodeWorkspace] = None,
     lse_out: Optional[torch.Tensor] = None,
+    merge: bool = True,
 ) -> torch.Tensor:
     """Absorbed attention of query rows over the latent cache (+ merge).
 
@@ -231,7 +232,9 @@ def decode_attention(
     (start_pos [rows / rows_per_seq], causal).  Returns o_lat [rows, H, R]
     (``out`` may be a strided view, e.g. a transpose of a [H, rows, R]
     buffer).  With more than one split, mla_merge runs after the decode
-    kernel (and writes the log-sum-exp to ``lse_out`` if given).
+    kernel (and writes the log-sum-exp to ``lse_out`` if given) unless
+    ``merge`` is False: then rows with several splits leave their partials in
+    ``workspace`` for merge_project.
     Reference: models/mla.py:417-487.
     """
     cache.validate()
@@ -272,7 +275,7 @@ def decode_attention(
             _abi.dtype_code(dt), cache.cache_code, stream,
         )
     )
-    if n_splits > 1:
+    if n_splits > 1 and merge:
         _abi.check(
             lib.mla_merge(
                 workspace.o_part.data_ptr(), workspace.lse_part.data_ptr(), p_len, p_sp, int(rows_per_seq),
@@ -330,3 +333,52 @@ def linear(
         )
     )
     return out[0] if squeeze else out
+
+
+def merge_project(
+    o_lat: torch.Tensor,
+    w_uv: torch.Tensor,
+    out: torch.Tensor,
+    cache: LatentCache,
+    *,
+    n_splits: int,
+    min_chunk: int,
+    workspace: Optional[DecodeWorkspace] = None,
+    row_seq: Optional[torch.Tensor] = None,
+    kv_len: Optional[torch.Tensor] = None,
+    start_pos: Optional[torch.Tensor] = None,
+    rows_per_seq: int = 1,
+) -> torch.Tensor:
+    """out[r, h, :] = W_uv[h] . o_lat[r, h, :] where o_lat is merged from the
+    split partials left by ``decode_attention(..., merge=False)`` (or read
+    from ``o_lat`` for single-split rows); mla_merge_project.  w_uv [H, Dv, R]
+    may be a view of wkv_b.weight; out [rows, H, Dv] may be a view of wo's
+    [rows, H*Dv] input.  Addressing and split plan must be the ones the
+    decode call used.  Reference: models/mla.py:433, :490-491."""
+    dev = _need_gpu(o_lat, w_uv, out, row_seq, kv_len, start_pos)
+    rows = o_lat.shape[0]
+    Dv = w_uv.shape[1]
+    if o_lat.dim() != 3 or tuple(o_lat.shape[1:]) != (H, R) or o_lat.stride(2) != 1:
+        raise ValueError(f"o_lat must be [rows, {H}, {R}] with unit last stride")
+    if w_uv.dim() != 3 or tuple(w_uv.shape) != (H, Dv, R) or w_uv.stride(2) != 1:
+        raise ValueError(f"w_uv must be [{H}, Dv, {R}] with unit last stride")
+    if tuple(out.shape) != (rows, H, Dv) or out.stride(2) != 1:
+        raise ValueError(f"out must be [{rows}, {H}, {Dv}] with unit last stride")
+    if not (o_lat.dtype == w_uv.dtype == out.dtype == torch.bfloat16):
+        raise TypeError("merge_project: bf16 tensors only")
+    (p_seq, p_len, _), p_sp = _addressing(
+        rows, (row_seq, kv_len, None), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
+    if n_splits > 1 and (workspace is None or not workspace.fits(rows, n_splits)):
+        raise ValueError("merge_project needs the decode call's workspace")
+    _abi.check(
+        _abi.lib().mla_merge_project(
+            _abi.ptr(workspace.o_part if n_splits > 1 else None),
+            _abi.ptr(workspace.lse_part if n_splits > 1 else None),
+            o_lat.data_ptr(), o_lat.stride(0), o_lat.stride(1),
+            p_len, p_seq, p_sp, int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1],
+            rows, H, R, n_splits, min_chunk,
+            w_uv.data_ptr(), w_uv.stride(1), w_uv.stride(0), Dv,
+            out.data_ptr(), out.stride(0), out.stride(1), _abi.DTYPE_BF16, _abi.stream_handle(dev),
+        )
+    )
+    return out

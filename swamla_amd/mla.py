@@ -106,7 +106,7 @@ class MLA(nn.Module):
         self.pe_cache = None
         self.kv_scale = None
         self._absorbed = None  # (key, W_uk [H,nope,R], W_uv^T [H,R,v])
-        self._decode_w = None  # (key, stacked wq/wkv_a, stacked bias, W_uk^T [H,R,nope])
+        self._decode_w = None  # (key, stacked absorbed-query / q_pe / wkv_a weight, stacked bias)
         self._workspace: Optional[DecodeWorkspace] = None
         self._num_cus: Optional[int] = None
 
@@ -208,23 +208,44 @@ class MLA(nn.Module):
             self._absorbed = (key, w_uk, w_uv_t)
         return self._absorbed[1], self._absorbed[2]
 
-    def decode_weights(self) -> tuple[torch.Tensor, Optional[torch.Tensor], torch.Tensor]:
-        """Weights of the fused decode-step projections: wq and wkv_a stacked
-        ([H*192 + R + P, dim], one product for both, mla.py:281-288, :307),
-        their stacked bias (or None), and W_uk transposed per head
-        ([H, R, nope]) so that q_abs = q_nope . W_uk is a row-major product.
-        Rebuilt when any source weight changes."""
+    def decode_weights(self) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """Stacked weight of the fused decode-step input product, rows
+        [W_uk[h]^T . wq_nope[h] for every head (H*R) | wq_pe (H*P) | wkv_a
+        (R+P)] over the model width, and its stacked bias (or None).  One
+        product x . W^T then yields q_abs = q_nope . W_uk (the absorbed query,
+        re-associating mla.py:427), q_pe and the wkv_a rows (mla.py:281-288,
+        :307).  The absorbed block is formed in fp32 and rounded once to the
+        model dtype; rebuilt when any source weight changes."""
         ws = (self.wq.weight, self.wkv_a.weight, self.wkv_b.weight)
         key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in ws)
         if self._decode_w is None or self._decode_w[0] != key:
-            w_in = torch.cat([self.wq.weight.detach(), self.wkv_a.weight.detach()], 0).contiguous()
+            H, Dn, R = self.n_heads, self.qk_nope_head_dim, self.kv_lora_rank
+            wq = self.wq.weight.detach().view(H, self.qk_head_dim, self.dim)
+            w_uk = self.wkv_b.weight.detach().view(H, -1, R)[:, :Dn]  # [H, Dn, R]
+            w_abs = torch.bmm(w_uk.float().transpose(1, 2).contiguous(), wq[:, :Dn].float().contiguous())
+            w_in = torch.cat(
+                [w_abs.reshape(H * R, self.dim), wq[:, Dn:].float().reshape(-1, self.dim),
+                 self.wkv_a.weight.detach().float()], 0,
+            ).to(self.wq.weight.dtype).contiguous()
             b_in = None
             if self.wq.bias is not None and self.wkv_a.bias is not None:
-                b_in = torch.cat([self.wq.bias.detach(), self.wkv_a.bias.detach()], 0).contiguous()
-            wv = self.wkv_b.weight.detach().view(self.n_heads, -1, self.kv_lora_rank)
-            w_uk_t = wv[:, : self.qk_nope_head_dim].transpose(1, 2).contiguous()
-            self._decode_w = (key, w_in, b_in, w_uk_t)
-        return self._decode_w[1], self._decode_w[2], self._decode_w[3]
+                bq = self.wq.bias.detach().view(H, self.qk_head_dim)
+                b_abs = torch.bmm(bq[:, None, :Dn].float(), w_uk.float()).reshape(H * R)
+                b_in = torch.cat([b_abs, bq[:, Dn:].float().reshape(-1), self.wkv_a.bias.detach().float()]
+                                 ).to(self.wq.bias.dtype).contiguous()
+            self._decode_w = (key, w_in, b_in)
+        return self._decode_w[1], self._decode_w[2]
+
+    def _fused_projections(self, x: torch.Tensor):
+        """q_abs [n, H, R], q_pe [n, H, P] and kv [n, R+P] from one mla_linear
+        product over decode_weights() (column views of one [n, H*(R+P)+R+P]
+        buffer)."""
+        n, H, R, P = x.shape[0] * x.shape[1], self.n_heads, self.kv_lora_rank, self.qk_rope_head_dim
+        w_in, b_in = self.decode_weights()
+        y = kernels.linear(x.reshape(n, self.dim), w_in, bias=b_in)
+        q_abs = y[:, : H * R].view(n, H, R)
+        q_pe = y[:, H * R: H * (R + P)].view(n, H, P)
+        return q_abs, q_pe, y[:, H * (R + P):]
 
     def _fused_step_ok(self, x: torch.Tensor, n: int) -> bool:
         """The decode-step kernels cover bf16 modules with at most 64 query
@@ -237,6 +258,7 @@ class MLA(nn.Module):
             and self.dim % 128 == 0
             and (self.n_heads * self.v_head_dim) % 128 == 0
             and (self.wq.bias is None) == (self.wkv_a.bias is None)
+            and self.v_head_dim == 128
         )
 
     def _check_geometry(self) -> None:
@@ -307,19 +329,17 @@ class MLA(nn.Module):
                            start_pos=sp, tokens_per_seq=T, rope_abs=self.rope_positions == "absolute")
 
     def input_projections(self, x: torch.Tensor, need_q: bool = True) -> tuple[Optional[torch.Tensor], torch.Tensor]:
-        """q [B*T, H, 192] and the wkv_a rows kv [B*T, R + P] that forward
-        feeds the kernels (mla.py:281-288, :307-308).  Decode-sized bf16
-        inputs use one mla_linear product over the stacked wq / wkv_a weights
-        (q and kv are column views of it); other inputs use the ATen
-        projections (q is skipped when not needed)."""
+        """(q [B*T, H, 192] or None, kv [B*T, R + P]): the wkv_a rows that
+        forward feeds the append kernel (mla.py:281-288, :307-308).
+        Decode-sized bf16 inputs take kv from the fused input product (and
+        return no q: forward uses the absorbed query directly); other inputs
+        use the ATen projections (q is skipped when not needed)."""
         B, T, _ = x.size()
         n, H = B * T, self.n_heads
         with torch.no_grad():
             if self._fused_step_ok(x, n):
-                w_in, b_in, _ = self.decode_weights()
-                y = kernels.linear(x.reshape(n, self.dim), w_in, bias=b_in)
-                q = y[:, : H * self.qk_head_dim].view(n, H, self.qk_head_dim)
-                return q, y[:, H * self.qk_head_dim:]
+                _, _, kv = self._fused_projections(x)
+                return None, kv
             kv = self.wkv_a(x).view(n, -1)
             if not need_q:
                 return None, kv
@@ -362,7 +382,10 @@ class MLA(nn.Module):
             max_len = T
 
         fused = self._fused_step_ok(x, n)
-        q, kv = self.input_projections(x)
+        if fused:
+            q_abs, q_pe, kv = self._fused_projections(x)
+        else:
+            q, kv = self.input_projections(x)
 
         cos, sin = self.rope.half_tables()
         kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
@@ -370,20 +393,19 @@ class MLA(nn.Module):
 
         n_splits, min_chunk = self._split_plan(n, max_len, dev)
         if fused:
-            _, _, w_uk_t = self.decode_weights()
-            # q_abs[r, h] = q_nope[r, h] . W_uk[h]  (batched over heads)
-            q_abs = torch.empty(n, H, R, dtype=x.dtype, device=dev)
-            kernels.linear(q[:, :, :Dn].transpose(0, 1), w_uk_t, out=q_abs.transpose(0, 1))
             o_lat = torch.empty(n, H, R, dtype=x.dtype, device=dev)
+            ws = self._workspace_for(n, n_splits, dev)
             kernels.decode_attention(
-                q_abs, q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
+                q_abs, q_pe, cos, sin, cache, self.softmax_scale,
                 start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
-                out=o_lat, workspace=self._workspace_for(n, n_splits, dev),
+                out=o_lat, workspace=ws, merge=False,
             )
-            # o[r, h*Dv + d] = W_uv[h][d] . o_lat[r, h]: written straight in wo's input layout
+            # o[r, h*Dv + d] = W_uv[h][d] . merged o_lat[r, h]: split merge and
+            # read-out in one launch, written straight in wo's input layout
             w_uv = self.wkv_b.weight.detach().view(H, Dn + Dv, R)[:, Dn:, :]
             o = torch.empty(n, H * Dv, dtype=x.dtype, device=dev)
-            kernels.linear(o_lat.transpose(0, 1), w_uv, out=o.view(n, H, Dv).transpose(0, 1))
+            kernels.merge_project(o_lat, w_uv, o.view(n, H, Dv), cache, n_splits=n_splits, min_chunk=min_chunk,
+                                  workspace=ws, start_pos=sp, rows_per_seq=T)
             wo_b = None if self.wo.bias is None else self.wo.bias.detach()
             out = kernels.linear(o, self.wo.weight.detach(), bias=wo_b).view(B, T, self.dim)
             return self.resid_dropout(out)  # mla.py:490-495

@@ -168,6 +168,41 @@ def test_linear_empty_is_a_noop(lib):
     assert _linear(lib, batch=0, x=None, w=None, y=None) == 0
 
 
+def _merge_project(lib, **kw):
+    args = dict(o_part=FAKE, lse=FAKE, o_lat=FAKE, o_rs=4096, o_hs=256, kv_len=FAKE, row_seq=FAKE, sp=None, T=1,
+                cb=4, cs=64, n_rows=8, H=16, R=256, ns=4, mc=64, w=FAKE, w_rs=256, w_hs=65536, Dv=128, y=FAKE,
+                y_rs=2048, y_hs=128, dt=1, stream=None)
+    args.update(kw)
+    return lib.mla_merge_project(*args.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(dt=0), -2),
+        (dict(Dv=64), -2),
+        (dict(R=128), -2),
+        (dict(ns=0), -1),
+        (dict(o_part=None), -1),
+        (dict(row_seq=None), -1),
+        (dict(w=None), -1),
+        (dict(cs=0), -1),
+        (dict(o_hs=128), -1),
+        (dict(o_lat=FAKE + 8), -3),
+        (dict(w_rs=260), -3),
+        (dict(sp=FAKE), -1),
+    ],
+)
+def test_merge_project_rejects(lib, kw, code):
+    assert _merge_project(lib, **kw) == code
+    assert lib.mla_last_error().decode()
+
+
+def test_merge_project_single_split_needs_no_partials(lib):
+    # validation passes without partial buffers when n_splits == 1 (n_rows = 0: no launch)
+    assert _merge_project(lib, ns=1, o_part=None, lse=None, n_rows=0) == 0
+
+
 def test_python_check_raises_with_message(lib):
     rc = _append(lib, R=128)
     with pytest.raises(_abi.SwamlaError, match="UNSUPPORTED.*R=128"):

@@ -34,7 +34,7 @@ def assert_within_ulp(out, ref):
 
 
 @pytest.mark.parametrize("M", [1, 7, 16, 17, 32, 33, 64])
-@pytest.mark.parametrize("K", [128, 1024, 2048])
+@pytest.mark.parametrize("K", [128, 1024, 1152, 1536, 2048])
 def test_linear_shapes(gpu, M, K):
     say(f"linear M={M} K={K}")
     g = torch.Generator().manual_seed(M * 7 + K)
@@ -90,3 +90,50 @@ def test_linear_rows_beyond_m_untouched(gpu):
     torch.cuda.synchronize()
     assert bool((buf[5:] == 7.0).all())
     assert_within_ulp(buf[:5], ref_linear(x.cpu(), w.cpu()))
+
+
+@pytest.mark.parametrize("n_splits,min_chunk", [(1, 64), (8, 64), (47, 64)])
+def test_merge_project_equals_merge_then_product(gpu, n_splits, min_chunk):
+    """mla_merge_project == mla_merge followed by the W_uv product, on ragged
+    rows (empty, single-split and multi-split rows in one call)."""
+    from swamla_amd.kernels import DecodeWorkspace, LatentCache
+    from swamla_amd.rope import rope_tables
+
+    say(f"merge_project n_splits={n_splits}")
+    g = torch.Generator().manual_seed(20 + n_splits)
+    B, S, H, R = 5, 3000, 16, 256
+    dt = torch.bfloat16
+    cache = LatentCache(torch.randn(B, S, R, generator=g).to(dt).to(gpu),
+                        torch.randn(B, S, 64, generator=g).to(dt).to(gpu))
+    cos, sin = rope_tables(64, S)
+    cos = cos.to(dt)[0, 0, :, :32].contiguous().to(gpu)
+    sin = sin.to(dt)[0, 0, :, :32].contiguous().to(gpu)
+    rows = 11
+    row_seq = torch.tensor([0, 1, 2, 3, 4, 0, 1, 2, 3, 4, 1], dtype=torch.int32, device=gpu)
+    kv_len = torch.tensor([2999, 1, 64, 65, 0, 777, 3000, 1500, 130, 17, 2048], dtype=torch.int32, device=gpu)
+    qrp = torch.zeros(rows, dtype=torch.int32, device=gpu)
+    q_abs = (torch.randn(rows, H, R, generator=g) * 0.3).to(dt).to(gpu)
+    q_pe = (torch.randn(rows, H, 64, generator=g) * 0.3).to(dt).to(gpu)
+    wkv_b = (torch.randn(H * 256, R, generator=g) * 0.05).to(dt).to(gpu)
+    w_uv = wkv_b.view(H, 256, R)[:, 128:, :]
+    ws = DecodeWorkspace.allocate(rows, n_splits, gpu) if n_splits > 1 else None
+    o_lat = torch.empty(rows, H, R, dtype=dt, device=gpu)
+    kernels.decode_attention(q_abs, q_pe, cos, sin, cache, 0.0721, row_seq=row_seq, kv_len=kv_len,
+                             q_rope_pos=qrp, n_splits=n_splits, min_chunk=min_chunk, out=o_lat,
+                             workspace=ws, merge=False)
+    got = torch.full((rows, H * 128), float("nan"), dtype=dt, device=gpu)
+    kernels.merge_project(o_lat, w_uv, got.view(rows, H, 128), cache, n_splits=n_splits, min_chunk=min_chunk,
+                          workspace=ws, row_seq=row_seq, kv_len=kv_len)
+    # reference: the same decode with its own merge, then the per-head product
+    o_ref = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, 0.0721, row_seq=row_seq, kv_len=kv_len,
+                                     q_rope_pos=qrp, n_splits=n_splits, min_chunk=min_chunk)
+    torch.cuda.synchronize()
+    ref = ref_linear(o_ref.transpose(0, 1).cpu(), w_uv.cpu())  # [H, rows, 128], fp32
+    got_h = got.view(rows, H, 128).transpose(0, 1).float().cpu()
+    assert not bool(torch.isnan(got_h).any())
+    # The output is rounded to bf16 (up to 2^-8 relative, ~2^-10 on average);
+    # merged rows are rounded to bf16 before the product in both paths, and the
+    # two merges may differ by one bf16 ulp in a few channels.
+    err = (got_h - ref).abs()
+    assert float(err.max()) <= 2e-2 * float(ref.abs().max()), float(err.max())
+    assert float(err.mean()) <= 3e-3 * float(ref.abs().mean()), float(err.mean())
