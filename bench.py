@@ -43,23 +43,55 @@ HBM_PEAK_GBS = 8000.0
 R, P, H = 256, 64, 16
 
 
+CONFIGS = {
+    # BASELINE.json configs[1..4]; config 1 is the CPU-runnable fp32 case (a parity test)
+    2: dict(batch=32, ctx=4096, dim=1024, steps=128, warmup=8, layers=8, cache="bf16", ragged=False),
+    3: dict(batch=64, ctx=16384, dim=1024, steps=32, warmup=4, layers=2, cache="bf16", ragged=True),
+    4: dict(batch=8, ctx=131072, dim=1536, steps=32, warmup=4, layers=1, cache="bf16", ragged=False),
+    5: dict(batch=128, ctx=8192, dim=1024, steps=64, warmup=4, layers=6, cache="fp8", ragged=False),
+}
+WORKLOADS = {
+    2: "BASELINE config 2: MLA decode, batch 32, prefill 4096 then append+attention steps",
+    3: "BASELINE config 3: ragged batch of 64 sequences, cache lengths U[256, 16384] (seed 0), per-sequence start_pos",
+    4: "BASELINE config 4: long-context split-KV, n_embd 1536, batch 8, cache length 131072",
+    5: "BASELINE config 5: 6-layer decode stack, fp8-e4m3 latent cache, batch 128, cache length 8192",
+}
+
+
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=128)
-    p.add_argument("--warmup", type=int, default=8)
-    p.add_argument("--layers", type=int, default=8, help="independent layers rotated per step")
-    p.add_argument("--batch", type=int, default=32)
-    p.add_argument("--ctx", type=int, default=4096)
-    p.add_argument("--dim", type=int, default=1024)
-    p.add_argument("--cache", choices=["bf16", "fp8"], default="bf16")
+    p.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS),
+                   help="BASELINE configuration (2 = the headline metric)")
+    p.add_argument("--steps", type=int, default=None)
+    p.add_argument("--warmup", type=int, default=None)
+    p.add_argument("--layers", type=int, default=None, help="independent layers rotated per step")
+    p.add_argument("--batch", type=int, default=None)
+    p.add_argument("--ctx", type=int, default=None, help="prefilled context (the maximum for the ragged config)")
+    p.add_argument("--dim", type=int, default=None)
+    p.add_argument("--cache", choices=["bf16", "fp8"], default=None)
     p.add_argument("--kernel-reps", type=int, default=50, help="roofline launches per layer")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--cpu-batch", type=int, default=4)
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run plain device copies of known size (calibrates FETCH_SIZE / WRITE_SIZE)")
-    return p.parse_args()
+    args = p.parse_args()
+    preset = CONFIGS[args.config]
+    for k, v in preset.items():
+        if getattr(args, k, None) is None:
+            setattr(args, k, v)
+    if args.config != 2:
+        args.no_cpu_baseline = True  # the CPU leg samples the headline workload only
+    return args
+
+
+def start_lengths(args, torch):
+    """Per-sequence prefilled lengths: all ctx, or U[256, ctx] from seed 0."""
+    if not args.ragged:
+        return torch.full((args.batch,), args.ctx, dtype=torch.int32)
+    g = torch.Generator().manual_seed(0)
+    return torch.randint(256, args.ctx + 1, (args.batch,), generator=g, dtype=torch.int32)
 
 
 def log(*a):
@@ -100,6 +132,13 @@ def attention_bytes(B: int, L: int, fp8: bool) -> int:
     return B * L * per_tok + B * H * (R + P) * 2 + B * H * R * 2
 
 
+def attention_bytes_rows(lens, fp8: bool) -> int:
+    """Algorithmic bytes of one decode launch over rows of lengths ``lens``."""
+    per_tok = R * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0)
+    B = int(lens.numel())
+    return int(lens.sum()) * per_tok + B * H * (R + P) * 2 + B * H * R * 2
+
+
 def init_linear_weights(module, seed: int, torch) -> None:
     """N(0, 0.02) Linear weights in parameter order from a CPU generator and
     zero biases; LayerNorm stays at weight 1 / bias 0, as the reference model
@@ -134,7 +173,7 @@ def build_layers(args, dev, torch):
     return layers
 
 
-def time_decode_kernel(layers, xs, args, dev, torch):
+def time_decode_kernel(layers, xs, lens, args, dev, torch):
     """Average duration of one decode-attention launch from HIP events
     recorded on its stream around back-to-back launches that rotate over the
     layers' caches ("cold": the working set exceeds the MALL) or repeat on one
@@ -153,8 +192,8 @@ def time_decode_kernel(layers, xs, args, dev, torch):
             w_uk, _ = m.absorbed_weights()
             q_abs = torch.bmm(q[:, :, :128].transpose(0, 1).contiguous(), w_uk)  # [H, B, R]
             cache = m.latent_cache()
-            L = int(args.ctx + args.steps)
-            sp = torch.full((B,), L - 1, dtype=torch.int32, device=dev)  # attend [0, L)
+            L = int(lens.max())
+            sp = (lens - 1).to(device=dev, dtype=torch.int32)  # row b attends [0, lens[b])
             n_splits, min_chunk = m._split_plan(B, L, dev)
             ws = kernels.DecodeWorkspace.allocate(B, n_splits, dev)
             o_lat = torch.empty(H, B, R, dtype=torch.bfloat16, device=dev)
@@ -279,7 +318,9 @@ def main() -> int:
     xs = [torch.randn(args.batch, 1, args.dim, generator=g, device=dev, dtype=torch.bfloat16) for _ in layers]
     # one start-position tensor for the whole stack, advanced once per step
     # (every layer of a decoder sees the same positions)
-    sp = torch.full((args.batch,), args.ctx, dtype=torch.int32, device=dev)
+    lens0 = start_lengths(args, torch)
+    sp0 = lens0.to(dev)
+    sp = sp0.clone()
     outs = [None] * len(layers)
 
     def stack_step():
@@ -297,10 +338,10 @@ def main() -> int:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             stack_step()
-        sp.fill_(args.ctx)
+        sp.copy_(sp0)
         for _ in range(args.warmup):
             graph.replay()
-        sp.fill_(args.ctx)  # timed steps decode positions ctx .. ctx+K-1
+        sp.copy_(sp0)  # timed steps decode positions start .. start+K-1
         log("timing")
         if torch.distributed.is_available() and torch.distributed.is_initialized():
             torch.distributed.barrier()
@@ -319,17 +360,18 @@ def main() -> int:
     ms_per_step = elapsed / layer_steps * 1e3
     log(f"decode: {value:.0f} layer-token/s, {ms_per_step * 1e3:.1f} us per layer-step, finite={ok}")
 
-    cold_us, warm_us, merge_us, L, B, n_splits = time_decode_kernel(layers, xs, args, dev, torch)
-    abytes = attention_bytes(B, L, fp8)
-    traffic, traffic_src = measured_traffic(B, L, args.cache)
+    lens = lens0 + args.steps  # lengths after the timed steps
+    cold_us, warm_us, merge_us, L, B, n_splits = time_decode_kernel(layers, xs, lens, args, dev, torch)
+    abytes = attention_bytes_rows(lens, fp8)
+    traffic, traffic_src = measured_traffic(B, L, args.cache) if not args.ragged else (None, None)
     achieved = abytes / (cold_us * 1e-6) / 1e9
     warm = abytes / (warm_us * 1e-6) / 1e9
     log(f"decode kernel: {cold_us:.2f} us cold ({achieved:.0f} GB/s), {warm_us:.2f} us warm ({warm:.0f} GB/s); "
         f"merge {merge_us:.2f} us")
     # algorithmic bytes of one full layer-step (attention + append + weights), mean context
-    mean_L = args.ctx + (args.steps + 1) / 2
     w_bytes = sum(p.numel() * p.element_size() for p in layers[0].parameters())
-    step_bytes = attention_bytes(args.batch, int(mean_L), fp8) + w_bytes + args.batch * (R + P) * 2 * 2
+    mid = lens0 + (args.steps + 1) // 2
+    step_bytes = attention_bytes_rows(mid, fp8) + w_bytes + args.batch * (R + P) * 2 * 2
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -338,7 +380,8 @@ def main() -> int:
         log(f"cpu: {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
 
     line = {
-        "metric": "MLA decode tok/s + achieved HBM GB/s (% peak), bs=32 ctx=4096 bf16",
+        "metric": ("MLA decode tok/s + achieved HBM GB/s (% peak), bs=32 ctx=4096 bf16" if args.config == 2
+                   else f"MLA decode tok/s + achieved HBM GB/s (% peak), config {args.config}"),
         "value": value,
         "unit": "tok/s",
         "n_gpus": 1,
@@ -351,7 +394,7 @@ def main() -> int:
         "dtype": "bf16" if not fp8 else "bf16+e4m3-cache",
         "data": "synthetic: N(0,1) hidden states, N(0,0.02) random-init weights (no checkpoint)",
         "config": {
-            "workload": "BASELINE config 2: MLA decode, batch 32, prefill 4096 then append+attention steps",
+            "workload": WORKLOADS[args.config],
             "batch": args.batch, "ctx": args.ctx, "decode_steps": args.steps, "n_embd": args.dim,
             "heads": H, "kv_lora_rank": R, "rope_dim": P, "cache": args.cache,
             "layers_rotated": len(layers),
@@ -372,7 +415,9 @@ def main() -> int:
                                else "no committed PMC summary for this kernel source and launch shape"),
             "bytes_per_launch": abytes,
             "avg_launch_us": cold_us,
-            "launch": f"B={B} L={L} splits<={n_splits}, caches rotated over {len(layers)} layers",
+            "launch": (f"B={B} L={L} splits<={n_splits}, caches rotated over {len(layers)} layers" if not args.ragged
+                       else f"B={B} ragged L in [{int(lens.min())}, {L}] (sum {int(lens.sum())}), splits<={n_splits}, "
+                            f"caches rotated over {len(layers)} layers"),
             "warm_mall_achieved": warm,
             "warm_mall_avg_launch_us": warm_us,
             "merge_avg_launch_us": merge_us,

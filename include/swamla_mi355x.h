@@ -160,7 +160,7 @@ int mla_merge(const float* o_part, const float* lse_part,
  * Element strides: x row x_rs / batch x_bs, w row w_rs / batch w_bs, y row
  * y_rs / batch y_bs, bias batch bias_bs; the k and n dimensions are
  * contiguous.  bias may be NULL.
- * Limits: 1 <= M <= 64, N a multiple of 16, K a multiple of 128, x and w
+ * Limits: 1 <= M <= 128, N a multiple of 16, K a multiple of 128, x and w
  * 16-byte aligned with row / batch strides that are multiples of 8.
  */
 int mla_linear(const void* x, int64_t x_rs, int64_t x_bs, const void* w,

@@ -230,7 +230,7 @@ int mla_linear(const void* x, int64_t x_rs, int64_t x_bs, const void* w, int64_t
                const void* bias, int64_t bias_bs, void* y, int64_t y_rs, int64_t y_bs, int32_t M,
                int32_t N, int32_t K, int32_t batch, int32_t dtype, void* stream) {
   if (dtype != SWAMLA_DTYPE_BF16) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: dtype %d not built (bf16 only)", dtype);
-  if (M < 0 || M > 64) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: M=%d outside [0, 64]", M);
+  if (M < 0 || M > 128) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: M=%d outside [0, 128]", M);
   if (N < 0 || N % 16 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: N=%d is not a multiple of 16", N);
   if (K < 128 || K % 128 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_linear: K=%d is not a positive multiple of 128", K);
   if (batch < 0 || batch > 65535) return fail(SWAMLA_ERR_INVALID_ARG, "mla_linear: batch=%d outside [0, 65535]", batch);

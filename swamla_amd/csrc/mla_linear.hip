@@ -2,7 +2,7 @@
 //
 //   Y[b, m, n] = sum_k X[b, m, k] W[b, n, k] (+ bias[b, n]),  bf16 in/out,
 //   fp32 accumulation, one rounding of the result (what a bf16 nn.Linear
-//   returns).  M <= 64 rows (the query rows of a decode step).
+//   returns).  M <= 128 rows (the query rows of a decode step).
 //
 // One launch covers the step's projections that surround attention: wq and
 // wkv_a as one product over their stacked weights (models/mla.py:281-288,
@@ -29,7 +29,12 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-constexpr int kLinBatch = 8;  // K steps of 32 whose loads are issued together
+// K steps of 32 whose loads are issued together: eight for up to 32 rows,
+// fewer for more row tiles so the staged operands stay within the registers.
+template <int MT>
+constexpr int lin_batch() {
+  return MT <= 2 ? 8 : (MT <= 4 ? 4 : 2);
+}
 
 // Block: 16 output columns [16*blockIdx.x, +16) of batch entry blockIdx.y
 // for all M rows (MT tiles of 16 rows).  Wave w of NW reduces K range
@@ -63,6 +68,7 @@ __global__ __launch_bounds__(NW * 64) void mla_linear_kernel(LinearArgs a) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  constexpr int kLinBatch = lin_batch<MT>();
   const int steps = kw / 32;
   for (int s0 = 0; s0 < steps; s0 += kLinBatch) {
     const int cnt = min(kLinBatch, steps - s0);  // block-uniform
@@ -229,16 +235,20 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
 template <int NW>
 void launch_linear_nw(const LinearArgs& a, dim3 grid, int mt, hipStream_t s) {
   const dim3 block(NW * 64);
-  if (mt == 1) hipLaunchKernelGGL((mla_linear_kernel<1, NW>), grid, block, 0, s, a);
-  else if (mt == 2) hipLaunchKernelGGL((mla_linear_kernel<2, NW>), grid, block, 0, s, a);
-  else if (mt == 3) hipLaunchKernelGGL((mla_linear_kernel<3, NW>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((mla_linear_kernel<4, NW>), grid, block, 0, s, a);
+  switch (mt) {
+    case 1: hipLaunchKernelGGL((mla_linear_kernel<1, NW>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((mla_linear_kernel<2, NW>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((mla_linear_kernel<3, NW>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((mla_linear_kernel<4, NW>), grid, block, 0, s, a); break;
+    case 5: case 6: hipLaunchKernelGGL((mla_linear_kernel<6, NW>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((mla_linear_kernel<8, NW>), grid, block, 0, s, a); break;
+  }
 }
 
 int launch_linear(const LinearArgs& a, int batch, hipStream_t s) {
   if (a.M == 0 || a.N == 0 || batch == 0) return 0;
   const int mt = (a.M + 15) / 16;
-  if (mt < 1 || mt > 4) return -1;
+  if (mt < 1 || mt > 8) return -1;
   const dim3 grid(a.N / 16, batch);
   // each wave's K range must be a whole number of 32-wide steps
   if (a.K >= 1024 && a.K % 256 == 0) launch_linear_nw<8>(a, grid, mt, s);

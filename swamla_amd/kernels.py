@@ -286,7 +286,7 @@ def decode_attention(
     return out
 
 
-LINEAR_MAX_ROWS = 64
+LINEAR_MAX_ROWS = 128
 
 
 def linear(
@@ -299,7 +299,7 @@ def linear(
     accumulation (mla_linear).  x [batch, M, K], w [batch, N, K], out
     [batch, M, N] and bias [batch, N] may be strided views with a unit last
     stride; 2-D x / w / out (and 1-D bias) are one batch entry.  For the
-    decode step's products (M <= 64): wq / wkv_a (models/mla.py:281-288,
+    decode step's products (M <= 128): wq / wkv_a (models/mla.py:281-288,
     :307), the absorbed W_uk / W_uv products (re-associating :427, :433) and
     wo (:490-495)."""
     squeeze = x.dim() == 2

@@ -248,7 +248,7 @@ class MLA(nn.Module):
         return q_abs, q_pe, y[:, H * (R + P):]
 
     def _fused_step_ok(self, x: torch.Tensor, n: int) -> bool:
-        """The decode-step kernels cover bf16 modules with at most 64 query
+        """The decode-step kernels cover bf16 modules with at most 128 query
         rows, no q low-rank path and 128-aligned model widths."""
         return (
             x.dtype == torch.bfloat16

@@ -145,7 +145,7 @@ def _linear(lib, **kw):
     "kw,code",
     [
         (dict(dt=0), -2),
-        (dict(M=65), -2),
+        (dict(M=129), -2),
         (dict(N=40), -2),
         (dict(K=100), -2),
         (dict(K=0), -2),

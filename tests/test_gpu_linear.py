@@ -33,7 +33,7 @@ def assert_within_ulp(out, ref):
     assert not bool(bad.any()), f"{int(bad.sum())} / {bad.numel()} beyond 1 ulp; max err {float(err.max()):.3e}"
 
 
-@pytest.mark.parametrize("M", [1, 7, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("M", [1, 7, 16, 17, 32, 33, 64, 80, 128])
 @pytest.mark.parametrize("K", [128, 1024, 1152, 1536, 2048])
 def test_linear_shapes(gpu, M, K):
     say(f"linear M={M} K={K}")
