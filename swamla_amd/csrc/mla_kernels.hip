@@ -295,7 +295,8 @@ constexpr int kCRow = 2 * kR + 16;         // 528 B per LDS latent row
 constexpr int kPeRow = 2 * kP + 16;        // 144 B per LDS rope row
 constexpr int kCBytes = kTileTok * kCRow;  // 33792 B
 constexpr int kPeBytes = kTileTok * kPeRow;  // 9216 B
-constexpr int kPRow = 2 * kTileTok + 16;   // bytes per head row of P (128 + 16 pad)
+constexpr int kPRow = 2 * kTileTok + 8;    // bytes per head row of P (128 + 8 pad: the 16 heads
+                                           // of an 8-byte access fall on distinct banks)
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 __device__ __forceinline__ bf16x8_t cat_bf16x8(s16x4_t lo, s16x4_t hi) {
