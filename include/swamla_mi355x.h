@@ -135,6 +135,40 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
                     int32_t cache_dtype, void* stream);
 
 /*
+ * mla_decode_attn_append — one decode step (one new token per sequence) with
+ * the append folded into the attention launch.  Replaces, for T = 1,
+ * models/mla.py:307-323 and :409-414 (mla_append's part) together with
+ * :417-487 (mla_decode_attn's part).
+ *
+ * Dense addressing only, one query row per sequence: row r is cache row r,
+ * its new token kv_in[r] is written at start_pos[r] exactly as mla_append
+ * writes it (same LayerNorm / RoPE / e4m3 numerics), and row r then attends
+ * over [0, start_pos[r] + 1) including that token, as mla_decode_attn does.
+ * kv_in, in_row_stride, ln_w, ln_b, eps, err_flag: as for mla_append (bf16;
+ * the k_pe RoPE uses cos_tab / sin_tab at the row's RoPE row).  The other
+ * arguments are those of mla_decode_attn with row_seq / kv_len / q_rope_pos
+ * absent and rows_per_seq = 1.  bf16 models only (bf16 or e4m3 cache).
+ * kv_in, ln_w and ln_b need 8-byte aligned bases and in_row_stride a
+ * multiple of 4.
+ * Results are identical to mla_append followed by mla_decode_attn.
+ */
+int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
+                           const void* ln_w, const void* ln_b, float eps,
+                           int32_t* err_flag, const void* q_abs,
+                           int64_t q_abs_rs, int64_t q_abs_hs,
+                           const void* q_pe, int64_t q_pe_rs, int64_t q_pe_hs,
+                           const void* cos_tab, const void* sin_tab,
+                           int64_t rope_len, void* ckv_cache, void* kpe_cache,
+                           float* ckv_scale, int64_t cache_batch,
+                           int64_t cache_seq, const int32_t* start_pos,
+                           int32_t rope_abs, int32_t n_rows, int32_t H,
+                           int32_t R, int32_t P, float sm_scale,
+                           int32_t n_splits, int32_t min_chunk, float* o_part,
+                           float* lse_part, void* o_lat, int64_t o_rs,
+                           int64_t o_hs, int32_t dtype, int32_t cache_dtype,
+                           void* stream);
+
+/*
  * mla_merge — log-sum-exp merge of split-KV partials (no reference
  * counterpart: the reference attends in one SDPA call, mla.py:581-595).
  * o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M), M = max_s lse_s, for

@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "mla_last_error",
     "mla_append",
     "mla_decode_attn",
+    "mla_decode_attn_append",
     "mla_merge",
     "mla_split_count",
     "mla_linear",
@@ -75,6 +76,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_decode_attn.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
         _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
+        _F, _I32, _I32, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
+    ]
+    lib.mla_decode_attn_append.restype = ctypes.c_int
+    lib.mla_decode_attn_append.argtypes = [
+        _P, _I64, _P, _P, _F, _P,
+        _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
+        _P, _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _I32, _I32,
         _F, _I32, _I32, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
     ]
     lib.mla_merge.restype = ctypes.c_int

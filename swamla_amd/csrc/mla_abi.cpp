@@ -138,6 +138,72 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const in
   return ok();
 }
 
+}  // extern "C"
+
+namespace {
+
+// Validation shared by mla_decode_attn and mla_decode_attn_append; fills *a.
+int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const void* q_pe,
+                 int64_t q_pe_rs, int64_t q_pe_hs, const void* cos_tab, const void* sin_tab, int64_t rope_len,
+                 const void* ckv_cache, const void* kpe_cache, const float* ckv_scale, int64_t cache_batch,
+                 int64_t cache_seq, const int32_t* row_seq, const int32_t* kv_len, const int32_t* q_rope_pos,
+                 const int32_t* start_pos, int32_t rows_per_seq, int32_t rope_abs, int32_t n_rows, int32_t H,
+                 int32_t R, int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk, float* o_part,
+                 float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype, int32_t cache_dtype,
+                 swamla::DecodeArgs* a) {
+  if (int e = check_geometry(H, R, P)) return e;
+  if (int e = check_pair(dtype, cache_dtype)) return e;
+  if (n_rows < 0 || n_rows > 65535)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_rows=%d outside [0, 65535]", fn, n_rows);
+  if (n_splits < 1 || n_splits > 1024)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_splits=%d outside [1, 1024]", fn, n_splits);
+  if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "%s: min_chunk=%d < 1", fn, min_chunk);
+  if (!(sm_scale > 0.f)) return fail(SWAMLA_ERR_INVALID_ARG, "%s: sm_scale must be > 0", fn);
+  if (!ckv_cache || !kpe_cache || !cos_tab || !sin_tab || !o_lat)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: null cache / RoPE / output pointer", fn);
+  if (n_rows > 0 && (!q_abs || !q_pe)) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null query pointer", fn);
+  swamla::Addressing ad;
+  if (int e = check_addressing(fn, n_rows, row_seq, kv_len, q_rope_pos, start_pos, rows_per_seq, true, true,
+                               &ad, rope_abs))
+    return e;
+  if (n_splits > 1 && (!o_part || !lse_part))
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_splits > 1 needs o_part and lse_part", fn);
+  if (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: fp8 cache needs ckv_scale", fn);
+  if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1 || rope_len < 1)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: bad cache / rope table shape", fn);
+  if (q_abs_hs < R || q_pe_hs < P || o_hs < R || q_abs_rs < 0 || q_pe_rs < 0 || o_rs < 0)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: head strides must cover R / P values", fn);
+  if (dtype == SWAMLA_DTYPE_BF16) {
+    // 16-byte vector loads / stores of 8 bf16.
+    if (!aligned(q_abs, 16) || !aligned(q_pe, 16) || !aligned(o_lat, 16) || !aligned(ckv_cache, 16) ||
+        !aligned(kpe_cache, 16) || !aligned(cos_tab, 8) || !aligned(sin_tab, 8) ||
+        (q_abs_rs | q_abs_hs | q_pe_rs | q_pe_hs | o_rs | o_hs) % 8 != 0)
+      return fail(SWAMLA_ERR_MISALIGNED,
+                  "%s: bf16 operands need 16-byte aligned bases (RoPE tables: 8-byte) and strides "
+                  "that are multiples of 8 elements", fn);
+  } else {
+    if (!aligned(q_abs, 4) || !aligned(q_pe, 4) || !aligned(o_lat, 16) || !aligned(ckv_cache, 4) ||
+        !aligned(kpe_cache, 4) || !aligned(cos_tab, 4) || !aligned(sin_tab, 4) || (o_rs | o_hs) % 4 != 0)
+      return fail(SWAMLA_ERR_MISALIGNED,
+                  "%s: fp32 output needs a 16-byte aligned base and strides that are "
+                  "multiples of 4", fn);
+  }
+  if ((o_part && !aligned(o_part, 16)) || (lse_part && !aligned(lse_part, 4)) ||
+      (ckv_scale && !aligned(ckv_scale, 4)))
+    return fail(SWAMLA_ERR_MISALIGNED, "%s: o_part must be 16-byte aligned", fn);
+  const float log2e = 1.4426950408889634f;
+  *a = swamla::DecodeArgs{q_abs,     q_abs_rs,  q_abs_hs,  q_pe,      q_pe_rs,     q_pe_hs,
+                          cos_tab,   sin_tab,   rope_len,  ckv_cache, kpe_cache,   ckv_scale,
+                          cache_batch, cache_seq, ad,      n_rows,    sm_scale * log2e, n_splits,
+                          min_chunk, o_part,    lse_part,  o_lat,     o_rs,      o_hs, swamla::AppendArgs{}};
+  return SWAMLA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const void* q_pe,
                     int64_t q_pe_rs, int64_t q_pe_hs, const void* cos_tab, const void* sin_tab,
                     int64_t rope_len, const void* ckv_cache, const void* kpe_cache,
@@ -147,54 +213,54 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const
                     int32_t H, int32_t R, int32_t P, float sm_scale, int32_t n_splits,
                     int32_t min_chunk, float* o_part, float* lse_part, void* o_lat,
                     int64_t o_rs, int64_t o_hs, int32_t dtype, int32_t cache_dtype, void* stream) {
-  if (int e = check_geometry(H, R, P)) return e;
-  if (int e = check_pair(dtype, cache_dtype)) return e;
-  if (n_rows < 0 || n_rows > 65535)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: n_rows=%d outside [0, 65535]", n_rows);
-  if (n_splits < 1 || n_splits > 1024)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: n_splits=%d outside [1, 1024]", n_splits);
-  if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: min_chunk=%d < 1", min_chunk);
-  if (!(sm_scale > 0.f)) return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: sm_scale must be > 0");
-  if (!ckv_cache || !kpe_cache || !cos_tab || !sin_tab || !o_lat)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: null cache / RoPE / output pointer");
-  if (n_rows > 0 && (!q_abs || !q_pe)) return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: null query pointer");
-  swamla::Addressing ad;
-  if (int e = check_addressing("mla_decode_attn", n_rows, row_seq, kv_len, q_rope_pos, start_pos, rows_per_seq,
-                               true, true, &ad, rope_abs))
+  swamla::DecodeArgs a;
+  if (int e = check_decode("mla_decode_attn", q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab,
+                           sin_tab, rope_len, ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, row_seq,
+                           kv_len, q_rope_pos, start_pos, rows_per_seq, rope_abs, n_rows, H, R, P, sm_scale,
+                           n_splits, min_chunk, o_part, lse_part, o_lat, o_rs, o_hs, dtype, cache_dtype, &a))
     return e;
-  if (n_splits > 1 && (!o_part || !lse_part))
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: n_splits > 1 needs o_part and lse_part");
-  if (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: fp8 cache needs ckv_scale");
-  if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1 || rope_len < 1)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: bad cache / rope table shape");
-  if (q_abs_hs < R || q_pe_hs < P || o_hs < R || q_abs_rs < 0 || q_pe_rs < 0 || o_rs < 0)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_attn: head strides must cover R / P values");
-  if (dtype == SWAMLA_DTYPE_BF16) {
-    // 16-byte vector loads / stores of 8 bf16.
-    if (!aligned(q_abs, 16) || !aligned(q_pe, 16) || !aligned(o_lat, 16) || !aligned(ckv_cache, 16) ||
-        !aligned(kpe_cache, 16) || (q_abs_rs | q_abs_hs | q_pe_rs | q_pe_hs | o_rs | o_hs) % 8 != 0)
-      return fail(SWAMLA_ERR_MISALIGNED,
-                  "mla_decode_attn: bf16 operands need 16-byte aligned bases and strides that are "
-                  "multiples of 8 elements");
-  } else {
-    if (!aligned(q_abs, 4) || !aligned(q_pe, 4) || !aligned(o_lat, 16) || !aligned(ckv_cache, 4) ||
-        !aligned(kpe_cache, 4) || (o_rs | o_hs) % 4 != 0)
-      return fail(SWAMLA_ERR_MISALIGNED,
-                  "mla_decode_attn: fp32 output needs a 16-byte aligned base and strides that are "
-                  "multiples of 4");
-  }
-  if ((o_part && !aligned(o_part, 16)) || (lse_part && !aligned(lse_part, 4)) ||
-      (ckv_scale && !aligned(ckv_scale, 4)))
-    return fail(SWAMLA_ERR_MISALIGNED, "mla_decode_attn: o_part must be 16-byte aligned");
-  const float log2e = 1.4426950408889634f;
-  swamla::DecodeArgs a{q_abs,     q_abs_rs,  q_abs_hs,  q_pe,      q_pe_rs,     q_pe_hs,
-                       cos_tab,   sin_tab,   rope_len,  ckv_cache, kpe_cache,   ckv_scale,
-                       cache_batch, cache_seq, ad,      n_rows,    sm_scale * log2e, n_splits,
-                       min_chunk, o_part,    lse_part,  o_lat,     o_rs,      o_hs};
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_attn: no kernel for this dtype pair");
   if (rc != 0) return hip_fail("mla_decode_attn");
+  return ok();
+}
+
+int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void* ln_w, const void* ln_b,
+                           float eps, int32_t* err_flag, const void* q_abs, int64_t q_abs_rs,
+                           int64_t q_abs_hs, const void* q_pe, int64_t q_pe_rs, int64_t q_pe_hs,
+                           const void* cos_tab, const void* sin_tab, int64_t rope_len, void* ckv_cache,
+                           void* kpe_cache, float* ckv_scale, int64_t cache_batch, int64_t cache_seq,
+                           const int32_t* start_pos, int32_t rope_abs, int32_t n_rows, int32_t H, int32_t R,
+                           int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk, float* o_part,
+                           float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
+                           int32_t cache_dtype, void* stream) {
+  const char* fn = "mla_decode_attn_append";
+  if (dtype != SWAMLA_DTYPE_BF16)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "%s: model dtype %d not built (bf16 only)", fn, dtype);
+  if (!start_pos) return fail(SWAMLA_ERR_INVALID_ARG, "%s: needs dense addressing (start_pos)", fn);
+  swamla::DecodeArgs a;
+  if (int e = check_decode(fn, q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab, sin_tab, rope_len,
+                           ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, nullptr, nullptr, nullptr,
+                           start_pos, 1, rope_abs, n_rows, H, R, P, sm_scale, n_splits, min_chunk, o_part,
+                           lse_part, o_lat, o_rs, o_hs, dtype, cache_dtype, &a))
+    return e;
+  if (n_rows > 0 && !kv_in) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null input rows", fn);
+  if (!ln_w || !ln_b) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null LayerNorm pointer", fn);
+  if (in_row_stride < R + P)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: in_row_stride=%lld < R+P=%d", fn, (long long)in_row_stride, R + P);
+  // a lane reads four channels of the row and of the LayerNorm parameters at once
+  if ((kv_in && !aligned(kv_in, 8)) || in_row_stride % 4 != 0 || !aligned(ln_w, 8) || !aligned(ln_b, 8) ||
+      !aligned(cos_tab, 2) || !aligned(sin_tab, 2))
+    return fail(SWAMLA_ERR_MISALIGNED,
+                "%s: input rows and LayerNorm parameters need 8-byte aligned bases and a row stride that is a "
+                "multiple of 4 elements", fn);
+  if (n_rows == 0) return ok();
+  a.fa = swamla::AppendArgs{kv_in,   in_row_stride, n_rows,      a.ad,      ln_w,      ln_b,   eps,
+                            cos_tab, sin_tab,       rope_len,    ckv_cache, kpe_cache, ckv_scale,
+                            cache_batch, cache_seq, err_flag};
+  const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair", fn);
+  if (rc != 0) return hip_fail(fn);
   return ok();
 }
 

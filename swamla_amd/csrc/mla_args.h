@@ -59,6 +59,9 @@ struct DecodeArgs {
   float* lse_part;
   void* o_lat;
   int64_t o_rs, o_hs;
+  // Optional fused append of one new token per row (fa.kv_in == nullptr:
+  // none): the block owning a row's last split appends row r's token r.
+  AppendArgs fa;
 };
 
 struct MergeArgs {

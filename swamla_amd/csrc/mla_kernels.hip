@@ -89,32 +89,17 @@ __device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xo
 // ---------------------------------------------------------------------------
 // IN_DT: 0 fp32 / 1 bf16 (model dtype; also k_pe cache dtype).
 // C_DT : 0 fp32 / 1 bf16 / 2 e4m3 (latent cache dtype).
-template <int IN_DT, int C_DT>
-__global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
-  // Every multiply / add below is rounded on its own: the LayerNorm must
-  // reproduce the fixed-order fp64 statement exactly.
-#pragma clang fp contract(off)
-  using E = Elem<IN_DT>;
-  using T = typename E::T;
-  const int lane = threadIdx.x & 63;
-  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tok >= a.n_tok) return;
-  const TokAddr ta = tok_addr(a.ad, tok);
-  const int b = ta.b, pos = ta.pos, rp = ta.rope;
-  if (b < 0 || b >= a.cache_b || pos < 0 || pos >= a.cache_s || rp < 0 || rp >= a.rope_len) {
-    if (lane == 0 && a.err_flag) a.err_flag[0] = 1;
-    return;
-  }
-  const T* row = static_cast<const T*>(a.kv_in) + static_cast<int64_t>(tok) * a.in_rs;
-  const T* w = static_cast<const T*>(a.ln_w);
-  const T* bb = static_cast<const T*>(a.ln_b);
+// The arithmetic below is shared by the append kernel and the decode kernel's
+// fused one-token append, so both write identical bits.
 
-  // --- LayerNorm over c[0..255]: lane owns channels 4*lane .. 4*lane+3.
-  // Statistics in fp64; fixed order: in-lane left-to-right, then xor
-  // butterfly 1,2,4,...,32 (every lane ends with the same total).
-  double x[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = static_cast<double>(E::ld(row, 4 * lane + i));
+// LayerNorm of one R = 256 channel row held by a wavefront, lane owning
+// channels 4*lane .. 4*lane+3.  Every multiply / add is rounded on its own:
+// the result must reproduce the fixed-order fp64 statement exactly.
+// Statistics in fp64; fixed order: in-lane left-to-right, then xor butterfly
+// 1,2,4,...,32 (every lane ends with the same total).
+__device__ __forceinline__ void layernorm_quad(const double x[4], const double wt[4], const double bs[4],
+                                               float eps, double y[4]) {
+#pragma clang fp contract(off)
   double s = ((x[0] + x[1]) + x[2]) + x[3];
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) s = s + shfl_xor_f64(s, m);
@@ -127,14 +112,63 @@ __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
   for (int m = 1; m < 64; m <<= 1) q = q + shfl_xor_f64(q, m);
   const double var = q * (1.0 / 256.0);
   // correctly rounded square root and IEEE division
-  const double rstd = 1.0 / __dsqrt_rn(var + static_cast<double>(a.eps));
-  double y[4];
+  const double rstd = 1.0 / __dsqrt_rn(var + static_cast<double>(eps));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i] = (d[i] * rstd) * wt[i] + bs[i];
+}
+
+// bf16 cache: the four channels rounded once from fp64.
+__device__ __forceinline__ uint2 encode_bf16_quad(const double y[4]) {
+  uint2 o;
+  o.x = f64_to_bf16(y[0]) | (static_cast<uint32_t>(f64_to_bf16(y[1])) << 16);
+  o.y = f64_to_bf16(y[2]) | (static_cast<uint32_t>(f64_to_bf16(y[3])) << 16);
+  return o;
+}
+
+// e4m3 per-token: y is first rounded to bf16 (the value a bf16 cache would
+// hold), amax over the token, scale = max(amax,1e-12)/448, code = RNE(y/scale).
+// Returns the lane's four codes (byte i = channel 4*lane+i).
+__device__ __forceinline__ uint32_t encode_e4m3_quad(const double y[4], float& scale) {
+  float yb[4];
+  float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const double wi = static_cast<double>(E::ld(w, 4 * lane + i));
-    const double bi = static_cast<double>(E::ld(bb, 4 * lane + i));
-    y[i] = (d[i] * rstd) * wi + bi;
+    yb[i] = bf16_to_f32(f64_to_bf16(y[i]));
+    amax = fmaxf(amax, fabsf(yb[i]));
   }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, m));
+  scale = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
+  uint32_t codes = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) codes |= static_cast<uint32_t>(f32_to_e4m3(__fdiv_rn(yb[i], scale))) << (8 * i);
+  return codes;
+}
+
+// The work of one wavefront: token `tok` of the append.
+template <int IN_DT, int C_DT>
+__device__ __forceinline__ void append_token(const AppendArgs& a, int tok, int lane) {
+  using E = Elem<IN_DT>;
+  using T = typename E::T;
+  const TokAddr ta = tok_addr(a.ad, tok);
+  const int b = ta.b, pos = ta.pos, rp = ta.rope;
+  if (b < 0 || b >= a.cache_b || pos < 0 || pos >= a.cache_s || rp < 0 || rp >= a.rope_len) {
+    if (lane == 0 && a.err_flag) a.err_flag[0] = 1;
+    return;
+  }
+  const T* row = static_cast<const T*>(a.kv_in) + static_cast<int64_t>(tok) * a.in_rs;
+  const T* w = static_cast<const T*>(a.ln_w);
+  const T* bb = static_cast<const T*>(a.ln_b);
+
+  // --- LayerNorm over c[0..255]: lane owns channels 4*lane .. 4*lane+3.
+  double x[4], wt[4], bs[4], y[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = static_cast<double>(E::ld(row, 4 * lane + i));
+    wt[i] = static_cast<double>(E::ld(w, 4 * lane + i));
+    bs[i] = static_cast<double>(E::ld(bb, 4 * lane + i));
+  }
+  layernorm_quad(x, wt, bs, a.eps, y);
 
   const int64_t crow = static_cast<int64_t>(b) * a.cache_s + pos;
   if constexpr (C_DT == 0) {
@@ -142,27 +176,10 @@ __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
                            static_cast<float>(y[2]), static_cast<float>(y[3]));
     reinterpret_cast<float4*>(static_cast<float*>(a.ckv) + crow * kR)[lane] = o;
   } else if constexpr (C_DT == 1) {
-    uint2 o;
-    o.x = f64_to_bf16(y[0]) | (static_cast<uint32_t>(f64_to_bf16(y[1])) << 16);
-    o.y = f64_to_bf16(y[2]) | (static_cast<uint32_t>(f64_to_bf16(y[3])) << 16);
-    reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.ckv) + crow * kR)[lane] = o;
+    reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.ckv) + crow * kR)[lane] = encode_bf16_quad(y);
   } else {
-    // e4m3 per-token: y is first rounded to bf16 (the value a bf16 cache
-    // would hold), amax over the token, scale = max(amax,1e-12)/448.
-    float yb[4];
-    float amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      yb[i] = bf16_to_f32(f64_to_bf16(y[i]));
-      amax = fmaxf(amax, fabsf(yb[i]));
-    }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, m));
-    const float scale = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
-    uint32_t codes = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      codes |= static_cast<uint32_t>(f32_to_e4m3(__fdiv_rn(yb[i], scale))) << (8 * i);
+    float scale;
+    const uint32_t codes = encode_e4m3_quad(y, scale);
     reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.ckv) + crow * kR)[lane] = codes;
     if (lane == 0) a.ckv_scale[crow] = scale;
   }
@@ -178,6 +195,13 @@ __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
     dst[0] = E::from_f32(o1);
     dst[1] = E::from_f32(o2);
   }
+}
+
+template <int IN_DT, int C_DT>
+__global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= a.n_tok) return;
+  append_token<IN_DT, C_DT>(a, tok, threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------------------
@@ -364,6 +388,81 @@ __device__ __forceinline__ uint2 e4m3x4_to_bf16x4_hw(uint32_t w) {
   return make_uint2(a, b);
 }
 
+// ---- Fused one-token append inside the decode kernel (bf16 model).
+// Inputs of one token as loaded by one wavefront: lane owns latent channels
+// 4*lane .. +3 and (lanes 0..31) the k_pe pair `lane`; raw bf16 bits.
+struct FusedIn {
+  uint2 x, wt, bs;
+  uint32_t pe;
+  uint16_t c, s;
+};
+
+__device__ __forceinline__ FusedIn fused_load(const AppendArgs& a, int tok, int rope, int lane) {
+  const uint16_t* row = static_cast<const uint16_t*>(a.kv_in) + static_cast<int64_t>(tok) * a.in_rs;
+  const int pl = lane & (kP / 2 - 1);  // lanes 32..63 repeat pairs 0..31 (unused)
+  const int64_t tab = static_cast<int64_t>(rope) * (kP / 2) + pl;
+  FusedIn f;
+  f.x = *reinterpret_cast<const uint2*>(row + 4 * lane);
+  f.wt = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.ln_w) + 4 * lane);
+  f.bs = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.ln_b) + 4 * lane);
+  f.pe = *reinterpret_cast<const uint32_t*>(row + kR + 2 * pl);
+  f.c = static_cast<const uint16_t*>(a.cos_tab)[tab];
+  f.s = static_cast<const uint16_t*>(a.sin_tab)[tab];
+  return f;
+}
+
+// The token in cache form: `row` is the lane's four latent channels as the
+// attention reads them (bf16; for e4m3 the decoded codes), `pe` its rotated
+// k_pe pair, plus the e4m3 codes and scale.
+template <int C_DT>
+struct FusedTok {
+  uint2 row;
+  uint32_t pe, codes;
+  float scale;
+};
+
+__device__ __forceinline__ void bf16x4_to_f64(uint2 v, double o[4]) {
+  o[0] = static_cast<double>(u2f(v.x << 16));
+  o[1] = static_cast<double>(u2f(v.x & 0xFFFF0000u));
+  o[2] = static_cast<double>(u2f(v.y << 16));
+  o[3] = static_cast<double>(u2f(v.y & 0xFFFF0000u));
+}
+
+// Same arithmetic as append_token<1, C_DT>.
+template <int C_DT>
+__device__ __forceinline__ FusedTok<C_DT> fused_compute(const FusedIn& f, float eps, int lane) {
+  double x[4], wt[4], bs[4], y[4];
+  bf16x4_to_f64(f.x, x);
+  bf16x4_to_f64(f.wt, wt);
+  bf16x4_to_f64(f.bs, bs);
+  layernorm_quad(x, wt, bs, eps, y);
+  FusedTok<C_DT> t;
+  t.codes = 0;
+  t.scale = 1.f;
+  if constexpr (C_DT == 1) {
+    t.row = encode_bf16_quad(y);
+  } else {
+    t.codes = encode_e4m3_quad(y, t.scale);
+    t.row = e4m3x4_to_bf16x4_hw(t.codes);
+  }
+  float o1, o2;
+  rope_pair<1>(u2f(f.pe << 16), u2f(f.pe & 0xFFFF0000u), u2f(static_cast<uint32_t>(f.c) << 16),
+               u2f(static_cast<uint32_t>(f.s) << 16), o1, o2);
+  t.pe = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+  return t;
+}
+
+template <int C_DT>
+__device__ __forceinline__ void fused_store(const AppendArgs& a, int64_t crow, const FusedTok<C_DT>& t, int lane) {
+  if constexpr (C_DT == 1) {
+    reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.ckv) + crow * kR)[lane] = t.row;
+  } else {
+    reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.ckv) + crow * kR)[lane] = t.codes;
+    if (lane == 0) a.ckv_scale[crow] = t.scale;
+  }
+  if (lane < kP / 2) reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.kpe) + crow * kP)[lane] = t.pe;
+}
+
 // 16-byte global load marked non-temporal: the cache is streamed once, and
 // the non-temporal hint keeps it from thrashing the vector L1 (measured
 // ~10 % more read bandwidth for this kernel on MI355X).
@@ -373,7 +472,7 @@ __device__ __forceinline__ uint4 ld_stream16(const void* p) {
   return make_uint4(t.x, t.y, t.z, t.w);
 }
 
-template <int C_DT, int DEPTH>
+template <int C_DT, int DEPTH, bool FUSE>
 __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t c_lds[kCBytes];
   __shared__ __attribute__((aligned(16))) uint8_t pe_lds[kPeBytes];
@@ -402,6 +501,42 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
   const int t0 = split * chunk;
   const int t1 = min(L, t0 + chunk);
   const int n_tiles = t1 > t0 ? (t1 - t0 + kTileTok - 1) / kTileTok : 0;  // block-uniform
+
+  // Fused one-token append (FUSE): the block owning row r's last split turns
+  // the row's wkv_a output into its new cache token (position L - 1, the last
+  // token of that split), writes it to the cache at the end, and puts the
+  // computed row into LDS in place of the cache row it loaded, so no load of
+  // this launch depends on the store.  One wave (the one whose 16 tokens hold
+  // position L - 1) does the work; its input loads go out first and the
+  // arithmetic runs while the first tiles are in flight.
+  bool fa_own = false;  // block-uniform
+  int fa_w = 0, fa_k = 0;
+  TokAddr fa_t{0, 0, 0};
+  if constexpr (FUSE) {
+    if (split == (ns > 0 ? ns - 1 : 0)) {
+      fa_t = tok_addr(a.fa.ad, r);
+      if (fa_t.b < 0 || fa_t.b >= a.fa.cache_b || fa_t.pos < 0 || fa_t.pos >= a.fa.cache_s || fa_t.rope < 0 ||
+          fa_t.rope >= a.fa.rope_len) {
+        if (threadIdx.x == 0 && a.fa.err_flag) a.fa.err_flag[0] = 1;  // skipped, as mla_append does
+      } else {
+        fa_own = true;  // then L = pos + 1 <= cache_s and t1 = L
+        const int tn = fa_t.pos - t0;
+        fa_w = (tn & (kTileTok - 1)) >> 4;
+        fa_k = tn & (kSub - 1);
+      }
+    }
+  }
+  const bool fa_wave = FUSE && fa_own && w == fa_w;  // wave-uniform
+  // Every wave of a fused launch issues these loads (valid addresses: its
+  // own input row, RoPE row 0 unless it owns the append) so that no value
+  // crosses a branch: the loaded registers are consumed only by fa_wave,
+  // well after the tile loads behind them have been issued.
+  FusedIn fin;
+  if constexpr (FUSE) {
+    fin = fused_load(a.fa, r, fa_own ? fa_t.rope : 0, lane);
+    // keep these loads ahead of the tile loads (they are waited for first)
+    asm volatile("" ::: "memory");
+  }
 
   // Loads are issued unconditionally, so every address is clamped to a valid
   // cache element: an invalid or empty row reads row 0, token 0.
@@ -468,6 +603,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
     // Q leaves every tile load in flight.
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) load_tile(d, kt[d]);
+    // the fused append's arithmetic below must not pull these loads after it
+    if constexpr (FUSE) asm volatile("" ::: "memory");
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const uint32_t wv_in[4] = {raw[s].x, raw[s].y, raw[s].z, raw[s].w};
@@ -485,6 +622,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
       qb[8 + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
     }
   }
+
+  // The new token in cache form (fused append), computed while the first
+  // tiles load.
+  FusedTok<C_DT> ftok;
+  if constexpr (FUSE)
+    if (fa_wave) ftok = fused_compute<C_DT>(fin, a.fa.eps, lane);
 
   f32x4_t oacc[4];
 #pragma unroll
@@ -531,6 +674,23 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
     *reinterpret_cast<uint4*>(pe_st + 8 * kPeRow) = kt.p[1];
     float4 scv = make_float4(1.f, 1.f, 1.f, 1.f);
     if constexpr (C_DT == 2) scv = kt.sc;
+    if constexpr (FUSE) {
+      if (fa_wave && j == n_tiles - 1) {
+        // The new token's row: the computed values replace what was loaded
+        // (this wave's own rows, so its reads below see them in order).
+        *reinterpret_cast<uint2*>(c_lds + (kSub * w + fa_k) * kCRow + 8 * lane) = ftok.row;
+        if (lane < kP / 2) *reinterpret_cast<uint32_t*>(pe_lds + (kSub * w + fa_k) * kPeRow + 4 * lane) = ftok.pe;
+        if constexpr (C_DT == 2) {
+          if (g == (fa_k >> 2)) {
+            const int i = fa_k & 3;
+            scv.x = i == 0 ? ftok.scale : scv.x;
+            scv.y = i == 1 ? ftok.scale : scv.y;
+            scv.z = i == 2 ? ftok.scale : scv.z;
+            scv.w = i == 3 ? ftok.scale : scv.w;
+          }
+        }
+      }
+    }
 
     // The registers of kt are free: refill them with the tile DEPTH ahead
     // (unconditionally, see above).
@@ -637,6 +797,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
 #pragma unroll
   for (int d = 0; d < DEPTH - 1; ++d)
     if (it + d < n_tiles) process(it + d, kt[d]);
+
+  if constexpr (FUSE)
+    if (fa_wave) fused_store<C_DT>(a.fa, static_cast<int64_t>(fa_t.b) * a.fa.cache_s + fa_t.pos, ftok, lane);
 
   // ---- Sum of the weights per head over the four waves.
   float l_w = l_part + shfl_xor_f32(l_part, 16);
@@ -812,9 +975,16 @@ constexpr int kDecodeDepth = SWAMLA_DECODE_DEPTH;  // tiles of loads in flight p
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
   const dim3 grid(a.n_splits, a.n_rows);
-  if (dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth>), grid, dim3(256), 0, s, a);
-  else if (dt == 1 && c_dt == 2) hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth>), grid, dim3(256), 0, s, a);
-  else if (dt == 0 && c_dt == 0) hipLaunchKernelGGL(mla_decode_f32, grid, dim3(256), 0, s, a);
+  const bool fuse = a.fa.kv_in != nullptr;
+  if (dt == 1 && c_dt == 1 && !fuse)
+    hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, false>), grid, dim3(256), 0, s, a);
+  else if (dt == 1 && c_dt == 2 && !fuse)
+    hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, false>), grid, dim3(256), 0, s, a);
+  else if (dt == 1 && c_dt == 1)
+    hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, true>), grid, dim3(256), 0, s, a);
+  else if (dt == 1 && c_dt == 2)
+    hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, true>), grid, dim3(256), 0, s, a);
+  else if (dt == 0 && c_dt == 0 && !fuse) hipLaunchKernelGGL(mla_decode_f32, grid, dim3(256), 0, s, a);
   else return -1;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }

@@ -204,6 +204,20 @@ class DecodeWorkspace:
         return self.o_part.shape[0] >= n_rows and self.o_part.shape[1] == n_splits
 
 
+@dataclass
+class FusedAppend:
+    """The append that decode_attention folds into its launch for a one-token
+    step: row r's new token ``kv[r]`` ([rows, >=R+P] bf16, unit last stride,
+    the wkv_a output) goes through kv_norm (``ln_w``, ``ln_b``, ``eps``) and
+    RoPE and is written at ``start_pos[r]`` before row r attends."""
+
+    kv: torch.Tensor
+    ln_w: torch.Tensor
+    ln_b: torch.Tensor
+    eps: float
+    err_flag: Optional[torch.Tensor] = None
+
+
 def decode_attention(
     q_abs: torch.Tensor,
     q_pe: torch.Tensor,
@@ -224,6 +238,7 @@ def decode_attention(
     workspace: Optional[DecodeWorkspace] = None,
     lse_out: Optional[torch.Tensor] = None,
     merge: bool = True,
+    append: Optional[FusedAppend] = None,
 ) -> torch.Tensor:
     """Absorbed attention of query rows over the latent cache (+ merge).
 
@@ -234,8 +249,11 @@ def decode_attention(
     buffer).  With more than one split, mla_merge runs after the decode
     kernel (and writes the log-sum-exp to ``lse_out`` if given) unless
     ``merge`` is False: then rows with several splits leave their partials in
-    ``workspace`` for merge_project.
-    Reference: models/mla.py:417-487.
+    ``workspace`` for merge_project.  With ``append`` (bf16, dense
+    addressing, one row per sequence) the step's new tokens are appended in
+    the same launch (mla_decode_attn_append); the result equals append()
+    followed by this call.
+    Reference: models/mla.py:417-487 (and :307-323, :409-414 with append).
     """
     cache.validate()
     dev = _need_gpu(q_abs, q_pe, cos_tab, sin_tab, cache.ckv, row_seq, kv_len, q_rope_pos, start_pos)
@@ -260,21 +278,49 @@ def decode_attention(
             raise ValueError("workspace too small for (rows, n_splits)")
     lib = _abi.lib()
     stream = _abi.stream_handle(dev)
-    _abi.check(
-        lib.mla_decode_attn(
-            q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1),
-            q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
-            cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
-            cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
-            cache.ckv.shape[0], cache.ckv.shape[1],
-            p_seq, p_len, p_rope, p_sp, int(rows_per_seq), int(bool(rope_abs)),
-            rows, H, R, P, float(sm_scale), n_splits, min_chunk,
-            _abi.ptr(workspace.o_part if workspace else None),
-            _abi.ptr(workspace.lse_part if workspace else None),
-            out.data_ptr(), out.stride(0), out.stride(1),
-            _abi.dtype_code(dt), cache.cache_code, stream,
+    if append is not None:
+        kv, ln_w, ln_b = append.kv, append.ln_w, append.ln_b
+        if start_pos is None or rows_per_seq != 1:
+            raise ValueError("a fused append needs dense addressing with one row per sequence")
+        if kv.dim() != 2 or kv.shape[0] != rows or kv.shape[1] < R + P or kv.stride(1) != 1:
+            raise ValueError("append.kv must be [rows, >=R+P] with unit last-dim stride")
+        if kv.dtype != dt or ln_w.dtype != dt or ln_b.dtype != dt:
+            raise TypeError(f"append tensors must be {dt}")
+        if not (ln_w.is_contiguous() and ln_b.is_contiguous() and ln_w.numel() == R and ln_b.numel() == R):
+            raise ValueError("LayerNorm weight / bias must be contiguous [R]")
+        _need_gpu(kv, ln_w, ln_b, append.err_flag)
+        _abi.check(
+            lib.mla_decode_attn_append(
+                kv.data_ptr(), kv.stride(0), ln_w.data_ptr(), ln_b.data_ptr(), float(append.eps),
+                _abi.ptr(append.err_flag),
+                q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1),
+                q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
+                cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+                cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
+                cache.ckv.shape[0], cache.ckv.shape[1], p_sp, int(bool(rope_abs)),
+                rows, H, R, P, float(sm_scale), n_splits, min_chunk,
+                _abi.ptr(workspace.o_part if workspace else None),
+                _abi.ptr(workspace.lse_part if workspace else None),
+                out.data_ptr(), out.stride(0), out.stride(1),
+                _abi.dtype_code(dt), cache.cache_code, stream,
+            )
         )
-    )
+    else:
+        _abi.check(
+            lib.mla_decode_attn(
+                q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1),
+                q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
+                cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+                cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
+                cache.ckv.shape[0], cache.ckv.shape[1],
+                p_seq, p_len, p_rope, p_sp, int(rows_per_seq), int(bool(rope_abs)),
+                rows, H, R, P, float(sm_scale), n_splits, min_chunk,
+                _abi.ptr(workspace.o_part if workspace else None),
+                _abi.ptr(workspace.lse_part if workspace else None),
+                out.data_ptr(), out.stride(0), out.stride(1),
+                _abi.dtype_code(dt), cache.cache_code, stream,
+            )
+        )
     if n_splits > 1 and merge:
         _abi.check(
             lib.mla_merge(

@@ -388,17 +388,24 @@ class MLA(nn.Module):
             q, kv = self.input_projections(x)
 
         cos, sin = self.rope.half_tables()
-        kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
-                       start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
+        # A one-token step appends inside the attention launch; longer chunks
+        # append first (their rows attend to each other's new tokens).
+        fold_append = fused and T == 1
+        if not fold_append:
+            kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
+                           start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
 
         n_splits, min_chunk = self._split_plan(n, max_len, dev)
         if fused:
             o_lat = torch.empty(n, H, R, dtype=x.dtype, device=dev)
             ws = self._workspace_for(n, n_splits, dev)
+            fa = None
+            if fold_append:
+                fa = kernels.FusedAppend(kv, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps)
             kernels.decode_attention(
                 q_abs, q_pe, cos, sin, cache, self.softmax_scale,
                 start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
-                out=o_lat, workspace=ws, merge=False,
+                out=o_lat, workspace=ws, merge=False, append=fa,
             )
             # o[r, h*Dv + d] = W_uv[h][d] . merged o_lat[r, h]: split merge and
             # read-out in one launch, written straight in wo's input layout

@@ -117,6 +117,45 @@ def test_decode_rejects(lib, kw, code):
     assert lib.mla_last_error().decode()
 
 
+def _decode_append(lib, **kw):
+    args = dict(kv_in=FAKE, in_rs=320, w=FAKE, b=FAKE, eps=1e-5, err=None,
+                qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, cos=FAKE, sin=FAKE,
+                rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, sp=FAKE, rope_abs=0, n_rows=2,
+                H=16, R=256, P=64, sm=0.07, ns=1, mc=64, o_part=None, lse=None, o=FAKE, o_rs=4096, o_hs=256,
+                dt=1, c_dt=1, stream=None)
+    args.update(kw)
+    return lib.mla_decode_attn_append(*args.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(dt=0, c_dt=0), -2),  # fp32 models keep the separate append
+        (dict(c_dt=0), -2),
+        (dict(H=8), -2),
+        (dict(sp=None), -1),  # dense addressing only
+        (dict(kv_in=None), -1),
+        (dict(w=None), -1),
+        (dict(in_rs=300), -1),
+        (dict(kv_in=FAKE + 4), -3),
+        (dict(in_rs=322), -3),
+        (dict(w=FAKE + 2), -3),
+        (dict(c_dt=2), -1),  # fp8 without a scale buffer
+        (dict(ns=4), -1),
+        (dict(o=None), -1),
+        (dict(rope_abs=3), -1),
+        (dict(qa=FAKE + 4), -3),
+    ],
+)
+def test_decode_append_rejects(lib, kw, code):
+    assert _decode_append(lib, **kw) == code
+    assert "mla_decode_attn_append" in lib.mla_last_error().decode() or code == -2
+
+
+def test_decode_append_zero_rows_is_a_noop(lib):
+    assert _decode_append(lib, n_rows=0, kv_in=None, qa=None, qp=None) == 0
+
+
 def _merge(lib, **kw):
     args = dict(o_part=FAKE, lse=FAKE, kv_len=FAKE, sp=None, T=1, n_rows=2, H=16, R=256, ns=4, mc=64, o=FAKE,
                 o_rs=4096, o_hs=256, lse_out=None, dt=1, stream=None)
