@@ -4,9 +4,10 @@
 Workload: one MLA layer geometry (n_embd 1024, 16
 heads, kv_lora_rank 256, rope 64, nope 128, v 128), bf16, batch 32, every
 sequence pre-filled to 4096 cached tokens by the append path on N(0,1)
-hidden states, then K decode steps of append + attention through the drop-in
-``swamla_amd.MLA.forward`` (GEMMs in ATen, append / attention / merge in the
-HIP kernels), captured as one HIP graph per step.
+hidden states, then K decode steps through the drop-in
+``swamla_amd.MLA.forward``, captured as one HIP graph per step: four HIP
+launches (stacked input product, one-token append + decode attention, split
+merge + W_uv read-out, wo).
 
 One layer's cache (86.5 MB) fits MI355X's 256 MB Infinity Cache, so a single
 layer decoded back to back would be served from there, not from HBM.  The
@@ -15,13 +16,14 @@ cache: 8 x 86.5 MB by default), like a decoder stack, and counts each token
 once per layer it passes: value = batch * steps * layers / seconds
 ("layer-token decodes per second"); ms_per_step is per layer-step.
 
-roofline: the decode-attention kernel (mla_decode_mfma, split-KV), timed with
-HIP events on its stream around back-to-back launches rotating over the
-layers' caches (each launch does its full work; the split merge, a separate
-small kernel, is timed the same way and reported beside it);
-achieved = algorithmic bytes per launch / average launch duration, with
-bytes = sum_b L_b*(R+P)*2 (latent + rope cache) + B*H*(R+P)*2 (queries) +
-B*H*R*2 (latent outputs).
+roofline: the step's attention launch (mla_decode_attn_append: the decode
+kernel with the one-token append folded in, split-KV), timed with HIP events
+on its stream around back-to-back launches rotating over the layers' caches
+(each launch does its full work; the stand-alone split merge is timed the
+same way and reported beside it); achieved = algorithmic bytes per launch /
+average launch duration, with bytes = sum_b L_b*(R+P)*2 (latent + rope
+cache) + B*H*(R+P)*2 (queries) + B*H*R*2 (latent outputs) + the append's
+B*(R+P)*2 read and B*(R+P)*2 written (+ LayerNorm parameters).
 
 cpu_baseline: the oracle's op-for-op CPU restatement of the reference MLA
 (oracle/mla_ref.py, which re-projects the cache and runs SDPA exactly as
@@ -139,6 +141,12 @@ def attention_bytes_rows(lens, fp8: bool) -> int:
     return int(lens.sum()) * per_tok + B * H * (R + P) * 2 + B * H * R * 2
 
 
+def append_bytes(B: int, fp8: bool) -> int:
+    """Algorithmic bytes of a one-token append of B rows: the wkv_a rows and
+    LayerNorm parameters read, the cache tokens (and e4m3 scales) written."""
+    return B * ((R + P) * 2 + R * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0)) + 2 * R * 2
+
+
 def init_linear_weights(module, seed: int, torch) -> None:
     """N(0, 0.02) Linear weights in parameter order from a CPU generator and
     zero biases; LayerNorm stays at weight 1 / bias 0, as the reference model
@@ -191,6 +199,7 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
             q = m.wq(x).view(B, H, -1)
             w_uk, _ = m.absorbed_weights()
             q_abs = torch.bmm(q[:, :, :128].transpose(0, 1).contiguous(), w_uk)  # [H, B, R]
+            kv = m.wkv_a(x).view(B, -1)  # the step's new tokens (wkv_a output rows)
             cache = m.latent_cache()
             L = int(lens.max())
             sp = (lens - 1).to(device=dev, dtype=torch.int32)  # row b attends [0, lens[b])
@@ -199,18 +208,21 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
             o_lat = torch.empty(H, B, R, dtype=torch.bfloat16, device=dev)
             cos, sin = m.rope.half_tables()
             qa, qp, ol = q_abs.transpose(0, 1), q[:, :, 128:], o_lat.transpose(0, 1)
+            # the step's attention launch: one-token append folded into decode
             dargs = (
+                kv.data_ptr(), kv.stride(0), m.kv_norm.weight.data_ptr(), m.kv_norm.bias.data_ptr(),
+                float(m.kv_norm.eps), None,
                 qa.data_ptr(), qa.stride(0), qa.stride(1), qp.data_ptr(), qp.stride(0), qp.stride(1),
                 cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
-                cache.ckv.shape[0], cache.ckv.shape[1], None, None, None, sp.data_ptr(), 1, 0,
+                cache.ckv.shape[0], cache.ckv.shape[1], sp.data_ptr(), 0,
                 B, H, R, P, float(m.softmax_scale), n_splits, min_chunk,
                 ws.o_part.data_ptr(), ws.lse_part.data_ptr(),
                 ol.data_ptr(), ol.stride(0), ol.stride(1), _abi.DTYPE_BF16, cache.cache_code, h,
             )
             margs = (ws.o_part.data_ptr(), ws.lse_part.data_ptr(), None, sp.data_ptr(), 1, B, H, R, n_splits,
                      min_chunk, ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16, h)
-            preps.append((dargs, (q, q_abs, sp, ws, o_lat, cos, sin), L, B, n_splits, margs))
+            preps.append((dargs, (q, q_abs, kv, sp, ws, o_lat, cos, sin), L, B, n_splits, margs))
 
     def run(indices, reps, which=0):
         e0 = torch.cuda.Event(enable_timing=True)
@@ -219,7 +231,7 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
         for _ in range(reps):
             for i in indices:
                 if which == 0:
-                    _abi.check(lib.mla_decode_attn(*preps[i][0]))
+                    _abi.check(lib.mla_decode_attn_append(*preps[i][0]))
                 else:
                     _abi.check(lib.mla_merge(*preps[i][5]))
         e1.record(stream)
@@ -362,7 +374,7 @@ def main() -> int:
 
     lens = lens0 + args.steps  # lengths after the timed steps
     cold_us, warm_us, merge_us, L, B, n_splits = time_decode_kernel(layers, xs, lens, args, dev, torch)
-    abytes = attention_bytes_rows(lens, fp8)
+    abytes = attention_bytes_rows(lens, fp8) + append_bytes(B, fp8)
     traffic, traffic_src = measured_traffic(B, L, args.cache) if not args.ragged else (None, None)
     achieved = abytes / (cold_us * 1e-6) / 1e9
     warm = abytes / (warm_us * 1e-6) / 1e9
@@ -371,7 +383,7 @@ def main() -> int:
     # algorithmic bytes of one full layer-step (attention + append + weights), mean context
     w_bytes = sum(p.numel() * p.element_size() for p in layers[0].parameters())
     mid = lens0 + (args.steps + 1) // 2
-    step_bytes = attention_bytes_rows(mid, fp8) + w_bytes + args.batch * (R + P) * 2 * 2
+    step_bytes = attention_bytes_rows(mid, fp8) + w_bytes + append_bytes(args.batch, fp8)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -399,12 +411,14 @@ def main() -> int:
             "heads": H, "kv_lora_rank": R, "rope_dim": P, "cache": args.cache,
             "layers_rotated": len(layers),
             "value_counts": "tokens x layers per second (each token counted once per MLA layer)",
-            "step": "full drop-in MLA.forward (wq, wkv_a, append, absorption bmm, decode, merge, "
-                    "W_uv bmm, wo) as one HIP graph per layer-step",
+            "step": "full drop-in MLA.forward as one HIP graph per layer-step: stacked input product "
+                    "(wq with W_uk absorbed, wkv_a), append + decode attention, split merge + W_uv, wo "
+                    "(four launches)",
         },
         "hbm_gbs_step": step_bytes / (ms_per_step * 1e-3) / 1e9,
         "roofline": {
-            "kernel": "mla_decode_mfma (split-KV decode attention)",
+            "kernel": "mla_decode_mfma, fused-append instance (mla_decode_attn_append: one-token append + "
+                      "split-KV decode attention)",
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
