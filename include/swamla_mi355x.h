@@ -203,6 +203,32 @@ int mla_linear(const void* x, int64_t x_rs, int64_t x_bs, const void* w,
                int32_t K, int32_t batch, int32_t dtype, void* stream);
 
 /*
+ * mla_pack_weight — lays a [N, K] row-major weight out for
+ * mla_linear_packed (no reference counterpart: a one-time re-layout of the
+ * weights of wq / wkv_a (stacked) and wo, models/mla.py:281-288, :307,
+ * :490-495).  Packed element (n, k) sits at
+ *   (((n / 8) * (K / 64) + k / 64) * 8 + (k % 64) / 8) * 64 + (n % 8) * 8 + k % 8,
+ * i.e. 1 KB tiles of 8 rows x 64 k, each read whole by one wavefront load.
+ * w_packed holds N*K elements.  bf16; N a multiple of 8, K of 64; 16-byte
+ * aligned bases, w_rs a multiple of 8 elements.
+ */
+int mla_pack_weight(const void* w, int64_t w_rs, int32_t N, int32_t K,
+                    void* w_packed, int32_t dtype, void* stream);
+
+/*
+ * mla_linear_packed — y[m][n] = sum_k x[m][k] * w[n][k] (+ bias[n]) with w
+ * packed by mla_pack_weight; bf16 in / out, fp32 accumulation, one rounding
+ * per output.  Replaces the decode step's two large products: the stacked
+ * wq / wkv_a product (models/mla.py:281-288, :307, with W_uk absorbed) and
+ * wo (:490-495).
+ * Limits: 0 <= M <= 128, N a multiple of 8, K in {512, 1024, 1536, 2048};
+ * x and w_packed 16-byte aligned, x_rs a multiple of 8; y_rs >= N.
+ */
+int mla_linear_packed(const void* x, int64_t x_rs, const void* w_packed,
+                      const void* bias, void* y, int64_t y_rs, int32_t M,
+                      int32_t N, int32_t K, int32_t dtype, void* stream);
+
+/*
  * mla_merge_project — split-KV merge fused with the W_uv read-out:
  *   y[r][h][d] = sum_c W_uv[h][d][c] * o_lat[r][h][c],
  * where o_lat is the log-sum-exp merge of the mla_decode_attn partials

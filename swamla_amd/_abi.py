@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "mla_merge",
     "mla_split_count",
     "mla_linear",
+    "mla_pack_weight",
+    "mla_linear_packed",
     "mla_merge_project",
     "mla_host_f32_to_e4m3",
     "mla_host_e4m3_to_f32",
@@ -89,6 +91,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_merge.argtypes = [
         _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I32, _P,
     ]
+    lib.mla_pack_weight.restype = ctypes.c_int
+    lib.mla_pack_weight.argtypes = [_P, _I64, _I32, _I32, _P, _I32, _P]
+    lib.mla_linear_packed.restype = ctypes.c_int
+    lib.mla_linear_packed.argtypes = [_P, _I64, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]
     lib.mla_linear.restype = ctypes.c_int
     lib.mla_linear.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P,

@@ -316,6 +316,44 @@ int mla_linear(const void* x, int64_t x_rs, int64_t x_bs, const void* w, int64_t
   return ok();
 }
 
+int mla_pack_weight(const void* w, int64_t w_rs, int32_t N, int32_t K, void* w_packed, int32_t dtype,
+                    void* stream) {
+  if (dtype != SWAMLA_DTYPE_BF16)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "mla_pack_weight: dtype %d not built (bf16 only)", dtype);
+  if (N < 0 || N % 8 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_pack_weight: N=%d is not a multiple of 8", N);
+  if (K < 0 || K % 64 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_pack_weight: K=%d is not a multiple of 64", K);
+  if (N == 0 || K == 0) return ok();
+  if (!w || !w_packed) return fail(SWAMLA_ERR_INVALID_ARG, "mla_pack_weight: null pointer");
+  if (w_rs < K) return fail(SWAMLA_ERR_INVALID_ARG, "mla_pack_weight: row stride %lld < K=%d", (long long)w_rs, K);
+  if (!aligned(w, 16) || !aligned(w_packed, 16) || w_rs % 8 != 0)
+    return fail(SWAMLA_ERR_MISALIGNED, "mla_pack_weight: 16-byte aligned bases and a row stride that is a "
+                "multiple of 8 are required");
+  swamla::PackWeightArgs a{w, w_rs, w_packed, N, K};
+  if (swamla::launch_pack_weight(a, static_cast<hipStream_t>(stream)) != 0) return hip_fail("mla_pack_weight");
+  return ok();
+}
+
+int mla_linear_packed(const void* x, int64_t x_rs, const void* w_packed, const void* bias, void* y, int64_t y_rs,
+                      int32_t M, int32_t N, int32_t K, int32_t dtype, void* stream) {
+  const char* fn = "mla_linear_packed";
+  if (dtype != SWAMLA_DTYPE_BF16) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: dtype %d not built (bf16 only)", fn, dtype);
+  if (M < 0 || M > 128) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: M=%d outside [0, 128]", fn, M);
+  if (N < 0 || N % 8 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: N=%d is not a multiple of 8", fn, N);
+  if (K != 512 && K != 1024 && K != 1536 && K != 2048)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "%s: K=%d (built: 512, 1024, 1536, 2048)", fn, K);
+  if (M == 0 || N == 0) return ok();
+  if (!x || !w_packed || !y) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null x / w_packed / y", fn);
+  if (x_rs < K || y_rs < N) return fail(SWAMLA_ERR_INVALID_ARG, "%s: row strides must cover K (x) and N (y)", fn);
+  if (!aligned(x, 16) || !aligned(w_packed, 16) || x_rs % 8 != 0 || !aligned(y, 2) || (bias && !aligned(bias, 2)))
+    return fail(SWAMLA_ERR_MISALIGNED, "%s: x and w_packed need 16-byte aligned bases and x a row stride that is "
+                "a multiple of 8", fn);
+  swamla::PackedLinearArgs a{x, x_rs, w_packed, bias, y, y_rs, M, N, K};
+  const int rc = swamla::launch_linear_packed(a, static_cast<hipStream_t>(stream));
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for M=%d K=%d", fn, M, K);
+  if (rc != 0) return hip_fail(fn);
+  return ok();
+}
+
 int mla_merge_project(const float* o_part, const float* lse_part, const void* o_lat, int64_t o_rs,
                       int64_t o_hs, const int32_t* kv_len, const int32_t* row_seq,
                       const int32_t* start_pos, int32_t rows_per_seq, int64_t cache_batch,

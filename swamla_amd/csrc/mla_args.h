@@ -107,7 +107,27 @@ struct MergeProjectArgs {
 int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s);
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s);
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s);
+// Product with a packed weight (see mla_pack_weight): Y = X . W^T (+ bias).
+struct PackedLinearArgs {
+  const void* x;
+  int64_t x_rs;
+  const void* wp;  // packed W
+  const void* bias;
+  void* y;
+  int64_t y_rs;
+  int M, N, K;
+};
+
+struct PackWeightArgs {
+  const void* w;
+  int64_t w_rs;
+  void* wp;
+  int N, K;
+};
+
 int launch_linear(const LinearArgs& a, int batch, hipStream_t s);
+int launch_linear_packed(const PackedLinearArgs& a, hipStream_t s);
+int launch_pack_weight(const PackWeightArgs& a, hipStream_t s);
 int launch_merge_project(const MergeProjectArgs& a, hipStream_t s);
 
 }  // namespace swamla

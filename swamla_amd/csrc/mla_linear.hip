@@ -29,6 +29,13 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// 16-byte global load marked non-temporal (weights are streamed once).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+
 // K steps of 32 whose loads are issued together: eight for up to 32 rows,
 // fewer for more row tiles so the staged operands stay within the registers.
 template <int MT>
@@ -230,6 +237,141 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
   }
 }
 
+// ---------------------------------------------------------------------------
+// Packed-weight product for the decode step's two large products (the
+// stacked input product and wo): Y[m, n] = sum_k X[m, k] W[n, k] (+ bias[n]).
+//
+// The weight is packed once per weight version (mla_pack_weight) into 1 KB
+// tiles P[o][kb][c][r][e] = W[8o + r][64kb + 8c + e]: an "octet" of 8 output
+// rows times 64 k.  One 16-byte load per lane reads a whole tile, i.e. eight
+// complete 128-byte lines, and lane l = 8c + r holds row r, k chunk c, which
+// is directly an MFMA B operand: for mfma_f32_16x16x32_bf16 lane l is column
+// j = l % 16 with k group g = l / 16, so column j holds W row j % 8 at k chunk
+// 2g + j / 8.  Columns 0..7 therefore see the even k chunks of rows 0..7 and
+// columns 8..15 the odd chunks of the same rows; two MFMAs per tile, one with
+// X's even chunks and one with its odd chunks as the A operand, give the
+// even and odd halves of each output in separate accumulators, added at the
+// end.
+//
+// Block (bx, slab): X rows [MS*slab, +MS) staged once in LDS with whole-line
+// loads, and the block's octets [o0, o1) (at most OPB); the 8 waves split K
+// (wave w: k blocks [w*KQ, (w+1)*KQ)).  One block per CU: every CU reads X
+// once and an equal share of W.  The waves' partial sums meet in LDS and are
+// added in a fixed order (even + odd half per wave, waves 0..7), then the
+// bias; one rounding to bf16.
+// ---------------------------------------------------------------------------
+constexpr int kPkWaves = 8;
+
+template <int MS, int KQ, int OPB>
+__global__ __launch_bounds__(kPkWaves * 64) void mla_linear_packed_kernel(PackedLinearArgs a, int n_oct, int gx) {
+  constexpr int K = kPkWaves * 64 * KQ;
+  constexpr int XS = 2 * K + 16;  // LDS row pitch (bytes): 8 rows of a read pass hit distinct banks
+  constexpr int MT = MS / 16;
+  constexpr int RS = 16 * OPB;    // partial-sum row pitch (floats)
+  constexpr int kLds = MS * XS > kPkWaves * MS * RS * 4 ? MS * XS : kPkWaves * MS * RS * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t xl[kLds];  // X, then the partial sums
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int slab = blockIdx.y;
+  const int o0 = static_cast<int>(static_cast<int64_t>(blockIdx.x) * n_oct / gx);
+  const int o1 = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * n_oct / gx);
+
+  // X rows of the slab, 16 bytes per thread and load (rows past M repeat the
+  // last row; their results are dropped).
+  constexpr int kRowB = 2 * K;
+  constexpr int XPT = MS * kRowB / (kPkWaves * 64 * 16);
+  uint4 xv[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int f = (i * kPkWaves * 64 + static_cast<int>(threadIdx.x)) * 16;
+    const int row = f / kRowB, col = f - row * kRowB;
+    const int srow = min(MS * slab + row, a.M - 1);
+    xv[i] = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.x) + srow * a.x_rs * 2 + col);
+  }
+  // W tiles of this wave (octets past o1 - 1 repeat the last one; dropped).
+  uint4 wv[OPB][KQ];
+#pragma unroll
+  for (int o = 0; o < OPB; ++o) {
+    const int oc = min(o0 + o, o1 - 1);
+    const uint16_t* p = static_cast<const uint16_t*>(a.wp) +
+                        (static_cast<int64_t>(oc) * (K / 64) + w * KQ) * 512 + 8 * lane;
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) wv[o][q] = ld_stream16(p + 512 * q);
+  }
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int f = (i * kPkWaves * 64 + static_cast<int>(threadIdx.x)) * 16;
+    const int row = f / kRowB, col = f - row * kRowB;
+    *reinterpret_cast<uint4*>(xl + row * XS + col) = xv[i];
+  }
+  __syncthreads();
+
+  const int j = lane & 15, g = lane >> 4;
+  f32x4_t acc[OPB][MT][2];
+#pragma unroll
+  for (int o = 0; o < OPB; ++o)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[o][mt][0] = acc[o][mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < KQ; ++q) {
+    const int kb = w * KQ + q;
+    // A: X[16mt + j][64kb + 16g + 8h .. +8], h = 0 (even chunk) / 1 (odd)
+    uint4 av[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        av[mt][h] = *reinterpret_cast<const uint4*>(xl + (16 * mt + j) * XS + 2 * (64 * kb + 16 * g + 8 * h));
+#pragma unroll
+    for (int o = 0; o < OPB; ++o)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          acc[o][mt][h] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[mt][h]), as_bf16x8(wv[o][q]), acc[o][mt][h], 0, 0, 0);
+  }
+  __syncthreads();  // X is no longer read: its LDS takes the partial sums
+
+  // part[w][row][16o + j]: lanes j < 8 keep the even half of output column
+  // 8o + j, lanes j >= 8 the odd half of column 8o + j - 8 (D lane layout:
+  // column j, rows 4g + i).
+  float* part = reinterpret_cast<float*>(xl);
+#pragma unroll
+  for (int o = 0; o < OPB; ++o)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        part[(w * MS + 16 * mt + 4 * g + i) * RS + 16 * o + j] = j < 8 ? acc[o][mt][0][i] : acc[o][mt][1][i];
+  __syncthreads();
+  const int nco = 8 * (o1 - o0);
+  const uint16_t* bias = static_cast<const uint16_t*>(a.bias);
+  for (int e = threadIdx.x; e < MS * nco; e += kPkWaves * 64) {
+    const int r = e / nco, c = e - r * nco;
+    const int row = MS * slab + r;
+    const int sc = 16 * (c >> 3) + (c & 7);
+    if (row < a.M) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < kPkWaves; ++k) v += part[(k * MS + r) * RS + sc] + part[(k * MS + r) * RS + sc + 8];
+      if (bias) v += bf16_to_f32(bias[8 * o0 + c]);
+      static_cast<uint16_t*>(a.y)[row * a.y_rs + 8 * o0 + c] = f32_to_bf16(v);
+    }
+  }
+}
+
+// Packing: thread -> 8 consecutive k of one row (one 16-byte load and store).
+__global__ __launch_bounds__(256) void mla_pack_weight_kernel(PackWeightArgs a) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int kc = a.K / 8;
+  if (t >= static_cast<int64_t>(a.N) * kc) return;
+  const int n = static_cast<int>(t / kc), k = 8 * static_cast<int>(t - static_cast<int64_t>(n) * kc);
+  const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.w) + n * a.w_rs + k);
+  const int64_t dst = ((static_cast<int64_t>(n >> 3) * (a.K / 64) + (k >> 6)) * 8 + ((k >> 3) & 7)) * 64 + (n & 7) * 8;
+  *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.wp) + dst) = v;
+}
+
 }  // namespace
 
 template <int NW>
@@ -253,6 +395,62 @@ int launch_linear(const LinearArgs& a, int batch, hipStream_t s) {
   // each wave's K range must be a whole number of 32-wide steps
   if (a.K >= 1024 && a.K % 256 == 0) launch_linear_nw<8>(a, grid, mt, s);
   else launch_linear_nw<4>(a, grid, mt, s);  // K is a multiple of 128 (checked by the caller)
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// Rows per slab: as many as keep enough blocks for every CU busy while the
+// staged X fits the 160 KB of LDS.
+int packed_slab_rows(int M, int N, int K) {
+  if (K <= 1024 && M > 32) return 64;
+  if (K <= 1024 || (K <= 2048 && N / 8 >= 256)) return M > 16 ? 32 : 16;
+  return 16;
+}
+
+template <int MS, int KQ>
+int launch_packed_ms(const PackedLinearArgs& a, int n_oct, int gx, int slabs, hipStream_t s) {
+  const int opb = (n_oct + gx - 1) / gx;
+  const dim3 grid(gx, slabs), block(kPkWaves * 64);
+  switch (opb) {
+    case 1: hipLaunchKernelGGL((mla_linear_packed_kernel<MS, KQ, 1>), grid, block, 0, s, a, n_oct, gx); break;
+    case 2: hipLaunchKernelGGL((mla_linear_packed_kernel<MS, KQ, 2>), grid, block, 0, s, a, n_oct, gx); break;
+    case 3: hipLaunchKernelGGL((mla_linear_packed_kernel<MS, KQ, 3>), grid, block, 0, s, a, n_oct, gx); break;
+    case 4: hipLaunchKernelGGL((mla_linear_packed_kernel<MS, KQ, 4>), grid, block, 0, s, a, n_oct, gx); break;
+    default: return -1;
+  }
+  return 0;
+}
+
+template <int MS>
+int launch_packed_k(const PackedLinearArgs& a, int n_oct, int gx, int slabs, hipStream_t s) {
+  switch (a.K) {
+    case 512: return launch_packed_ms<MS, 1>(a, n_oct, gx, slabs, s);
+    case 1024: return launch_packed_ms<MS, 2>(a, n_oct, gx, slabs, s);
+    case 1536: if constexpr (MS <= 32) return launch_packed_ms<MS, 3>(a, n_oct, gx, slabs, s); else return -1;
+    case 2048: if constexpr (MS <= 32) return launch_packed_ms<MS, 4>(a, n_oct, gx, slabs, s); else return -1;
+    default: return -1;
+  }
+}
+
+int launch_linear_packed(const PackedLinearArgs& a, hipStream_t s) {
+  if (a.M == 0 || a.N == 0) return 0;
+  const int MS = packed_slab_rows(a.M, a.N, a.K);
+  const int slabs = (a.M + MS - 1) / MS;
+  const int n_oct = a.N / 8;
+  int gx = (256 + slabs - 1) / slabs;      // about one block per CU
+  gx = max(gx, (n_oct + 3) / 4);           // at most four octets per block
+  gx = min(gx, n_oct);
+  int rc;
+  if (MS == 16) rc = launch_packed_k<16>(a, n_oct, gx, slabs, s);
+  else if (MS == 32) rc = launch_packed_k<32>(a, n_oct, gx, slabs, s);
+  else rc = launch_packed_k<64>(a, n_oct, gx, slabs, s);
+  if (rc) return rc;
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_pack_weight(const PackWeightArgs& a, hipStream_t s) {
+  const int64_t n = static_cast<int64_t>(a.N) * (a.K / 8);
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(mla_pack_weight_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -381,6 +381,65 @@ def linear(
     return out[0] if squeeze else out
 
 
+PACKED_K = (512, 1024, 1536, 2048)
+
+
+@dataclass
+class PackedWeight:
+    """A [N, K] bf16 weight in mla_pack_weight's 1 KB-tile layout (flat
+    storage of N*K elements)."""
+
+    data: torch.Tensor
+    N: int
+    K: int
+
+
+def packed_ok(M: int, N: int, K: int) -> bool:
+    """Whether mla_linear_packed covers a product of this shape."""
+    return 0 < M <= LINEAR_MAX_ROWS and N > 0 and N % 8 == 0 and K in PACKED_K
+
+
+def pack_weight(w: torch.Tensor) -> PackedWeight:
+    """Re-lay a [N, K] bf16 weight (unit last stride) for linear_packed."""
+    dev = _need_gpu(w)
+    if w.dim() != 2 or w.dtype != torch.bfloat16 or w.stride(1) != 1:
+        raise ValueError("pack_weight: w must be a [N, K] bf16 matrix with a unit last stride")
+    N, K = w.shape
+    out = torch.empty(N * K, dtype=w.dtype, device=dev)
+    _abi.check(_abi.lib().mla_pack_weight(w.data_ptr(), w.stride(0), N, K, out.data_ptr(), _abi.DTYPE_BF16,
+                                          _abi.stream_handle(dev)))
+    return PackedWeight(out, N, K)
+
+
+def linear_packed(
+    x: torch.Tensor,
+    wp: PackedWeight,
+    out: Optional[torch.Tensor] = None,
+    bias: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """out[m, n] = x[m, :] . w[n, :] (+ bias[n]) with w packed by pack_weight
+    (mla_linear_packed): the decode step's stacked input product and wo
+    (models/mla.py:281-288, :307, :490-495)."""
+    dev = _need_gpu(x, wp.data, out, bias)
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1 or x.shape[1] != wp.K:
+        raise ValueError(f"x must be [M, {wp.K}] bf16 with a unit last stride")
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty(M, wp.N, dtype=x.dtype, device=dev)
+    if tuple(out.shape) != (M, wp.N) or out.dtype != x.dtype or out.stride(1) != 1:
+        raise ValueError(f"out must be [{M}, {wp.N}] bf16 with a unit last stride")
+    if bias is not None and (bias.dim() != 1 or bias.numel() != wp.N or bias.stride(0) != 1
+                             or bias.dtype != x.dtype):
+        raise ValueError(f"bias must be a contiguous [{wp.N}] bf16 vector")
+    _abi.check(
+        _abi.lib().mla_linear_packed(
+            x.data_ptr(), x.stride(0), wp.data.data_ptr(), _abi.ptr(bias), out.data_ptr(), out.stride(0),
+            M, wp.N, wp.K, _abi.DTYPE_BF16, _abi.stream_handle(dev),
+        )
+    )
+    return out
+
+
 def merge_project(
     o_lat: torch.Tensor,
     w_uv: torch.Tensor,

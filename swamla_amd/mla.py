@@ -106,7 +106,8 @@ class MLA(nn.Module):
         self.pe_cache = None
         self.kv_scale = None
         self._absorbed = None  # (key, W_uk [H,nope,R], W_uv^T [H,R,v])
-        self._decode_w = None  # (key, stacked absorbed-query / q_pe / wkv_a weight, stacked bias)
+        self._decode_w = None  # (key, stacked absorbed-query / q_pe / wkv_a weight, stacked bias, packed)
+        self._wo_packed = None  # (key, wo.weight packed for mla_linear_packed)
         self._workspace: Optional[DecodeWorkspace] = None
         self._num_cus: Optional[int] = None
 
@@ -233,16 +234,35 @@ class MLA(nn.Module):
                 b_abs = torch.bmm(bq[:, None, :Dn].float(), w_uk.float()).reshape(H * R)
                 b_in = torch.cat([b_abs, bq[:, Dn:].float().reshape(-1), self.wkv_a.bias.detach().float()]
                                  ).to(self.wq.bias.dtype).contiguous()
-            self._decode_w = (key, w_in, b_in)
+            wp = None
+            if w_in.is_cuda and kernels.packed_ok(1, w_in.shape[0], w_in.shape[1]):
+                wp = kernels.pack_weight(w_in)
+            self._decode_w = (key, w_in, b_in, wp)
         return self._decode_w[1], self._decode_w[2]
 
+    def _packed_wo(self) -> Optional["kernels.PackedWeight"]:
+        """wo.weight in mla_linear_packed's layout (None when its shape is not
+        covered); rebuilt when the weight changes."""
+        w = self.wo.weight
+        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        if self._wo_packed is None or self._wo_packed[0] != key:
+            wp = None
+            if w.is_cuda and w.dtype == torch.bfloat16 and kernels.packed_ok(1, w.shape[0], w.shape[1]):
+                wp = kernels.pack_weight(w.detach())
+            self._wo_packed = (key, wp)
+        return self._wo_packed[1]
+
     def _fused_projections(self, x: torch.Tensor):
-        """q_abs [n, H, R], q_pe [n, H, P] and kv [n, R+P] from one mla_linear
-        product over decode_weights() (column views of one [n, H*(R+P)+R+P]
-        buffer)."""
+        """q_abs [n, H, R], q_pe [n, H, P] and kv [n, R+P] from one product
+        over decode_weights() (mla_linear_packed with its packed copy, else
+        mla_linear; column views of one [n, H*(R+P)+R+P] buffer)."""
         n, H, R, P = x.shape[0] * x.shape[1], self.n_heads, self.kv_lora_rank, self.qk_rope_head_dim
         w_in, b_in = self.decode_weights()
-        y = kernels.linear(x.reshape(n, self.dim), w_in, bias=b_in)
+        wp = self._decode_w[3]
+        if wp is not None and kernels.packed_ok(n, wp.N, wp.K):
+            y = kernels.linear_packed(x.reshape(n, self.dim), wp, bias=b_in)
+        else:
+            y = kernels.linear(x.reshape(n, self.dim), w_in, bias=b_in)
         q_abs = y[:, : H * R].view(n, H, R)
         q_pe = y[:, H * R: H * (R + P)].view(n, H, P)
         return q_abs, q_pe, y[:, H * (R + P):]
@@ -414,7 +434,11 @@ class MLA(nn.Module):
             kernels.merge_project(o_lat, w_uv, o.view(n, H, Dv), cache, n_splits=n_splits, min_chunk=min_chunk,
                                   workspace=ws, start_pos=sp, rows_per_seq=T)
             wo_b = None if self.wo.bias is None else self.wo.bias.detach()
-            out = kernels.linear(o, self.wo.weight.detach(), bias=wo_b).view(B, T, self.dim)
+            wo_p = self._packed_wo()
+            if wo_p is not None and kernels.packed_ok(n, wo_p.N, wo_p.K):
+                out = kernels.linear_packed(o, wo_p, bias=wo_b).view(B, T, self.dim)
+            else:
+                out = kernels.linear(o, self.wo.weight.detach(), bias=wo_b).view(B, T, self.dim)
             return self.resid_dropout(out)  # mla.py:490-495
 
         w_uk, w_uv_t = self.absorbed_weights()

@@ -202,6 +202,37 @@ def test_linear_rejects(lib, kw, code):
     assert lib.mla_last_error().decode()
 
 
+def test_pack_weight_and_packed_linear_reject(lib):
+    assert lib.mla_pack_weight(FAKE, 1024, 48, 1024, FAKE, 0, None) == -2  # fp32
+    assert lib.mla_pack_weight(FAKE, 1024, 44, 1024, FAKE, 1, None) == -2  # N % 8
+    assert lib.mla_pack_weight(FAKE, 1024, 48, 1000, FAKE, 1, None) == -2  # K % 64
+    assert lib.mla_pack_weight(FAKE, 512, 48, 1024, FAKE, 1, None) == -1  # row stride < K
+    assert lib.mla_pack_weight(None, 1024, 48, 1024, FAKE, 1, None) == -1
+    assert lib.mla_pack_weight(FAKE + 8, 1024, 48, 1024, FAKE, 1, None) == -3
+    assert lib.mla_pack_weight(FAKE, 1028, 48, 1024, FAKE, 1, None) == -3
+    assert lib.mla_pack_weight(FAKE, 1024, 0, 1024, None, 1, None) == 0  # empty
+    args = dict(x=FAKE, x_rs=1024, wp=FAKE, bias=None, y=FAKE, y_rs=64, M=32, N=64, K=1024, dt=1, stream=None)
+
+    def lp(**kw):
+        a = dict(args)
+        a.update(kw)
+        return lib.mla_linear_packed(*a.values())
+
+    assert lp(dt=0) == -2
+    assert lp(M=129) == -2
+    assert lp(N=60) == -2
+    assert lp(K=768) == -2
+    assert lp(K=4096) == -2
+    assert lp(x=None) == -1
+    assert lp(x_rs=512) == -1
+    assert lp(y_rs=32) == -1
+    assert lp(x=FAKE + 8) == -3
+    assert lp(x_rs=1028) == -3
+    assert lp(bias=FAKE + 1) == -3
+    assert lp(M=0, x=None, wp=None, y=None) == 0
+    assert "mla_linear_packed" in lib.mla_last_error().decode() or lp(M=129) == -2
+
+
 def test_linear_empty_is_a_noop(lib):
     assert _linear(lib, M=0, x=None, w=None, y=None) == 0
     assert _linear(lib, batch=0, x=None, w=None, y=None) == 0

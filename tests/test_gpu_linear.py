@@ -137,3 +137,75 @@ def test_merge_project_equals_merge_then_product(gpu, n_splits, min_chunk):
     err = (got_h - ref).abs()
     assert float(err.max()) <= 2e-2 * float(ref.abs().max()), float(err.max())
     assert float(err.mean()) <= 3e-3 * float(ref.abs().mean()), float(err.mean())
+
+
+def test_pack_weight_layout(gpu):
+    """Packed element (n, k) sits at (((n/8)*(K/64) + k/64)*8 + (k%64)/8)*64 + (n%8)*8 + k%8."""
+    N, K = 24, 192
+    w = torch.arange(N * K, dtype=torch.float32).view(N, K)  # distinct values, exact in bf16 up to 256
+    w = (w % 251).to(torch.bfloat16)
+    buf = torch.zeros(N, K + 64, dtype=torch.bfloat16)
+    buf[:, :K] = w
+    wp = kernels.pack_weight(buf.to(gpu)[:, :K])
+    torch.cuda.synchronize()
+    n = torch.arange(N).view(N, 1)
+    k = torch.arange(K).view(1, K)
+    idx = (((n // 8) * (K // 64) + k // 64) * 8 + (k % 64) // 8) * 64 + (n % 8) * 8 + k % 8
+    expect = torch.empty(N * K, dtype=torch.bfloat16)
+    expect[idx.reshape(-1)] = w.reshape(-1)
+    assert torch.equal(wp.data.cpu(), expect)
+
+
+@pytest.mark.parametrize("M", [1, 7, 16, 17, 32, 33, 64, 65, 100, 128])
+@pytest.mark.parametrize("N,K", [(5440, 1024), (1024, 2048), (1536, 1536), (40, 512), (8, 1024), (2056, 2048)])
+def test_linear_packed_shapes(gpu, M, N, K):
+    say(f"linear_packed M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M * 13 + N + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)
+    wp = kernels.pack_weight(w.to(gpu))
+    out = kernels.linear_packed(x.to(gpu), wp, bias=b.to(gpu))
+    torch.cuda.synchronize()
+    assert out.shape == (M, N)
+    assert_within_ulp(out, ref_linear(x, w, b))
+
+
+def test_linear_packed_strided_rows_and_untouched_tail(gpu):
+    """x and out as row-strided views (the decode step's wkv_a / wo buffers);
+    rows past M and columns past N of the output buffer are never written."""
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 32, 1024, 2048
+    xb = torch.randn(M, K + 128, generator=g).to(torch.bfloat16).to(gpu)
+    x = xb[:, 64:64 + K]
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    wp = kernels.pack_weight(w.to(gpu))
+    buf = torch.full((M + 3, N + 40), 7.0, dtype=torch.bfloat16, device=gpu)
+    kernels.linear_packed(x, wp, out=buf[:M, 8:8 + N])
+    torch.cuda.synchronize()
+    assert bool((buf[M:] == 7.0).all()) and bool((buf[:, :8] == 7.0).all()) and bool((buf[:, 8 + N:] == 7.0).all())
+    assert_within_ulp(buf[:M, 8:8 + N], ref_linear(x.cpu(), w))
+
+
+def test_linear_packed_equals_in_graph_replays(gpu):
+    """Captured in a HIP graph and replayed with eager work in between, every
+    replay equals the eager result bit for bit."""
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(32, 1024, generator=g).to(torch.bfloat16).to(gpu)
+    wp = kernels.pack_weight((torch.randn(5440, 1024, generator=g) * 0.05).to(torch.bfloat16).to(gpu))
+    eager = kernels.linear_packed(x, wp)
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream(gpu)
+    s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s):
+        kernels.linear_packed(x, wp, out=out)
+    torch.cuda.current_stream(gpu).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels.linear_packed(x, wp, out=out)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        _ = (x.float() * 2).sum()  # unrelated eager work between replays
