@@ -122,23 +122,24 @@ __global__ __launch_bounds__(NW * 64) void mla_linear_kernel(LinearArgs a) {
 
 
 // ---------------------------------------------------------------------------
-// Split merge + W_uv read-out.  Block = (8 query rows, head h), 4 waves.
+// Split merge + W_uv read-out.  Block = (ROWS query rows, head h), 4 waves;
+// ROWS (2, 4 or 8) keeps the grid near one block per CU.
 // The block first issues its W_uv[h] loads (wave w: output tiles w and w+4,
 // all 256 K), then merges its rows' split partials into bf16 rows in LDS
-// (thread t: row t/32, channels 8(t%32)..+8; one split: the decode kernel's
-// o_lat row), then multiplies: y[r, h, d] = sum_c W_uv[h][d][c] x[r][c].
+// (thread t < 32*ROWS: row t/32, channels 8(t%32)..+8; one split: the decode
+// kernel's o_lat row), then multiplies: y[r, h, d] = sum_c W_uv[h][d][c] x[r][c].
 // The merge is o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M) with
 // M = max_s lse_s, accumulated over groups of 8 splits in order.
 // ---------------------------------------------------------------------------
-constexpr int kMpRows = 8;              // query rows per block
 constexpr int kMpXRow = 2 * 256 + 16;   // LDS bytes per merged row (padded)
 
-template <int DV>
+template <int DV, int ROWS>
 __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs a) {
   constexpr int R = 256, H = 16;
   constexpr int kTilesPerWave = DV / 16 / 4;
-  __shared__ __attribute__((aligned(16))) uint8_t x_lds[kMpRows * kMpXRow];
-  const int h = blockIdx.y, r0 = blockIdx.x * kMpRows;
+  static_assert(ROWS == 2 || ROWS == 4 || ROWS == 8, "rows per block");
+  __shared__ __attribute__((aligned(16))) uint8_t x_lds[ROWS * kMpXRow];
+  const int h = blockIdx.y, r0 = blockIdx.x * ROWS;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
@@ -153,8 +154,8 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
     for (int s = 0; s < 8; ++s) wb[j][s] = *reinterpret_cast<const uint4*>(wp + 32 * s);
   }
 
-  // Merge: thread -> (row rr, 8 channels cc).
-  {
+  // Merge: thread -> (row rr, 8 channels cc); threads past ROWS rows idle.
+  if (threadIdx.x < ROWS * 32) {
     const int rr = threadIdx.x >> 5, cc = 8 * (threadIdx.x & 31);
     const int r = r0 + rr;
     uint4 xv = make_uint4(0, 0, 0, 0);
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
   f32x4_t acc[kTilesPerWave];
 #pragma unroll
   for (int j = 0; j < kTilesPerWave; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const uint8_t* xa = x_lds + (n & (kMpRows - 1)) * kMpXRow + 2 * (8 * g);
+  const uint8_t* xa = x_lds + (n & (ROWS - 1)) * kMpXRow + 2 * (8 * g);
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
     const bf16x8_t av = as_bf16x8(*reinterpret_cast<const uint4*>(xa + 2 * (32 * s)));
@@ -224,14 +225,15 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
       acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, as_bf16x8(wb[j][s]), acc[j], 0, 0, 0);
   }
   // lane (n, g) holds rows 4g+i of output column 16*tile + n
-  if (g < 2) {
+  if (4 * g < ROWS) {
 #pragma unroll
     for (int j = 0; j < kTilesPerWave; ++j) {
       const int d = 16 * (w + 4 * j) + n;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = r0 + 4 * g + i;
-        if (r < a.n_rows) static_cast<uint16_t*>(a.y)[r * a.y_rs + h * a.y_hs + d] = f32_to_bf16(acc[j][i]);
+        if (4 * g + i < ROWS && r < a.n_rows)
+          static_cast<uint16_t*>(a.y)[r * a.y_rs + h * a.y_hs + d] = f32_to_bf16(acc[j][i]);
       }
     }
   }
@@ -456,8 +458,13 @@ int launch_pack_weight(const PackWeightArgs& a, hipStream_t s) {
 
 int launch_merge_project(const MergeProjectArgs& a, hipStream_t s) {
   if (a.n_rows == 0) return 0;
-  const dim3 grid((a.n_rows + kMpRows - 1) / kMpRows, 16), block(256);
-  hipLaunchKernelGGL((mla_merge_project_kernel<128>), grid, block, 0, s, a);
+  // rows per block: about one (rows, head) block per CU; every block reads
+  // its head's whole W_uv slice, so fewer rows mean more re-reads of it
+  const int rows = a.n_rows * 16 <= 2 * 256 ? 2 : (a.n_rows * 16 <= 4 * 256 ? 4 : 8);
+  const dim3 grid((a.n_rows + rows - 1) / rows, 16), block(256);
+  if (rows == 2) hipLaunchKernelGGL((mla_merge_project_kernel<128, 2>), grid, block, 0, s, a);
+  else if (rows == 4) hipLaunchKernelGGL((mla_merge_project_kernel<128, 4>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((mla_merge_project_kernel<128, 8>), grid, block, 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
