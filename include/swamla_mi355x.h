@@ -169,6 +169,30 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
                            void* stream);
 
 /*
+ * mla_prefill_attn — absorbed attention of a prefill chunk: T new query
+ * tokens per sequence in dense addressing (row r = sequence r / T, token
+ * t = r % T), each attending causally over positions [0, start_pos + t + 1)
+ * of its cache row (bottom-right, as mla_decode_attn's dense mode).
+ * Replaces models/mla.py:417-487 for seqlen > 1 (the reference aligns its
+ * is_causal mask top-left, which differs only when start_pos > 0, :480-484).
+ * Arguments as mla_decode_attn's dense mode (start_pos [n_rows / T],
+ * tokens_per_seq = T, rope_abs), without split-KV: o_lat is written
+ * directly.  One workgroup serves four consecutive tokens of a sequence, so
+ * each cache tile is read once per four queries.  bf16 models only (bf16 or
+ * e4m3 cache).
+ */
+int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
+                     const void* q_pe, int64_t q_pe_rs, int64_t q_pe_hs,
+                     const void* cos_tab, const void* sin_tab, int64_t rope_len,
+                     const void* ckv_cache, const void* kpe_cache,
+                     const float* ckv_scale, int64_t cache_batch,
+                     int64_t cache_seq, const int32_t* start_pos,
+                     int32_t tokens_per_seq, int32_t rope_abs, int32_t n_rows,
+                     int32_t H, int32_t R, int32_t P, float sm_scale,
+                     void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
+                     int32_t cache_dtype, void* stream);
+
+/*
  * mla_merge — log-sum-exp merge of split-KV partials (no reference
  * counterpart: the reference attends in one SDPA call, mla.py:581-595).
  * o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M), M = max_s lse_s, for

@@ -150,11 +150,11 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
                  const int32_t* start_pos, int32_t rows_per_seq, int32_t rope_abs, int32_t n_rows, int32_t H,
                  int32_t R, int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk, float* o_part,
                  float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype, int32_t cache_dtype,
-                 swamla::DecodeArgs* a) {
+                 swamla::DecodeArgs* a, int32_t max_rows = 65535) {
   if (int e = check_geometry(H, R, P)) return e;
   if (int e = check_pair(dtype, cache_dtype)) return e;
-  if (n_rows < 0 || n_rows > 65535)
-    return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_rows=%d outside [0, 65535]", fn, n_rows);
+  if (n_rows < 0 || n_rows > max_rows)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_rows=%d outside [0, %d]", fn, n_rows, max_rows);
   if (n_splits < 1 || n_splits > 1024)
     return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_splits=%d outside [1, 1024]", fn, n_splits);
   if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "%s: min_chunk=%d < 1", fn, min_chunk);
@@ -259,6 +259,31 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
                             cos_tab, sin_tab,       rope_len,    ckv_cache, kpe_cache, ckv_scale,
                             cache_batch, cache_seq, err_flag};
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair", fn);
+  if (rc != 0) return hip_fail(fn);
+  return ok();
+}
+
+int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const void* q_pe, int64_t q_pe_rs,
+                     int64_t q_pe_hs, const void* cos_tab, const void* sin_tab, int64_t rope_len,
+                     const void* ckv_cache, const void* kpe_cache, const float* ckv_scale, int64_t cache_batch,
+                     int64_t cache_seq, const int32_t* start_pos, int32_t tokens_per_seq, int32_t rope_abs,
+                     int32_t n_rows, int32_t H, int32_t R, int32_t P, float sm_scale, void* o_lat, int64_t o_rs,
+                     int64_t o_hs, int32_t dtype, int32_t cache_dtype, void* stream) {
+  const char* fn = "mla_prefill_attn";
+  if (dtype != SWAMLA_DTYPE_BF16)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "%s: model dtype %d not built (bf16 only)", fn, dtype);
+  if (!start_pos) return fail(SWAMLA_ERR_INVALID_ARG, "%s: needs dense addressing (start_pos)", fn);
+  swamla::DecodeArgs a;
+  if (int e = check_decode(fn, q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab, sin_tab, rope_len,
+                           ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, nullptr, nullptr, nullptr,
+                           start_pos, tokens_per_seq, rope_abs, n_rows, H, R, P, sm_scale, 1, 1, nullptr, nullptr,
+                           o_lat, o_rs, o_hs, dtype, cache_dtype, &a, 1 << 30))
+    return e;
+  // grid: (ceil(T / 4), sequences)
+  if (n_rows / tokens_per_seq > 65535)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: %d sequences exceed 65535", fn, n_rows / tokens_per_seq);
+  const int rc = swamla::launch_prefill(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair", fn);
   if (rc != 0) return hip_fail(fn);
   return ok();

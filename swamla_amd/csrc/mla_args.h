@@ -107,6 +107,7 @@ struct MergeProjectArgs {
 int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s);
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s);
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s);
+int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s);
 // Product with a packed weight (see mla_pack_weight): Y = X . W^T (+ bias).
 struct PackedLinearArgs {
   const void* x;

@@ -332,6 +332,65 @@ def decode_attention(
     return out
 
 
+PREFILL_QUERIES_PER_BLOCK = 4
+
+
+def use_prefill(n_seq: int, tokens_per_seq: int, num_cus: int = 256) -> bool:
+    """Whether a dense chunk of ``tokens_per_seq`` tokens per sequence is
+    better served by prefill_attention (four queries share each cache tile)
+    than by per-row decode_attention with split-KV: when the chunk alone
+    gives about one workgroup per CU."""
+    blocks = n_seq * -(-tokens_per_seq // PREFILL_QUERIES_PER_BLOCK)
+    return tokens_per_seq >= 8 and blocks >= num_cus
+
+
+def prefill_attention(
+    q_abs: torch.Tensor,
+    q_pe: torch.Tensor,
+    cos_tab: torch.Tensor,
+    sin_tab: torch.Tensor,
+    cache: LatentCache,
+    sm_scale: float,
+    *,
+    start_pos: torch.Tensor,
+    rows_per_seq: int,
+    rope_abs: bool = False,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Causal absorbed attention of a prefill chunk (mla_prefill_attn): row r
+    is token r % T of sequence r / T and attends to [0, start_pos + r % T + 1).
+    Same operands as decode_attention in dense mode; no split-KV.
+    Reference: models/mla.py:417-487 (seqlen > 1)."""
+    cache.validate()
+    dev = _need_gpu(q_abs, q_pe, cos_tab, sin_tab, cache.ckv, start_pos)
+    dt = cache.model_dtype
+    rows = q_abs.shape[0]
+    if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (H, R) or q_abs.stride(2) != 1:
+        raise ValueError(f"q_abs must be [rows, {H}, {R}] with unit last stride")
+    if q_pe.dim() != 3 or tuple(q_pe.shape) != (rows, H, P) or q_pe.stride(2) != 1:
+        raise ValueError(f"q_pe must be [rows, {H}, {P}] with unit last stride")
+    if q_abs.dtype != dt or q_pe.dtype != dt or cos_tab.dtype != dt:
+        raise TypeError(f"query and RoPE tensors must be {dt}")
+    _, p_sp = _addressing(rows, (None, None, None), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
+    if out is None:
+        out = torch.empty(rows, H, R, dtype=dt, device=dev)
+    if tuple(out.shape) != (rows, H, R) or out.stride(2) != 1 or out.dtype != dt:
+        raise ValueError("out must be [rows, H, R] in the model dtype with unit last stride")
+    _abi.check(
+        _abi.lib().mla_prefill_attn(
+            q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1),
+            q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
+            cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+            cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
+            cache.ckv.shape[0], cache.ckv.shape[1], p_sp, int(rows_per_seq), int(bool(rope_abs)),
+            rows, H, R, P, float(sm_scale),
+            out.data_ptr(), out.stride(0), out.stride(1),
+            _abi.dtype_code(dt), cache.cache_code, _abi.stream_handle(dev),
+        )
+    )
+    return out
+
+
 LINEAR_MAX_ROWS = 128
 
 

@@ -416,17 +416,26 @@ class MLA(nn.Module):
                            start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
 
         n_splits, min_chunk = self._split_plan(n, max_len, dev)
+        # A chunk of many tokens per sequence: four queries share each cache
+        # tile (no split-KV) instead of one row per workgroup.
+        prefill = x.dtype == torch.bfloat16 and kernels.use_prefill(B, T, self._num_cus)
+        if prefill:
+            n_splits = 1
         if fused:
             o_lat = torch.empty(n, H, R, dtype=x.dtype, device=dev)
             ws = self._workspace_for(n, n_splits, dev)
-            fa = None
-            if fold_append:
-                fa = kernels.FusedAppend(kv, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps)
-            kernels.decode_attention(
-                q_abs, q_pe, cos, sin, cache, self.softmax_scale,
-                start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
-                out=o_lat, workspace=ws, merge=False, append=fa,
-            )
+            if prefill:
+                kernels.prefill_attention(q_abs, q_pe, cos, sin, cache, self.softmax_scale, start_pos=sp,
+                                          rows_per_seq=T, rope_abs=rope_abs, out=o_lat)
+            else:
+                fa = None
+                if fold_append:
+                    fa = kernels.FusedAppend(kv, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps)
+                kernels.decode_attention(
+                    q_abs, q_pe, cos, sin, cache, self.softmax_scale,
+                    start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
+                    out=o_lat, workspace=ws, merge=False, append=fa,
+                )
             # o[r, h*Dv + d] = W_uv[h][d] . merged o_lat[r, h]: split merge and
             # read-out in one launch, written straight in wo's input layout
             w_uv = self.wkv_b.weight.detach().view(H, Dn + Dv, R)[:, Dn:, :]
@@ -445,11 +454,15 @@ class MLA(nn.Module):
         q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]
         q_abs = torch.bmm(q_nope, w_uk)  # [H, n, R]
         o_lat = torch.empty(H, n, R, dtype=x.dtype, device=dev)
-        kernels.decode_attention(
-            q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
-            start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
-            out=o_lat.transpose(0, 1), workspace=self._workspace_for(n, n_splits, dev),
-        )
+        if prefill:
+            kernels.prefill_attention(q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
+                                      start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, out=o_lat.transpose(0, 1))
+        else:
+            kernels.decode_attention(
+                q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
+                start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
+                out=o_lat.transpose(0, 1), workspace=self._workspace_for(n, n_splits, dev),
+            )
         o = torch.bmm(o_lat, w_uv_t)  # [H, n, Dv]
         out = o.transpose(0, 1).reshape(B, T, H * Dv)
         return self.resid_dropout(self.wo(out))  # mla.py:490-495

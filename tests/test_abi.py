@@ -152,6 +152,38 @@ def test_decode_append_rejects(lib, kw, code):
     assert "mla_decode_attn_append" in lib.mla_last_error().decode() or code == -2
 
 
+def _prefill(lib, **kw):
+    args = dict(qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, cos=FAKE, sin=FAKE,
+                rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, sp=FAKE, T=4, rope_abs=0, n_rows=8,
+                H=16, R=256, P=64, sm=0.07, o=FAKE, o_rs=4096, o_hs=256, dt=1, c_dt=1, stream=None)
+    args.update(kw)
+    return lib.mla_prefill_attn(*args.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(dt=0, c_dt=0), -2),  # fp32 models use the per-row path
+        (dict(H=8), -2),
+        (dict(sp=None), -1),  # dense addressing only
+        (dict(T=3), -1),  # 8 rows are not a multiple of 3
+        (dict(T=0), -1),
+        (dict(n_rows=70000 * 4, T=4), -1),  # more than 65535 sequences
+        (dict(c_dt=2), -1),
+        (dict(o=None), -1),
+        (dict(qa=FAKE + 4), -3),
+        (dict(cos=FAKE + 4), -3),
+    ],
+)
+def test_prefill_rejects(lib, kw, code):
+    assert _prefill(lib, **kw) == code
+    assert lib.mla_last_error().decode()
+
+
+def test_prefill_zero_rows_is_a_noop(lib):
+    assert _prefill(lib, n_rows=0, qa=None, qp=None) == 0
+
+
 def test_decode_append_zero_rows_is_a_noop(lib):
     assert _decode_append(lib, n_rows=0, kv_in=None, qa=None, qp=None) == 0
 
