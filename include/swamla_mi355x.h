@@ -177,9 +177,9 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
  * is_causal mask top-left, which differs only when start_pos > 0, :480-484).
  * Arguments as mla_decode_attn's dense mode (start_pos [n_rows / T],
  * tokens_per_seq = T, rope_abs), without split-KV: o_lat is written
- * directly.  One workgroup serves four consecutive tokens of a sequence, so
- * each cache tile is read once per four queries.  bf16 models only (bf16 or
- * e4m3 cache).
+ * directly.  One workgroup serves eight consecutive tokens of a sequence,
+ * so each cache tile is read once per eight queries.  bf16 models only (bf16
+ * or e4m3 cache).
  */
 int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
                      const void* q_pe, int64_t q_pe_rs, int64_t q_pe_hs,

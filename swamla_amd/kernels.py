@@ -332,12 +332,12 @@ def decode_attention(
     return out
 
 
-PREFILL_QUERIES_PER_BLOCK = 4
+PREFILL_QUERIES_PER_BLOCK = 8  # mla_prefill_attn: one query per wave, eight waves
 
 
 def use_prefill(n_seq: int, tokens_per_seq: int, num_cus: int = 256) -> bool:
     """Whether a dense chunk of ``tokens_per_seq`` tokens per sequence is
-    better served by prefill_attention (four queries share each cache tile)
+    better served by prefill_attention (eight queries share each cache tile)
     than by per-row decode_attention with split-KV: when the chunk alone
     gives about one workgroup per CU."""
     blocks = n_seq * -(-tokens_per_seq // PREFILL_QUERIES_PER_BLOCK)
