@@ -100,7 +100,19 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-KERNEL_SOURCE = os.path.join(ROOT, "swamla_amd", "csrc", "mla_kernels.hip")
+# the decode kernel's translation unit (its traffic summary is keyed by these)
+KERNEL_SOURCES = [os.path.join(ROOT, "swamla_amd", "csrc", f)
+                  for f in ("mla_kernels.hip", "mla_device.h", "mla_plan.h", "mla_args.h", "numerics.h")]
+
+
+def kernel_source_hash() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for path in KERNEL_SOURCES:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
 
 
 def measured_traffic(B: int, L: int, cache: str):
@@ -109,10 +121,9 @@ def measured_traffic(B: int, L: int, cache: str):
     this launch shape, else None (counters cannot be read from inside this
     process).  Returns (bytes, summary file name)."""
     import glob
-    import hashlib
 
     try:
-        src = hashlib.sha256(open(KERNEL_SOURCE, "rb").read()).hexdigest()[:16]
+        src = kernel_source_hash()
     except OSError:
         return None, None
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_traffic.md"))):

@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = [
     os.path.join(HERE, "csrc", "mla_kernels.hip"),
+    os.path.join(HERE, "csrc", "mla_prefill.hip"),
     os.path.join(HERE, "csrc", "mla_linear.hip"),
     os.path.join(HERE, "csrc", "mla_abi.cpp"),
 ]

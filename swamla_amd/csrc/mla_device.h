@@ -1,0 +1,225 @@
+// mla_device.h — device code shared by the gfx950 kernels: geometry and tile
+// constants, the per-op-rounded arithmetic of the append path (LayerNorm,
+// RoPE, e4m3 encoding), bf16 / e4m3 conversions, MFMA operand helpers, the
+// LDS-only barrier and the non-temporal 16-byte load.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "numerics.h"
+
+namespace swamla {
+
+constexpr int kR = 256;
+constexpr int kP = 64;
+constexpr int kH = 16;
+constexpr int kKC = kR + kP;  // 320 channels scored per cached token
+
+// ---------------------------------------------------------------------------
+// Small helpers
+// ---------------------------------------------------------------------------
+template <int DT>
+struct Elem;
+template <>
+struct Elem<0> {  // fp32
+  using T = float;
+  static __device__ __forceinline__ float ld(const T* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ T from_f32(float f) { return f; }
+  static __device__ __forceinline__ T from_f64(double d) { return static_cast<float>(d); }
+  // op-by-op rounding of eager fp32 math: contraction into a fused
+  // multiply-add is switched off (HIP's __fmul_rn is a plain multiply that
+  // the compiler may otherwise fuse with the following add).
+  static __device__ __forceinline__ float mul(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+  }
+  static __device__ __forceinline__ float add(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+  }
+  static __device__ __forceinline__ float sub(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+  }
+};
+template <>
+struct Elem<1> {  // bf16
+  using T = uint16_t;
+  static __device__ __forceinline__ float ld(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
+  static __device__ __forceinline__ T from_f32(float f) { return f32_to_bf16(f); }
+  static __device__ __forceinline__ T from_f64(double d) { return f64_to_bf16(d); }
+  // eager bf16 math: compute in fp32, round to bf16 after every op
+  static __device__ __forceinline__ float mul(float a, float b) {
+#pragma clang fp contract(off)
+    return round_bf16(a * b);
+  }
+  static __device__ __forceinline__ float add(float a, float b) {
+#pragma clang fp contract(off)
+    return round_bf16(a + b);
+  }
+  static __device__ __forceinline__ float sub(float a, float b) {
+#pragma clang fp contract(off)
+    return round_bf16(a - b);
+  }
+};
+
+// Interleaved-pair RoPE of one pair (positional_encoding.py:37-41, :57-60):
+// o1 = x1*c - x2*s, o2 = x2*c + x1*s, rounded after every op in the model dtype.
+template <int DT>
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float& o1,
+                                          float& o2) {
+  using E = Elem<DT>;
+  o1 = E::sub(E::mul(x1, c), E::mul(x2, s));
+  o2 = E::add(E::mul(x2, c), E::mul(x1, s));
+}
+
+__device__ __forceinline__ double shfl_xor_f64(double v, int m) { return __shfl_xor(v, m, 64); }
+__device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// The arithmetic below is shared by the append kernel and the decode kernel's
+// fused one-token append, so both write identical bits.
+
+// LayerNorm of one R = 256 channel row held by a wavefront, lane owning
+// channels 4*lane .. 4*lane+3.  Every multiply / add is rounded on its own:
+// the result must reproduce the fixed-order fp64 statement exactly.
+// Statistics in fp64; fixed order: in-lane left-to-right, then xor butterfly
+// 1,2,4,...,32 (every lane ends with the same total).
+__device__ __forceinline__ void layernorm_quad(const double x[4], const double wt[4], const double bs[4],
+                                               float eps, double y[4]) {
+#pragma clang fp contract(off)
+  double s = ((x[0] + x[1]) + x[2]) + x[3];
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) s = s + shfl_xor_f64(s, m);
+  const double mean = s * (1.0 / 256.0);
+  double d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[i] = x[i] - mean;
+  double q = ((d[0] * d[0] + d[1] * d[1]) + d[2] * d[2]) + d[3] * d[3];
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) q = q + shfl_xor_f64(q, m);
+  const double var = q * (1.0 / 256.0);
+  // correctly rounded square root and IEEE division
+  const double rstd = 1.0 / __dsqrt_rn(var + static_cast<double>(eps));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i] = (d[i] * rstd) * wt[i] + bs[i];
+}
+
+// bf16 cache: the four channels rounded once from fp64.
+__device__ __forceinline__ uint2 encode_bf16_quad(const double y[4]) {
+  uint2 o;
+  o.x = f64_to_bf16(y[0]) | (static_cast<uint32_t>(f64_to_bf16(y[1])) << 16);
+  o.y = f64_to_bf16(y[2]) | (static_cast<uint32_t>(f64_to_bf16(y[3])) << 16);
+  return o;
+}
+
+// e4m3 per-token: y is first rounded to bf16 (the value a bf16 cache would
+// hold), amax over the token, scale = max(amax,1e-12)/448, code = RNE(y/scale).
+// Returns the lane's four codes (byte i = channel 4*lane+i).
+__device__ __forceinline__ uint32_t encode_e4m3_quad(const double y[4], float& scale) {
+  float yb[4];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    yb[i] = bf16_to_f32(f64_to_bf16(y[i]));
+    amax = fmaxf(amax, fabsf(yb[i]));
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, m));
+  scale = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
+  uint32_t codes = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) codes |= static_cast<uint32_t>(f32_to_e4m3(__fdiv_rn(yb[i], scale))) << (8 * i);
+  return codes;
+}
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kSub = 16;                   // tokens per wave in a tile
+constexpr int kWaves = 4;                  // waves per block
+constexpr int kTileTok = kSub * kWaves;    // 64 tokens per lockstep tile
+constexpr int kCRow = 2 * kR + 16;         // 528 B per LDS latent row
+constexpr int kPeRow = 2 * kP + 16;        // 144 B per LDS rope row
+constexpr int kCBytes = kTileTok * kCRow;  // 33792 B
+constexpr int kPeBytes = kTileTok * kPeRow;  // 9216 B
+constexpr int kPRow = 2 * kTileTok + 8;    // bytes per head row of P (128 + 8 pad: the 16 heads
+                                           // of an 8-byte access fall on distinct banks)
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+__device__ __forceinline__ bf16x8_t cat_bf16x8(s16x4_t lo, s16x4_t hi) {
+  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+  return as_bf16x8(make_uint4(a.x, a.y, b.x, b.y));
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16x2 with the hardware RNE converter.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
+// Max over lanes l, l^16, l^32, l^48 (the four lane groups sharing a head)
+// with the gfx950 row-swap permutes: after permlane16_swap(v, v) the pair of
+// results holds v[l] and v[l^16] in some order, likewise l^32 for
+// permlane32_swap, so their max is order-free.
+__device__ __forceinline__ float wave_max_rows(float v) {
+  const uint32_t u = f2u(v);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(u2f(r16[0]), u2f(r16[1]));
+  const uint32_t u2 = f2u(v);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(u2, u2, false, false);
+  return fmaxf(u2f(r32[0]), u2f(r32[1]));
+}
+
+constexpr float kLazy = 8.0f;  // log2 headroom before the softmax reference moves
+
+// Workgroup barrier that orders LDS only: global loads stay in flight across
+// it (a full fence would also wait for them).  The release half completes
+// this wave's earlier LDS reads and writes before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Registers of one in-flight tile (this wave's 16 tokens), loaded as whole
+// lines: element s of c covers tokens 8(s&1)..+8, bytes 128(s>>1)..+128 of
+// the latent rows (lane: token l%8, 16 B at 16(l/8)); p[j] the same for
+// rope rows, tokens 8j..+8.  e4m3: 4 segments of codes plus the 4 scales this
+// lane's scores need.
+template <int C_DT>
+struct KTile;
+template <>
+struct KTile<1> {
+  uint4 c[8];
+  uint4 p[2];
+};
+template <>
+struct KTile<2> {
+  uint4 c[4];
+  uint4 p[2];
+  float4 sc;
+};
+
+// e4m3 x 4 (one dword) -> 4 bf16 with the hardware converter (exact: every
+// e4m3fn value is a bf16 value, so keeping the high halves is exact).
+__device__ __forceinline__ uint2 e4m3x4_to_bf16x4_hw(uint32_t w) {
+  const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  const uint32_t a = __builtin_amdgcn_perm(f2u(lo[1]), f2u(lo[0]), 0x07060302u);
+  const uint32_t b = __builtin_amdgcn_perm(f2u(hi[1]), f2u(hi[0]), 0x07060302u);
+  return make_uint2(a, b);
+}
+
+// 16-byte global load marked non-temporal: the cache is streamed once, and
+// the non-temporal hint keeps it from thrashing the vector L1 (measured
+// ~10 % more read bandwidth for this kernel on MI355X).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+}  // namespace swamla

@@ -7,144 +7,25 @@
 //                     split-KV partials (reference: models/mla.py:417-487)
 //   mla_decode_f32    the same maths in fp32 on the VALU, for fp32 models
 //   mla_merge_kernel  log-sum-exp merge of split-KV partials
+// (the prefill kernel is in mla_prefill.hip, shared device code in
+// mla_device.h)
 //
 // Geometry is fixed at R = 256 (kv_lora_rank), P = 64 (rope dim), H = 16.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "mla_args.h"
+#include "mla_device.h"
 #include "mla_plan.h"
 #include "numerics.h"
 
 namespace swamla {
-
-constexpr int kR = 256;
-constexpr int kP = 64;
-constexpr int kH = 16;
-constexpr int kKC = kR + kP;  // 320 channels scored per cached token
-
-// ---------------------------------------------------------------------------
-// Small helpers
-// ---------------------------------------------------------------------------
-template <int DT>
-struct Elem;
-template <>
-struct Elem<0> {  // fp32
-  using T = float;
-  static __device__ __forceinline__ float ld(const T* p, int64_t i) { return p[i]; }
-  static __device__ __forceinline__ T from_f32(float f) { return f; }
-  static __device__ __forceinline__ T from_f64(double d) { return static_cast<float>(d); }
-  // op-by-op rounding of eager fp32 math: contraction into a fused
-  // multiply-add is switched off (HIP's __fmul_rn is a plain multiply that
-  // the compiler may otherwise fuse with the following add).
-  static __device__ __forceinline__ float mul(float a, float b) {
-#pragma clang fp contract(off)
-    return a * b;
-  }
-  static __device__ __forceinline__ float add(float a, float b) {
-#pragma clang fp contract(off)
-    return a + b;
-  }
-  static __device__ __forceinline__ float sub(float a, float b) {
-#pragma clang fp contract(off)
-    return a - b;
-  }
-};
-template <>
-struct Elem<1> {  // bf16
-  using T = uint16_t;
-  static __device__ __forceinline__ float ld(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
-  static __device__ __forceinline__ T from_f32(float f) { return f32_to_bf16(f); }
-  static __device__ __forceinline__ T from_f64(double d) { return f64_to_bf16(d); }
-  // eager bf16 math: compute in fp32, round to bf16 after every op
-  static __device__ __forceinline__ float mul(float a, float b) {
-#pragma clang fp contract(off)
-    return round_bf16(a * b);
-  }
-  static __device__ __forceinline__ float add(float a, float b) {
-#pragma clang fp contract(off)
-    return round_bf16(a + b);
-  }
-  static __device__ __forceinline__ float sub(float a, float b) {
-#pragma clang fp contract(off)
-    return round_bf16(a - b);
-  }
-};
-
-// Interleaved-pair RoPE of one pair (positional_encoding.py:37-41, :57-60):
-// o1 = x1*c - x2*s, o2 = x2*c + x1*s, rounded after every op in the model dtype.
-template <int DT>
-__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float& o1,
-                                          float& o2) {
-  using E = Elem<DT>;
-  o1 = E::sub(E::mul(x1, c), E::mul(x2, s));
-  o2 = E::add(E::mul(x2, c), E::mul(x1, s));
-}
-
-__device__ __forceinline__ double shfl_xor_f64(double v, int m) { return __shfl_xor(v, m, 64); }
-__device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xor(v, m, 64); }
 
 // ---------------------------------------------------------------------------
 // Kernel 1: fused append.  One wavefront per token, 4 tokens per block.
 // ---------------------------------------------------------------------------
 // IN_DT: 0 fp32 / 1 bf16 (model dtype; also k_pe cache dtype).
 // C_DT : 0 fp32 / 1 bf16 / 2 e4m3 (latent cache dtype).
-// The arithmetic below is shared by the append kernel and the decode kernel's
-// fused one-token append, so both write identical bits.
-
-// LayerNorm of one R = 256 channel row held by a wavefront, lane owning
-// channels 4*lane .. 4*lane+3.  Every multiply / add is rounded on its own:
-// the result must reproduce the fixed-order fp64 statement exactly.
-// Statistics in fp64; fixed order: in-lane left-to-right, then xor butterfly
-// 1,2,4,...,32 (every lane ends with the same total).
-__device__ __forceinline__ void layernorm_quad(const double x[4], const double wt[4], const double bs[4],
-                                               float eps, double y[4]) {
-#pragma clang fp contract(off)
-  double s = ((x[0] + x[1]) + x[2]) + x[3];
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) s = s + shfl_xor_f64(s, m);
-  const double mean = s * (1.0 / 256.0);
-  double d[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) d[i] = x[i] - mean;
-  double q = ((d[0] * d[0] + d[1] * d[1]) + d[2] * d[2]) + d[3] * d[3];
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) q = q + shfl_xor_f64(q, m);
-  const double var = q * (1.0 / 256.0);
-  // correctly rounded square root and IEEE division
-  const double rstd = 1.0 / __dsqrt_rn(var + static_cast<double>(eps));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) y[i] = (d[i] * rstd) * wt[i] + bs[i];
-}
-
-// bf16 cache: the four channels rounded once from fp64.
-__device__ __forceinline__ uint2 encode_bf16_quad(const double y[4]) {
-  uint2 o;
-  o.x = f64_to_bf16(y[0]) | (static_cast<uint32_t>(f64_to_bf16(y[1])) << 16);
-  o.y = f64_to_bf16(y[2]) | (static_cast<uint32_t>(f64_to_bf16(y[3])) << 16);
-  return o;
-}
-
-// e4m3 per-token: y is first rounded to bf16 (the value a bf16 cache would
-// hold), amax over the token, scale = max(amax,1e-12)/448, code = RNE(y/scale).
-// Returns the lane's four codes (byte i = channel 4*lane+i).
-__device__ __forceinline__ uint32_t encode_e4m3_quad(const double y[4], float& scale) {
-  float yb[4];
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    yb[i] = bf16_to_f32(f64_to_bf16(y[i]));
-    amax = fmaxf(amax, fabsf(yb[i]));
-  }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, m));
-  scale = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
-  uint32_t codes = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) codes |= static_cast<uint32_t>(f32_to_e4m3(__fdiv_rn(yb[i], scale))) << (8 * i);
-  return codes;
-}
-
 // The work of one wavefront: token `tok` of the append.
 template <int IN_DT, int C_DT>
 __device__ __forceinline__ void append_token(const AppendArgs& a, int tok, int lane) {
@@ -307,87 +188,6 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ o_part, con
 // conflicts beyond its minimum: latent rows 528 B (16 tokens x 16 B at one
 // column hit 16 distinct 16-byte slots), rope rows 144 B.
 // ---------------------------------------------------------------------------
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-constexpr int kSub = 16;                   // tokens per wave in a tile
-constexpr int kWaves = 4;                  // waves per block
-constexpr int kTileTok = kSub * kWaves;    // 64 tokens per lockstep tile
-constexpr int kCRow = 2 * kR + 16;         // 528 B per LDS latent row
-constexpr int kPeRow = 2 * kP + 16;        // 144 B per LDS rope row
-constexpr int kCBytes = kTileTok * kCRow;  // 33792 B
-constexpr int kPeBytes = kTileTok * kPeRow;  // 9216 B
-constexpr int kPRow = 2 * kTileTok + 8;    // bytes per head row of P (128 + 8 pad: the 16 heads
-                                           // of an 8-byte access fall on distinct banks)
-
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
-__device__ __forceinline__ bf16x8_t cat_bf16x8(s16x4_t lo, s16x4_t hi) {
-  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
-  return as_bf16x8(make_uint4(a.x, a.y, b.x, b.y));
-}
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-// Two floats -> packed bf16x2 with the hardware RNE converter.
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
-}
-
-// Max over lanes l, l^16, l^32, l^48 (the four lane groups sharing a head)
-// with the gfx950 row-swap permutes: after permlane16_swap(v, v) the pair of
-// results holds v[l] and v[l^16] in some order, likewise l^32 for
-// permlane32_swap, so their max is order-free.
-__device__ __forceinline__ float wave_max_rows(float v) {
-  const uint32_t u = f2u(v);
-  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  v = fmaxf(u2f(r16[0]), u2f(r16[1]));
-  const uint32_t u2 = f2u(v);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(u2, u2, false, false);
-  return fmaxf(u2f(r32[0]), u2f(r32[1]));
-}
-
-constexpr float kLazy = 8.0f;  // log2 headroom before the softmax reference moves
-
-// Workgroup barrier that orders LDS only: global loads stay in flight across
-// it (a full fence would also wait for them).  The release half completes
-// this wave's earlier LDS reads and writes before the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// Registers of one in-flight tile (this wave's 16 tokens), loaded as whole
-// lines: element s of c covers tokens 8(s&1)..+8, bytes 128(s>>1)..+128 of
-// the latent rows (lane: token l%8, 16 B at 16(l/8)); p[j] the same for
-// rope rows, tokens 8j..+8.  e4m3: 4 segments of codes plus the 4 scales this
-// lane's scores need.
-template <int C_DT>
-struct KTile;
-template <>
-struct KTile<1> {
-  uint4 c[8];
-  uint4 p[2];
-};
-template <>
-struct KTile<2> {
-  uint4 c[4];
-  uint4 p[2];
-  float4 sc;
-};
-
-// e4m3 x 4 (one dword) -> 4 bf16 with the hardware converter (exact: every
-// e4m3fn value is a bf16 value, so keeping the high halves is exact).
-__device__ __forceinline__ uint2 e4m3x4_to_bf16x4_hw(uint32_t w) {
-  const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
-  const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
-  const uint32_t a = __builtin_amdgcn_perm(f2u(lo[1]), f2u(lo[0]), 0x07060302u);
-  const uint32_t b = __builtin_amdgcn_perm(f2u(hi[1]), f2u(hi[0]), 0x07060302u);
-  return make_uint2(a, b);
-}
-
 // ---- Fused one-token append inside the decode kernel (bf16 model).
 // Inputs of one token as loaded by one wavefront: lane owns latent channels
 // 4*lane .. +3 and (lanes 0..31) the k_pe pair `lane`; raw bf16 bits.
@@ -461,15 +261,6 @@ __device__ __forceinline__ void fused_store(const AppendArgs& a, int64_t crow, c
     if (lane == 0) a.ckv_scale[crow] = t.scale;
   }
   if (lane < kP / 2) reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.kpe) + crow * kP)[lane] = t.pe;
-}
-
-// 16-byte global load marked non-temporal: the cache is streamed once, and
-// the non-temporal hint keeps it from thrashing the vector L1 (measured
-// ~10 % more read bandwidth for this kernel on MI355X).
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld_stream16(const void* p) {
-  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-  return make_uint4(t.x, t.y, t.z, t.w);
 }
 
 template <int C_DT, int DEPTH, bool FUSE>
@@ -832,298 +623,6 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
 }
 
 // ---------------------------------------------------------------------------
-// Prefill attention (a chunk of T > 1 new tokens per sequence, dense
-// addressing, bf16 model): query token t of sequence b attends causally to
-// cache positions [0, start_pos[b] + t + 1) (bottom-right).  A block of NW
-// waves takes NW * QPW consecutive query tokens of one sequence, QPW per
-// wave, so each 64-token tile of the cache is loaded once for all of them x
-// 16 heads.  The tile is staged in LDS as in mla_decode_mfma (each wave loads
-// 64 / NW of its tokens as whole lines); every wave then scores all 64 tokens for its own
-// queries (S^T = K . Q^T: each K operand read from LDS feeds QPW MFMAs),
-// keeps its own online softmax per (query, head) and accumulates O^T for all
-// 256 latent channels (each C^T operand read transposed feeds QPW MFMAs).
-// The weights stay in registers: the 8 k slots of lane group g in the PV
-// product are tokens 32kb + 4g + {0..3} and 32kb + 16 + 4g + {0..3}, exactly
-// the tokens whose scores the lane holds.  No split-KV: the output is o_lat
-// directly.  Built with NW = 8 waves of one query each (QPW = 1) and one tile
-// of loads in flight: 178 VGPRs, two waves per SIMD.
-// ---------------------------------------------------------------------------
-#ifndef SWAMLA_PREFILL_OCC
-#define SWAMLA_PREFILL_OCC 1  // prefill workgroups per CU the registers must allow
-#endif
-// One wave's share of a prefill tile: RPL rows of 8 tokens (lane: token l%8,
-// 16 bytes at 16(l/8) of each 128-byte segment), plus the rows' e4m3 scales.
-template <int C_DT, int RPL>
-struct PTile {
-  uint4 c[RPL * (C_DT == 2 ? 2 : 4)];
-  uint4 p[RPL];
-  float sc[RPL];
-};
-
-template <int C_DT, int DEPTH, int QPW, int NW>
-__global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(DecodeArgs a) {
-  constexpr int TPW = kTileTok / NW;  // tokens each wave loads per tile
-  constexpr int RPL = TPW / 8;        // ... rows of 8 tokens per lane
-  constexpr int SEG = C_DT == 2 ? 2 : 4;  // 128-byte latent segments per row
-  constexpr int CB = C_DT == 2 ? kR : 2 * kR;  // latent bytes per cached token
-  __shared__ __attribute__((aligned(16))) uint8_t c_lds[kCBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t pe_lds[kPeBytes];
-  __shared__ __attribute__((aligned(16))) float sc_lds[kTileTok];
-
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int n = lane & 15, g = lane >> 4;
-  const int lt = lane & 7, lc = lane >> 3;
-  const int T = a.ad.T;
-  const int b = blockIdx.y;
-  const int t_first = NW * QPW * blockIdx.x;
-  const int t_last_q = min(t_first + NW * QPW - 1, T - 1);  // last query token of the block
-  const int sp = a.ad.start_pos[b];
-  const bool b_ok = b < a.cache_b;
-
-  // This wave's queries (surplus ones repeat the block's last) and lengths.
-  int tq[QPW], rq[QPW], Lq[QPW];
-  bool valid[QPW];
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi) {
-    const int tt = t_first + QPW * w + qi;
-    valid[qi] = tt < T;
-    tq[qi] = min(tt, t_last_q);
-    rq[qi] = b * T + tq[qi];
-    const int l = b_ok ? sp + tq[qi] + 1 : 0;
-    Lq[qi] = min(max(l, 0), static_cast<int>(a.cache_s));
-  }
-  int Lb = b_ok ? sp + t_last_q + 1 : 0;  // the block's range: its last query's
-  Lb = min(max(Lb, 0), static_cast<int>(a.cache_s));
-  const int n_tiles = (Lb + kTileTok - 1) / kTileTok;  // block-uniform
-  const int64_t cache_row0 = static_cast<int64_t>(b_ok ? b : 0) * a.cache_s;
-  const int t_last = Lb > 0 ? Lb - 1 : 0;
-
-  auto load_tile = [&](int j, PTile<C_DT, RPL>& kt) {
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) {
-      const int64_t row = cache_row0 + min(j * kTileTok + TPW * w + 8 * rr + lt, t_last);
-      const uint8_t* cp = static_cast<const uint8_t*>(a.ckv) + row * CB + 16 * lc;
-#pragma unroll
-      for (int q = 0; q < SEG; ++q) kt.c[rr * SEG + q] = ld_stream16(cp + 128 * q);
-      kt.p[rr] = ld_stream16(static_cast<const uint8_t*>(a.kpe) + row * (2 * kP) + 16 * lc);
-      if constexpr (C_DT == 2) kt.sc[rr] = a.ckv_scale[row];
-    }
-  };
-
-  // ---- Q^T operands of this wave's queries (as in mla_decode_mfma).
-  PTile<C_DT, RPL> kt[DEPTH];
-  bf16x8_t qb[QPW][10];
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi) {
-    const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + rq[qi] * a.qa_rs + n * a.qa_hs;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qb[qi][s] = as_bf16x8(*reinterpret_cast<const uint4*>(qa + 32 * s + 8 * g));
-  }
-  uint4 raw[QPW][2];
-  uint2 cr[QPW][2], sr[QPW][2];
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi) {
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + rq[qi] * a.qp_rs + n * a.qp_hs;
-    int rp = a.ad.rope_abs ? sp + tq[qi] : tq[qi];
-    rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
-    const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
-    const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int c0 = 32 * s + 8 * g;
-      raw[qi][s] = *reinterpret_cast<const uint4*>(qp + c0);
-      cr[qi][s] = *reinterpret_cast<const uint2*>(ct + c0 / 2);
-      sr[qi][s] = *reinterpret_cast<const uint2*>(st + c0 / 2);
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d) load_tile(d, kt[d]);
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi)
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const uint32_t wv_in[4] = {raw[qi][s].x, raw[qi][s].y, raw[qi][s].z, raw[qi][s].w};
-      const uint32_t cw2[2] = {cr[qi][s].x, cr[qi][s].y}, sw2[2] = {sr[qi][s].x, sr[qi][s].y};
-      uint32_t wv[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const uint32_t cj = (jj & 1) ? (cw2[jj >> 1] >> 16) : (cw2[jj >> 1] & 0xFFFF);
-        const uint32_t sj = (jj & 1) ? (sw2[jj >> 1] >> 16) : (sw2[jj >> 1] & 0xFFFF);
-        float o1, o2;
-        rope_pair<1>(bf16_to_f32(wv_in[jj] & 0xFFFF), bf16_to_f32(wv_in[jj] >> 16), bf16_to_f32(cj),
-                     bf16_to_f32(sj), o1, o2);
-        wv[jj] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
-      }
-      qb[qi][8 + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
-    }
-
-  f32x4_t oacc[QPW][16];
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) oacc[qi][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run[QPW], l_part[QPW];
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi) {
-    m_run[qi] = -INFINITY;
-    l_part[qi] = 0.f;
-  }
-
-  uint8_t* const c_st = c_lds + (TPW * w + lt) * kCRow + 16 * lc;
-  uint8_t* const pe_st = pe_lds + (TPW * w + lt) * kPeRow + 16 * lc;
-  // operand reads of token block tb: token 16tb + n, 8 channels at 32s + 8g
-  const uint8_t* const c_op = c_lds + n * kCRow + 2 * (8 * g);
-  const uint8_t* const pe_op = pe_lds + n * kPeRow + 2 * (8 * g);
-  // C^T reads: token row 4g + n/4 of each 16-token block, channel 4(n%4) (+16 mb)
-  const uint8_t* const c_tr = c_lds + (4 * g + (n >> 2)) * kCRow + 8 * (n & 3);
-
-  auto process = [&](int j, PTile<C_DT, RPL>& kt) {
-    // This wave's rows (e4m3 decoded to bf16, with their scales) into the tile.
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) {
-      if constexpr (C_DT == 2) {
-#pragma unroll
-        for (int q = 0; q < SEG; ++q) {
-          const uint4 v = kt.c[rr * SEG + q];
-          const uint2 a0 = e4m3x4_to_bf16x4_hw(v.x), a1 = e4m3x4_to_bf16x4_hw(v.y);
-          const uint2 a2 = e4m3x4_to_bf16x4_hw(v.z), a3 = e4m3x4_to_bf16x4_hw(v.w);
-          uint8_t* dst = c_st + 8 * rr * kCRow + 2 * (128 * q);  // channels 128q + 16lc .. +16
-          *reinterpret_cast<uint4*>(dst + 16 * lc) = make_uint4(a0.x, a0.y, a1.x, a1.y);
-          *reinterpret_cast<uint4*>(dst + 16 * lc + 16) = make_uint4(a2.x, a2.y, a3.x, a3.y);
-        }
-        if (lc == 0) sc_lds[TPW * w + 8 * rr + lt] = kt.sc[rr];
-      } else {
-#pragma unroll
-        for (int q = 0; q < SEG; ++q) {
-          const uint4 v = kt.c[rr * SEG + q];
-          *reinterpret_cast<uint4*>(c_st + 8 * rr * kCRow + 128 * q) = make_uint4(v.x, v.y, v.z, v.w);
-        }
-      }
-      const uint4 pv = kt.p[rr];
-      *reinterpret_cast<uint4*>(pe_st + 8 * rr * kPeRow) = make_uint4(pv.x, pv.y, pv.z, pv.w);
-    }
-    load_tile(j + DEPTH, kt);
-    lds_barrier();  // the whole tile is visible
-
-    // Scores of all 64 tokens for this wave's queries: token 16tb + 4g + i, head n.
-    float x[QPW][4][4];
-    const int tile0 = j * kTileTok;
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      f32x4_t s_c[QPW], s_p[QPW];
-#pragma unroll
-      for (int qi = 0; qi < QPW; ++qi) s_c[qi] = s_p[qi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const bf16x8_t ka = as_bf16x8(*reinterpret_cast<const uint4*>(c_op + 16 * tb * kCRow + 2 * (32 * s)));
-#pragma unroll
-        for (int qi = 0; qi < QPW; ++qi) s_c[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[qi][s], s_c[qi], 0, 0, 0);
-      }
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8_t pa = as_bf16x8(*reinterpret_cast<const uint4*>(pe_op + 16 * tb * kPeRow + 2 * (32 * s)));
-#pragma unroll
-        for (int qi = 0; qi < QPW; ++qi)
-          s_p[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, qb[qi][8 + s], s_p[qi], 0, 0, 0);
-      }
-      float4 scv = make_float4(1.f, 1.f, 1.f, 1.f);
-      if constexpr (C_DT == 2) scv = *reinterpret_cast<const float4*>(sc_lds + 16 * tb + 4 * g);
-      const float sc4[4] = {scv.x, scv.y, scv.z, scv.w};
-#pragma unroll
-      for (int qi = 0; qi < QPW; ++qi)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float sv = (C_DT == 2) ? (sc4[i] * s_c[qi][i] + s_p[qi][i]) : (s_c[qi][i] + s_p[qi][i]);
-          const int tok = tile0 + 16 * tb + 4 * g + i;
-          x[qi][tb][i] = tok < Lq[qi] ? sv * a.scale_log2 : -INFINITY;
-        }
-    }
-    bf16x8_t pb[QPW][2];
-#pragma unroll
-    for (int qi = 0; qi < QPW; ++qi) {
-      float mt = -INFINITY;
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mt = fmaxf(mt, x[qi][tb][i]);
-      mt = wave_max_rows(mt);  // this query's tile maximum for head n
-      if (__any(mt > m_run[qi] + kLazy)) {
-        const float m_new = fmaxf(m_run[qi], mt);
-        const float alpha = exp2f(m_run[qi] - m_new);  // m_new is finite: tile 0 holds token 0
-        m_run[qi] = m_new;
-        l_part[qi] *= alpha;
-#pragma unroll
-        for (int mb = 0; mb < 16; ++mb) oacc[qi][mb] = oacc[qi][mb] * alpha;
-      }
-      // bf16 weights (fp8: times the token's scale) in the PV operand order.
-      uint2 pw[4];
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        float pr[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pr[i] = exp2f(x[qi][tb][i] - m_run[qi]);
-        const uint32_t w01 = pack_bf16x2(pr[0], pr[1]), w23 = pack_bf16x2(pr[2], pr[3]);
-        l_part[qi] += (u2f(w01 << 16) + u2f(w01 & 0xFFFF0000u)) + (u2f(w23 << 16) + u2f(w23 & 0xFFFF0000u));
-        if constexpr (C_DT == 2) {
-          const float4 scv = *reinterpret_cast<const float4*>(sc_lds + 16 * tb + 4 * g);
-          pw[tb].x = pack_bf16x2(u2f(w01 << 16) * scv.x, u2f(w01 & 0xFFFF0000u) * scv.y);
-          pw[tb].y = pack_bf16x2(u2f(w23 << 16) * scv.z, u2f(w23 & 0xFFFF0000u) * scv.w);
-        } else {
-          pw[tb] = make_uint2(w01, w23);
-        }
-      }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-        pb[qi][kb] = as_bf16x8(make_uint4(pw[2 * kb].x, pw[2 * kb].y, pw[2 * kb + 1].x, pw[2 * kb + 1].y));
-    }
-    // O^T[16mb + ., head] += C^T . P^T over the tile's two 32-token halves.
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int mb = 0; mb < 16; ++mb) {
-        const s16x4_t c0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4_t*)(c_tr + (32 * kb) * kCRow + 32 * mb));
-        const s16x4_t c1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4_t*)(c_tr + (32 * kb + 16) * kCRow + 32 * mb));
-        const bf16x8_t cv = cat_bf16x8(c0, c1);
-#pragma unroll
-        for (int qi = 0; qi < QPW; ++qi)
-          oacc[qi][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cv, pb[qi][kb], oacc[qi][mb], 0, 0, 0);
-      }
-    }
-    lds_barrier();  // every wave is done with the tile's rows
-  };
-
-  int it = 0;
-  for (; it + DEPTH <= n_tiles; it += DEPTH) {
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) process(it + d, kt[d]);
-  }
-#pragma unroll
-  for (int d = 0; d < DEPTH - 1; ++d)
-    if (it + d < n_tiles) process(it + d, kt[d]);
-
-#pragma unroll
-  for (int qi = 0; qi < QPW; ++qi) {
-    float l_w = l_part[qi] + shfl_xor_f32(l_part[qi], 16);
-    l_w += shfl_xor_f32(l_w, 32);
-    const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
-    if (valid[qi]) {
-      // lane (n, g): head n, channels 16mb + 4g + {0..3}
-      uint16_t* op = static_cast<uint16_t*>(a.o_lat) + rq[qi] * a.o_rs + n * a.o_hs + 4 * g;
-#pragma unroll
-      for (int mb = 0; mb < 16; ++mb) {
-        uint2 pk;
-        pk.x = f32_to_bf16(oacc[qi][mb][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(oacc[qi][mb][1] * inv)) << 16);
-        pk.y = f32_to_bf16(oacc[qi][mb][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(oacc[qi][mb][3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(op + 16 * mb) = pk;
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Kernel 2 (fp32 models): the same maths on the VALU in fp32.  One block of
 // 256 threads per (row, split); 16-token tiles staged in LDS.
 // ---------------------------------------------------------------------------
@@ -1262,16 +761,6 @@ int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s) {
 #ifndef SWAMLA_DECODE_DEPTH
 #define SWAMLA_DECODE_DEPTH 2
 #endif
-#ifndef SWAMLA_PREFILL_QPW
-#define SWAMLA_PREFILL_QPW 1  // prefill queries per wave
-#endif
-#ifndef SWAMLA_PREFILL_WAVES
-#define SWAMLA_PREFILL_WAVES 8  // prefill waves (= query groups) per workgroup
-#endif
-#ifndef SWAMLA_PREFILL_DEPTH
-#define SWAMLA_PREFILL_DEPTH 1  // prefill tiles of loads in flight per wave
-#endif
-constexpr int kPrefillDepth = SWAMLA_PREFILL_DEPTH;
 constexpr int kDecodeDepth = SWAMLA_DECODE_DEPTH;  // tiles of loads in flight per wave
 
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
@@ -1287,17 +776,6 @@ int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   else if (dt == 1 && c_dt == 2)
     hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, true>), grid, dim3(256), 0, s, a);
   else if (dt == 0 && c_dt == 0 && !fuse) hipLaunchKernelGGL(mla_decode_f32, grid, dim3(256), 0, s, a);
-  else return -1;
-  return hipGetLastError() == hipSuccess ? 0 : -2;
-}
-
-int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
-  if (a.n_rows == 0) return 0;
-  const int T = a.ad.T;
-  constexpr int kQpw = SWAMLA_PREFILL_QPW, kNw = SWAMLA_PREFILL_WAVES;
-  const dim3 grid((T + kNw * kQpw - 1) / (kNw * kQpw), a.n_rows / T), block(kNw * 64);
-  if (dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_prefill_mfma<1, kPrefillDepth, kQpw, kNw>), grid, block, 0, s, a);
-  else if (dt == 1 && c_dt == 2) hipLaunchKernelGGL((mla_prefill_mfma<2, kPrefillDepth, kQpw, kNw>), grid, block, 0, s, a);
   else return -1;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
