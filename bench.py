@@ -19,8 +19,9 @@ once per layer it passes: value = batch * steps * layers / seconds
 roofline: the step's attention launch (mla_decode_attn_append: the decode
 kernel with the one-token append folded in, split-KV), timed with HIP events
 on its stream around back-to-back launches rotating over the layers' caches
-(each launch does its full work; the stand-alone split merge is timed the
-same way and reported beside it); achieved = algorithmic bytes per launch /
+(each launch does its full work; the same launches replayed from a HIP graph
+and the stand-alone split merge are timed too and reported beside it);
+achieved = algorithmic bytes per launch /
 average launch duration, with bytes = sum_b L_b*(R+P)*2 (latent + rope
 cache) + B*H*(R+P)*2 (queries) + B*H*R*2 (latent outputs) + the append's
 B*(R+P)*2 read and B*(R+P)*2 written (+ LayerNorm parameters).
@@ -249,12 +250,32 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (reps * len(indices))  # us
 
+    def run_graph(indices, reps):
+        """The same launches captured once in a HIP graph (as the decode step
+        runs them) and replayed: no host launch work between them."""
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            hc = torch.cuda.current_stream(dev).cuda_stream
+            for i in indices:
+                _abi.check(lib.mla_decode_attn_append(*(preps[i][0][:-1] + (hc,))))
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * len(indices))  # us
+
     run(range(len(preps)), 3)  # warm-up
     cold_us = run(range(len(preps)), args.kernel_reps)
+    graph_us = run_graph(range(len(preps)), args.kernel_reps)
     warm_us = run([0], args.kernel_reps * len(preps))
     merge_us = run(range(len(preps)), args.kernel_reps, which=1)
     L, B, n_splits = preps[0][2], preps[0][3], preps[0][4]
-    return cold_us, warm_us, merge_us, L, B, n_splits
+    return cold_us, graph_us, warm_us, merge_us, L, B, n_splits
 
 
 def cpu_baseline(args, torch):
@@ -384,7 +405,7 @@ def main() -> int:
     log(f"decode: {value:.0f} layer-token/s, {ms_per_step * 1e3:.1f} us per layer-step, finite={ok}")
 
     lens = lens0 + args.steps  # lengths after the timed steps
-    cold_us, warm_us, merge_us, L, B, n_splits = time_decode_kernel(layers, xs, lens, args, dev, torch)
+    cold_us, graph_us, warm_us, merge_us, L, B, n_splits = time_decode_kernel(layers, xs, lens, args, dev, torch)
     abytes = attention_bytes_rows(lens, fp8) + append_bytes(B, fp8)
     traffic, traffic_src = measured_traffic(B, L, args.cache) if not args.ragged else (None, None)
     achieved = abytes / (cold_us * 1e-6) / 1e9
@@ -440,6 +461,9 @@ def main() -> int:
                                else "no committed PMC summary for this kernel source and launch shape"),
             "bytes_per_launch": abytes,
             "avg_launch_us": cold_us,
+            "timing": ("HIP events on the launch stream around back-to-back launches, one per layer in turn "
+                       "(caches rotated); avg_launch_us_graph: the same launches replayed from a HIP graph"),
+            "avg_launch_us_graph": graph_us,
             "launch": (f"B={B} L={L} splits<={n_splits}, caches rotated over {len(layers)} layers" if not args.ragged
                        else f"B={B} ragged L in [{int(lens.min())}, {L}] (sum {int(lens.sum())}), splits<={n_splits}, "
                             f"caches rotated over {len(layers)} layers"),
