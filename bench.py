@@ -184,6 +184,11 @@ def build_layers(args, dev, torch):
         init_linear_weights(m, 100 + i, torch)
         m.eval().to(torch.bfloat16).to(dev)
         m.set_inference_mode(True)
+        # The start_pos tensor only lets the replayed graph advance the
+        # position; a uniform batch gets the plan the reference's int
+        # start_pos gets (each row cut by its own length).  The ragged batch
+        # balances its rows' splits over the CUs on the device.
+        m.split_plan = "auto" if args.ragged else "static"
         with torch.no_grad():
             x = torch.randn(args.batch, args.ctx, args.dim, generator=g, device=dev, dtype=torch.bfloat16)
             m.prefill_cache(x, 0)  # append path over the whole prompt (RoPE positions 0..ctx-1)
@@ -215,8 +220,10 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
             cache = m.latent_cache()
             L = int(lens.max())
             sp = (lens - 1).to(device=dev, dtype=torch.int32)  # row b attends [0, lens[b])
-            n_splits, min_chunk = m._split_plan(B, L, dev)
+            # the plan MLA.forward uses for a start_pos tensor
+            n_splits, min_chunk, balance = m._decode_plan(B, L, dev, True)
             ws = kernels.DecodeWorkspace.allocate(B, n_splits, dev)
+            plan = _abi.ptr(ws.plan if balance else None)
             o_lat = torch.empty(H, B, R, dtype=torch.bfloat16, device=dev)
             cos, sin = m.rope.half_tables()
             qa, qp, ol = q_abs.transpose(0, 1), q[:, :, 128:], o_lat.transpose(0, 1)
@@ -228,13 +235,14 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
                 cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
                 cache.ckv.shape[0], cache.ckv.shape[1], sp.data_ptr(), 0,
-                B, H, R, P, float(m.softmax_scale), n_splits, min_chunk,
+                B, H, R, P, float(m.softmax_scale), n_splits, min_chunk, balance, plan,
                 ws.o_part.data_ptr(), ws.lse_part.data_ptr(),
                 ol.data_ptr(), ol.stride(0), ol.stride(1), _abi.DTYPE_BF16, cache.cache_code, h,
             )
-            margs = (ws.o_part.data_ptr(), ws.lse_part.data_ptr(), None, sp.data_ptr(), 1, B, H, R, n_splits,
-                     min_chunk, ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16, h)
-            preps.append((dargs, (q, q_abs, kv, sp, ws, o_lat, cos, sin), L, B, n_splits, margs))
+            margs = (ws.o_part.data_ptr(), ws.lse_part.data_ptr(), None, None, sp.data_ptr(), 1,
+                     cache.ckv.shape[0], cache.ckv.shape[1], B, H, R, n_splits, min_chunk, plan,
+                     ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16, h)
+            preps.append((dargs, (q, q_abs, kv, sp, ws, o_lat, cos, sin), L, B, n_splits, margs, balance))
 
     def run(indices, reps, which=0):
         e0 = torch.cuda.Event(enable_timing=True)
@@ -275,7 +283,7 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
     warm_us = run([0], args.kernel_reps * len(preps))
     merge_us = run(range(len(preps)), args.kernel_reps, which=1)
     L, B, n_splits = preps[0][2], preps[0][3], preps[0][4]
-    return cold_us, graph_us, warm_us, merge_us, L, B, n_splits
+    return cold_us, graph_us, warm_us, merge_us, L, B, n_splits, preps[0][6]
 
 
 def cpu_baseline(args, torch):
@@ -405,7 +413,8 @@ def main() -> int:
     log(f"decode: {value:.0f} layer-token/s, {ms_per_step * 1e3:.1f} us per layer-step, finite={ok}")
 
     lens = lens0 + args.steps  # lengths after the timed steps
-    cold_us, graph_us, warm_us, merge_us, L, B, n_splits = time_decode_kernel(layers, xs, lens, args, dev, torch)
+    cold_us, graph_us, warm_us, merge_us, L, B, n_splits, balance = time_decode_kernel(layers, xs, lens, args, dev,
+                                                                                   torch)
     abytes = attention_bytes_rows(lens, fp8) + append_bytes(B, fp8)
     traffic, traffic_src = measured_traffic(B, L, args.cache) if not args.ragged else (None, None)
     achieved = abytes / (cold_us * 1e-6) / 1e9
@@ -465,8 +474,10 @@ def main() -> int:
                        "(caches rotated); avg_launch_us_graph: the same launches replayed from a HIP graph"),
             "avg_launch_us_graph": graph_us,
             "launch": (f"B={B} L={L} splits<={n_splits}, caches rotated over {len(layers)} layers" if not args.ragged
-                       else f"B={B} ragged L in [{int(lens.min())}, {L}] (sum {int(lens.sum())}), splits<={n_splits}, "
-                            f"caches rotated over {len(layers)} layers"),
+                       else f"B={B} ragged L in [{int(lens.min())}, {L}] (sum {int(lens.sum())}), "
+                            + (f"splits balanced over {balance} workgroups (per-row cap {n_splits})" if balance
+                               else f"splits<={n_splits}")
+                            + f", caches rotated over {len(layers)} layers"),
             "warm_mall_achieved": warm,
             "warm_mall_avg_launch_us": warm_us,
             "merge_avg_launch_us": merge_us,

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SWAMLA_ABI_VERSION 1
+#define SWAMLA_ABI_VERSION 2
 
 enum {
   SWAMLA_OK = 0,
@@ -114,7 +114,19 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok,
  * q_pe         row r, head h at q_pe + r*q_pe_rs + h*q_pe_hs, P values before
  *              RoPE; rotated in-kernel.
  * Split-KV: each row is cut into ns = ceil(L / chunk) splits of
- *   chunk = round_up(max(min_chunk, ceil(L / n_splits)), 16) tokens.
+ *   chunk = round_up(max(min_chunk, ceil(L / n_splits)), 16) tokens,
+ * one workgroup each on a grid of n_splits x n_rows.
+ * Balanced plan (balance_blocks > 0; for ragged batches): the launch is a
+ * grid of balance_blocks workgroups and min_chunk is replaced by one chunk
+ * c chosen on the device from all rows' lengths — the smallest multiple of
+ * 64 tokens >= min_chunk with ceil(L_r / c) <= n_splits for every row and
+ * sum_r max(1, ceil(L_r / c)) <= balance_blocks (mla_balanced_chunk
+ * computes the same value on the host).  Row r gets ns_r =
+ * ceil(ceil(L_r / 64) / (c / 64)) workgroups and is cut into near-equal
+ * splits (the formula above with n_splits = ns_r and min_chunk = 1); the
+ * workgroups take the rows' splits in row-major order.  c is written to
+ * *plan (int32, may be NULL) for mla_merge / mla_merge_project.  Needs
+ * n_rows <= balance_blocks, n_rows <= 256 and cache_seq <= 2^24.
  * Rows with ns == 1 are written straight to o_lat.  Others write normalised
  * partials o_part [n_rows, n_splits, H, R] fp32 and log-sum-exp lse_part
  * [n_rows, n_splits, H] (natural log of sum exp(s)) that mla_merge combines.
@@ -130,9 +142,10 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
                     const int32_t* start_pos, int32_t rows_per_seq,
                     int32_t rope_abs, int32_t n_rows, int32_t H, int32_t R,
                     int32_t P, float sm_scale, int32_t n_splits,
-                    int32_t min_chunk, float* o_part, float* lse_part,
-                    void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
-                    int32_t cache_dtype, void* stream);
+                    int32_t min_chunk, int32_t balance_blocks, int32_t* plan,
+                    float* o_part, float* lse_part, void* o_lat, int64_t o_rs,
+                    int64_t o_hs, int32_t dtype, int32_t cache_dtype,
+                    void* stream);
 
 /*
  * mla_decode_attn_append — one decode step (one new token per sequence) with
@@ -163,7 +176,8 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
                            int64_t cache_seq, const int32_t* start_pos,
                            int32_t rope_abs, int32_t n_rows, int32_t H,
                            int32_t R, int32_t P, float sm_scale,
-                           int32_t n_splits, int32_t min_chunk, float* o_part,
+                           int32_t n_splits, int32_t min_chunk,
+                           int32_t balance_blocks, int32_t* plan, float* o_part,
                            float* lse_part, void* o_lat, int64_t o_rs,
                            int64_t o_hs, int32_t dtype, int32_t cache_dtype,
                            void* stream);
@@ -197,14 +211,19 @@ int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
  * counterpart: the reference attends in one SDPA call, mla.py:581-595).
  * o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M), M = max_s lse_s, for
  * every row whose split count (same formula as mla_decode_attn) exceeds 1.
- * Row lengths: kv_len (explicit) or start_pos / rows_per_seq (dense).
+ * Row lengths as mla_decode_attn derives them: row_seq / kv_len (explicit)
+ * or start_pos / rows_per_seq (dense), clamped to cache_seq, 0 for a cache
+ * row outside [0, cache_batch).  plan: the chunk a balanced mla_decode_attn
+ * wrote (NULL when that launch used min_chunk).
  * lse_out [n_rows, H] fp32 is optional (NULL = not written).
  */
 int mla_merge(const float* o_part, const float* lse_part,
-              const int32_t* kv_len, const int32_t* start_pos,
-              int32_t rows_per_seq, int32_t n_rows, int32_t H, int32_t R,
-              int32_t n_splits, int32_t min_chunk, void* o_lat, int64_t o_rs,
-              int64_t o_hs, float* lse_out, int32_t dtype, void* stream);
+              const int32_t* row_seq, const int32_t* kv_len,
+              const int32_t* start_pos, int32_t rows_per_seq,
+              int64_t cache_batch, int64_t cache_seq, int32_t n_rows,
+              int32_t H, int32_t R, int32_t n_splits, int32_t min_chunk,
+              const int32_t* plan, void* o_lat, int64_t o_rs, int64_t o_hs,
+              float* lse_out, int32_t dtype, void* stream);
 
 /*
  * mla_linear — batched linear layer for the few query rows of a decode step:
@@ -262,7 +281,8 @@ int mla_linear_packed(const void* x, int64_t x_rs, const void* w_packed,
  * wkv_b, i.e. the re-associated einsum of models/mla.py:433 and the reshape
  * to wo's input layout at :490-491.
  * Row lengths and splits are derived exactly as mla_decode_attn does (same
- * addressing arguments, same cache_batch / cache_seq clamping).
+ * addressing arguments, same cache_batch / cache_seq clamping; plan as for
+ * mla_merge).
  * w            head h, output d at w + h*w_hs + d*w_rs, R values (a view of
  *              wkv_b.weight: w_hs = (nope + Dv)*R, w_rs = R, base + nope*R).
  * y            row r, head h at y + r*y_rs + h*y_hs, Dv values (wo's input
@@ -275,13 +295,22 @@ int mla_merge_project(const float* o_part, const float* lse_part,
                       const int32_t* start_pos, int32_t rows_per_seq,
                       int64_t cache_batch, int64_t cache_seq, int32_t n_rows,
                       int32_t H, int32_t R, int32_t n_splits,
-                      int32_t min_chunk, const void* w, int64_t w_rs,
-                      int64_t w_hs, int32_t Dv, void* y, int64_t y_rs,
-                      int64_t y_hs, int32_t dtype, void* stream);
+                      int32_t min_chunk, const int32_t* plan, const void* w,
+                      int64_t w_rs, int64_t w_hs, int32_t Dv, void* y,
+                      int64_t y_rs, int64_t y_hs, int32_t dtype, void* stream);
 
 /* Split plan used by both kernels, exported so hosts and tests can size the
  * partial buffers: number of splits of a row of length L (0 for L <= 0). */
 int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk);
+
+/* The chunk (tokens) of a balanced plan over host-side row lengths (already
+ * clamped to the cache, at most 2^24; <= 0 for an empty row), as
+ * mla_decode_attn chooses
+ * it on the device; negative SWAMLA_ERR_* on bad arguments.  No reference
+ * counterpart (the reference does not split the KV range). */
+int32_t mla_balanced_chunk(const int32_t* lens, int32_t n_rows,
+                           int32_t n_splits, int32_t min_chunk,
+                           int32_t balance_blocks);
 
 #ifdef __cplusplus
 }

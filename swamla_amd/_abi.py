@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libswamla_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_F32, DTYPE_BF16, DTYPE_FP8 = 0, 1, 2
 ERR_NAMES = {
     -1: "INVALID_ARG",
@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "mla_prefill_attn",
     "mla_merge",
     "mla_split_count",
+    "mla_balanced_chunk",
     "mla_linear",
     "mla_pack_weight",
     "mla_linear_packed",
@@ -70,6 +71,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_last_error.argtypes = []
     lib.mla_split_count.restype = _I32
     lib.mla_split_count.argtypes = [_I32, _I32, _I32]
+    lib.mla_balanced_chunk.restype = _I32
+    lib.mla_balanced_chunk.argtypes = [_P, _I32, _I32, _I32, _I32]
     lib.mla_append.restype = ctypes.c_int
     lib.mla_append.argtypes = [
         _P, _I64, _I32, _P, _P, _P, _P, _I32, _I32, _P, _P, _F, _P, _P, _I64,
@@ -79,14 +82,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_decode_attn.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
         _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
-        _F, _I32, _I32, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
+        _F, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
     ]
     lib.mla_decode_attn_append.restype = ctypes.c_int
     lib.mla_decode_attn_append.argtypes = [
         _P, _I64, _P, _P, _F, _P,
         _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
         _P, _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _I32, _I32,
-        _F, _I32, _I32, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
+        _F, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
     ]
     lib.mla_prefill_attn.restype = ctypes.c_int
     lib.mla_prefill_attn.argtypes = [
@@ -96,7 +99,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     ]
     lib.mla_merge.restype = ctypes.c_int
     lib.mla_merge.argtypes = [
-        _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I64, _I64, _P, _I32, _P,
+        _P, _P, _P, _P, _P, _I32, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _I64, _I64, _P, _I32, _P,
     ]
     lib.mla_pack_weight.restype = ctypes.c_int
     lib.mla_pack_weight.argtypes = [_P, _I64, _I32, _I32, _P, _I32, _P]
@@ -109,7 +112,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_merge_project.restype = ctypes.c_int
     lib.mla_merge_project.argtypes = [
         _P, _P, _P, _I64, _I64, _P, _P, _P, _I32, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
-        _P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P,
+        _P, _P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P,
     ]
     lib.mla_host_f32_to_e4m3.restype = None
     lib.mla_host_f32_to_e4m3.argtypes = [_P, _P, _I64]

@@ -9,6 +9,7 @@
 #include "../../include/swamla_mi355x.h"
 #include "../../include/swamla_mi355x_testing.h"
 #include "mla_args.h"
+#include "mla_plan.h"
 #include "numerics.h"
 
 namespace {
@@ -97,6 +98,19 @@ int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk) {
   return split_count_impl(L, n_splits, min_chunk);
 }
 
+int32_t mla_balanced_chunk(const int32_t* lens, int32_t n_rows, int32_t n_splits, int32_t min_chunk,
+                           int32_t balance_blocks) {
+  if (n_rows < 0 || n_rows > swamla::kBalanceMaxRows || (n_rows > 0 && !lens) || n_splits < 1 ||
+      n_splits > 1024 || min_chunk < 1 || balance_blocks < 1 || balance_blocks > 65535 || n_rows > balance_blocks)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_balanced_chunk: bad arguments (n_rows=%d, n_splits=%d, "
+                "min_chunk=%d, balance_blocks=%d)", n_rows, n_splits, min_chunk, balance_blocks);
+  for (int r = 0; r < n_rows; ++r)
+    if (lens[r] > swamla::kBalanceMaxSeq)
+      return fail(SWAMLA_ERR_INVALID_ARG, "mla_balanced_chunk: length %d above %lld", lens[r],
+                  (long long)swamla::kBalanceMaxSeq);
+  return swamla::balanced_chunk_host(lens, n_rows, n_splits, min_chunk, balance_blocks);
+}
+
 int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const int32_t* seq_idx,
                const int32_t* dst_pos, const int32_t* rope_pos, const int32_t* start_pos,
                int32_t tokens_per_seq, int32_t rope_abs, const void* ln_w, const void* ln_b, float eps,
@@ -148,9 +162,9 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
                  const void* ckv_cache, const void* kpe_cache, const float* ckv_scale, int64_t cache_batch,
                  int64_t cache_seq, const int32_t* row_seq, const int32_t* kv_len, const int32_t* q_rope_pos,
                  const int32_t* start_pos, int32_t rows_per_seq, int32_t rope_abs, int32_t n_rows, int32_t H,
-                 int32_t R, int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk, float* o_part,
-                 float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype, int32_t cache_dtype,
-                 swamla::DecodeArgs* a, int32_t max_rows = 65535) {
+                 int32_t R, int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk, int32_t balance,
+                 int32_t* plan, float* o_part, float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs,
+                 int32_t dtype, int32_t cache_dtype, swamla::DecodeArgs* a, int32_t max_rows = 65535) {
   if (int e = check_geometry(H, R, P)) return e;
   if (int e = check_pair(dtype, cache_dtype)) return e;
   if (n_rows < 0 || n_rows > max_rows)
@@ -158,6 +172,16 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
   if (n_splits < 1 || n_splits > 1024)
     return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_splits=%d outside [1, 1024]", fn, n_splits);
   if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "%s: min_chunk=%d < 1", fn, min_chunk);
+  if (balance < 0 || balance > 65535)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: balance_blocks=%d outside [0, 65535]", fn, balance);
+  if (balance > 0 && (n_rows > balance || n_rows > swamla::kBalanceMaxRows))
+    return fail(SWAMLA_ERR_INVALID_ARG,
+                "%s: a balanced plan needs n_rows <= balance_blocks and n_rows <= %d (n_rows=%d, "
+                "balance_blocks=%d)", fn, swamla::kBalanceMaxRows, n_rows, balance);
+  if (balance > 0 && cache_seq > swamla::kBalanceMaxSeq)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "%s: a balanced plan covers caches of at most %lld positions", fn,
+                (long long)swamla::kBalanceMaxSeq);
+  if (plan && !aligned(plan, 4)) return fail(SWAMLA_ERR_MISALIGNED, "%s: plan must be 4-byte aligned", fn);
   if (!(sm_scale > 0.f)) return fail(SWAMLA_ERR_INVALID_ARG, "%s: sm_scale must be > 0", fn);
   if (!ckv_cache || !kpe_cache || !cos_tab || !sin_tab || !o_lat)
     return fail(SWAMLA_ERR_INVALID_ARG, "%s: null cache / RoPE / output pointer", fn);
@@ -196,7 +220,8 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
   *a = swamla::DecodeArgs{q_abs,     q_abs_rs,  q_abs_hs,  q_pe,      q_pe_rs,     q_pe_hs,
                           cos_tab,   sin_tab,   rope_len,  ckv_cache, kpe_cache,   ckv_scale,
                           cache_batch, cache_seq, ad,      n_rows,    sm_scale * log2e, n_splits,
-                          min_chunk, o_part,    lse_part,  o_lat,     o_rs,      o_hs, swamla::AppendArgs{}};
+                          min_chunk, balance,   plan,      o_part,    lse_part,  o_lat,
+                          o_rs,      o_hs,      swamla::AppendArgs{}};
   return SWAMLA_OK;
 }
 
@@ -211,13 +236,15 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const
                     const int32_t* row_seq, const int32_t* kv_len, const int32_t* q_rope_pos,
                     const int32_t* start_pos, int32_t rows_per_seq, int32_t rope_abs, int32_t n_rows,
                     int32_t H, int32_t R, int32_t P, float sm_scale, int32_t n_splits,
-                    int32_t min_chunk, float* o_part, float* lse_part, void* o_lat,
-                    int64_t o_rs, int64_t o_hs, int32_t dtype, int32_t cache_dtype, void* stream) {
+                    int32_t min_chunk, int32_t balance_blocks, int32_t* plan, float* o_part,
+                    float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
+                    int32_t cache_dtype, void* stream) {
   swamla::DecodeArgs a;
   if (int e = check_decode("mla_decode_attn", q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab,
                            sin_tab, rope_len, ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, row_seq,
                            kv_len, q_rope_pos, start_pos, rows_per_seq, rope_abs, n_rows, H, R, P, sm_scale,
-                           n_splits, min_chunk, o_part, lse_part, o_lat, o_rs, o_hs, dtype, cache_dtype, &a))
+                           n_splits, min_chunk, balance_blocks, plan, o_part, lse_part, o_lat, o_rs, o_hs, dtype,
+                           cache_dtype, &a))
     return e;
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_attn: no kernel for this dtype pair");
@@ -231,9 +258,9 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
                            const void* cos_tab, const void* sin_tab, int64_t rope_len, void* ckv_cache,
                            void* kpe_cache, float* ckv_scale, int64_t cache_batch, int64_t cache_seq,
                            const int32_t* start_pos, int32_t rope_abs, int32_t n_rows, int32_t H, int32_t R,
-                           int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk, float* o_part,
-                           float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
-                           int32_t cache_dtype, void* stream) {
+                           int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk,
+                           int32_t balance_blocks, int32_t* plan, float* o_part, float* lse_part, void* o_lat,
+                           int64_t o_rs, int64_t o_hs, int32_t dtype, int32_t cache_dtype, void* stream) {
   const char* fn = "mla_decode_attn_append";
   if (dtype != SWAMLA_DTYPE_BF16)
     return fail(SWAMLA_ERR_UNSUPPORTED, "%s: model dtype %d not built (bf16 only)", fn, dtype);
@@ -241,8 +268,8 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
   swamla::DecodeArgs a;
   if (int e = check_decode(fn, q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab, sin_tab, rope_len,
                            ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, nullptr, nullptr, nullptr,
-                           start_pos, 1, rope_abs, n_rows, H, R, P, sm_scale, n_splits, min_chunk, o_part,
-                           lse_part, o_lat, o_rs, o_hs, dtype, cache_dtype, &a))
+                           start_pos, 1, rope_abs, n_rows, H, R, P, sm_scale, n_splits, min_chunk,
+                           balance_blocks, plan, o_part, lse_part, o_lat, o_rs, o_hs, dtype, cache_dtype, &a))
     return e;
   if (n_rows > 0 && !kv_in) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null input rows", fn);
   if (!ln_w || !ln_b) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null LayerNorm pointer", fn);
@@ -277,8 +304,8 @@ int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, cons
   swamla::DecodeArgs a;
   if (int e = check_decode(fn, q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab, sin_tab, rope_len,
                            ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, nullptr, nullptr, nullptr,
-                           start_pos, tokens_per_seq, rope_abs, n_rows, H, R, P, sm_scale, 1, 1, nullptr, nullptr,
-                           o_lat, o_rs, o_hs, dtype, cache_dtype, &a, 1 << 30))
+                           start_pos, tokens_per_seq, rope_abs, n_rows, H, R, P, sm_scale, 1, 1, 0, nullptr,
+                           nullptr, nullptr, o_lat, o_rs, o_hs, dtype, cache_dtype, &a, 1 << 30))
     return e;
   // grid: (ceil(T / 4), sequences)
   if (n_rows / tokens_per_seq > 65535)
@@ -289,10 +316,10 @@ int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, cons
   return ok();
 }
 
-int mla_merge(const float* o_part, const float* lse_part, const int32_t* kv_len,
-              const int32_t* start_pos, int32_t rows_per_seq, int32_t n_rows, int32_t H, int32_t R,
-              int32_t n_splits, int32_t min_chunk, void* o_lat, int64_t o_rs, int64_t o_hs,
-              float* lse_out, int32_t dtype, void* stream) {
+int mla_merge(const float* o_part, const float* lse_part, const int32_t* row_seq, const int32_t* kv_len,
+              const int32_t* start_pos, int32_t rows_per_seq, int64_t cache_batch, int64_t cache_seq,
+              int32_t n_rows, int32_t H, int32_t R, int32_t n_splits, int32_t min_chunk, const int32_t* plan,
+              void* o_lat, int64_t o_rs, int64_t o_hs, float* lse_out, int32_t dtype, void* stream) {
   if (int e = check_geometry(H, R, 64)) return e;
   if (!model_elem(dtype)) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: dtype %d not built", dtype);
   if (n_rows < 0 || n_rows > 65535)
@@ -302,15 +329,19 @@ int mla_merge(const float* o_part, const float* lse_part, const int32_t* kv_len,
   if (min_chunk < 1) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: min_chunk=%d < 1", min_chunk);
   if (n_splits == 1 || n_rows == 0) return ok();  // nothing to merge
   swamla::Addressing ad;
-  if (int e = check_addressing("mla_merge", n_rows, nullptr, kv_len, nullptr, start_pos, rows_per_seq, false,
+  if (int e = check_addressing("mla_merge", n_rows, row_seq, kv_len, nullptr, start_pos, rows_per_seq, true,
                                false, &ad, 0))
     return e;
+  if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: bad cache shape");
   if (!o_part || !lse_part || !o_lat) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: null pointer");
   if (o_hs < R || o_rs < 0) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: bad output strides");
   // a lane writes 4 channels: 16 B (fp32) or 8 B (bf16)
-  if (!aligned(o_part, 16) || !aligned(o_lat, dtype == SWAMLA_DTYPE_F32 ? 16 : 8) || (o_rs | o_hs) % 4 != 0)
-    return fail(SWAMLA_ERR_MISALIGNED, "mla_merge: misaligned partials or output");
-  swamla::MergeArgs a{o_part, lse_part, ad, n_rows, n_splits, min_chunk, o_lat, o_rs, o_hs, lse_out};
+  if (!aligned(o_part, 16) || !aligned(o_lat, dtype == SWAMLA_DTYPE_F32 ? 16 : 8) || (o_rs | o_hs) % 4 != 0 ||
+      (plan && !aligned(plan, 4)))
+    return fail(SWAMLA_ERR_MISALIGNED, "mla_merge: misaligned partials, plan or output");
+  swamla::MergeArgs a{o_part, lse_part, ad,   cache_batch, cache_seq, n_rows, n_splits,
+                      min_chunk, plan, o_lat, o_rs, o_hs, lse_out};
   const int rc = swamla::launch_merge(a, dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: no kernel for dtype %d", dtype);
   if (rc != 0) return hip_fail("mla_merge");
@@ -383,7 +414,8 @@ int mla_merge_project(const float* o_part, const float* lse_part, const void* o_
                       int64_t o_hs, const int32_t* kv_len, const int32_t* row_seq,
                       const int32_t* start_pos, int32_t rows_per_seq, int64_t cache_batch,
                       int64_t cache_seq, int32_t n_rows, int32_t H, int32_t R, int32_t n_splits,
-                      int32_t min_chunk, const void* w, int64_t w_rs, int64_t w_hs, int32_t Dv,
+                      int32_t min_chunk, const int32_t* plan, const void* w, int64_t w_rs, int64_t w_hs,
+                      int32_t Dv,
                       void* y, int64_t y_rs, int64_t y_hs, int32_t dtype, void* stream) {
   if (int e = check_geometry(H, R, 64)) return e;
   if (dtype != SWAMLA_DTYPE_BF16)
@@ -407,11 +439,11 @@ int mla_merge_project(const float* o_part, const float* lse_part, const void* o_
   if (o_hs < R || w_rs < R || y_hs < Dv || o_rs < 0 || w_hs < 0 || y_rs < 0)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: strides must cover R / Dv values");
   if (!aligned(o_lat, 16) || !aligned(w, 16) || !aligned(y, 2) || (o_part && !aligned(o_part, 16)) ||
-      (lse_part && !aligned(lse_part, 4)) || (o_rs | o_hs | w_rs | w_hs) % 8 != 0)
+      (lse_part && !aligned(lse_part, 4)) || (plan && !aligned(plan, 4)) || (o_rs | o_hs | w_rs | w_hs) % 8 != 0)
     return fail(SWAMLA_ERR_MISALIGNED,
                 "mla_merge_project: o_lat and w need 16-byte aligned bases and strides that are multiples of 8");
   swamla::MergeProjectArgs a{o_part, lse_part, o_lat, o_rs, o_hs, ad, cache_batch, cache_seq, n_rows,
-                             n_splits, min_chunk, w, w_rs, w_hs, y, y_rs, y_hs};
+                             n_splits, min_chunk, plan, w, w_rs, w_hs, y, y_rs, y_hs};
   const int rc = swamla::launch_merge_project(a, static_cast<hipStream_t>(stream));
   if (rc != 0) return hip_fail("mla_merge_project");
   return ok();

@@ -55,20 +55,28 @@ struct DecodeArgs {
   int n_rows;
   float scale_log2;  // softmax_scale * log2(e)
   int n_splits, min_chunk;
+  // Length-balanced plan (balance > 0: a one-dimensional grid of `balance`
+  // workgroups, the chunk chosen on the device and written to *plan).
+  int balance;
+  int32_t* plan;
   float* o_part;
   float* lse_part;
   void* o_lat;
   int64_t o_rs, o_hs;
   // Optional fused append of one new token per row (fa.kv_in == nullptr:
   // none): the block owning a row's last split appends row r's token r.
+  // fa.ad is always this launch's `ad` (dense, T = 1): the kernel derives the
+  // token's position from the row's.
   AppendArgs fa;
 };
 
 struct MergeArgs {
   const float* o_part;
   const float* lse_part;
-  Addressing ad;  // only the row lengths are used
+  Addressing ad;  // row lengths, clamped to the cache as the decode kernel does
+  int64_t cache_b, cache_s;
   int n_rows, n_splits, min_chunk;
+  const int32_t* plan;  // balanced plan: the chunk the decode launch chose (else null)
   void* o_lat;
   int64_t o_rs, o_hs;
   float* lse_out;
@@ -98,6 +106,7 @@ struct MergeProjectArgs {
   Addressing ad;  // row lengths, clamped to the cache as the decode kernel does
   int64_t cache_b, cache_s;
   int n_rows, n_splits, min_chunk;
+  const int32_t* plan;  // balanced plan: the chunk the decode launch chose (else null)
   const void* w;
   int64_t w_rs, w_hs;
   void* y;

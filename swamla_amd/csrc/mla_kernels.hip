@@ -271,8 +271,23 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
   __shared__ float mx_lds[kWaves][kH];
   __shared__ float l_lds[kWaves][kH];
 
-  const int r = blockIdx.y;
-  const int split = blockIdx.x;
+  // Workgroup -> (row, split): the grid's (x, y), or with a balanced plan the
+  // position of blockIdx.x among all rows' splits (every wave computes the
+  // same plan; the values are uniform).
+  int r = blockIdx.y, split = blockIdx.x, bal_chunk = 0;
+  TokAddr ra;
+  if (a.balance > 0) {
+    const BalancedSlot bs =
+        balanced_slot(a.ad, a.n_rows, a.cache_b, a.cache_s, a.n_splits, a.min_chunk, a.balance, blockIdx.x);
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.plan) *a.plan = bs.chunk;
+    if (!bs.ok) return;
+    r = __builtin_amdgcn_readfirstlane(bs.r);
+    split = __builtin_amdgcn_readfirstlane(bs.split);
+    bal_chunk = bs.chunk;
+    ra = bs.addr;  // no second dependent load of the row's position
+  } else {
+    ra = row_addr(a.ad, r);
+  }
   // The wave index is read into a scalar register so loop control below is
   // uniform (scalar branches, no exec masking) and the compiler can track
   // the in-flight loads across iterations.
@@ -281,14 +296,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
   const int n = lane & 15, g = lane >> 4;
   const int lt = lane & 7, lc = lane >> 3;  // whole-line loads: token, 16-byte column
 
-  const TokAddr ra = row_addr(a.ad, r);
   const int b = ra.b;
   int L = ra.pos;
   if (L > a.cache_s) L = static_cast<int>(a.cache_s);
   if (b < 0 || b >= a.cache_b) L = 0;
-  const int ns = split_count(L, a.n_splits, a.min_chunk);
+  const RowSplits rsp = row_splits(L, a.n_splits, a.min_chunk, bal_chunk);
+  const int ns = rsp.ns;
   if (split >= ns && !(ns == 0 && split == 0)) return;
-  const int chunk = ns ? split_chunk(L, a.n_splits, a.min_chunk) : 0;
+  const int chunk = rsp.chunk;
   const int t0 = split * chunk;
   const int t1 = min(L, t0 + chunk);
   const int n_tiles = t1 > t0 ? (t1 - t0 + kTileTok - 1) / kTileTok : 0;  // block-uniform
@@ -305,7 +320,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
   TokAddr fa_t{0, 0, 0};
   if constexpr (FUSE) {
     if (split == (ns > 0 ? ns - 1 : 0)) {
-      fa_t = tok_addr(a.fa.ad, r);
+      // fa.ad is the launch's own dense addressing with one row per sequence,
+      // so the new token's cache row, position and RoPE row follow from ra.
+      fa_t = TokAddr{ra.b, ra.pos - 1, ra.rope};
       if (fa_t.b < 0 || fa_t.b >= a.fa.cache_b || fa_t.pos < 0 || fa_t.pos >= a.fa.cache_s || fa_t.rope < 0 ||
           fa_t.rope >= a.fa.rope_len) {
         if (threadIdx.x == 0 && a.fa.err_flag) a.fa.err_flag[0] = 1;  // skipped, as mla_append does
@@ -634,15 +651,29 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
   __shared__ float alpha_s[kH];
   __shared__ float m_s[kH], l_s[kH];
 
-  const int r = blockIdx.y, split = blockIdx.x, t = threadIdx.x;
-  const TokAddr ra = row_addr(a.ad, r);
+  int r = blockIdx.y, split = blockIdx.x, bal_chunk = 0;
+  const int t = threadIdx.x;
+  TokAddr ra;
+  if (a.balance > 0) {  // as in mla_decode_mfma
+    const BalancedSlot bs =
+        balanced_slot(a.ad, a.n_rows, a.cache_b, a.cache_s, a.n_splits, a.min_chunk, a.balance, blockIdx.x);
+    if (blockIdx.x == 0 && t == 0 && a.plan) *a.plan = bs.chunk;
+    if (!bs.ok) return;
+    r = __builtin_amdgcn_readfirstlane(bs.r);
+    split = __builtin_amdgcn_readfirstlane(bs.split);
+    bal_chunk = bs.chunk;
+    ra = bs.addr;
+  } else {
+    ra = row_addr(a.ad, r);
+  }
   const int b = ra.b;
   int L = ra.pos;
   if (L > a.cache_s) L = static_cast<int>(a.cache_s);
   if (b < 0 || b >= a.cache_b) L = 0;
-  const int ns = split_count(L, a.n_splits, a.min_chunk);
+  const RowSplits rsp = row_splits(L, a.n_splits, a.min_chunk, bal_chunk);
+  const int ns = rsp.ns;
   if (split >= ns && !(ns == 0 && split == 0)) return;
-  const int chunk = ns ? split_chunk(L, a.n_splits, a.min_chunk) : 0;
+  const int chunk = rsp.chunk;
   const int t0 = split * chunk, t1 = min(L, t0 + chunk);
   const int64_t row0 = static_cast<int64_t>(b < 0 ? 0 : b) * a.cache_s;
 
@@ -735,7 +766,8 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
 template <int DT>
 __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
   const int h = blockIdx.x, r = blockIdx.y;
-  const int ns = split_count(row_len(a.ad, r), a.n_splits, a.min_chunk);
+  const int ns = row_splits(clamped_row_len(a.ad, r, a.cache_b, a.cache_s), a.n_splits, a.min_chunk,
+                            a.plan ? *a.plan : 0).ns;
   if (ns <= 1) return;  // written by the decode kernel
   merge_head<DT>(a.o_part, a.lse_part, r, h, ns, a.n_splits, a.o_lat, a.o_rs, a.o_hs, a.lse_out);
 }
@@ -765,7 +797,7 @@ constexpr int kDecodeDepth = SWAMLA_DECODE_DEPTH;  // tiles of loads in flight p
 
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
-  const dim3 grid(a.n_splits, a.n_rows);
+  const dim3 grid = a.balance > 0 ? dim3(a.balance, 1) : dim3(a.n_splits, a.n_rows);
   const bool fuse = a.fa.kv_in != nullptr;
   if (dt == 1 && c_dt == 1 && !fuse)
     hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, false>), grid, dim3(256), 0, s, a);

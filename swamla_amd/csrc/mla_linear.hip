@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
     uint4 xv = make_uint4(0, 0, 0, 0);
     if (r < a.n_rows) {
       const int L = clamped_row_len(a.ad, r, a.cache_b, a.cache_s);
-      const int ns = split_count(L, a.n_splits, a.min_chunk);
+      const int ns = row_splits(L, a.n_splits, a.min_chunk, a.plan ? *a.plan : 0).ns;
       if (ns <= 1) {
         xv = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.o_lat) + r * a.ol_rs + h * a.ol_hs + cc);
       } else {

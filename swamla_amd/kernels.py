@@ -8,6 +8,7 @@ that is not on a ROCm device is an error.
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Optional
 
@@ -185,12 +186,40 @@ def plan_splits(n_rows: int, max_len: int, num_cus: int = 256, blocks_per_cu: in
     return int(max(1, min(target, by_len, 1024))), int(min_chunk)
 
 
+BALANCE_MAX_ROWS = 256  # rows a balanced plan covers (mla_decode_attn)
+
+
+def balanced_splits(n_rows: int, num_cus: int = 256) -> tuple[int, int]:
+    """Host side of a length-balanced plan (ragged batches): returns
+    (balance_blocks, n_splits) for decode_attention's ``balance`` and
+    ``n_splits``: one workgroup per CU, and a per-row split cap of
+    4 * ceil(num_cus / n_rows), so one row may take several times its share
+    while the partial buffers stay near 4 * num_cus splits.  (0, 0) when
+    the batch has more rows than a balanced plan covers."""
+    if n_rows <= 0 or n_rows > min(num_cus, BALANCE_MAX_ROWS):
+        return 0, 0
+    return int(num_cus), int(min(1024, 4 * -(-num_cus // n_rows)))
+
+
+def balanced_chunk(lens, n_splits: int, min_chunk: int, balance_blocks: int) -> int:
+    """The chunk (tokens) a balanced decode launch chooses for these row
+    lengths (host integers, clamped to the cache); mla_balanced_chunk."""
+    arr = (ctypes.c_int32 * max(len(lens), 1))(*[int(v) for v in lens])
+    c = int(_abi.lib().mla_balanced_chunk(arr, len(lens), int(n_splits), int(min_chunk), int(balance_blocks)))
+    if c < 0:
+        raise _abi.SwamlaError(c, _abi.lib().mla_last_error().decode())
+    return c
+
+
 @dataclass
 class DecodeWorkspace:
-    """Split-KV partial buffers: o_part [rows, splits, H, R], lse [rows, splits, H]."""
+    """Split-KV partial buffers: o_part [rows, splits, H, R], lse [rows, splits, H],
+    and ``plan`` (int32 [1]): the chunk a balanced decode launch chose, read
+    by the merge that follows it."""
 
     o_part: torch.Tensor
     lse_part: torch.Tensor
+    plan: torch.Tensor
 
     @staticmethod
     def allocate(n_rows: int, n_splits: int, device) -> "DecodeWorkspace":
@@ -198,6 +227,7 @@ class DecodeWorkspace:
         return DecodeWorkspace(
             torch.empty(rows, n_splits, H, R, dtype=torch.float32, device=device),
             torch.empty(rows, n_splits, H, dtype=torch.float32, device=device),
+            torch.zeros(1, dtype=torch.int32, device=device),
         )
 
     def fits(self, n_rows: int, n_splits: int) -> bool:
@@ -239,6 +269,7 @@ def decode_attention(
     lse_out: Optional[torch.Tensor] = None,
     merge: bool = True,
     append: Optional[FusedAppend] = None,
+    balance: int = 0,
 ) -> torch.Tensor:
     """Absorbed attention of query rows over the latent cache (+ merge).
 
@@ -252,7 +283,10 @@ def decode_attention(
     ``workspace`` for merge_project.  With ``append`` (bf16, dense
     addressing, one row per sequence) the step's new tokens are appended in
     the same launch (mla_decode_attn_append); the result equals append()
-    followed by this call.
+    followed by this call.  ``balance`` > 0 asks for a length-balanced
+    plan: ``balance`` workgroups share all rows' splits, with one chunk chosen
+    on the device from every row's length (see ``balanced_splits``); the
+    chunk lands in ``workspace.plan`` for a later merge_project(balanced=True).
     Reference: models/mla.py:417-487 (and :307-323, :409-414 with append).
     """
     cache.validate()
@@ -276,6 +310,7 @@ def decode_attention(
             workspace = DecodeWorkspace.allocate(rows, n_splits, dev)
         if not workspace.fits(rows, n_splits):
             raise ValueError("workspace too small for (rows, n_splits)")
+    plan = workspace.plan if (balance > 0 and workspace is not None) else None
     lib = _abi.lib()
     stream = _abi.stream_handle(dev)
     if append is not None:
@@ -298,7 +333,7 @@ def decode_attention(
                 cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
                 cache.ckv.shape[0], cache.ckv.shape[1], p_sp, int(bool(rope_abs)),
-                rows, H, R, P, float(sm_scale), n_splits, min_chunk,
+                rows, H, R, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
                 _abi.ptr(workspace.o_part if workspace else None),
                 _abi.ptr(workspace.lse_part if workspace else None),
                 out.data_ptr(), out.stride(0), out.stride(1),
@@ -314,7 +349,7 @@ def decode_attention(
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
                 cache.ckv.shape[0], cache.ckv.shape[1],
                 p_seq, p_len, p_rope, p_sp, int(rows_per_seq), int(bool(rope_abs)),
-                rows, H, R, P, float(sm_scale), n_splits, min_chunk,
+                rows, H, R, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
                 _abi.ptr(workspace.o_part if workspace else None),
                 _abi.ptr(workspace.lse_part if workspace else None),
                 out.data_ptr(), out.stride(0), out.stride(1),
@@ -324,8 +359,9 @@ def decode_attention(
     if n_splits > 1 and merge:
         _abi.check(
             lib.mla_merge(
-                workspace.o_part.data_ptr(), workspace.lse_part.data_ptr(), p_len, p_sp, int(rows_per_seq),
-                rows, H, R, n_splits, min_chunk, out.data_ptr(), out.stride(0), out.stride(1),
+                workspace.o_part.data_ptr(), workspace.lse_part.data_ptr(), p_seq, p_len, p_sp,
+                int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1], rows, H, R, n_splits, min_chunk,
+                _abi.ptr(plan), out.data_ptr(), out.stride(0), out.stride(1),
                 _abi.ptr(lse_out), _abi.dtype_code(dt), stream,
             )
         )
@@ -512,13 +548,16 @@ def merge_project(
     kv_len: Optional[torch.Tensor] = None,
     start_pos: Optional[torch.Tensor] = None,
     rows_per_seq: int = 1,
+    balanced: bool = False,
 ) -> torch.Tensor:
     """out[r, h, :] = W_uv[h] . o_lat[r, h, :] where o_lat is merged from the
     split partials left by ``decode_attention(..., merge=False)`` (or read
     from ``o_lat`` for single-split rows); mla_merge_project.  w_uv [H, Dv, R]
     may be a view of wkv_b.weight; out [rows, H, Dv] may be a view of wo's
     [rows, H*Dv] input.  Addressing and split plan must be the ones the
-    decode call used.  Reference: models/mla.py:433, :490-491."""
+    decode call used (``balanced``: the decode call had ``balance`` > 0 and
+    left its chunk in ``workspace.plan``).  Reference: models/mla.py:433,
+    :490-491."""
     dev = _need_gpu(o_lat, w_uv, out, row_seq, kv_len, start_pos)
     rows = o_lat.shape[0]
     Dv = w_uv.shape[1]
@@ -532,7 +571,7 @@ def merge_project(
         raise TypeError("merge_project: bf16 tensors only")
     (p_seq, p_len, _), p_sp = _addressing(
         rows, (row_seq, kv_len, None), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
-    if n_splits > 1 and (workspace is None or not workspace.fits(rows, n_splits)):
+    if (n_splits > 1 or balanced) and (workspace is None or not workspace.fits(rows, n_splits)):
         raise ValueError("merge_project needs the decode call's workspace")
     _abi.check(
         _abi.lib().mla_merge_project(
@@ -540,7 +579,7 @@ def merge_project(
             _abi.ptr(workspace.lse_part if n_splits > 1 else None),
             o_lat.data_ptr(), o_lat.stride(0), o_lat.stride(1),
             p_len, p_seq, p_sp, int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1],
-            rows, H, R, n_splits, min_chunk,
+            rows, H, R, n_splits, min_chunk, _abi.ptr(workspace.plan if balanced else None),
             w_uv.data_ptr(), w_uv.stride(1), w_uv.stride(0), Dv,
             out.data_ptr(), out.stride(0), out.stride(1), _abi.DTYPE_BF16, _abi.stream_handle(dev),
         )

@@ -110,6 +110,11 @@ class MLA(nn.Module):
         self._wo_packed = None  # (key, wo.weight packed for mla_linear_packed)
         self._workspace: Optional[DecodeWorkspace] = None
         self._num_cus: Optional[int] = None
+        # Split-KV plan of decode launches: "auto" balances the rows' splits
+        # over the CUs on the device when positions come as a tensor (ragged
+        # batches), "static" always cuts each row by its own length (the plan
+        # an int start_pos gets: all rows alike), "balanced" always balances.
+        self.split_plan = "auto"
 
     # ------------------------------------------------------------------ cache
     @property
@@ -294,6 +299,21 @@ class MLA(nn.Module):
             self._num_cus = torch.cuda.get_device_properties(device).multi_processor_count
         return kernels.plan_splits(n_rows, max_len, num_cus=self._num_cus)
 
+    def _decode_plan(self, n_rows: int, max_len: int, device, per_row_positions: bool) -> tuple[int, int, int]:
+        """(n_splits, min_chunk, balance) of a decode launch.  With per-sequence
+        positions (a start_pos tensor: lengths unknown to the host, ragged in
+        general) the launch balances the rows' splits over the CUs from the
+        lengths on the device, so the plan follows them in a replayed graph;
+        ``split_plan`` overrides the choice."""
+        if self.split_plan not in ("auto", "static", "balanced"):
+            raise ValueError(f"split_plan must be 'auto', 'static' or 'balanced', got {self.split_plan!r}")
+        n_splits, min_chunk = self._split_plan(n_rows, max_len, device)
+        if self.split_plan == "balanced" or (self.split_plan == "auto" and per_row_positions):
+            bal, cap = kernels.balanced_splits(n_rows, self._num_cus)
+            if bal:
+                return cap, min_chunk, bal
+        return n_splits, min_chunk, 0
+
     def _workspace_for(self, n_rows: int, n_splits: int, device) -> Optional[DecodeWorkspace]:
         if n_splits <= 1:
             return None
@@ -415,12 +435,13 @@ class MLA(nn.Module):
             kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
                            start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
 
-        n_splits, min_chunk = self._split_plan(n, max_len, dev)
+        n_splits, min_chunk, balance = self._decode_plan(
+            n, max_len, dev, isinstance(start_pos, torch.Tensor) and self.inference_mode)
         # A chunk of many tokens per sequence: four queries share each cache
         # tile (no split-KV) instead of one row per workgroup.
         prefill = x.dtype == torch.bfloat16 and kernels.use_prefill(B, T, self._num_cus)
         if prefill:
-            n_splits = 1
+            n_splits, balance = 1, 0
         if fused:
             o_lat = torch.empty(n, H, R, dtype=x.dtype, device=dev)
             ws = self._workspace_for(n, n_splits, dev)
@@ -434,14 +455,14 @@ class MLA(nn.Module):
                 kernels.decode_attention(
                     q_abs, q_pe, cos, sin, cache, self.softmax_scale,
                     start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
-                    out=o_lat, workspace=ws, merge=False, append=fa,
+                    out=o_lat, workspace=ws, merge=False, append=fa, balance=balance,
                 )
             # o[r, h*Dv + d] = W_uv[h][d] . merged o_lat[r, h]: split merge and
             # read-out in one launch, written straight in wo's input layout
             w_uv = self.wkv_b.weight.detach().view(H, Dn + Dv, R)[:, Dn:, :]
             o = torch.empty(n, H * Dv, dtype=x.dtype, device=dev)
             kernels.merge_project(o_lat, w_uv, o.view(n, H, Dv), cache, n_splits=n_splits, min_chunk=min_chunk,
-                                  workspace=ws, start_pos=sp, rows_per_seq=T)
+                                  workspace=ws, start_pos=sp, rows_per_seq=T, balanced=balance > 0)
             wo_b = None if self.wo.bias is None else self.wo.bias.detach()
             wo_p = self._packed_wo()
             if wo_p is not None and kernels.packed_ok(n, wo_p.N, wo_p.K):
@@ -461,7 +482,7 @@ class MLA(nn.Module):
             kernels.decode_attention(
                 q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
                 start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
-                out=o_lat.transpose(0, 1), workspace=self._workspace_for(n, n_splits, dev),
+                out=o_lat.transpose(0, 1), workspace=self._workspace_for(n, n_splits, dev), balance=balance,
             )
         o = torch.bmm(o_lat, w_uv_t)  # [H, n, Dv]
         out = o.transpose(0, 1).reshape(B, T, H * Dv)

@@ -36,7 +36,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mla_abi_version() == _abi.ABI_VERSION == 1
+    assert lib.mla_abi_version() == _abi.ABI_VERSION == 2
 
 
 def _append(lib, **kw):
@@ -50,8 +50,8 @@ def _append(lib, **kw):
 def _decode(lib, **kw):
     args = dict(qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, cos=FAKE, sin=FAKE,
                 rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, row_seq=FAKE, kv_len=FAKE, qrp=FAKE,
-                sp=None, T=1, rope_abs=0, n_rows=2, H=16, R=256, P=64, sm=0.07, ns=1, mc=64, o_part=None,
-                lse=None, o=FAKE, o_rs=4096, o_hs=256, dt=1, c_dt=1, stream=None)
+                sp=None, T=1, rope_abs=0, n_rows=2, H=16, R=256, P=64, sm=0.07, ns=1, mc=64, bal=0, plan=None,
+                o_part=None, lse=None, o=FAKE, o_rs=4096, o_hs=256, dt=1, c_dt=1, stream=None)
     args.update(kw)
     return lib.mla_decode_attn(*args.values())
 
@@ -110,6 +110,12 @@ def test_append_zero_tokens_is_a_noop(lib):
         (dict(sp=FAKE), -1),
         (dict(row_seq=None, kv_len=None, qrp=None, sp=FAKE, T=3), -1),
         (dict(row_seq=None), -1),
+        (dict(bal=-1), -1),
+        (dict(bal=70000), -1),
+        (dict(bal=1), -1),  # 2 rows need at least 2 workgroups
+        (dict(bal=300, n_rows=257), -1),  # a balanced plan covers at most 256 rows
+        (dict(bal=256, plan=FAKE + 2), -3),
+        (dict(bal=256, cs=(1 << 24) + 1), -2),  # balanced plans cover caches up to 2^24 positions
     ],
 )
 def test_decode_rejects(lib, kw, code):
@@ -121,8 +127,8 @@ def _decode_append(lib, **kw):
     args = dict(kv_in=FAKE, in_rs=320, w=FAKE, b=FAKE, eps=1e-5, err=None,
                 qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, cos=FAKE, sin=FAKE,
                 rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, sp=FAKE, rope_abs=0, n_rows=2,
-                H=16, R=256, P=64, sm=0.07, ns=1, mc=64, o_part=None, lse=None, o=FAKE, o_rs=4096, o_hs=256,
-                dt=1, c_dt=1, stream=None)
+                H=16, R=256, P=64, sm=0.07, ns=1, mc=64, bal=0, plan=None, o_part=None, lse=None, o=FAKE,
+                o_rs=4096, o_hs=256, dt=1, c_dt=1, stream=None)
     args.update(kw)
     return lib.mla_decode_attn_append(*args.values())
 
@@ -145,6 +151,8 @@ def _decode_append(lib, **kw):
         (dict(o=None), -1),
         (dict(rope_abs=3), -1),
         (dict(qa=FAKE + 4), -3),
+        (dict(bal=1), -1),
+        (dict(bal=256, plan=FAKE + 1), -3),
     ],
 )
 def test_decode_append_rejects(lib, kw, code):
@@ -189,8 +197,8 @@ def test_decode_append_zero_rows_is_a_noop(lib):
 
 
 def _merge(lib, **kw):
-    args = dict(o_part=FAKE, lse=FAKE, kv_len=FAKE, sp=None, T=1, n_rows=2, H=16, R=256, ns=4, mc=64, o=FAKE,
-                o_rs=4096, o_hs=256, lse_out=None, dt=1, stream=None)
+    args = dict(o_part=FAKE, lse=FAKE, row_seq=FAKE, kv_len=FAKE, sp=None, T=1, cb=2, cs=64, n_rows=2, H=16,
+                R=256, ns=4, mc=64, plan=None, o=FAKE, o_rs=4096, o_hs=256, lse_out=None, dt=1, stream=None)
     args.update(kw)
     return lib.mla_merge(*args.values())
 
@@ -202,7 +210,10 @@ def test_merge_rejects_and_noop(lib):
     assert _merge(lib, dt=2) == -2
     assert _merge(lib, o_part=FAKE + 4) == -3
     assert _merge(lib, kv_len=None) == -1
+    assert _merge(lib, row_seq=None) == -1  # the decode call's cache rows
     assert _merge(lib, sp=FAKE) == -1
+    assert _merge(lib, cs=0) == -1
+    assert _merge(lib, plan=FAKE + 2) == -3
 
 
 def _linear(lib, **kw):
@@ -272,8 +283,8 @@ def test_linear_empty_is_a_noop(lib):
 
 def _merge_project(lib, **kw):
     args = dict(o_part=FAKE, lse=FAKE, o_lat=FAKE, o_rs=4096, o_hs=256, kv_len=FAKE, row_seq=FAKE, sp=None, T=1,
-                cb=4, cs=64, n_rows=8, H=16, R=256, ns=4, mc=64, w=FAKE, w_rs=256, w_hs=65536, Dv=128, y=FAKE,
-                y_rs=2048, y_hs=128, dt=1, stream=None)
+                cb=4, cs=64, n_rows=8, H=16, R=256, ns=4, mc=64, plan=None, w=FAKE, w_rs=256, w_hs=65536, Dv=128,
+                y=FAKE, y_rs=2048, y_hs=128, dt=1, stream=None)
     args.update(kw)
     return lib.mla_merge_project(*args.values())
 
@@ -293,6 +304,7 @@ def _merge_project(lib, **kw):
         (dict(o_lat=FAKE + 8), -3),
         (dict(w_rs=260), -3),
         (dict(sp=FAKE), -1),
+        (dict(plan=FAKE + 2), -3),
     ],
 )
 def test_merge_project_rejects(lib, kw, code):
@@ -380,3 +392,52 @@ def test_unsupported_paths_raise():
         m(x, 0, position_ids=torch.zeros(1, 2, dtype=torch.long))
     with pytest.raises(NotImplementedError):
         m(x.requires_grad_(), 0)
+
+
+def _brute_balanced_chunk(lens, n_splits, min_chunk, target):
+    """The definition, searched directly: the smallest multiple of 64 tokens
+    >= min_chunk with every row in at most n_splits pieces and at most
+    target workgroups in all (an empty row takes one)."""
+    c = 64 * max(1, -(-min_chunk // 64))
+    while True:
+        pieces = [(-(-L // c) if L > 0 else 1) for L in lens]
+        if max([p for p, L in zip(pieces, lens) if L > 0] or [0]) <= n_splits and sum(pieces) <= target:
+            return c
+        c += 64
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_balanced_chunk_matches_its_definition(seed):
+    import random
+
+    from swamla_amd import kernels
+
+    rng = random.Random(seed)
+    for _ in range(40):
+        n = rng.randint(1, 64)
+        hi = rng.choice([70, 700, 17000, 140000])
+        lens = [rng.choice([0, rng.randint(1, hi), rng.randint(1, 64)]) for _ in range(n)]
+        target = rng.choice([n, n + 1, 64, 256, 1000]) if n <= 64 else 256
+        target = max(target, n)
+        n_splits = rng.choice([1, 4, 16, 129, 1024])
+        min_chunk = rng.choice([1, 64, 100, 256, 4096])
+        want = _brute_balanced_chunk(lens, n_splits, min_chunk, target)
+        assert kernels.balanced_chunk(lens, n_splits, min_chunk, target) == want, (lens, n_splits, min_chunk, target)
+
+
+def test_balanced_chunk_examples_and_rejects(lib):
+    from swamla_amd import kernels
+
+    # uniform rows: the static plan's tile count per workgroup
+    assert kernels.balanced_chunk([4224] * 32, 16, 256, 256) == 9 * 64
+    # one long row among short ones takes many workgroups
+    c = kernels.balanced_chunk([16000] + [100] * 15, 256, 64, 256)
+    assert -(-16000 // c) + 15 <= 256 and c <= 128
+    arr = (ctypes.c_int32 * 4)(1, 2, 3, 4)
+    assert lib.mla_balanced_chunk(arr, 4, 8, 64, 3) == -1  # fewer workgroups than rows
+    assert lib.mla_balanced_chunk(arr, 4, 0, 64, 8) == -1
+    assert lib.mla_balanced_chunk(None, 4, 8, 64, 8) == -1
+    assert lib.mla_balanced_chunk(arr, 0, 8, 64, 8) == 64
+    big = (ctypes.c_int32 * 2)(1 << 24, (1 << 24) + 1)
+    assert lib.mla_balanced_chunk(big, 1, 8, 64, 8) > 0
+    assert lib.mla_balanced_chunk(big, 2, 8, 64, 8) == -1

@@ -65,8 +65,9 @@ def rotated_q_pe(q_pe, cos, sin, rope_pos):
     return lo.rope_interleaved(q_pe.cpu(), cos.cpu()[rp][:, None], sin.cpu()[rp][:, None]).to(q_pe.device)
 
 
-def test_config3_ragged_batch(gpu):
-    say("config 3: 64 ragged rows, L in [256, 16384]")
+@pytest.mark.parametrize("plan", ["static", "balanced"])
+def test_config3_ragged_batch(gpu, plan):
+    say(f"config 3: 64 ragged rows, L in [256, 16384], {plan} split plan")
     g = torch.Generator().manual_seed(0)
     B, S = 64, 16384
     lens = torch.randint(256, S + 1, (B,), generator=g, dtype=torch.int32)  # bench.py's draw
@@ -79,9 +80,17 @@ def test_config3_ragged_batch(gpu):
     q_pe = torch.randn(B, H, P, generator=gd, device=gpu).to(torch.bfloat16)
     rope_pos = (lens - 1).to(gpu)
     n_splits, min_chunk = kernels.plan_splits(B, int(lens.max()))
+    balance = 0
+    if plan == "balanced":
+        balance, n_splits = kernels.balanced_splits(B, 256)
+    ws = kernels.DecodeWorkspace.allocate(B, n_splits, gpu)
     out = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE,
                                    row_seq=torch.arange(B, dtype=torch.int32, device=gpu), kv_len=lens.to(gpu),
-                                   q_rope_pos=rope_pos, n_splits=n_splits, min_chunk=min_chunk)
+                                   q_rope_pos=rope_pos, n_splits=n_splits, min_chunk=min_chunk, workspace=ws,
+                                   balance=balance)
+    if balance:
+        torch.cuda.synchronize()
+        assert int(ws.plan.item()) == kernels.balanced_chunk(lens.tolist(), n_splits, min_chunk, balance)
     ref = ref_attention_fp32(q_abs, rotated_q_pe(q_pe, cos, sin, rope_pos),
                              lambda r, L: ckv[r, :L].float(), lambda r, L: kpe[r, :L].float(), lens)
     torch.cuda.synchronize()

@@ -289,3 +289,106 @@ def test_dense_addressing_equals_explicit(gpu):
                                       rope_abs=rope_abs, n_splits=4, min_chunk=64)
         torch.cuda.synchronize()
         assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.bfloat16, True), (torch.float32, False)])
+def test_balanced_plan_matches_oracle_and_host_chunk(gpu, dtype, fp8):
+    """A balanced launch (one chunk chosen on the device from all rows'
+    lengths, 256 workgroups sharing the rows' splits) matches the fp64 oracle,
+    writes the chunk mla_balanced_chunk computes on the host, and merges
+    through mla_merge with that chunk.  Rows: empty, one token, ragged, a
+    cache row past the batch (empty) and a length past the cache (clamped)."""
+    say(f"balanced plan dtype={dtype} fp8={fp8}")
+    g = torch.Generator().manual_seed(21 + fp8)
+    B, S = 9, 5000
+    cdt = torch.bfloat16 if fp8 else dtype
+    ckv = torch.randn(B, S, R, generator=g).to(cdt)
+    kpe = torch.randn(B, S, P, generator=g).to(dtype)
+    if fp8:
+        codes, scale = lo.fp8_quantize(ckv.reshape(-1, R))
+        cache = LatentCache(codes.view(B, S, R).to(gpu), kpe.to(gpu), scale.view(B, S).to(gpu))
+    else:
+        cache = LatentCache(ckv.to(gpu), kpe.to(gpu))
+    lens = [4999, 0, 1, 700, 64, 65, 3000, 129, 2500, 5000 + 300, 40]
+    seqs = [0, 1, 2, 3, 4, 5, 6, 7, 8, 3, B + 2]  # row 9 longer than the cache, row 10 past the batch
+    rows = len(lens)
+    q_abs = torch.randn(rows, H, R, generator=g).to(dtype)
+    q_pe = torch.randn(rows, H, P, generator=g).to(dtype)
+    rp = torch.zeros(rows, dtype=torch.int32)
+    cos, sin = tables(dtype, S, gpu)
+    seq_t, len_t = torch.tensor(seqs, dtype=torch.int32), torch.tensor(lens, dtype=torch.int32)
+    bal, cap = kernels.balanced_splits(rows, 256)
+    ws = DecodeWorkspace.allocate(rows, cap, gpu)
+    ws.plan.fill_(-7)
+    out = kernels.decode_attention(q_abs.to(gpu), q_pe.to(gpu), cos, sin, cache, SCALE, row_seq=seq_t.to(gpu),
+                                   kv_len=len_t.to(gpu), q_rope_pos=rp.to(gpu), n_splits=cap, min_chunk=64,
+                                   workspace=ws, balance=bal)
+    torch.cuda.synchronize()
+    clamped = [0 if s >= B else min(L, S) for s, L in zip(seqs, lens)]
+    assert int(ws.plan.item()) == kernels.balanced_chunk(clamped, cap, 64, bal)
+    q_pe_rot = lo.rope_interleaved(q_pe, cos.cpu()[rp.long()][:, None], sin.cpu()[rp.long()][:, None])
+    seq_ref = torch.tensor([min(s, B - 1) for s in seqs], dtype=torch.int32)
+    ref, _ = lo.absorbed_attention_f64(q_abs, q_pe_rot, cache.ckv.cpu(), kpe, torch.tensor(clamped, dtype=torch.int32),
+                                       seq_ref, SCALE, cache.scale.cpu() if fp8 else None)
+    tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
+    close(out, ref, **tol)
+    assert bool((out[1].float() == 0).all()) and bool((out[10].float() == 0).all())
+
+
+def test_balanced_plan_follows_lengths_in_graph_replays(gpu):
+    """The plan is computed in the launch, so a captured graph replayed with
+    new lengths re-balances: each replay equals an eager fixed-plan call on the
+    same lengths (decode with the split merge fused into W_uv, as MLA runs it)."""
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(23)
+    B, S, Dv = 24, 6000, 128
+    cache = LatentCache(torch.randn(B, S, R, generator=g).to(dtype).to(gpu),
+                        torch.randn(B, S, P, generator=g).to(dtype).to(gpu))
+    cos, sin = tables(dtype, S, gpu)
+    q_abs = torch.randn(B, H, R, generator=g).to(dtype).to(gpu)
+    q_pe = torch.randn(B, H, P, generator=g).to(dtype).to(gpu)
+    w_uv = (0.05 * torch.randn(H, Dv, R, generator=g)).to(dtype).to(gpu)
+    sp = torch.zeros(B, dtype=torch.int32, device=gpu)
+    bal, cap = kernels.balanced_splits(B, 256)
+    ws = DecodeWorkspace.allocate(B, cap, gpu)
+    o_lat = torch.empty(B, H, R, dtype=dtype, device=gpu)
+    y = torch.empty(B, H, Dv, dtype=dtype, device=gpu)
+
+    def step():
+        kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE, start_pos=sp, n_splits=cap, min_chunk=64,
+                                 out=o_lat, workspace=ws, merge=False, balance=bal)
+        kernels.merge_project(o_lat, w_uv, y, cache, n_splits=cap, min_chunk=64, workspace=ws, start_pos=sp,
+                              balanced=True)
+
+    def fixed(lengths_sp):
+        ns, mc = kernels.plan_splits(B, S)
+        w2 = DecodeWorkspace.allocate(B, ns, gpu)
+        o2 = torch.empty(B, H, R, dtype=dtype, device=gpu)
+        y2 = torch.empty(B, H, Dv, dtype=dtype, device=gpu)
+        kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE, start_pos=lengths_sp, n_splits=ns,
+                                 min_chunk=mc, out=o2, workspace=w2, merge=False)
+        kernels.merge_project(o2, w_uv, y2, cache, n_splits=ns, min_chunk=mc, workspace=w2, start_pos=lengths_sp)
+        return y2
+
+    rng = np.random.default_rng(24)
+    sp.copy_(torch.tensor(rng.integers(0, S, B), dtype=torch.int32))
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for i in range(4):
+        lens = rng.integers(0, S, B) if i != 2 else np.full(B, S - 1)
+        if i == 3:
+            lens[:20] = 5  # a few long rows among short ones
+        new_sp = torch.tensor(lens, dtype=torch.int32, device=gpu)
+        sp.copy_(new_sp)
+        y.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = fixed(new_sp.clone())
+        torch.cuda.synchronize()
+        clamped = [min(int(v) + 1, S) for v in lens]
+        assert int(ws.plan.item()) == kernels.balanced_chunk(clamped, cap, 64, bal)
+        err = float((y.float() - want.float()).abs().max())
+        assert err <= 2 ** -7 * float(want.float().abs().max()) + 1e-3, (i, err)

@@ -139,10 +139,12 @@ def test_config1_prefill_512_then_decode(gpu, dtype):
     close(ours.kv_cache[:1, :528], ref.kv_cache[:1, :528], dtype)
 
 
-def test_per_sequence_start_pos(gpu):
+@pytest.mark.parametrize("split_plan", ["auto", "static"])
+def test_per_sequence_start_pos(gpu, split_plan):
     """Ragged batch through a start_pos tensor equals each sequence run alone
-    through the reference (whose interface takes one int per call)."""
-    say("ragged start_pos")
+    through the reference (whose interface takes one int per call), with the
+    device-balanced split plan (auto, for a tensor) and the per-row one."""
+    say(f"ragged start_pos, split_plan={split_plan}")
     dtype = torch.bfloat16
     cfg = MLAConfig(n_embd=256, max_batch_size=3, max_seq_len=128)
     lens = [40, 7, 90]
@@ -156,6 +158,7 @@ def test_per_sequence_start_pos(gpu):
             r(prompts[i], 0)
             refs.append(r(step[i:i + 1], lens[i]))
     _, ours = make_pair(cfg, 24, dtype, gpu)
+    ours.split_plan = split_plan
     with torch.no_grad():
         # fill each batch slot with its own prompt through the append path
         # (padding rows beyond a slot's length are overwritten by the step)
