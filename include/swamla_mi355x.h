@@ -17,9 +17,15 @@
  *   SWAMLA_DTYPE_FP8   OCP float8 e4m3fn with one fp32 scale per cached token
  *                      (latent c_kv only; k_pe stays in the model dtype)
  *
- * Fixed geometry of this build: kv_lora_rank R = 256, qk_rope_head_dim P = 64,
- * heads H = 16 (the BASELINE configurations).  Other values return
- * SWAMLA_ERR_UNSUPPORTED.
+ * Geometry of this build: heads H = 16, qk_rope_head_dim P = 64 and any
+ * kv_lora_rank 1 <= R <= 512 (the real model scales the rank per layer).
+ * Other values return SWAMLA_ERR_UNSUPPORTED.  Latent rows are laid out with
+ * R_pad = 64 * ceil(R / 64) channels (R_pad = R for the BASELINE rank 256):
+ * caches, queries, outputs, partials and the latent half of input rows hold
+ * R_pad values per token / head.  The kernels write zeros into channels
+ * R .. R_pad-1 of cache rows and outputs and ignore those channels of their
+ * inputs, except that a cache's padding must hold the zeros mla_append wrote
+ * (a zero-filled allocation does).
  */
 #ifndef SWAMLA_MI355X_H
 #define SWAMLA_MI355X_H
@@ -72,14 +78,17 @@ const char* mla_last_error(void);
  * pe_cache at [:bsz, start_pos:end_pos]).
  *
  * kv_in        [n_tok, in_row_stride] rows in in_dtype; columns 0..R-1 are the
- *              latent c, R..R+P-1 are k_pe (the wkv_a output, no copy needed).
+ *              latent c (R..R_pad-1 ignored), R_pad..R_pad+P-1 are k_pe (for
+ *              R = R_pad the wkv_a output itself, no copy needed).
  * seq_idx, dst_pos, rope_pos   explicit addressing: cache row, cache position
  *              and RoPE table row of each token.
  * start_pos, tokens_per_seq, rope_abs   dense addressing (see above).
- * ln_w, ln_b   [R] LayerNorm affine parameters in in_dtype; eps as in torch.
+ * ln_w, ln_b   [R_pad] LayerNorm affine parameters in in_dtype (entries
+ *              R.. ignored); eps as in torch.
  * cos_tab,     [rope_len, P/2] in in_dtype: the first P/2 columns of the
  * sin_tab      reference cos_cached / sin_cached (positional_encoding.py:21-28).
- * ckv_cache    [cache_batch, cache_seq, R] in cache_dtype (u8 codes for FP8).
+ * ckv_cache    [cache_batch, cache_seq, R_pad] in cache_dtype (u8 codes for
+ *              FP8); the LayerNorm covers the R channels, R.. are written 0.
  * kpe_cache    [cache_batch, cache_seq, P] in in_dtype.
  * ckv_scale    [cache_batch, cache_seq] fp32, written only for FP8 (else NULL).
  * err_flag     optional device int32; a token whose cache row / position /
@@ -110,7 +119,8 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok,
  * Query row r attends to its cache row over positions [0, L): explicit mode
  * row_seq[r], L = kv_len[r], RoPE row q_rope_pos[r]; dense mode L = start +
  * r % T + 1 (causal, bottom-right for a prefill chunk).
- * q_abs        row r, head h at q_abs + r*q_abs_rs + h*q_abs_hs, R values.
+ * q_abs        row r, head h at q_abs + r*q_abs_rs + h*q_abs_hs, R_pad values
+ *              read (channels R.. ignored).
  * q_pe         row r, head h at q_pe + r*q_pe_rs + h*q_pe_hs, P values before
  *              RoPE; rotated in-kernel.
  * Split-KV: each row is cut into ns = ceil(L / chunk) splits of
@@ -128,9 +138,10 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok,
  * *plan (int32, may be NULL) for mla_merge / mla_merge_project.  Needs
  * n_rows <= balance_blocks, n_rows <= 256 and cache_seq <= 2^24.
  * Rows with ns == 1 are written straight to o_lat.  Others write normalised
- * partials o_part [n_rows, n_splits, H, R] fp32 and log-sum-exp lse_part
+ * partials o_part [n_rows, n_splits, H, R_pad] fp32 and log-sum-exp lse_part
  * [n_rows, n_splits, H] (natural log of sum exp(s)) that mla_merge combines.
- * o_lat        row r, head h at o_lat + r*o_rs + h*o_hs, R values, in dtype.
+ * o_lat        row r, head h at o_lat + r*o_rs + h*o_hs, R_pad values (R..
+ *              written 0), in dtype.
  */
 int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
                     const void* q_pe, int64_t q_pe_rs, int64_t q_pe_hs,
@@ -161,8 +172,10 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
  * the k_pe RoPE uses cos_tab / sin_tab at the row's RoPE row).  The other
  * arguments are those of mla_decode_attn with row_seq / kv_len / q_rope_pos
  * absent and rows_per_seq = 1.  bf16 models only (bf16 or e4m3 cache).
- * kv_in, ln_w and ln_b need 8-byte aligned bases and in_row_stride a
- * multiple of 4.
+ * A lane reads the R_pad / 64 channels it owns at once: kv_in, ln_w and
+ * ln_b need bases aligned to A bytes, A the largest power of two from 4 to
+ * 16 that divides 2 * (R_pad / 64) (4 if none does; 8 for R = 256), and
+ * in_row_stride a multiple of A / 2 elements.
  * Results are identical to mla_append followed by mla_decode_attn.
  */
 int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
@@ -192,7 +205,8 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
  * Arguments as mla_decode_attn's dense mode (start_pos [n_rows / T],
  * tokens_per_seq = T, rope_abs), without split-KV: o_lat is written
  * directly.  One workgroup serves eight consecutive tokens of a sequence,
- * so each cache tile is read once per eight queries.  bf16 models only (bf16
+ * so each cache tile is read once per eight queries.  kv_lora_rank up to 256
+ * (larger ranks: mla_decode_attn).  bf16 models only (bf16
  * or e4m3 cache).
  */
 int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
@@ -283,8 +297,9 @@ int mla_linear_packed(const void* x, int64_t x_rs, const void* w_packed,
  * Row lengths and splits are derived exactly as mla_decode_attn does (same
  * addressing arguments, same cache_batch / cache_seq clamping; plan as for
  * mla_merge).
- * w            head h, output d at w + h*w_hs + d*w_rs, R values (a view of
- *              wkv_b.weight: w_hs = (nope + Dv)*R, w_rs = R, base + nope*R).
+ * w            head h, output d at w + h*w_hs + d*w_rs, R_pad values (for R =
+ *              R_pad a view of wkv_b.weight: w_hs = (nope + Dv)*R, w_rs = R,
+ *              base + nope*R; otherwise a zero-padded copy).
  * y            row r, head h at y + r*y_rs + h*y_hs, Dv values (wo's input
  *              [rows, H*Dv]: y_rs = H*Dv, y_hs = Dv).
  * o_part / lse_part may be NULL when n_splits == 1.  bf16 only, Dv = 128.

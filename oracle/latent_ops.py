@@ -64,20 +64,38 @@ def _butterfly(s: np.ndarray) -> np.ndarray:
 
 def layernorm_f64(c: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np.ndarray:
     """kv_norm (mla.py:107, :409) in fp64 with the append kernel's reduction
-    order: lane l holds channels 4l..4l+3 summed left to right, then an xor
-    butterfly.  Returns unrounded fp64 y [N, 256].  ``eps`` is used as its
-    fp32 value, as torch's LayerNorm does.  Pinned against
-    torch.nn.functional.layer_norm in fp64 (agreement ~1e-15) and the mean-0 /
-    var-1 invariants."""
-    x = np.asarray(c, dtype=np.float64).reshape(-1, 64, 4)
-    s = ((x[..., 0] + x[..., 1]) + x[..., 2]) + x[..., 3]
-    mean = _butterfly(s)[..., :1] * (1.0 / 256.0)  # [N, 1]
-    d = x - mean[..., None]
-    q = ((d[..., 0] * d[..., 0] + d[..., 1] * d[..., 1]) + d[..., 2] * d[..., 2]) + d[..., 3] * d[..., 3]
-    var = _butterfly(q)[..., :1] * (1.0 / 256.0)
+    order, for any rank R = c.shape[-1] up to 512: the row is padded with
+    zeros to R_pad = 64 * ceil(R / 64), lane l holds channels K*l .. K*l+K-1
+    (K = R_pad / 64) summed left to right (padding adds +0.0), then an xor
+    butterfly, divided by R; the variance sums only the R real channels.
+    Returns unrounded fp64 y [N, R].  ``eps`` is used as its fp32 value, as
+    torch's LayerNorm does.  Pinned against torch.nn.functional.layer_norm in
+    fp64 (agreement ~1e-15) and the mean-0 / var-1 invariants; for R = 256
+    the order is lane l holding channels 4l..4l+3."""
+    x0 = np.asarray(c, dtype=np.float64)
+    Rr = x0.shape[-1]
+    K = -(-Rr // 64)
+    rp = 64 * K
+    x = np.zeros(x0.shape[:-1] + (rp,), dtype=np.float64)
+    x[..., :Rr] = x0
+    x = x.reshape(-1, 64, K)
+    valid = (np.arange(rp) < Rr).reshape(64, K)
+    s = x[..., 0].copy()
+    for i in range(1, K):
+        s = s + x[..., i]
+    mean = _butterfly(s)[..., :1] / float(Rr)  # [N, 1]
+    d = np.where(valid, x - mean[..., None], 0.0)
+    q = d[..., 0] * d[..., 0]
+    for i in range(1, K):
+        q = q + d[..., i] * d[..., i]
+    var = _butterfly(q)[..., :1] / float(Rr)
     rstd = 1.0 / np.sqrt(var + float(np.float32(eps)))
-    y = (d * rstd[..., None]) * np.asarray(w, np.float64).reshape(64, 4) + np.asarray(b, np.float64).reshape(64, 4)
-    return y.reshape(-1, 256)
+    wp = np.zeros(rp, np.float64)
+    bp = np.zeros(rp, np.float64)
+    wp[:Rr] = np.asarray(w, np.float64).reshape(-1)
+    bp[:Rr] = np.asarray(b, np.float64).reshape(-1)
+    y = np.where(valid, (d * rstd[..., None]) * wp.reshape(64, K) + bp.reshape(64, K), 0.0)
+    return y.reshape(-1, rp)[:, :Rr]
 
 
 def layernorm_exact(c, w, b, eps: float, dtype: torch.dtype) -> torch.Tensor:

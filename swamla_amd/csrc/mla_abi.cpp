@@ -32,10 +32,21 @@ int ok() {
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
 int check_geometry(int32_t H, int32_t R, int32_t P) {
-  if (H != 16 || R != 256 || P != 64)
+  if (H != 16 || P != 64 || R < 1 || R > 64 * swamla::kMaxNB)
     return fail(SWAMLA_ERR_UNSUPPORTED,
-                "unsupported geometry H=%d R=%d P=%d (this build: H=16, R=256, P=64)", H, R, P);
+                "unsupported geometry H=%d R=%d P=%d (this build: H=16, P=64, 1 <= R <= %d)", H, R, P,
+                64 * swamla::kMaxNB);
   return SWAMLA_OK;
+}
+
+// Bytes a lane of the append arithmetic moves at once: its R_pad / 64 bf16
+// channels, as the widest power of two dividing them (at least 4: the k_pe
+// pair is one 4-byte word), at most 16.
+uintptr_t lane_align(int32_t R) {
+  const int b = 2 * (swamla::padded_rank(R) / 64);
+  uintptr_t a = 16;
+  while (a > 4 && b % a != 0) a >>= 1;
+  return a;
 }
 
 // Element size of the model (query/output/k_pe) dtype; 0 if not a model dtype.
@@ -131,9 +142,10 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const in
     return e;
   if (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: fp8 cache needs ckv_scale");
-  if (in_row_stride < R + P)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: in_row_stride=%lld < R+P=%d",
-                (long long)in_row_stride, R + P);
+  const int RP = swamla::padded_rank(R);
+  if (in_row_stride < RP + P)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: in_row_stride=%lld < R_pad+P=%d",
+                (long long)in_row_stride, RP + P);
   if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_append: bad cache shape [%lld, %lld]",
                 (long long)cache_batch, (long long)cache_seq);
@@ -143,7 +155,7 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const in
       !aligned(ln_w, es) || !aligned(ln_b, es) || !aligned(cos_tab, es) || !aligned(sin_tab, es) ||
       (ckv_scale && !aligned(ckv_scale, 4)))
     return fail(SWAMLA_ERR_MISALIGNED, "mla_append: ckv_cache must be 16-byte aligned, others element-aligned");
-  swamla::AppendArgs a{kv_in,    in_row_stride, n_tok,     ad,          ln_w,      ln_b,    eps,
+  swamla::AppendArgs a{kv_in,    in_row_stride, n_tok,     R,           ad,        ln_w,    ln_b,    eps,
                        cos_tab,  sin_tab,       rope_len,  ckv_cache,   kpe_cache, ckv_scale,
                        cache_batch, cache_seq,  err_flag};
   const int rc = swamla::launch_append(a, in_dtype, cache_dtype, static_cast<hipStream_t>(stream));
@@ -196,8 +208,9 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
     return fail(SWAMLA_ERR_INVALID_ARG, "%s: fp8 cache needs ckv_scale", fn);
   if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1 || rope_len < 1)
     return fail(SWAMLA_ERR_INVALID_ARG, "%s: bad cache / rope table shape", fn);
-  if (q_abs_hs < R || q_pe_hs < P || o_hs < R || q_abs_rs < 0 || q_pe_rs < 0 || o_rs < 0)
-    return fail(SWAMLA_ERR_INVALID_ARG, "%s: head strides must cover R / P values", fn);
+  const int RP = swamla::padded_rank(R);
+  if (q_abs_hs < RP || q_pe_hs < P || o_hs < RP || q_abs_rs < 0 || q_pe_rs < 0 || o_rs < 0)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: head strides must cover R_pad / P values", fn);
   if (dtype == SWAMLA_DTYPE_BF16) {
     // 16-byte vector loads / stores of 8 bf16.
     if (!aligned(q_abs, 16) || !aligned(q_pe, 16) || !aligned(o_lat, 16) || !aligned(ckv_cache, 16) ||
@@ -217,7 +230,7 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
       (ckv_scale && !aligned(ckv_scale, 4)))
     return fail(SWAMLA_ERR_MISALIGNED, "%s: o_part must be 16-byte aligned", fn);
   const float log2e = 1.4426950408889634f;
-  *a = swamla::DecodeArgs{q_abs,     q_abs_rs,  q_abs_hs,  q_pe,      q_pe_rs,     q_pe_hs,
+  *a = swamla::DecodeArgs{R,         q_abs,     q_abs_rs,  q_abs_hs,  q_pe,      q_pe_rs,     q_pe_hs,
                           cos_tab,   sin_tab,   rope_len,  ckv_cache, kpe_cache,   ckv_scale,
                           cache_batch, cache_seq, ad,      n_rows,    sm_scale * log2e, n_splits,
                           min_chunk, balance,   plan,      o_part,    lse_part,  o_lat,
@@ -273,16 +286,20 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
     return e;
   if (n_rows > 0 && !kv_in) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null input rows", fn);
   if (!ln_w || !ln_b) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null LayerNorm pointer", fn);
-  if (in_row_stride < R + P)
-    return fail(SWAMLA_ERR_INVALID_ARG, "%s: in_row_stride=%lld < R+P=%d", fn, (long long)in_row_stride, R + P);
-  // a lane reads four channels of the row and of the LayerNorm parameters at once
-  if ((kv_in && !aligned(kv_in, 8)) || in_row_stride % 4 != 0 || !aligned(ln_w, 8) || !aligned(ln_b, 8) ||
+  const int RP = swamla::padded_rank(R);
+  if (in_row_stride < RP + P)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: in_row_stride=%lld < R_pad+P=%d", fn, (long long)in_row_stride,
+                RP + P);
+  // a lane reads its R_pad / 64 channels of the row and of the LayerNorm
+  // parameters at once
+  const uintptr_t la = lane_align(R);
+  if ((kv_in && !aligned(kv_in, la)) || in_row_stride % (la / 2) != 0 || !aligned(ln_w, la) || !aligned(ln_b, la) ||
       !aligned(cos_tab, 2) || !aligned(sin_tab, 2))
     return fail(SWAMLA_ERR_MISALIGNED,
-                "%s: input rows and LayerNorm parameters need 8-byte aligned bases and a row stride that is a "
-                "multiple of 4 elements", fn);
+                "%s: input rows and LayerNorm parameters need %d-byte aligned bases and a row stride that is a "
+                "multiple of %d elements", fn, static_cast<int>(la), static_cast<int>(la / 2));
   if (n_rows == 0) return ok();
-  a.fa = swamla::AppendArgs{kv_in,   in_row_stride, n_rows,      a.ad,      ln_w,      ln_b,   eps,
+  a.fa = swamla::AppendArgs{kv_in,   in_row_stride, n_rows,      R,         a.ad,      ln_w,      ln_b,   eps,
                             cos_tab, sin_tab,       rope_len,    ckv_cache, kpe_cache, ckv_scale,
                             cache_batch, cache_seq, err_flag};
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
@@ -301,6 +318,9 @@ int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, cons
   if (dtype != SWAMLA_DTYPE_BF16)
     return fail(SWAMLA_ERR_UNSUPPORTED, "%s: model dtype %d not built (bf16 only)", fn, dtype);
   if (!start_pos) return fail(SWAMLA_ERR_INVALID_ARG, "%s: needs dense addressing (start_pos)", fn);
+  if (swamla::padded_rank(R) > 256)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "%s: kv_lora_rank %d above 256 (the per-row mla_decode_attn path serves it)",
+                fn, R);
   swamla::DecodeArgs a;
   if (int e = check_decode(fn, q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab, sin_tab, rope_len,
                            ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, nullptr, nullptr, nullptr,
@@ -335,13 +355,13 @@ int mla_merge(const float* o_part, const float* lse_part, const int32_t* row_seq
   if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: bad cache shape");
   if (!o_part || !lse_part || !o_lat) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: null pointer");
-  if (o_hs < R || o_rs < 0) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: bad output strides");
+  if (o_hs < swamla::padded_rank(R) || o_rs < 0) return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: bad output strides");
   // a lane writes 4 channels: 16 B (fp32) or 8 B (bf16)
   if (!aligned(o_part, 16) || !aligned(o_lat, dtype == SWAMLA_DTYPE_F32 ? 16 : 8) || (o_rs | o_hs) % 4 != 0 ||
       (plan && !aligned(plan, 4)))
     return fail(SWAMLA_ERR_MISALIGNED, "mla_merge: misaligned partials, plan or output");
   swamla::MergeArgs a{o_part, lse_part, ad,   cache_batch, cache_seq, n_rows, n_splits,
-                      min_chunk, plan, o_lat, o_rs, o_hs, lse_out};
+                      min_chunk, plan, R, o_lat, o_rs, o_hs, lse_out};
   const int rc = swamla::launch_merge(a, dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: no kernel for dtype %d", dtype);
   if (rc != 0) return hip_fail("mla_merge");
@@ -436,14 +456,15 @@ int mla_merge_project(const float* o_part, const float* lse_part, const void* o_
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: n_splits > 1 needs o_part and lse_part");
   if (cache_batch < 1 || cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: bad cache shape");
-  if (o_hs < R || w_rs < R || y_hs < Dv || o_rs < 0 || w_hs < 0 || y_rs < 0)
-    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: strides must cover R / Dv values");
+  if (o_hs < swamla::padded_rank(R) || w_rs < swamla::padded_rank(R) || y_hs < Dv || o_rs < 0 || w_hs < 0 ||
+      y_rs < 0)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge_project: strides must cover R_pad / Dv values");
   if (!aligned(o_lat, 16) || !aligned(w, 16) || !aligned(y, 2) || (o_part && !aligned(o_part, 16)) ||
       (lse_part && !aligned(lse_part, 4)) || (plan && !aligned(plan, 4)) || (o_rs | o_hs | w_rs | w_hs) % 8 != 0)
     return fail(SWAMLA_ERR_MISALIGNED,
                 "mla_merge_project: o_lat and w need 16-byte aligned bases and strides that are multiples of 8");
   swamla::MergeProjectArgs a{o_part, lse_part, o_lat, o_rs, o_hs, ad, cache_batch, cache_seq, n_rows,
-                             n_splits, min_chunk, plan, w, w_rs, w_hs, y, y_rs, y_hs};
+                             n_splits, min_chunk, plan, R, w, w_rs, w_hs, y, y_rs, y_hs};
   const int rc = swamla::launch_merge_project(a, static_cast<hipStream_t>(stream));
   if (rc != 0) return hip_fail("mla_merge_project");
   return ok();

@@ -7,6 +7,11 @@
 
 namespace swamla {
 
+constexpr int kMaxNB = 8;  // latent rows of at most 64 kMaxNB = 512 channels (kv_lora_rank)
+
+// Padded latent width of a rank: R_pad = 64 ceil(R / 64).
+inline constexpr int padded_rank(int R) { return 64 * ((R + 63) / 64); }
+
 // Where token / query-row positions come from.  Explicit mode: per-entry
 // arrays.  Dense mode (start_pos != nullptr): entry i belongs to sequence
 // i / T at position start_pos[i / T] + i % T, the layout of the reference's
@@ -21,9 +26,10 @@ struct Addressing {
 };
 
 struct AppendArgs {
-  const void* kv_in;
+  const void* kv_in;  // rows [R_pad latent | P rope]
   int64_t in_rs;
   int n_tok;
+  int R;  // kv_lora_rank; rows are R_pad = 64 ceil(R / 64) channels
   Addressing ad;
   const void* ln_w;
   const void* ln_b;
@@ -40,6 +46,7 @@ struct AppendArgs {
 };
 
 struct DecodeArgs {
+  int R;  // kv_lora_rank; latent rows (cache, queries, outputs) are R_pad = 64 ceil(R / 64) channels
   const void* q_abs;
   int64_t qa_rs, qa_hs;
   const void* q_pe;
@@ -77,6 +84,7 @@ struct MergeArgs {
   int64_t cache_b, cache_s;
   int n_rows, n_splits, min_chunk;
   const int32_t* plan;  // balanced plan: the chunk the decode launch chose (else null)
+  int R;                // kv_lora_rank (rows of R_pad channels)
   void* o_lat;
   int64_t o_rs, o_hs;
   float* lse_out;
@@ -107,6 +115,7 @@ struct MergeProjectArgs {
   int64_t cache_b, cache_s;
   int n_rows, n_splits, min_chunk;
   const int32_t* plan;  // balanced plan: the chunk the decode launch chose (else null)
+  int R;                // kv_lora_rank (rows of R_pad channels)
   const void* w;
   int64_t w_rs, w_hs;
   void* y;

@@ -10,10 +10,12 @@
 
 namespace swamla {
 
-constexpr int kR = 256;
 constexpr int kP = 64;
 constexpr int kH = 16;
-constexpr int kKC = kR + kP;  // 320 channels scored per cached token
+// Latent rows: kv_lora_rank R is stored padded to R_pad = 64 NB channels
+// (NB = ceil(R / 64), at most kMaxNB); channels R .. R_pad - 1 hold zeros.
+// Kernels are instantiated per NB; R itself only enters the LayerNorm and
+// the masking of query padding.
 
 // ---------------------------------------------------------------------------
 // Small helpers
@@ -79,57 +81,123 @@ __device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xo
 // The arithmetic below is shared by the append kernel and the decode kernel's
 // fused one-token append, so both write identical bits.
 
-// LayerNorm of one R = 256 channel row held by a wavefront, lane owning
-// channels 4*lane .. 4*lane+3.  Every multiply / add is rounded on its own:
-// the result must reproduce the fixed-order fp64 statement exactly.
-// Statistics in fp64; fixed order: in-lane left-to-right, then xor butterfly
-// 1,2,4,...,32 (every lane ends with the same total).
-__device__ __forceinline__ void layernorm_quad(const double x[4], const double wt[4], const double bs[4],
-                                               float eps, double y[4]) {
+// LayerNorm of one latent row held by a wavefront, lane owning the K = R_pad /
+// 64 channels K*lane .. K*lane + K - 1.  Channels >= R are padding: they take
+// no part in the statistics and come out as exactly 0.  Every multiply / add
+// is rounded on its own: the result must reproduce the fixed-order fp64
+// statement exactly.  Statistics in fp64; fixed order: in-lane left to
+// right, then xor butterfly 1,2,4,...,32 (every lane ends with the same total),
+// divided by R.
+template <int K>
+__device__ __forceinline__ void layernorm_lane(const double (&x)[K], const double (&wt)[K], const double (&bs)[K],
+                                               int R, int lane, float eps, double (&y)[K]) {
 #pragma clang fp contract(off)
-  double s = ((x[0] + x[1]) + x[2]) + x[3];
+  bool v[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) v[i] = K * lane + i < R;
+  double s = v[0] ? x[0] : 0.0;
+#pragma unroll
+  for (int i = 1; i < K; ++i) s = s + (v[i] ? x[i] : 0.0);
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) s = s + shfl_xor_f64(s, m);
-  const double mean = s * (1.0 / 256.0);
-  double d[4];
+  const double mean = s / static_cast<double>(R);
+  double d[K];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) d[i] = x[i] - mean;
-  double q = ((d[0] * d[0] + d[1] * d[1]) + d[2] * d[2]) + d[3] * d[3];
+  for (int i = 0; i < K; ++i) d[i] = v[i] ? x[i] - mean : 0.0;
+  double q = d[0] * d[0];
+#pragma unroll
+  for (int i = 1; i < K; ++i) q = q + d[i] * d[i];
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) q = q + shfl_xor_f64(q, m);
-  const double var = q * (1.0 / 256.0);
+  const double var = q / static_cast<double>(R);
   // correctly rounded square root and IEEE division
   const double rstd = 1.0 / __dsqrt_rn(var + static_cast<double>(eps));
 #pragma unroll
-  for (int i = 0; i < 4; ++i) y[i] = (d[i] * rstd) * wt[i] + bs[i];
+  for (int i = 0; i < K; ++i) y[i] = v[i] ? (d[i] * rstd) * wt[i] + bs[i] : 0.0;
 }
 
-// bf16 cache: the four channels rounded once from fp64.
-__device__ __forceinline__ uint2 encode_bf16_quad(const double y[4]) {
-  uint2 o;
-  o.x = f64_to_bf16(y[0]) | (static_cast<uint32_t>(f64_to_bf16(y[1])) << 16);
-  o.y = f64_to_bf16(y[2]) | (static_cast<uint32_t>(f64_to_bf16(y[3])) << 16);
-  return o;
+// bf16 cache: each channel rounded once from fp64.
+template <int K>
+__device__ __forceinline__ void encode_bf16_lane(const double (&y)[K], uint16_t (&o)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) o[i] = f64_to_bf16(y[i]);
 }
 
-// e4m3 per-token: y is first rounded to bf16 (the value a bf16 cache would
+// e4m3 per token: y is first rounded to bf16 (the value a bf16 cache would
 // hold), amax over the token, scale = max(amax,1e-12)/448, code = RNE(y/scale).
-// Returns the lane's four codes (byte i = channel 4*lane+i).
-__device__ __forceinline__ uint32_t encode_e4m3_quad(const double y[4], float& scale) {
-  float yb[4];
+// Padding channels (y = 0) encode as 0.
+template <int K>
+__device__ __forceinline__ void encode_e4m3_lane(const double (&y)[K], uint8_t (&codes)[K], float& scale) {
+  float yb[K];
   float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < K; ++i) {
     yb[i] = bf16_to_f32(f64_to_bf16(y[i]));
     amax = fmaxf(amax, fabsf(yb[i]));
   }
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, m));
   scale = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
-  uint32_t codes = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) codes |= static_cast<uint32_t>(f32_to_e4m3(__fdiv_rn(yb[i], scale))) << (8 * i);
-  return codes;
+  for (int i = 0; i < K; ++i) codes[i] = f32_to_e4m3(__fdiv_rn(yb[i], scale));
+}
+
+// K consecutive 16-bit / 8-bit values of one lane, moved with the widest
+// vector the lane's offset (a multiple of K elements) keeps aligned.
+template <int K, typename U>
+__device__ __forceinline__ void load_lane(const U* p, U (&v)[K]) {
+  constexpr int B = K * static_cast<int>(sizeof(U));
+  if constexpr (B % 16 == 0) {
+#pragma unroll
+    for (int c = 0; c < B / 16; ++c) {
+      const uint4 t = reinterpret_cast<const uint4*>(p)[c];
+      __builtin_memcpy(reinterpret_cast<uint8_t*>(v) + 16 * c, &t, 16);
+    }
+  } else if constexpr (B % 8 == 0) {
+#pragma unroll
+    for (int c = 0; c < B / 8; ++c) {
+      const uint2 t = reinterpret_cast<const uint2*>(p)[c];
+      __builtin_memcpy(reinterpret_cast<uint8_t*>(v) + 8 * c, &t, 8);
+    }
+  } else if constexpr (B % 4 == 0) {
+#pragma unroll
+    for (int c = 0; c < B / 4; ++c) {
+      const uint32_t t = reinterpret_cast<const uint32_t*>(p)[c];
+      __builtin_memcpy(reinterpret_cast<uint8_t*>(v) + 4 * c, &t, 4);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) v[i] = p[i];
+  }
+}
+template <int K, typename U>
+__device__ __forceinline__ void store_lane(U* p, const U (&v)[K]) {
+  constexpr int B = K * static_cast<int>(sizeof(U));
+  if constexpr (B % 16 == 0) {
+#pragma unroll
+    for (int c = 0; c < B / 16; ++c) {
+      uint4 t;
+      __builtin_memcpy(&t, reinterpret_cast<const uint8_t*>(v) + 16 * c, 16);
+      reinterpret_cast<uint4*>(p)[c] = t;
+    }
+  } else if constexpr (B % 8 == 0) {
+#pragma unroll
+    for (int c = 0; c < B / 8; ++c) {
+      uint2 t;
+      __builtin_memcpy(&t, reinterpret_cast<const uint8_t*>(v) + 8 * c, 8);
+      reinterpret_cast<uint2*>(p)[c] = t;
+    }
+  } else if constexpr (B % 4 == 0) {
+#pragma unroll
+    for (int c = 0; c < B / 4; ++c) {
+      uint32_t t;
+      __builtin_memcpy(&t, reinterpret_cast<const uint8_t*>(v) + 4 * c, 4);
+      reinterpret_cast<uint32_t*>(p)[c] = t;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < K; ++i) p[i] = v[i];
+  }
 }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -140,10 +208,17 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kSub = 16;                   // tokens per wave in a tile
 constexpr int kWaves = 4;                  // waves per block
 constexpr int kTileTok = kSub * kWaves;    // 64 tokens per lockstep tile
-constexpr int kCRow = 2 * kR + 16;         // 528 B per LDS latent row
 constexpr int kPeRow = 2 * kP + 16;        // 144 B per LDS rope row
-constexpr int kCBytes = kTileTok * kCRow;  // 33792 B
 constexpr int kPeBytes = kTileTok * kPeRow;  // 9216 B
+
+// Latent geometry of an instance: R_pad = 64 NB channels, LDS latent rows of
+// 2 R_pad + 16 bytes (528 for NB = 4).
+template <int NB>
+struct LatGeo {
+  static constexpr int RP = 64 * NB;
+  static constexpr int CRow = 2 * RP + 16;
+  static constexpr int CBytes = kTileTok * CRow;
+};
 constexpr int kPRow = 2 * kTileTok + 8;    // bytes per head row of P (128 + 8 pad: the 16 heads
                                            // of an 8-byte access fall on distinct banks)
 
@@ -151,6 +226,14 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_ca
 __device__ __forceinline__ bf16x8_t cat_bf16x8(s16x4_t lo, s16x4_t hi) {
   const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
   return as_bf16x8(make_uint4(a.x, a.y, b.x, b.y));
+}
+
+// The first n (clamped to 0..8) of eight packed bf16 kept, the rest zeroed.
+__device__ __forceinline__ uint4 mask_bf16x8(uint4 v, int n) {
+  auto m = [n](int k) {
+    return (2 * k < n ? 0x0000FFFFu : 0u) | (2 * k + 1 < n ? 0xFFFF0000u : 0u);
+  };
+  return make_uint4(v.x & m(0), v.y & m(1), v.z & m(2), v.w & m(3));
 }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -187,18 +270,20 @@ __device__ __forceinline__ void lds_barrier() {
 // Registers of one in-flight tile (this wave's 16 tokens), loaded as whole
 // lines: element s of c covers tokens 8(s&1)..+8, bytes 128(s>>1)..+128 of
 // the latent rows (lane: token l%8, 16 B at 16(l/8)); p[j] the same for
-// rope rows, tokens 8j..+8.  e4m3: 4 segments of codes plus the 4 scales this
-// lane's scores need.
-template <int C_DT>
+// rope rows, tokens 8j..+8.  bf16 rows of R_pad = 64 NB channels are NB
+// segments; e4m3 rows are ceil(NB / 2) segments of codes (for odd NB the last
+// one is half a row: its upper lanes re-read the row's first bytes, unused),
+// plus the 4 scales this lane's scores need.
+template <int C_DT, int NB>
 struct KTile;
-template <>
-struct KTile<1> {
-  uint4 c[8];
+template <int NB>
+struct KTile<1, NB> {
+  uint4 c[2 * NB];
   uint4 p[2];
 };
-template <>
-struct KTile<2> {
-  uint4 c[4];
+template <int NB>
+struct KTile<2, NB> {
+  uint4 c[2 * ((NB + 1) / 2)];
   uint4 p[2];
   float4 sc;
 };
@@ -211,6 +296,11 @@ __device__ __forceinline__ uint2 e4m3x4_to_bf16x4_hw(uint32_t w) {
   const uint32_t a = __builtin_amdgcn_perm(f2u(lo[1]), f2u(lo[0]), 0x07060302u);
   const uint32_t b = __builtin_amdgcn_perm(f2u(hi[1]), f2u(hi[0]), 0x07060302u);
   return make_uint2(a, b);
+}
+
+// One e4m3 code as bf16 bits (exact: every e4m3fn value is a bf16 value).
+__device__ __forceinline__ uint16_t e4m3_to_bf16_bits(uint8_t c) {
+  return static_cast<uint16_t>(f2u(e4m3_to_f32(c)) >> 16);
 }
 
 // 16-byte global load marked non-temporal: the cache is streamed once, and

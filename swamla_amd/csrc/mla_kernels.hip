@@ -10,9 +10,12 @@
 // (the prefill kernel is in mla_prefill.hip, shared device code in
 // mla_device.h)
 //
-// Geometry is fixed at R = 256 (kv_lora_rank), P = 64 (rope dim), H = 16.
+// Geometry: P = 64 (rope dim), H = 16; kv_lora_rank R up to 512, stored
+// padded to R_pad = 64 NB channels (kernels are instantiated per NB).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "mla_args.h"
 #include "mla_device.h"
@@ -27,10 +30,11 @@ namespace swamla {
 // IN_DT: 0 fp32 / 1 bf16 (model dtype; also k_pe cache dtype).
 // C_DT : 0 fp32 / 1 bf16 / 2 e4m3 (latent cache dtype).
 // The work of one wavefront: token `tok` of the append.
-template <int IN_DT, int C_DT>
+template <int IN_DT, int C_DT, int NB>
 __device__ __forceinline__ void append_token(const AppendArgs& a, int tok, int lane) {
   using E = Elem<IN_DT>;
   using T = typename E::T;
+  constexpr int RP = 64 * NB;
   const TokAddr ta = tok_addr(a.ad, tok);
   const int b = ta.b, pos = ta.pos, rp = ta.rope;
   if (b < 0 || b >= a.cache_b || pos < 0 || pos >= a.cache_s || rp < 0 || rp >= a.rope_len) {
@@ -41,35 +45,40 @@ __device__ __forceinline__ void append_token(const AppendArgs& a, int tok, int l
   const T* w = static_cast<const T*>(a.ln_w);
   const T* bb = static_cast<const T*>(a.ln_b);
 
-  // --- LayerNorm over c[0..255]: lane owns channels 4*lane .. 4*lane+3.
-  double x[4], wt[4], bs[4], y[4];
+  // --- LayerNorm over c[0..R): lane owns channels NB*lane .. NB*lane+NB-1 of
+  // the R_pad-channel input row and LayerNorm parameters (entries >= R unused).
+  double x[NB], wt[NB], bs[NB], y[NB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[i] = static_cast<double>(E::ld(row, 4 * lane + i));
-    wt[i] = static_cast<double>(E::ld(w, 4 * lane + i));
-    bs[i] = static_cast<double>(E::ld(bb, 4 * lane + i));
+  for (int i = 0; i < NB; ++i) {
+    x[i] = static_cast<double>(E::ld(row, NB * lane + i));
+    wt[i] = static_cast<double>(E::ld(w, NB * lane + i));
+    bs[i] = static_cast<double>(E::ld(bb, NB * lane + i));
   }
-  layernorm_quad(x, wt, bs, a.eps, y);
+  layernorm_lane<NB>(x, wt, bs, a.R, lane, a.eps, y);
 
   const int64_t crow = static_cast<int64_t>(b) * a.cache_s + pos;
   if constexpr (C_DT == 0) {
-    float4 o = make_float4(static_cast<float>(y[0]), static_cast<float>(y[1]),
-                           static_cast<float>(y[2]), static_cast<float>(y[3]));
-    reinterpret_cast<float4*>(static_cast<float*>(a.ckv) + crow * kR)[lane] = o;
+    uint32_t o[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) o[i] = f2u(static_cast<float>(y[i]));
+    store_lane<NB>(static_cast<uint32_t*>(a.ckv) + crow * RP + NB * lane, o);
   } else if constexpr (C_DT == 1) {
-    reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.ckv) + crow * kR)[lane] = encode_bf16_quad(y);
+    uint16_t o[NB];
+    encode_bf16_lane<NB>(y, o);
+    store_lane<NB>(static_cast<uint16_t*>(a.ckv) + crow * RP + NB * lane, o);
   } else {
     float scale;
-    const uint32_t codes = encode_e4m3_quad(y, scale);
-    reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.ckv) + crow * kR)[lane] = codes;
+    uint8_t codes[NB];
+    encode_e4m3_lane<NB>(y, codes, scale);
+    store_lane<NB>(static_cast<uint8_t*>(a.ckv) + crow * RP + NB * lane, codes);
     if (lane == 0) a.ckv_scale[crow] = scale;
   }
 
-  // --- RoPE on k_pe: lanes 0..31 own pair i = lane.
+  // --- RoPE on k_pe (input channels R_pad ..): lanes 0..31 own pair i = lane.
   if (lane < kP / 2) {
     const T* ct = static_cast<const T*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
     const T* st = static_cast<const T*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
-    const float x1 = E::ld(row, kR + 2 * lane), x2 = E::ld(row, kR + 2 * lane + 1);
+    const float x1 = E::ld(row, RP + 2 * lane), x2 = E::ld(row, RP + 2 * lane + 1);
     float o1, o2;
     rope_pair<IN_DT>(x1, x2, E::ld(ct, lane), E::ld(st, lane), o1, o2);
     T* dst = static_cast<T*>(a.kpe) + crow * kP + 2 * lane;
@@ -78,27 +87,28 @@ __device__ __forceinline__ void append_token(const AppendArgs& a, int tok, int l
   }
 }
 
-template <int IN_DT, int C_DT>
+template <int IN_DT, int C_DT, int NB>
 __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= a.n_tok) return;
-  append_token<IN_DT, C_DT>(a, tok, threadIdx.x & 63);
+  append_token<IN_DT, C_DT, NB>(a, tok, threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------------------
-// Split-KV merge of one (row, head) by one wavefront; lane owns 4 channels.
+// Split-KV merge of one (row, head) by one wavefront; lane owns 4 channels of
+// each 256-channel chunk of the R_pad-channel rows.
 //   o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M),  M = max_s lse_s
 // Splits are consumed 8 at a time with all their loads in flight, merged
 // online across chunks (the reference moves with each chunk's maximum).
 // ---------------------------------------------------------------------------
 constexpr float kLn2 = 0.6931471805599453f;
 
+// Channels c0 .. c0+3 of one (row, head); lse_out (lane 0 of the first chunk
+// only) receives the merged log-sum-exp.
 template <int DT>
-__device__ __forceinline__ void merge_head(const float* __restrict__ o_part, const float* __restrict__ lse_part,
-                                           int r, int h, int ns, int n_splits, void* o_lat, int64_t o_rs,
-                                           int64_t o_hs, float* lse_out) {
-  const int lane = threadIdx.x & 63;
-  const int64_t base = static_cast<int64_t>(r) * n_splits * kH + h;  // lse index of split 0
+__device__ __forceinline__ void merge_chunk(const float* __restrict__ o_part, const float* __restrict__ lse_part,
+                                            int64_t base, int c0, int r, int h, int ns, int rp, void* o_lat,
+                                            int64_t o_rs, int64_t o_hs, float* lse_out) {
   float M = -INFINITY, wsum = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s0 = 0; s0 < ns; s0 += 8) {
@@ -109,7 +119,7 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ o_part, con
       const int s = min(s0 + j, ns - 1);  // in range; duplicates are masked below
       const int64_t pi = base + static_cast<int64_t>(s) * kH;
       ls[j] = lse_part[pi];
-      v[j] = reinterpret_cast<const float4*>(o_part + pi * kR)[lane];
+      v[j] = *reinterpret_cast<const float4*>(o_part + pi * rp + c0);
     }
     float mc = -INFINITY;
 #pragma unroll
@@ -139,16 +149,27 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ o_part, con
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
   if constexpr (DT == 0) {
     float* op = static_cast<float*>(o_lat) + r * o_rs + h * o_hs;
-    reinterpret_cast<float4*>(op)[lane] = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    *reinterpret_cast<float4*>(op + c0) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
   } else {
     uint16_t* op = static_cast<uint16_t*>(o_lat) + r * o_rs + h * o_hs;
     uint2 pk;
     pk.x = f32_to_bf16(acc.x * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.y * inv)) << 16);
     pk.y = f32_to_bf16(acc.z * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.w * inv)) << 16);
-    reinterpret_cast<uint2*>(op)[lane] = pk;
+    *reinterpret_cast<uint2*>(op + c0) = pk;
   }
-  if (lse_out && lane == 0) lse_out[static_cast<int64_t>(r) * kH + h] = M + __logf(wsum);
+  if (lse_out) lse_out[static_cast<int64_t>(r) * kH + h] = M + __logf(wsum);
 }
+
+template <int DT>
+__device__ __forceinline__ void merge_head(const float* __restrict__ o_part, const float* __restrict__ lse_part,
+                                           int r, int h, int ns, int n_splits, int rp, void* o_lat, int64_t o_rs,
+                                           int64_t o_hs, float* lse_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t base = static_cast<int64_t>(r) * n_splits * kH + h;  // lse index of split 0
+  for (int c0 = 4 * lane; c0 < rp; c0 += 256) merge_chunk<DT>(o_part, lse_part, base, c0, r, h, ns, rp, o_lat,
+                                                              o_rs, o_hs, lse_out && c0 == 0 ? lse_out : nullptr);
+}
+
 
 // ---------------------------------------------------------------------------
 // Kernel 2: absorbed decode attention, bf16 MFMA (cache bf16 or e4m3).
@@ -190,60 +211,60 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ o_part, con
 // ---------------------------------------------------------------------------
 // ---- Fused one-token append inside the decode kernel (bf16 model).
 // Inputs of one token as loaded by one wavefront: lane owns latent channels
-// 4*lane .. +3 and (lanes 0..31) the k_pe pair `lane`; raw bf16 bits.
+// NB*lane .. +NB-1 (of the R_pad-channel input row and LayerNorm parameters)
+// and (lanes 0..31) the k_pe pair `lane`; raw bf16 bits.
+template <int NB>
 struct FusedIn {
-  uint2 x, wt, bs;
+  uint16_t x[NB], wt[NB], bs[NB];
   uint32_t pe;
   uint16_t c, s;
 };
 
-__device__ __forceinline__ FusedIn fused_load(const AppendArgs& a, int tok, int rope, int lane) {
+template <int NB>
+__device__ __forceinline__ FusedIn<NB> fused_load(const AppendArgs& a, int tok, int rope, int lane) {
   const uint16_t* row = static_cast<const uint16_t*>(a.kv_in) + static_cast<int64_t>(tok) * a.in_rs;
   const int pl = lane & (kP / 2 - 1);  // lanes 32..63 repeat pairs 0..31 (unused)
   const int64_t tab = static_cast<int64_t>(rope) * (kP / 2) + pl;
-  FusedIn f;
-  f.x = *reinterpret_cast<const uint2*>(row + 4 * lane);
-  f.wt = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.ln_w) + 4 * lane);
-  f.bs = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.ln_b) + 4 * lane);
-  f.pe = *reinterpret_cast<const uint32_t*>(row + kR + 2 * pl);
+  FusedIn<NB> f;
+  load_lane<NB>(row + NB * lane, f.x);
+  load_lane<NB>(static_cast<const uint16_t*>(a.ln_w) + NB * lane, f.wt);
+  load_lane<NB>(static_cast<const uint16_t*>(a.ln_b) + NB * lane, f.bs);
+  f.pe = *reinterpret_cast<const uint32_t*>(row + 64 * NB + 2 * pl);
   f.c = static_cast<const uint16_t*>(a.cos_tab)[tab];
   f.s = static_cast<const uint16_t*>(a.sin_tab)[tab];
   return f;
 }
 
-// The token in cache form: `row` is the lane's four latent channels as the
+// The token in cache form: `row` is the lane's NB latent channels as the
 // attention reads them (bf16; for e4m3 the decoded codes), `pe` its rotated
 // k_pe pair, plus the e4m3 codes and scale.
-template <int C_DT>
+template <int C_DT, int NB>
 struct FusedTok {
-  uint2 row;
-  uint32_t pe, codes;
+  uint16_t row[NB];
+  uint8_t codes[NB];
+  uint32_t pe;
   float scale;
 };
 
-__device__ __forceinline__ void bf16x4_to_f64(uint2 v, double o[4]) {
-  o[0] = static_cast<double>(u2f(v.x << 16));
-  o[1] = static_cast<double>(u2f(v.x & 0xFFFF0000u));
-  o[2] = static_cast<double>(u2f(v.y << 16));
-  o[3] = static_cast<double>(u2f(v.y & 0xFFFF0000u));
-}
-
-// Same arithmetic as append_token<1, C_DT>.
-template <int C_DT>
-__device__ __forceinline__ FusedTok<C_DT> fused_compute(const FusedIn& f, float eps, int lane) {
-  double x[4], wt[4], bs[4], y[4];
-  bf16x4_to_f64(f.x, x);
-  bf16x4_to_f64(f.wt, wt);
-  bf16x4_to_f64(f.bs, bs);
-  layernorm_quad(x, wt, bs, eps, y);
-  FusedTok<C_DT> t;
-  t.codes = 0;
+// Same arithmetic as append_token<1, C_DT, NB>.
+template <int C_DT, int NB>
+__device__ __forceinline__ FusedTok<C_DT, NB> fused_compute(const FusedIn<NB>& f, float eps, int R, int lane) {
+  double x[NB], wt[NB], bs[NB], y[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    x[i] = static_cast<double>(bf16_to_f32(f.x[i]));
+    wt[i] = static_cast<double>(bf16_to_f32(f.wt[i]));
+    bs[i] = static_cast<double>(bf16_to_f32(f.bs[i]));
+  }
+  layernorm_lane<NB>(x, wt, bs, R, lane, eps, y);
+  FusedTok<C_DT, NB> t;
   t.scale = 1.f;
   if constexpr (C_DT == 1) {
-    t.row = encode_bf16_quad(y);
+    encode_bf16_lane<NB>(y, t.row);
   } else {
-    t.codes = encode_e4m3_quad(y, t.scale);
-    t.row = e4m3x4_to_bf16x4_hw(t.codes);
+    encode_e4m3_lane<NB>(y, t.codes, t.scale);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) t.row[i] = e4m3_to_bf16_bits(t.codes[i]);
   }
   float o1, o2;
   rope_pair<1>(u2f(f.pe << 16), u2f(f.pe & 0xFFFF0000u), u2f(static_cast<uint32_t>(f.c) << 16),
@@ -252,20 +273,22 @@ __device__ __forceinline__ FusedTok<C_DT> fused_compute(const FusedIn& f, float 
   return t;
 }
 
-template <int C_DT>
-__device__ __forceinline__ void fused_store(const AppendArgs& a, int64_t crow, const FusedTok<C_DT>& t, int lane) {
+template <int C_DT, int NB>
+__device__ __forceinline__ void fused_store(const AppendArgs& a, int64_t crow, const FusedTok<C_DT, NB>& t,
+                                            int lane) {
   if constexpr (C_DT == 1) {
-    reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.ckv) + crow * kR)[lane] = t.row;
+    store_lane<NB>(static_cast<uint16_t*>(a.ckv) + crow * (64 * NB) + NB * lane, t.row);
   } else {
-    reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.ckv) + crow * kR)[lane] = t.codes;
+    store_lane<NB>(static_cast<uint8_t*>(a.ckv) + crow * (64 * NB) + NB * lane, t.codes);
     if (lane == 0) a.ckv_scale[crow] = t.scale;
   }
   if (lane < kP / 2) reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.kpe) + crow * kP)[lane] = t.pe;
 }
 
-template <int C_DT, int DEPTH, bool FUSE>
+template <int C_DT, int DEPTH, bool FUSE, int NB>
 __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t c_lds[kCBytes];
+  constexpr int RP = LatGeo<NB>::RP, kCRow = LatGeo<NB>::CRow;
+  __shared__ __attribute__((aligned(16))) uint8_t c_lds[LatGeo<NB>::CBytes];
   __shared__ __attribute__((aligned(16))) uint8_t pe_lds[kPeBytes];
   __shared__ __attribute__((aligned(16))) uint8_t p_lds[kH * kPRow];
   __shared__ float mx_lds[kWaves][kH];
@@ -339,9 +362,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
   // own input row, RoPE row 0 unless it owns the append) so that no value
   // crosses a branch: the loaded registers are consumed only by fa_wave,
   // well after the tile loads behind them have been issued.
-  FusedIn fin;
+  FusedIn<NB> fin;
   if constexpr (FUSE) {
-    fin = fused_load(a.fa, r, fa_own ? fa_t.rope : 0, lane);
+    fin = fused_load<NB>(a.fa, r, fa_own ? fa_t.rope : 0, lane);
     // keep these loads ahead of the tile loads (they are waited for first)
     asm volatile("" ::: "memory");
   }
@@ -353,17 +376,20 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
 
   // Global loads of this wave's 16 tokens of tile j (tokens clamped into
   // range; the surplus ones are masked in the softmax).
-  auto load_tile = [&](int j, KTile<C_DT>& kt) {
+  auto load_tile = [&](int j, KTile<C_DT, NB>& kt) {
     const int wbase = t0 + j * kTileTok + kSub * w;
     const int64_t row_a = cache_row0 + min(wbase + lt, t_last);
     const int64_t row_b = cache_row0 + min(wbase + 8 + lt, t_last);
     if constexpr (C_DT == 2) {
-      const uint8_t* ca = static_cast<const uint8_t*>(a.ckv) + row_a * kR + 16 * lc;
-      const uint8_t* cb = static_cast<const uint8_t*>(a.ckv) + row_b * kR + 16 * lc;
+      const uint8_t* ca = static_cast<const uint8_t*>(a.ckv) + row_a * RP;
+      const uint8_t* cb = static_cast<const uint8_t*>(a.ckv) + row_b * RP;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        kt.c[2 * q] = ld_stream16(ca + 128 * q);
-        kt.c[2 * q + 1] = ld_stream16(cb + 128 * q);
+      for (int q = 0; q < (NB + 1) / 2; ++q) {
+        // for odd NB the last segment is half a row: its upper lanes re-read
+        // the first half (in the row, not stored)
+        const int col = 128 * q + ((NB & 1) && q == NB / 2 ? 16 * (lc & 3) : 16 * lc);
+        kt.c[2 * q] = ld_stream16(ca + col);
+        kt.c[2 * q + 1] = ld_stream16(cb + col);
       }
       const int tb = wbase + 4 * g;  // scales of the 4 tokens this lane scores
       const float* sp = a.ckv_scale + cache_row0;
@@ -372,10 +398,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
       kt.sc.z = sp[min(tb + 2, t_last)];
       kt.sc.w = sp[min(tb + 3, t_last)];
     } else {
-      const uint8_t* ca = static_cast<const uint8_t*>(a.ckv) + row_a * (2 * kR) + 16 * lc;
-      const uint8_t* cb = static_cast<const uint8_t*>(a.ckv) + row_b * (2 * kR) + 16 * lc;
+      const uint8_t* ca = static_cast<const uint8_t*>(a.ckv) + row_a * (2 * RP) + 16 * lc;
+      const uint8_t* cb = static_cast<const uint8_t*>(a.ckv) + row_b * (2 * RP) + 16 * lc;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < NB; ++q) {
         kt.c[2 * q] = ld_stream16(ca + 128 * q);
         kt.c[2 * q + 1] = ld_stream16(cb + 128 * q);
       }
@@ -386,12 +412,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
   };
 
   // ---- Q^T operand (B of S^T): lane holds head n, channels 32s + 8g..+8.
-  KTile<C_DT> kt[DEPTH];
-  bf16x8_t qb[10];
+  KTile<C_DT, NB> kt[DEPTH];
+  bf16x8_t qb[2 * NB + 2];
   {
     const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + r * a.qa_rs + n * a.qa_hs;
+    // channels >= R (the padding of R_pad) are zeroed
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qb[s] = as_bf16x8(*reinterpret_cast<const uint4*>(qa + 32 * s + 8 * g));
+    for (int s = 0; s < 2 * NB; ++s)
+      qb[s] = as_bf16x8(mask_bf16x8(*reinterpret_cast<const uint4*>(qa + 32 * s + 8 * g), a.R - (32 * s + 8 * g)));
     // q_pe with interleaved RoPE at the row's table position
     const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + r * a.qp_rs + n * a.qp_hs;
     int rp = ra.rope;
@@ -427,51 +455,53 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
                      bf16_to_f32(sj), o1, o2);
         wv[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
       }
-      qb[8 + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
+      qb[2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
     }
   }
 
   // The new token in cache form (fused append), computed while the first
   // tiles load.
-  FusedTok<C_DT> ftok;
+  FusedTok<C_DT, NB> ftok;
   if constexpr (FUSE)
-    if (fa_wave) ftok = fused_compute<C_DT>(fin, a.fa.eps, lane);
+    if (fa_wave) ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, lane);
 
-  f32x4_t oacc[4];
+  f32x4_t oacc[NB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_part = 0.f;
 
   // LDS addresses of this lane.  Stores (whole-line layout): token
   // 16w + lt (+8), column 16*lc of a 128-byte segment.  Operand reads: token
   // 16w + n, 8 channels at 32s + 8g.  C^T reads: token row 4g + n/4 of each
-  // 16-token block, channel 64w + 4(n%4) (+16 mb).
+  // 16-token block, channel 16NB w + 4(n%4) (+16 mb).
   uint8_t* const c_st = c_lds + (kSub * w + lt) * kCRow + 16 * lc;
   uint8_t* const pe_st = pe_lds + (kSub * w + lt) * kPeRow + 16 * lc;
   const uint8_t* const c_op = c_lds + (kSub * w + n) * kCRow + 2 * (8 * g);
   const uint8_t* const pe_op = pe_lds + (kSub * w + n) * kPeRow + 2 * (8 * g);
-  const uint8_t* const c_tr = c_lds + (4 * g + (n >> 2)) * kCRow + 2 * (64 * w) + 8 * (n & 3);
+  const uint8_t* const c_tr = c_lds + (4 * g + (n >> 2)) * kCRow + 2 * (16 * NB * w) + 8 * (n & 3);
   uint8_t* const p_mine = p_lds + n * kPRow + 2 * (kSub * w + 4 * g);
   const uint8_t* const p_row = p_lds + n * kPRow + 2 * (4 * g);
 
-  auto process = [&](int j, KTile<C_DT>& kt) {
+  auto process = [&](int j, KTile<C_DT, NB>& kt) {
     const int wbase = t0 + j * kTileTok + kSub * w;
     const bool full = t0 + (j + 1) * kTileTok <= t1;  // block-uniform
 
     // This wave's latent and rope rows into the tile (e4m3 decoded to bf16).
     if constexpr (C_DT == 2) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < 2 * ((NB + 1) / 2); ++q) {
         const uint2 a0 = e4m3x4_to_bf16x4_hw(kt.c[q].x), a1 = e4m3x4_to_bf16x4_hw(kt.c[q].y);
         const uint2 a2 = e4m3x4_to_bf16x4_hw(kt.c[q].z), a3 = e4m3x4_to_bf16x4_hw(kt.c[q].w);
         // 16 codes: token 16w + 8(q&1) + lt, channels 128(q>>1) + 16lc..+16
+        // (the re-read upper half of an odd NB's last segment is not stored)
+        if ((NB & 1) && (q >> 1) == NB / 2 && lc >= 4) continue;
         uint8_t* dst = c_lds + (kSub * w + 8 * (q & 1) + lt) * kCRow + 2 * (128 * (q >> 1) + 16 * lc);
         *reinterpret_cast<uint4*>(dst) = make_uint4(a0.x, a0.y, a1.x, a1.y);
         *reinterpret_cast<uint4*>(dst + 16) = make_uint4(a2.x, a2.y, a3.x, a3.y);
       }
     } else {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 0; s < 2 * NB; ++s) {
         // element-wise: a whole-struct copy becomes a memcpy that keeps kt
         // out of registers
         const uint4 v = kt.c[s];
@@ -486,7 +516,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
       if (fa_wave && j == n_tiles - 1) {
         // The new token's row: the computed values replace what was loaded
         // (this wave's own rows, so its reads below see them in order).
-        *reinterpret_cast<uint2*>(c_lds + (kSub * w + fa_k) * kCRow + 8 * lane) = ftok.row;
+        store_lane<NB>(reinterpret_cast<uint16_t*>(c_lds + (kSub * w + fa_k) * kCRow) + NB * lane, ftok.row);
         if (lane < kP / 2) *reinterpret_cast<uint32_t*>(pe_lds + (kSub * w + fa_k) * kPeRow + 4 * lane) = ftok.pe;
         if constexpr (C_DT == 2) {
           if (g == (fa_k >> 2)) {
@@ -508,13 +538,13 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
     // complete in order, so no wait beyond the operand reads is needed).
     f32x4_t s_c = {0.f, 0.f, 0.f, 0.f}, s_p = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < 2 * NB; ++s)
       s_c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           as_bf16x8(*reinterpret_cast<const uint4*>(c_op + 2 * (32 * s))), qb[s], s_c, 0, 0, 0);
 #pragma unroll
     for (int s = 0; s < 2; ++s)
       s_p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          as_bf16x8(*reinterpret_cast<const uint4*>(pe_op + 2 * (32 * s))), qb[8 + s], s_p, 0, 0, 0);
+          as_bf16x8(*reinterpret_cast<const uint4*>(pe_op + 2 * (32 * s))), qb[2 * NB + s], s_p, 0, 0, 0);
 
     float x[4];
     const float sc4[4] = {scv.x, scv.y, scv.z, scv.w};
@@ -535,11 +565,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
 
     // C^T of this wave's channels for the whole tile; the reads' latency
     // hides under the softmax below.
-    s16x4_t ct[2][4][2];
+    s16x4_t ct[2][NB][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
           ct[kb][mb][h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -557,7 +587,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
       m_run = m_new;
       l_part *= alpha;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) oacc[mb] = oacc[mb] * alpha;
+      for (int mb = 0; mb < NB; ++mb) oacc[mb] = oacc[mb] * alpha;
     }
     float p[4];
 #pragma unroll
@@ -578,7 +608,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
     // completed, so the next tile may overwrite them.
     lds_barrier();
 
-    // O^T[64w + 16mb + ., head] += C^T . P^T over the tile's two 32-token
+    // O^T[16NB w + 16mb + ., head] += C^T . P^T over the tile's two 32-token
     // halves; the 8 K slots of lane group g are tokens 32kb + 4g + {0..3}
     // and 32kb + 16 + 4g + {0..3} in both operands.
 #pragma unroll
@@ -587,7 +617,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
       const uint2 phi = *reinterpret_cast<const uint2*>(p_row + 2 * (32 * kb + 16));
       const bf16x8_t pb = as_bf16x8(make_uint4(plo.x, plo.y, phi.x, phi.y));
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < NB; ++mb)
         oacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cat_bf16x8(ct[kb][mb][0], ct[kb][mb][1]), pb,
                                                            oacc[mb], 0, 0, 0);
     }
@@ -607,7 +637,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
     if (it + d < n_tiles) process(it + d, kt[d]);
 
   if constexpr (FUSE)
-    if (fa_wave) fused_store<C_DT>(a.fa, static_cast<int64_t>(fa_t.b) * a.fa.cache_s + fa_t.pos, ftok, lane);
+    if (fa_wave) fused_store<C_DT, NB>(a.fa, static_cast<int64_t>(fa_t.b) * a.fa.cache_s + fa_t.pos, ftok, lane);
 
   // ---- Sum of the weights per head over the four waves.
   float l_w = l_part + shfl_xor_f32(l_part, 16);
@@ -617,12 +647,13 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
   const float Ltot = (l_lds[0][n] + l_lds[1][n]) + (l_lds[2][n] + l_lds[3][n]);
   const float inv = Ltot > 0.f ? 1.f / Ltot : 0.f;
 
-  // Lane (n, g) holds head n, channels 64w + 16mb + 4g + {0..3}.
-  const int ch0 = 64 * w + 4 * g;
+  // Lane (n, g) holds head n, channels 16NB w + 16mb + 4g + {0..3} (the
+  // padding channels come out as 0: their cache channels hold 0).
+  const int ch0 = 16 * NB * w + 4 * g;
   if (ns <= 1) {
     uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + n * a.o_hs + ch0;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < NB; ++mb) {
       uint2 pk;
       pk.x = f32_to_bf16(oacc[mb][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(oacc[mb][1] * inv)) << 16);
       pk.y = f32_to_bf16(oacc[mb][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(oacc[mb][3] * inv)) << 16);
@@ -631,9 +662,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
     return;
   }
   const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * kH + n;
-  float* op = a.o_part + pidx * kR + ch0;
+  float* op = a.o_part + pidx * RP + ch0;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < NB; ++mb)
     *reinterpret_cast<float4*>(op + 16 * mb) =
         make_float4(oacc[mb][0] * inv, oacc[mb][1] * inv, oacc[mb][2] * inv, oacc[mb][3] * inv);
   if (w == 0 && g == 0) a.lse_part[pidx] = (Ltot > 0.f) ? (m_run + __log2f(Ltot)) * kLn2 : -INFINITY;
@@ -643,10 +674,13 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
 // Kernel 2 (fp32 models): the same maths on the VALU in fp32.  One block of
 // 256 threads per (row, split); 16-token tiles staged in LDS.
 // ---------------------------------------------------------------------------
+template <int NB>
 __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
   constexpr int TT = 16;
-  __shared__ float q_s[kH][kKC + 1];
-  __shared__ float k_s[TT][kKC + 1];
+  constexpr int RP = 64 * NB, KC = RP + kP;  // channels scored per cached token
+  constexpr int CPV = RP / 16;               // output channels per thread
+  __shared__ float q_s[kH][KC + 1];
+  __shared__ float k_s[TT][KC + 1];
   __shared__ float p_s[kH][TT];
   __shared__ float alpha_s[kH];
   __shared__ float m_s[kH], l_s[kH];
@@ -683,39 +717,42 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
   const float* qp = static_cast<const float*>(a.q_pe) + r * a.qp_rs;
   const float* ct = static_cast<const float*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
   const float* st = static_cast<const float*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
-  for (int i = t; i < kH * kR; i += 256) q_s[i / kR][i % kR] = qa[(i / kR) * a.qa_hs + (i % kR)];
+  for (int i = t; i < kH * RP; i += 256) {
+    const int h = i / RP, c = i % RP;
+    q_s[h][c] = c < a.R ? qa[h * a.qa_hs + c] : 0.f;  // the padding channels are zero
+  }
   for (int i = t; i < kH * kP / 2; i += 256) {
     const int h = i / (kP / 2), pi = i % (kP / 2);
     float o1, o2;
     rope_pair<0>(qp[h * a.qp_hs + 2 * pi], qp[h * a.qp_hs + 2 * pi + 1], ct[pi], st[pi], o1, o2);
-    q_s[h][kR + 2 * pi] = o1;
-    q_s[h][kR + 2 * pi + 1] = o2;
+    q_s[h][RP + 2 * pi] = o1;
+    q_s[h][RP + 2 * pi + 1] = o2;
   }
   if (t < kH) {
     m_s[t] = -INFINITY;
     l_s[t] = 0.f;
   }
-  const int h_pv = t >> 4, c_pv = (t & 15) * 16;
-  float o[16];
+  const int h_pv = t >> 4, c_pv = (t & 15) * CPV;
+  float o[CPV];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) o[j] = 0.f;
+  for (int j = 0; j < CPV; ++j) o[j] = 0.f;
 
   const float* ckv = static_cast<const float*>(a.ckv);
   const float* kpe = static_cast<const float*>(a.kpe);
   for (int base = t0; base < t1; base += TT) {
     __syncthreads();
-    for (int i = t; i < TT * kKC; i += 256) {
-      const int j = i / kKC, c = i % kKC;
+    for (int i = t; i < TT * KC; i += 256) {
+      const int j = i / KC, c = i % KC;
       const int tok = base + j;
       float v = 0.f;
-      if (tok < t1) v = c < kR ? ckv[(row0 + tok) * kR + c] : kpe[(row0 + tok) * kP + (c - kR)];
+      if (tok < t1) v = c < RP ? ckv[(row0 + tok) * RP + c] : kpe[(row0 + tok) * kP + (c - RP)];
       k_s[j][c] = v;
     }
     __syncthreads();
     {  // scores: thread -> head t/16, token t%16
       const int h = t >> 4, j = t & 15;
       float acc = 0.f;
-      for (int c = 0; c < kKC; ++c) acc += q_s[h][c] * k_s[j][c];
+      for (int c = 0; c < KC; ++c) acc += q_s[h][c] * k_s[j][c];
       p_s[h][j] = (base + j < t1) ? acc * a.scale_log2 : -INFINITY;
     }
     __syncthreads();
@@ -737,11 +774,11 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
     __syncthreads();
     const float al = alpha_s[h_pv];
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) o[jj] *= al;
+    for (int jj = 0; jj < CPV; ++jj) o[jj] *= al;
     for (int j = 0; j < TT; ++j) {
       const float p = p_s[h_pv][j];
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) o[jj] += p * k_s[j][c_pv + jj];
+      for (int jj = 0; jj < CPV; ++jj) o[jj] += p * k_s[j][c_pv + jj];
     }
   }
   __syncthreads();
@@ -750,13 +787,13 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
   if (ns <= 1) {
     float* op = static_cast<float*>(a.o_lat) + r * a.o_rs + h_pv * a.o_hs + c_pv;
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) op[jj] = o[jj] * inv;
+    for (int jj = 0; jj < CPV; ++jj) op[jj] = o[jj] * inv;
     return;
   }
   const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * kH + h_pv;
-  float* op = a.o_part + pidx * kR + c_pv;
+  float* op = a.o_part + pidx * RP + c_pv;
 #pragma unroll
-  for (int jj = 0; jj < 16; ++jj) op[jj] = o[jj] * inv;
+  for (int jj = 0; jj < CPV; ++jj) op[jj] = o[jj] * inv;
   if ((t & 15) == 0) a.lse_part[pidx] = (Lh > 0.f) ? (m_s[h_pv] + __log2f(Lh)) * kLn2 : -INFINITY;
 }
 
@@ -769,7 +806,8 @@ __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
   const int ns = row_splits(clamped_row_len(a.ad, r, a.cache_b, a.cache_s), a.n_splits, a.min_chunk,
                             a.plan ? *a.plan : 0).ns;
   if (ns <= 1) return;  // written by the decode kernel
-  merge_head<DT>(a.o_part, a.lse_part, r, h, ns, a.n_splits, a.o_lat, a.o_rs, a.o_hs, a.lse_out);
+  merge_head<DT>(a.o_part, a.lse_part, r, h, ns, a.n_splits, 64 * ((a.R + 63) / 64), a.o_lat, a.o_rs, a.o_hs,
+                 a.lse_out);
 }
 
 }  // namespace swamla
@@ -783,10 +821,15 @@ namespace swamla {
 int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s) {
   const dim3 grid((a.n_tok + 3) / 4), block(256);
   if (a.n_tok == 0) return 0;
-  if (in_dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_append_kernel<1, 1>), grid, block, 0, s, a);
-  else if (in_dt == 1 && c_dt == 2) hipLaunchKernelGGL((mla_append_kernel<1, 2>), grid, block, 0, s, a);
-  else if (in_dt == 0 && c_dt == 0) hipLaunchKernelGGL((mla_append_kernel<0, 0>), grid, block, 0, s, a);
-  else return -1;
+  const int rc = with_nb(a.R, [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    if (in_dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_append_kernel<1, 1, NB>), grid, block, 0, s, a);
+    else if (in_dt == 1 && c_dt == 2) hipLaunchKernelGGL((mla_append_kernel<1, 2, NB>), grid, block, 0, s, a);
+    else if (in_dt == 0 && c_dt == 0) hipLaunchKernelGGL((mla_append_kernel<0, 0, NB>), grid, block, 0, s, a);
+    else return -1;
+    return 0;
+  });
+  if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
@@ -799,16 +842,22 @@ int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
   const dim3 grid = a.balance > 0 ? dim3(a.balance, 1) : dim3(a.n_splits, a.n_rows);
   const bool fuse = a.fa.kv_in != nullptr;
-  if (dt == 1 && c_dt == 1 && !fuse)
-    hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, false>), grid, dim3(256), 0, s, a);
-  else if (dt == 1 && c_dt == 2 && !fuse)
-    hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, false>), grid, dim3(256), 0, s, a);
-  else if (dt == 1 && c_dt == 1)
-    hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, true>), grid, dim3(256), 0, s, a);
-  else if (dt == 1 && c_dt == 2)
-    hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, true>), grid, dim3(256), 0, s, a);
-  else if (dt == 0 && c_dt == 0 && !fuse) hipLaunchKernelGGL(mla_decode_f32, grid, dim3(256), 0, s, a);
-  else return -1;
+  const int rc = with_nb(a.R, [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    if (dt == 1 && c_dt == 1 && !fuse)
+      hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, false, NB>), grid, dim3(256), 0, s, a);
+    else if (dt == 1 && c_dt == 2 && !fuse)
+      hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, false, NB>), grid, dim3(256), 0, s, a);
+    else if (dt == 1 && c_dt == 1)
+      hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, true, NB>), grid, dim3(256), 0, s, a);
+    else if (dt == 1 && c_dt == 2)
+      hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, true, NB>), grid, dim3(256), 0, s, a);
+    else if (dt == 0 && c_dt == 0 && !fuse)
+      hipLaunchKernelGGL((mla_decode_f32<NB>), grid, dim3(256), 0, s, a);
+    else return -1;
+    return 0;
+  });
+  if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -125,17 +125,17 @@ __global__ __launch_bounds__(NW * 64) void mla_linear_kernel(LinearArgs a) {
 // Split merge + W_uv read-out.  Block = (ROWS query rows, head h), 4 waves;
 // ROWS (2, 4 or 8) keeps the grid near one block per CU.
 // The block first issues its W_uv[h] loads (wave w: output tiles w and w+4,
-// all 256 K), then merges its rows' split partials into bf16 rows in LDS
-// (thread t < 32*ROWS: row t/32, channels 8(t%32)..+8; one split: the decode
-// kernel's o_lat row), then multiplies: y[r, h, d] = sum_c W_uv[h][d][c] x[r][c].
+// all R_pad = 64 NB K; W_uv rows hold R_pad values), then merges its rows'
+// split partials into bf16 rows in LDS (thread t < 32*ROWS: row t/32,
+// channels 8(t%32) + 256k ..+8; one split: the decode kernel's o_lat row),
+// then multiplies: y[r, h, d] = sum_c W_uv[h][d][c] x[r][c].
 // The merge is o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M) with
 // M = max_s lse_s, accumulated over groups of 8 splits in order.
 // ---------------------------------------------------------------------------
-constexpr int kMpXRow = 2 * 256 + 16;   // LDS bytes per merged row (padded)
-
-template <int DV, int ROWS>
+template <int DV, int ROWS, int NB>
 __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs a) {
-  constexpr int R = 256, H = 16;
+  constexpr int R = 64 * NB, H = 16;  // R: the padded latent width R_pad
+  constexpr int kMpXRow = 2 * R + 16;  // LDS bytes per merged row (padded)
   constexpr int kTilesPerWave = DV / 16 / 4;
   static_assert(ROWS == 2 || ROWS == 4 || ROWS == 8, "rows per block");
   __shared__ __attribute__((aligned(16))) uint8_t x_lds[ROWS * kMpXRow];
@@ -145,18 +145,20 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
   const int n = lane & 15, g = lane >> 4;
 
   // W_uv[h] rows of this wave's output tiles (B operand: lane = output d).
-  uint4 wb[kTilesPerWave][8];
+  uint4 wb[kTilesPerWave][2 * NB];
 #pragma unroll
   for (int j = 0; j < kTilesPerWave; ++j) {
     const int d = 16 * (w + 4 * j) + n;
     const uint16_t* wp = static_cast<const uint16_t*>(a.w) + h * a.w_hs + static_cast<int64_t>(d) * a.w_rs + 8 * g;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) wb[j][s] = *reinterpret_cast<const uint4*>(wp + 32 * s);
+    for (int s = 0; s < 2 * NB; ++s) wb[j][s] = *reinterpret_cast<const uint4*>(wp + 32 * s);
   }
 
-  // Merge: thread -> (row rr, 8 channels cc); threads past ROWS rows idle.
-  if (threadIdx.x < ROWS * 32) {
-    const int rr = threadIdx.x >> 5, cc = 8 * (threadIdx.x & 31);
+  // Merge: thread -> (row rr, 8 channels cc per 256-channel chunk); threads
+  // past ROWS rows idle.
+  if (threadIdx.x < ROWS * 32)
+  for (int cc = 8 * (threadIdx.x & 31); cc < R; cc += 256) {
+    const int rr = threadIdx.x >> 5;
     const int r = r0 + rr;
     uint4 xv = make_uint4(0, 0, 0, 0);
     if (r < a.n_rows) {
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
   for (int j = 0; j < kTilesPerWave; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const uint8_t* xa = x_lds + (n & (ROWS - 1)) * kMpXRow + 2 * (8 * g);
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
+  for (int s = 0; s < 2 * NB; ++s) {
     const bf16x8_t av = as_bf16x8(*reinterpret_cast<const uint4*>(xa + 2 * (32 * s)));
 #pragma unroll
     for (int j = 0; j < kTilesPerWave; ++j)
@@ -462,9 +464,14 @@ int launch_merge_project(const MergeProjectArgs& a, hipStream_t s) {
   // its head's whole W_uv slice, so fewer rows mean more re-reads of it
   const int rows = a.n_rows * 16 <= 2 * 256 ? 2 : (a.n_rows * 16 <= 4 * 256 ? 4 : 8);
   const dim3 grid((a.n_rows + rows - 1) / rows, 16), block(256);
-  if (rows == 2) hipLaunchKernelGGL((mla_merge_project_kernel<128, 2>), grid, block, 0, s, a);
-  else if (rows == 4) hipLaunchKernelGGL((mla_merge_project_kernel<128, 4>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((mla_merge_project_kernel<128, 8>), grid, block, 0, s, a);
+  const int rc = with_nb(a.R, [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    if (rows == 2) hipLaunchKernelGGL((mla_merge_project_kernel<128, 2, NB>), grid, block, 0, s, a);
+    else if (rows == 4) hipLaunchKernelGGL((mla_merge_project_kernel<128, 4, NB>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((mla_merge_project_kernel<128, 8, NB>), grid, block, 0, s, a);
+    return 0;
+  });
+  if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "mla_args.h"
 #include "numerics.h"
 
@@ -275,6 +277,23 @@ __device__ __forceinline__ BalancedSlot balanced_slot(const Addressing& ad, int 
                                                       int bid) {
   if (n_rows <= 64) return balanced_slot_t<1>(ad, n_rows, cache_b, cache_s, n_splits, min_chunk, target, bid);
   return balanced_slot_t<kBalanceMaxRows / 64>(ad, n_rows, cache_b, cache_s, n_splits, min_chunk, target, bid);
+}
+
+// Runs f(std::integral_constant<int, NB>) for the instance of a latent row
+// of R channels (NB = ceil(R / 64), 1..kMaxNB); -1 when R is out of range.
+template <typename F>
+int with_nb(int R, F&& f) {
+  switch ((R + 63) / 64) {
+    case 1: return f(std::integral_constant<int, 1>{});
+    case 2: return f(std::integral_constant<int, 2>{});
+    case 3: return f(std::integral_constant<int, 3>{});
+    case 4: return f(std::integral_constant<int, 4>{});
+    case 5: return f(std::integral_constant<int, 5>{});
+    case 6: return f(std::integral_constant<int, 6>{});
+    case 7: return f(std::integral_constant<int, 7>{});
+    case 8: return f(std::integral_constant<int, 8>{});
+    default: return -1;
+  }
 }
 
 }  // namespace swamla

@@ -5,6 +5,7 @@
 
 #include "mla_args.h"
 #include "mla_device.h"
+#include "mla_plan.h"
 #include "numerics.h"
 
 namespace swamla {
@@ -41,20 +42,24 @@ namespace swamla {
 #endif
 // One wave's share of a prefill tile: RPL rows of 8 tokens (lane: token l%8,
 // 16 bytes at 16(l/8) of each 128-byte segment), plus the rows' e4m3 scales.
-template <int C_DT, int RPL>
+// Latent rows of R_pad = 64 NB channels are NB segments (bf16) or ceil(NB / 2)
+// (e4m3; for odd NB the last one is half a row, as in mla_decode_mfma).
+template <int C_DT, int RPL, int NB>
 struct PTile {
-  uint4 c[RPL * (C_DT == 2 ? 2 : 4)];
+  uint4 c[RPL * (C_DT == 2 ? (NB + 1) / 2 : NB)];
   uint4 p[RPL];
   float sc[RPL];
 };
 
-template <int C_DT, int DEPTH, int QPW, int NW>
+template <int C_DT, int DEPTH, int QPW, int NW, int NB>
 __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(DecodeArgs a) {
   constexpr int TPW = kTileTok / NW;  // tokens each wave loads per tile
   constexpr int RPL = TPW / 8;        // ... rows of 8 tokens per lane
-  constexpr int SEG = C_DT == 2 ? 2 : 4;  // 128-byte latent segments per row
-  constexpr int CB = C_DT == 2 ? kR : 2 * kR;  // latent bytes per cached token
-  __shared__ __attribute__((aligned(16))) uint8_t c_lds[kCBytes];
+  constexpr int SEG = C_DT == 2 ? (NB + 1) / 2 : NB;  // 128-byte latent segments per row
+  constexpr int RP = LatGeo<NB>::RP, kCRow = LatGeo<NB>::CRow;
+  constexpr int CB = C_DT == 2 ? RP : 2 * RP;  // latent bytes per cached token
+  constexpr int MB = 4 * NB;                   // 16-channel output blocks
+  __shared__ __attribute__((aligned(16))) uint8_t c_lds[LatGeo<NB>::CBytes];
   __shared__ __attribute__((aligned(16))) uint8_t pe_lds[kPeBytes];
   __shared__ __attribute__((aligned(16))) float sc_lds[kTileTok];
 
@@ -87,26 +92,30 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
   const int64_t cache_row0 = static_cast<int64_t>(b_ok ? b : 0) * a.cache_s;
   const int t_last = Lb > 0 ? Lb - 1 : 0;
 
-  auto load_tile = [&](int j, PTile<C_DT, RPL>& kt) {
+  auto load_tile = [&](int j, PTile<C_DT, RPL, NB>& kt) {
 #pragma unroll
     for (int rr = 0; rr < RPL; ++rr) {
       const int64_t row = cache_row0 + min(j * kTileTok + TPW * w + 8 * rr + lt, t_last);
-      const uint8_t* cp = static_cast<const uint8_t*>(a.ckv) + row * CB + 16 * lc;
+      const uint8_t* cp = static_cast<const uint8_t*>(a.ckv) + row * CB;
 #pragma unroll
-      for (int q = 0; q < SEG; ++q) kt.c[rr * SEG + q] = ld_stream16(cp + 128 * q);
+      for (int q = 0; q < SEG; ++q) {
+        const bool half = C_DT == 2 && (NB & 1) && q == SEG - 1;  // upper lanes re-read the first half
+        kt.c[rr * SEG + q] = ld_stream16(cp + 128 * q + (half ? 16 * (lc & 3) : 16 * lc));
+      }
       kt.p[rr] = ld_stream16(static_cast<const uint8_t*>(a.kpe) + row * (2 * kP) + 16 * lc);
       if constexpr (C_DT == 2) kt.sc[rr] = a.ckv_scale[row];
     }
   };
 
   // ---- Q^T operands of this wave's queries (as in mla_decode_mfma).
-  PTile<C_DT, RPL> kt[DEPTH];
-  bf16x8_t qb[QPW][10];
+  PTile<C_DT, RPL, NB> kt[DEPTH];
+  bf16x8_t qb[QPW][2 * NB + 2];
 #pragma unroll
   for (int qi = 0; qi < QPW; ++qi) {
     const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + rq[qi] * a.qa_rs + n * a.qa_hs;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qb[qi][s] = as_bf16x8(*reinterpret_cast<const uint4*>(qa + 32 * s + 8 * g));
+    for (int s = 0; s < 2 * NB; ++s)  // channels >= R zeroed
+      qb[qi][s] = as_bf16x8(mask_bf16x8(*reinterpret_cast<const uint4*>(qa + 32 * s + 8 * g), a.R - (32 * s + 8 * g)));
   }
   uint4 raw[QPW][2];
   uint2 cr[QPW][2], sr[QPW][2];
@@ -143,14 +152,14 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
                      bf16_to_f32(sj), o1, o2);
         wv[jj] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
       }
-      qb[qi][8 + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
+      qb[qi][2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
     }
 
-  f32x4_t oacc[QPW][16];
+  f32x4_t oacc[QPW][MB];
 #pragma unroll
   for (int qi = 0; qi < QPW; ++qi)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) oacc[qi][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < MB; ++i) oacc[qi][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run[QPW], l_part[QPW];
 #pragma unroll
   for (int qi = 0; qi < QPW; ++qi) {
@@ -166,7 +175,7 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
   // C^T reads: token row 4g + n/4 of each 16-token block, channel 4(n%4) (+16 mb)
   const uint8_t* const c_tr = c_lds + (4 * g + (n >> 2)) * kCRow + 8 * (n & 3);
 
-  auto process = [&](int j, PTile<C_DT, RPL>& kt) {
+  auto process = [&](int j, PTile<C_DT, RPL, NB>& kt) {
     // This wave's rows (e4m3 decoded to bf16, with their scales) into the tile.
 #pragma unroll
     for (int rr = 0; rr < RPL; ++rr) {
@@ -176,6 +185,7 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
           const uint4 v = kt.c[rr * SEG + q];
           const uint2 a0 = e4m3x4_to_bf16x4_hw(v.x), a1 = e4m3x4_to_bf16x4_hw(v.y);
           const uint2 a2 = e4m3x4_to_bf16x4_hw(v.z), a3 = e4m3x4_to_bf16x4_hw(v.w);
+          if ((NB & 1) && q == SEG - 1 && lc >= 4) continue;  // the re-read half is not stored
           uint8_t* dst = c_st + 8 * rr * kCRow + 2 * (128 * q);  // channels 128q + 16lc .. +16
           *reinterpret_cast<uint4*>(dst + 16 * lc) = make_uint4(a0.x, a0.y, a1.x, a1.y);
           *reinterpret_cast<uint4*>(dst + 16 * lc + 16) = make_uint4(a2.x, a2.y, a3.x, a3.y);
@@ -203,7 +213,7 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
 #pragma unroll
       for (int qi = 0; qi < QPW; ++qi) s_c[qi] = s_p[qi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 0; s < 2 * NB; ++s) {
         const bf16x8_t ka = as_bf16x8(*reinterpret_cast<const uint4*>(c_op + 16 * tb * kCRow + 2 * (32 * s)));
 #pragma unroll
         for (int qi = 0; qi < QPW; ++qi) s_c[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[qi][s], s_c[qi], 0, 0, 0);
@@ -213,7 +223,7 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
         const bf16x8_t pa = as_bf16x8(*reinterpret_cast<const uint4*>(pe_op + 16 * tb * kPeRow + 2 * (32 * s)));
 #pragma unroll
         for (int qi = 0; qi < QPW; ++qi)
-          s_p[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, qb[qi][8 + s], s_p[qi], 0, 0, 0);
+          s_p[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, qb[qi][2 * NB + s], s_p[qi], 0, 0, 0);
       }
       float4 scv = make_float4(1.f, 1.f, 1.f, 1.f);
       if constexpr (C_DT == 2) scv = *reinterpret_cast<const float4*>(sc_lds + 16 * tb + 4 * g);
@@ -242,7 +252,7 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
         m_run[qi] = m_new;
         l_part[qi] *= alpha;
 #pragma unroll
-        for (int mb = 0; mb < 16; ++mb) oacc[qi][mb] = oacc[qi][mb] * alpha;
+        for (int mb = 0; mb < MB; ++mb) oacc[qi][mb] = oacc[qi][mb] * alpha;
       }
       // bf16 weights (fp8: times the token's scale) in the PV operand order.
       uint2 pw[4];
@@ -269,7 +279,7 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int mb = 0; mb < 16; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         const s16x4_t c0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s16x4_t*)(c_tr + (32 * kb) * kCRow + 32 * mb));
         const s16x4_t c1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -301,7 +311,7 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
       // lane (n, g): head n, channels 16mb + 4g + {0..3}
       uint16_t* op = static_cast<uint16_t*>(a.o_lat) + rq[qi] * a.o_rs + n * a.o_hs + 4 * g;
 #pragma unroll
-      for (int mb = 0; mb < 16; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         uint2 pk;
         pk.x = f32_to_bf16(oacc[qi][mb][0] * inv) | (static_cast<uint32_t>(f32_to_bf16(oacc[qi][mb][1] * inv)) << 16);
         pk.y = f32_to_bf16(oacc[qi][mb][2] * inv) | (static_cast<uint32_t>(f32_to_bf16(oacc[qi][mb][3] * inv)) << 16);
@@ -318,9 +328,19 @@ int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   const int T = a.ad.T;
   constexpr int kQpw = SWAMLA_PREFILL_QPW, kNw = SWAMLA_PREFILL_WAVES;
   const dim3 grid((T + kNw * kQpw - 1) / (kNw * kQpw), a.n_rows / T), block(kNw * 64);
-  if (dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_prefill_mfma<1, kPrefillDepth, kQpw, kNw>), grid, block, 0, s, a);
-  else if (dt == 1 && c_dt == 2) hipLaunchKernelGGL((mla_prefill_mfma<2, kPrefillDepth, kQpw, kNw>), grid, block, 0, s, a);
-  else return -1;
+  // Each wave accumulates all R_pad output channels of its query: built for
+  // R_pad <= 256 (larger ranks take the per-row decode path).
+  if (a.R > 256) return -1;
+  const int rc = with_nb(a.R, [&](auto nb) {
+    constexpr int NB = decltype(nb)::value < 4 ? decltype(nb)::value : 4;
+    if (dt == 1 && c_dt == 1)
+      hipLaunchKernelGGL((mla_prefill_mfma<1, kPrefillDepth, kQpw, kNw, NB>), grid, block, 0, s, a);
+    else if (dt == 1 && c_dt == 2)
+      hipLaunchKernelGGL((mla_prefill_mfma<2, kPrefillDepth, kQpw, kNw, NB>), grid, block, 0, s, a);
+    else return -1;
+    return 0;
+  });
+  if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

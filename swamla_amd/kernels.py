@@ -16,7 +16,14 @@ import torch
 
 from . import _abi
 
-R, P, H = 256, 64, 16
+R, P, H = 256, 64, 16  # R: the default kv_lora_rank (any 1..MAX_RANK is built)
+MAX_RANK = 512
+
+
+def padded_rank(rank: int) -> int:
+    """Latent channels stored per token for kv_lora_rank ``rank``: R_pad =
+    64 * ceil(rank / 64) (the kernels' row layout; channels >= rank are 0)."""
+    return 64 * -(-int(rank) // 64)
 
 
 def _need_gpu(*ts: Optional[torch.Tensor]) -> torch.device:
@@ -46,14 +53,21 @@ def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
 class LatentCache:
     """Latent KV cache of one MLA layer.
 
-    ckv   [B, S, R]  model dtype (bf16 / fp32) or uint8 e4m3fn codes
-    kpe   [B, S, P]  model dtype
-    scale [B, S]     fp32 per-token scale (e4m3 caches only)
+    ckv   [B, S, R_pad]  model dtype (bf16 / fp32) or uint8 e4m3fn codes;
+                         channels rank .. R_pad-1 hold zeros
+    kpe   [B, S, P]      model dtype
+    scale [B, S]         fp32 per-token scale (e4m3 caches only)
+    rank                 kv_lora_rank R (R_pad = padded_rank(R))
     """
 
     ckv: torch.Tensor
     kpe: torch.Tensor
     scale: Optional[torch.Tensor] = None
+    rank: int = R
+
+    @property
+    def rank_pad(self) -> int:
+        return padded_rank(self.rank)
 
     @property
     def is_fp8(self) -> bool:
@@ -71,8 +85,10 @@ class LatentCache:
         c, p = self.ckv, self.kpe
         if c.dim() != 3 or p.dim() != 3 or c.shape[:2] != p.shape[:2]:
             raise ValueError(f"cache shapes {tuple(c.shape)} / {tuple(p.shape)} disagree")
-        if c.shape[2] != R or p.shape[2] != P:
-            raise ValueError(f"cache last dims must be R={R}, P={P}")
+        if not 1 <= self.rank <= MAX_RANK:
+            raise ValueError(f"kv_lora_rank {self.rank} outside 1..{MAX_RANK}")
+        if c.shape[2] != self.rank_pad or p.shape[2] != P:
+            raise ValueError(f"cache last dims must be R_pad={self.rank_pad} (rank {self.rank}), P={P}")
         if not (c.is_contiguous() and p.is_contiguous()):
             raise ValueError("cache buffers must be contiguous")
         if self.is_fp8:
@@ -85,17 +101,35 @@ class LatentCache:
             raise ValueError(f"latent cache dtype {c.dtype} != k_pe dtype {p.dtype}")
 
     @staticmethod
-    def allocate(batch: int, seq: int, dtype: torch.dtype, device, fp8: bool = False) -> "LatentCache":
+    def allocate(batch: int, seq: int, dtype: torch.dtype, device, fp8: bool = False, rank: int = R) -> "LatentCache":
+        rp = padded_rank(rank)
         if fp8:
             return LatentCache(
-                torch.zeros(batch, seq, R, dtype=torch.uint8, device=device),
+                torch.zeros(batch, seq, rp, dtype=torch.uint8, device=device),
                 torch.zeros(batch, seq, P, dtype=dtype, device=device),
                 torch.zeros(batch, seq, dtype=torch.float32, device=device),
+                rank,
             )
         return LatentCache(
-            torch.zeros(batch, seq, R, dtype=dtype, device=device),
+            torch.zeros(batch, seq, rp, dtype=dtype, device=device),
             torch.zeros(batch, seq, P, dtype=dtype, device=device),
+            rank=rank,
         )
+
+
+def pad_rank(t: torch.Tensor, rank: int, dim: int = -1) -> torch.Tensor:
+    """``t`` with dimension ``dim`` (of size rank) zero-padded to
+    padded_rank(rank); ``t`` itself when no padding is needed."""
+    rp = padded_rank(rank)
+    if t.shape[dim] == rp:
+        return t
+    if t.shape[dim] != rank:
+        raise ValueError(f"dimension {dim} has {t.shape[dim]} entries, expected {rank} or {rp}")
+    shape = list(t.shape)
+    shape[dim] = rp
+    out = torch.zeros(shape, dtype=t.dtype, device=t.device)
+    out.narrow(dim, 0, rank).copy_(t)
+    return out
 
 
 def _addressing(n, arrays, start_pos, per_seq, names):
@@ -138,23 +172,27 @@ def append(
 ) -> None:
     """Fused kv_norm + RoPE(k_pe) + (e4m3) + scatter of ``kv`` rows.
 
-    kv: [N, >=R+P] with unit stride in the last dim (the wkv_a output, or a
-    view of it).  Addressing: explicit (seq_idx, dst_pos, rope_pos) or dense
-    (start_pos [N / tokens_per_seq]).  Reference: models/mla.py:307-323,
-    :409-414.
+    kv: [N, >=R_pad+P] with unit stride in the last dim: the latent part in
+    channels [0, R) (R .. R_pad-1 ignored) and k_pe at [R_pad, R_pad+P) (the
+    wkv_a output for R = R_pad; the module's padded product otherwise).
+    ln_w / ln_b: [R] or [R_pad] (an [R] pair is padded here, one copy).
+    Addressing: explicit (seq_idx, dst_pos, rope_pos) or dense (start_pos
+    [N / tokens_per_seq]).  Reference: models/mla.py:307-323, :409-414.
     """
     cache.validate()
     dev = _need_gpu(kv, ln_w, ln_b, cos_tab, sin_tab, cache.ckv, seq_idx, dst_pos, rope_pos, start_pos)
-    if kv.dim() != 2 or kv.stride(1) != 1 or kv.shape[1] < R + P:
-        raise ValueError("kv must be [N, R+P] with unit last-dim stride")
+    rk, rp = cache.rank, cache.rank_pad
+    if kv.dim() != 2 or kv.stride(1) != 1 or kv.shape[1] < rp + P:
+        raise ValueError(f"kv must be [N, R_pad+P = {rp + P}] with unit last-dim stride")
     dt = cache.model_dtype
     if kv.dtype != dt or ln_w.dtype != dt or ln_b.dtype != dt or cos_tab.dtype != dt or sin_tab.dtype != dt:
         raise TypeError(f"kv / LayerNorm / RoPE tensors must all be {dt}")
     n = kv.shape[0]
     (p_seq, p_dst, p_rope), p_sp = _addressing(
         n, (seq_idx, dst_pos, rope_pos), start_pos, tokens_per_seq, ("seq_idx", "dst_pos", "rope_pos"))
-    if not (ln_w.is_contiguous() and ln_b.is_contiguous() and ln_w.numel() == R and ln_b.numel() == R):
-        raise ValueError("LayerNorm weight / bias must be contiguous [R]")
+    if not (ln_w.is_contiguous() and ln_b.is_contiguous() and ln_w.numel() in (rk, rp) and ln_b.numel() in (rk, rp)):
+        raise ValueError("LayerNorm weight / bias must be contiguous [R] or [R_pad]")
+    ln_w, ln_b = pad_rank(ln_w.reshape(-1), rk), pad_rank(ln_b.reshape(-1), rk)
     if cos_tab.dim() != 2 or cos_tab.shape[1] != P // 2 or cos_tab.shape != sin_tab.shape:
         raise ValueError("RoPE tables must be [S, P/2]")
     if not (cos_tab.is_contiguous() and sin_tab.is_contiguous()):
@@ -166,7 +204,7 @@ def append(
             ln_w.data_ptr(), ln_b.data_ptr(), float(eps), cos_tab.data_ptr(), sin_tab.data_ptr(),
             cos_tab.shape[0], cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
             cache.ckv.shape[0], cache.ckv.shape[1], _abi.ptr(err_flag),
-            _abi.dtype_code(dt), cache.cache_code, R, P, _abi.stream_handle(dev),
+            _abi.dtype_code(dt), cache.cache_code, rk, P, _abi.stream_handle(dev),
         )
     )
 
@@ -213,33 +251,35 @@ def balanced_chunk(lens, n_splits: int, min_chunk: int, balance_blocks: int) -> 
 
 @dataclass
 class DecodeWorkspace:
-    """Split-KV partial buffers: o_part [rows, splits, H, R], lse [rows, splits, H],
-    and ``plan`` (int32 [1]): the chunk a balanced decode launch chose, read
-    by the merge that follows it."""
+    """Split-KV partial buffers: o_part [rows, splits, H, R_pad], lse [rows,
+    splits, H], and ``plan`` (int32 [1]): the chunk a balanced decode launch
+    chose, read by the merge that follows it."""
 
     o_part: torch.Tensor
     lse_part: torch.Tensor
     plan: torch.Tensor
 
     @staticmethod
-    def allocate(n_rows: int, n_splits: int, device) -> "DecodeWorkspace":
+    def allocate(n_rows: int, n_splits: int, device, rank: int = R) -> "DecodeWorkspace":
         rows = max(n_rows, 1)
         return DecodeWorkspace(
-            torch.empty(rows, n_splits, H, R, dtype=torch.float32, device=device),
+            torch.empty(rows, n_splits, H, padded_rank(rank), dtype=torch.float32, device=device),
             torch.empty(rows, n_splits, H, dtype=torch.float32, device=device),
             torch.zeros(1, dtype=torch.int32, device=device),
         )
 
-    def fits(self, n_rows: int, n_splits: int) -> bool:
-        return self.o_part.shape[0] >= n_rows and self.o_part.shape[1] == n_splits
+    def fits(self, n_rows: int, n_splits: int, rank: int = R) -> bool:
+        return (self.o_part.shape[0] >= n_rows and self.o_part.shape[1] == n_splits
+                and self.o_part.shape[3] == padded_rank(rank))
 
 
 @dataclass
 class FusedAppend:
     """The append that decode_attention folds into its launch for a one-token
-    step: row r's new token ``kv[r]`` ([rows, >=R+P] bf16, unit last stride,
-    the wkv_a output) goes through kv_norm (``ln_w``, ``ln_b``, ``eps``) and
-    RoPE and is written at ``start_pos[r]`` before row r attends."""
+    step: row r's new token ``kv[r]`` ([rows, >=R_pad+P] bf16, unit last
+    stride, laid out as for append()) goes through kv_norm (``ln_w``,
+    ``ln_b``: [R] or [R_pad]) and RoPE and is written at ``start_pos[r]``
+    before row r attends."""
 
     kv: torch.Tensor
     ln_w: torch.Tensor
@@ -273,11 +313,12 @@ def decode_attention(
 ) -> torch.Tensor:
     """Absorbed attention of query rows over the latent cache (+ merge).
 
-    q_abs [rows, H, R] and q_pe [rows, H, P] may be strided views (unit last
-    stride).  Addressing: explicit (row_seq, kv_len, q_rope_pos) or dense
-    (start_pos [rows / rows_per_seq], causal).  Returns o_lat [rows, H, R]
-    (``out`` may be a strided view, e.g. a transpose of a [H, rows, R]
-    buffer).  With more than one split, mla_merge runs after the decode
+    q_abs [rows, H, R_pad] (channels >= the cache's rank are ignored) and
+    q_pe [rows, H, P] may be strided views (unit last stride).  Addressing:
+    explicit (row_seq, kv_len, q_rope_pos) or dense (start_pos [rows /
+    rows_per_seq], causal).  Returns o_lat [rows, H, R_pad], whose padding
+    channels are 0 (``out`` may be a strided view, e.g. a transpose of a
+    [H, rows, R_pad] buffer).  With more than one split, mla_merge runs after the decode
     kernel (and writes the log-sum-exp to ``lse_out`` if given) unless
     ``merge`` is False: then rows with several splits leave their partials in
     ``workspace`` for merge_project.  With ``append`` (bf16, dense
@@ -293,8 +334,9 @@ def decode_attention(
     dev = _need_gpu(q_abs, q_pe, cos_tab, sin_tab, cache.ckv, row_seq, kv_len, q_rope_pos, start_pos)
     dt = cache.model_dtype
     rows = q_abs.shape[0]
-    if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (H, R) or q_abs.stride(2) != 1:
-        raise ValueError(f"q_abs must be [rows, {H}, {R}] with unit last stride")
+    rk, rp = cache.rank, cache.rank_pad
+    if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (H, rp) or q_abs.stride(2) != 1:
+        raise ValueError(f"q_abs must be [rows, {H}, {rp}] (R_pad) with unit last stride")
     if q_pe.dim() != 3 or tuple(q_pe.shape) != (rows, H, P) or q_pe.stride(2) != 1:
         raise ValueError(f"q_pe must be [rows, {H}, {P}] with unit last stride")
     if q_abs.dtype != dt or q_pe.dtype != dt or cos_tab.dtype != dt:
@@ -302,14 +344,14 @@ def decode_attention(
     (p_seq, p_len, p_rope), p_sp = _addressing(
         rows, (row_seq, kv_len, q_rope_pos), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
     if out is None:
-        out = torch.empty(rows, H, R, dtype=dt, device=dev)
-    if tuple(out.shape) != (rows, H, R) or out.stride(2) != 1 or out.dtype != dt:
-        raise ValueError("out must be [rows, H, R] in the model dtype with unit last stride")
+        out = torch.empty(rows, H, rp, dtype=dt, device=dev)
+    if tuple(out.shape) != (rows, H, rp) or out.stride(2) != 1 or out.dtype != dt:
+        raise ValueError("out must be [rows, H, R_pad] in the model dtype with unit last stride")
     if n_splits > 1:
         if workspace is None:
-            workspace = DecodeWorkspace.allocate(rows, n_splits, dev)
-        if not workspace.fits(rows, n_splits):
-            raise ValueError("workspace too small for (rows, n_splits)")
+            workspace = DecodeWorkspace.allocate(rows, n_splits, dev, rank=rk)
+        if not workspace.fits(rows, n_splits, rk):
+            raise ValueError("workspace does not fit (rows, n_splits, rank)")
     plan = workspace.plan if (balance > 0 and workspace is not None) else None
     lib = _abi.lib()
     stream = _abi.stream_handle(dev)
@@ -317,12 +359,14 @@ def decode_attention(
         kv, ln_w, ln_b = append.kv, append.ln_w, append.ln_b
         if start_pos is None or rows_per_seq != 1:
             raise ValueError("a fused append needs dense addressing with one row per sequence")
-        if kv.dim() != 2 or kv.shape[0] != rows or kv.shape[1] < R + P or kv.stride(1) != 1:
-            raise ValueError("append.kv must be [rows, >=R+P] with unit last-dim stride")
+        if kv.dim() != 2 or kv.shape[0] != rows or kv.shape[1] < rp + P or kv.stride(1) != 1:
+            raise ValueError("append.kv must be [rows, >=R_pad+P] with unit last-dim stride")
         if kv.dtype != dt or ln_w.dtype != dt or ln_b.dtype != dt:
             raise TypeError(f"append tensors must be {dt}")
-        if not (ln_w.is_contiguous() and ln_b.is_contiguous() and ln_w.numel() == R and ln_b.numel() == R):
-            raise ValueError("LayerNorm weight / bias must be contiguous [R]")
+        if not (ln_w.is_contiguous() and ln_b.is_contiguous() and ln_w.numel() in (rk, rp)
+                and ln_b.numel() in (rk, rp)):
+            raise ValueError("LayerNorm weight / bias must be contiguous [R] or [R_pad]")
+        ln_w, ln_b = pad_rank(ln_w.reshape(-1), rk), pad_rank(ln_b.reshape(-1), rk)
         _need_gpu(kv, ln_w, ln_b, append.err_flag)
         _abi.check(
             lib.mla_decode_attn_append(
@@ -333,7 +377,7 @@ def decode_attention(
                 cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
                 cache.ckv.shape[0], cache.ckv.shape[1], p_sp, int(bool(rope_abs)),
-                rows, H, R, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
+                rows, H, rk, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
                 _abi.ptr(workspace.o_part if workspace else None),
                 _abi.ptr(workspace.lse_part if workspace else None),
                 out.data_ptr(), out.stride(0), out.stride(1),
@@ -349,7 +393,7 @@ def decode_attention(
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
                 cache.ckv.shape[0], cache.ckv.shape[1],
                 p_seq, p_len, p_rope, p_sp, int(rows_per_seq), int(bool(rope_abs)),
-                rows, H, R, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
+                rows, H, rk, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
                 _abi.ptr(workspace.o_part if workspace else None),
                 _abi.ptr(workspace.lse_part if workspace else None),
                 out.data_ptr(), out.stride(0), out.stride(1),
@@ -360,7 +404,7 @@ def decode_attention(
         _abi.check(
             lib.mla_merge(
                 workspace.o_part.data_ptr(), workspace.lse_part.data_ptr(), p_seq, p_len, p_sp,
-                int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1], rows, H, R, n_splits, min_chunk,
+                int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1], rows, H, rk, n_splits, min_chunk,
                 _abi.ptr(plan), out.data_ptr(), out.stride(0), out.stride(1),
                 _abi.ptr(lse_out), _abi.dtype_code(dt), stream,
             )
@@ -371,13 +415,14 @@ def decode_attention(
 PREFILL_QUERIES_PER_BLOCK = 8  # mla_prefill_attn: one query per wave, eight waves
 
 
-def use_prefill(n_seq: int, tokens_per_seq: int, num_cus: int = 256) -> bool:
+def use_prefill(n_seq: int, tokens_per_seq: int, num_cus: int = 256, rank: int = R) -> bool:
     """Whether a dense chunk of ``tokens_per_seq`` tokens per sequence is
     better served by prefill_attention (eight queries share each cache tile)
     than by per-row decode_attention with split-KV: when the chunk alone
-    gives about one workgroup per CU."""
+    gives about one workgroup per CU (prefill_attention covers ranks up to
+    256)."""
     blocks = n_seq * -(-tokens_per_seq // PREFILL_QUERIES_PER_BLOCK)
-    return tokens_per_seq >= 8 and blocks >= num_cus
+    return tokens_per_seq >= 8 and blocks >= num_cus and padded_rank(rank) <= 256
 
 
 def prefill_attention(
@@ -395,23 +440,25 @@ def prefill_attention(
 ) -> torch.Tensor:
     """Causal absorbed attention of a prefill chunk (mla_prefill_attn): row r
     is token r % T of sequence r / T and attends to [0, start_pos + r % T + 1).
-    Same operands as decode_attention in dense mode; no split-KV.
+    Same operands as decode_attention in dense mode; no split-KV; ranks up
+    to 256 (use_prefill says when it applies).
     Reference: models/mla.py:417-487 (seqlen > 1)."""
     cache.validate()
     dev = _need_gpu(q_abs, q_pe, cos_tab, sin_tab, cache.ckv, start_pos)
     dt = cache.model_dtype
     rows = q_abs.shape[0]
-    if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (H, R) or q_abs.stride(2) != 1:
-        raise ValueError(f"q_abs must be [rows, {H}, {R}] with unit last stride")
+    rk, rp = cache.rank, cache.rank_pad
+    if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (H, rp) or q_abs.stride(2) != 1:
+        raise ValueError(f"q_abs must be [rows, {H}, {rp}] (R_pad) with unit last stride")
     if q_pe.dim() != 3 or tuple(q_pe.shape) != (rows, H, P) or q_pe.stride(2) != 1:
         raise ValueError(f"q_pe must be [rows, {H}, {P}] with unit last stride")
     if q_abs.dtype != dt or q_pe.dtype != dt or cos_tab.dtype != dt:
         raise TypeError(f"query and RoPE tensors must be {dt}")
     _, p_sp = _addressing(rows, (None, None, None), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
     if out is None:
-        out = torch.empty(rows, H, R, dtype=dt, device=dev)
-    if tuple(out.shape) != (rows, H, R) or out.stride(2) != 1 or out.dtype != dt:
-        raise ValueError("out must be [rows, H, R] in the model dtype with unit last stride")
+        out = torch.empty(rows, H, rp, dtype=dt, device=dev)
+    if tuple(out.shape) != (rows, H, rp) or out.stride(2) != 1 or out.dtype != dt:
+        raise ValueError("out must be [rows, H, R_pad] in the model dtype with unit last stride")
     _abi.check(
         _abi.lib().mla_prefill_attn(
             q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1),
@@ -419,7 +466,7 @@ def prefill_attention(
             cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
             cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
             cache.ckv.shape[0], cache.ckv.shape[1], p_sp, int(rows_per_seq), int(bool(rope_abs)),
-            rows, H, R, P, float(sm_scale),
+            rows, H, rk, P, float(sm_scale),
             out.data_ptr(), out.stride(0), out.stride(1),
             _abi.dtype_code(dt), cache.cache_code, _abi.stream_handle(dev),
         )
@@ -552,8 +599,9 @@ def merge_project(
 ) -> torch.Tensor:
     """out[r, h, :] = W_uv[h] . o_lat[r, h, :] where o_lat is merged from the
     split partials left by ``decode_attention(..., merge=False)`` (or read
-    from ``o_lat`` for single-split rows); mla_merge_project.  w_uv [H, Dv, R]
-    may be a view of wkv_b.weight; out [rows, H, Dv] may be a view of wo's
+    from ``o_lat`` for single-split rows); mla_merge_project.  o_lat and w_uv
+    [H, Dv, R_pad] hold R_pad channels (w_uv a view of wkv_b.weight when R =
+    R_pad, else a zero-padded copy); out [rows, H, Dv] may be a view of wo's
     [rows, H*Dv] input.  Addressing and split plan must be the ones the
     decode call used (``balanced``: the decode call had ``balance`` > 0 and
     left its chunk in ``workspace.plan``).  Reference: models/mla.py:433,
@@ -561,17 +609,18 @@ def merge_project(
     dev = _need_gpu(o_lat, w_uv, out, row_seq, kv_len, start_pos)
     rows = o_lat.shape[0]
     Dv = w_uv.shape[1]
-    if o_lat.dim() != 3 or tuple(o_lat.shape[1:]) != (H, R) or o_lat.stride(2) != 1:
-        raise ValueError(f"o_lat must be [rows, {H}, {R}] with unit last stride")
-    if w_uv.dim() != 3 or tuple(w_uv.shape) != (H, Dv, R) or w_uv.stride(2) != 1:
-        raise ValueError(f"w_uv must be [{H}, Dv, {R}] with unit last stride")
+    rk, rp = cache.rank, cache.rank_pad
+    if o_lat.dim() != 3 or tuple(o_lat.shape[1:]) != (H, rp) or o_lat.stride(2) != 1:
+        raise ValueError(f"o_lat must be [rows, {H}, {rp}] (R_pad) with unit last stride")
+    if w_uv.dim() != 3 or tuple(w_uv.shape) != (H, Dv, rp) or w_uv.stride(2) != 1:
+        raise ValueError(f"w_uv must be [{H}, Dv, {rp}] (R_pad) with unit last stride")
     if tuple(out.shape) != (rows, H, Dv) or out.stride(2) != 1:
         raise ValueError(f"out must be [{rows}, {H}, {Dv}] with unit last stride")
     if not (o_lat.dtype == w_uv.dtype == out.dtype == torch.bfloat16):
         raise TypeError("merge_project: bf16 tensors only")
     (p_seq, p_len, _), p_sp = _addressing(
         rows, (row_seq, kv_len, None), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
-    if (n_splits > 1 or balanced) and (workspace is None or not workspace.fits(rows, n_splits)):
+    if (n_splits > 1 or balanced) and (workspace is None or not workspace.fits(rows, n_splits, rk)):
         raise ValueError("merge_project needs the decode call's workspace")
     _abi.check(
         _abi.lib().mla_merge_project(
@@ -579,7 +628,7 @@ def merge_project(
             _abi.ptr(workspace.lse_part if n_splits > 1 else None),
             o_lat.data_ptr(), o_lat.stride(0), o_lat.stride(1),
             p_len, p_seq, p_sp, int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1],
-            rows, H, R, n_splits, min_chunk, _abi.ptr(workspace.plan if balanced else None),
+            rows, H, rk, n_splits, min_chunk, _abi.ptr(workspace.plan if balanced else None),
             w_uv.data_ptr(), w_uv.stride(1), w_uv.stride(0), Dv,
             out.data_ptr(), out.stride(0), out.stride(1), _abi.DTYPE_BF16, _abi.stream_handle(dev),
         )

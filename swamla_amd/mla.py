@@ -24,6 +24,9 @@ Differences from the reference, all deliberate:
     allocates fp32 on the default device, mla.py:207-215);
   * ``cache_dtype="fp8_e4m3"`` stores the latent as e4m3fn codes with one
     fp32 scale per token (``kv_scale``);
+  * ``kv_cache`` holds R_pad = 64 * ceil(kv_lora_rank / 64) channels per
+    token, channels kv_lora_rank.. zero (the kernels' row layout; the same
+    shape as the reference's whenever kv_lora_rank is a multiple of 64);
   * ``clear_cache()`` also leaves inference mode, so the next
     ``set_inference_mode(True)`` reallocates (the reference leaves None
     caches behind and its next forward fails);
@@ -108,6 +111,7 @@ class MLA(nn.Module):
         self._absorbed = None  # (key, W_uk [H,nope,R], W_uv^T [H,R,v])
         self._decode_w = None  # (key, stacked absorbed-query / q_pe / wkv_a weight, stacked bias, packed)
         self._wo_packed = None  # (key, wo.weight packed for mla_linear_packed)
+        self._padded_w = {}  # name -> (key, zero-padded copy to R_pad): kv_norm, wkv_a, W_uv
         self._workspace: Optional[DecodeWorkspace] = None
         self._num_cus: Optional[int] = None
         # Split-KV plan of decode launches: "auto" balances the rows' splits
@@ -144,7 +148,7 @@ class MLA(nn.Module):
                 if self.fp8_cache:
                     self.register_buffer(
                         "kv_cache",
-                        torch.zeros(*shape, self.kv_lora_rank, dtype=torch.uint8, device=p.device),
+                        torch.zeros(*shape, self.rank_pad, dtype=torch.uint8, device=p.device),
                         persistent=False,
                     )
                     self.register_buffer(
@@ -153,7 +157,7 @@ class MLA(nn.Module):
                 else:
                     self.register_buffer(
                         "kv_cache",
-                        torch.zeros(*shape, self.kv_lora_rank, dtype=p.dtype, device=p.device),
+                        torch.zeros(*shape, self.rank_pad, dtype=p.dtype, device=p.device),
                         persistent=False,
                     )
             if getattr(self, "pe_cache", None) is None:
@@ -200,24 +204,81 @@ class MLA(nn.Module):
                 f"cache dtype ({self.kv_cache.dtype}/{self.pe_cache.dtype}) does not match the "
                 f"parameters ({dt}); convert the module before set_inference_mode(True)"
             )
-        return LatentCache(self.kv_cache, self.pe_cache, self.kv_scale if self.fp8_cache else None)
+        return LatentCache(self.kv_cache, self.pe_cache, self.kv_scale if self.fp8_cache else None,
+                           self.kv_lora_rank)
+
+    @property
+    def rank_pad(self) -> int:
+        """Latent channels stored per token: kv_lora_rank rounded up to 64."""
+        return kernels.padded_rank(self.kv_lora_rank)
+
+    def _padded(self, name: str, src: torch.Tensor, build) -> torch.Tensor:
+        """A derived weight, rebuilt when ``src`` changes: ``build()`` pads it
+        to R_pad; ``src`` itself is used when kv_lora_rank needs no padding."""
+        if self.rank_pad == self.kv_lora_rank:
+            return src.detach()
+        key = (src.data_ptr(), src._version, src.dtype, src.device)
+        hit = self._padded_w.get(name)
+        if hit is None or hit[0] != key:
+            hit = (key, build().contiguous())
+            self._padded_w[name] = hit
+        return hit[1]
+
+    def kv_norm_params(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """kv_norm's weight and bias zero-padded to R_pad (the kernels read
+        R_pad entries; the padding takes no part in the LayerNorm)."""
+        R = self.kv_lora_rank
+        w = self._padded("kv_norm.weight", self.kv_norm.weight,
+                         lambda: kernels.pad_rank(self.kv_norm.weight.detach(), R))
+        b = self._padded("kv_norm.bias", self.kv_norm.bias,
+                         lambda: kernels.pad_rank(self.kv_norm.bias.detach(), R))
+        return w, b
+
+    def _wkv_a_padded(self) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """wkv_a with its R latent rows followed by R_pad - R zero rows, so its
+        output rows are [R_pad latent | P rope], the append kernels' layout."""
+        R, rp, P = self.kv_lora_rank, self.rank_pad, self.qk_rope_head_dim
+
+        def pad_rows(t):
+            out = torch.zeros((rp + P,) + tuple(t.shape[1:]), dtype=t.dtype, device=t.device)
+            out[:R] = t[:R]
+            out[rp:] = t[R:]
+            return out
+
+        w = self._padded("wkv_a.weight", self.wkv_a.weight, lambda: pad_rows(self.wkv_a.weight.detach()))
+        b = None
+        if self.wkv_a.bias is not None:
+            b = self._padded("wkv_a.bias", self.wkv_a.bias, lambda: pad_rows(self.wkv_a.bias.detach()))
+        return w, b
+
+    def _w_uv(self) -> torch.Tensor:
+        """W_uv [H, Dv, R_pad] for mla_merge_project: a view of wkv_b.weight,
+        or its zero-padded copy."""
+        H, Dn, Dv, R = self.n_heads, self.qk_nope_head_dim, self.v_head_dim, self.kv_lora_rank
+        view = lambda: self.wkv_b.weight.detach().view(H, Dn + Dv, R)[:, Dn:, :]
+        if self.rank_pad == R:
+            return view()
+        return self._padded("w_uv", self.wkv_b.weight, lambda: kernels.pad_rank(view(), R))
 
     # ------------------------------------------------------------- weights
     def absorbed_weights(self) -> tuple[torch.Tensor, torch.Tensor]:
-        """W_uk [H, nope, R] and W_uv^T [H, R, v] from wkv_b (mla.py:404-406, :427, :433)."""
+        """W_uk [H, nope, R_pad] and W_uv^T [H, R_pad, v] from wkv_b
+        (mla.py:404-406, :427, :433), zero beyond kv_lora_rank."""
         w = self.wkv_b.weight
         key = (w.data_ptr(), w._version, w.dtype, w.device)
         if self._absorbed is None or self._absorbed[0] != key:
-            wv = w.detach().view(self.n_heads, -1, self.kv_lora_rank)
-            w_uk = wv[:, : self.qk_nope_head_dim].contiguous()
-            w_uv_t = wv[:, -self.v_head_dim:].transpose(1, 2).contiguous()
+            R = self.kv_lora_rank
+            wv = w.detach().view(self.n_heads, -1, R)
+            w_uk = kernels.pad_rank(wv[:, : self.qk_nope_head_dim], R).contiguous()
+            w_uv_t = kernels.pad_rank(wv[:, -self.v_head_dim:].transpose(1, 2), R, dim=1).contiguous()
             self._absorbed = (key, w_uk, w_uv_t)
         return self._absorbed[1], self._absorbed[2]
 
     def decode_weights(self) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
         """Stacked weight of the fused decode-step input product, rows
-        [W_uk[h]^T . wq_nope[h] for every head (H*R) | wq_pe (H*P) | wkv_a
-        (R+P)] over the model width, and its stacked bias (or None).  One
+        [W_uk[h]^T . wq_nope[h] for every head (H*R_pad) | wq_pe (H*P) | wkv_a
+        (R_pad+P)] over the model width, and its stacked bias (or None); the
+        rows of the latent padding are zero.  One
         product x . W^T then yields q_abs = q_nope . W_uk (the absorbed query,
         re-associating mla.py:427), q_pe and the wkv_a rows (mla.py:281-288,
         :307).  The absorbed block is formed in fp32 and rounded once to the
@@ -225,19 +286,19 @@ class MLA(nn.Module):
         ws = (self.wq.weight, self.wkv_a.weight, self.wkv_b.weight)
         key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in ws)
         if self._decode_w is None or self._decode_w[0] != key:
-            H, Dn, R = self.n_heads, self.qk_nope_head_dim, self.kv_lora_rank
+            H, Dn, R, rp = self.n_heads, self.qk_nope_head_dim, self.kv_lora_rank, self.rank_pad
             wq = self.wq.weight.detach().view(H, self.qk_head_dim, self.dim)
-            w_uk = self.wkv_b.weight.detach().view(H, -1, R)[:, :Dn]  # [H, Dn, R]
-            w_abs = torch.bmm(w_uk.float().transpose(1, 2).contiguous(), wq[:, :Dn].float().contiguous())
+            w_uk = kernels.pad_rank(self.wkv_b.weight.detach().view(H, -1, R)[:, :Dn].float(), R)  # [H, Dn, R_pad]
+            w_abs = torch.bmm(w_uk.transpose(1, 2).contiguous(), wq[:, :Dn].float().contiguous())
+            wkv_a, bkv_a = self._wkv_a_padded()
             w_in = torch.cat(
-                [w_abs.reshape(H * R, self.dim), wq[:, Dn:].float().reshape(-1, self.dim),
-                 self.wkv_a.weight.detach().float()], 0,
+                [w_abs.reshape(H * rp, self.dim), wq[:, Dn:].float().reshape(-1, self.dim), wkv_a.float()], 0,
             ).to(self.wq.weight.dtype).contiguous()
             b_in = None
             if self.wq.bias is not None and self.wkv_a.bias is not None:
                 bq = self.wq.bias.detach().view(H, self.qk_head_dim)
-                b_abs = torch.bmm(bq[:, None, :Dn].float(), w_uk.float()).reshape(H * R)
-                b_in = torch.cat([b_abs, bq[:, Dn:].float().reshape(-1), self.wkv_a.bias.detach().float()]
+                b_abs = torch.bmm(bq[:, None, :Dn].float(), w_uk).reshape(H * rp)
+                b_in = torch.cat([b_abs, bq[:, Dn:].float().reshape(-1), bkv_a.float()]
                                  ).to(self.wq.bias.dtype).contiguous()
             wp = None
             if w_in.is_cuda and kernels.packed_ok(1, w_in.shape[0], w_in.shape[1]):
@@ -258,10 +319,10 @@ class MLA(nn.Module):
         return self._wo_packed[1]
 
     def _fused_projections(self, x: torch.Tensor):
-        """q_abs [n, H, R], q_pe [n, H, P] and kv [n, R+P] from one product
-        over decode_weights() (mla_linear_packed with its packed copy, else
-        mla_linear; column views of one [n, H*(R+P)+R+P] buffer)."""
-        n, H, R, P = x.shape[0] * x.shape[1], self.n_heads, self.kv_lora_rank, self.qk_rope_head_dim
+        """q_abs [n, H, R_pad], q_pe [n, H, P] and kv [n, R_pad+P] from one
+        product over decode_weights() (mla_linear_packed with its packed copy,
+        else mla_linear; column views of one [n, H*(R_pad+P)+R_pad+P] buffer)."""
+        n, H, R, P = x.shape[0] * x.shape[1], self.n_heads, self.rank_pad, self.qk_rope_head_dim
         w_in, b_in = self.decode_weights()
         wp = self._decode_w[3]
         if wp is not None and kernels.packed_ok(n, wp.N, wp.K):
@@ -276,10 +337,10 @@ class MLA(nn.Module):
         """The decode-step kernels cover bf16 modules with at most 128 query
         rows, no q low-rank path and 128-aligned model widths."""
         return (
-            x.dtype == torch.bfloat16
+            self.q_lora_rank == 0
+            and x.dtype == torch.bfloat16
             and self.wq.weight.dtype == torch.bfloat16
             and 0 < n <= kernels.LINEAR_MAX_ROWS
-            and self.q_lora_rank == 0
             and self.dim % 128 == 0
             and (self.n_heads * self.v_head_dim) % 128 == 0
             and (self.wq.bias is None) == (self.wkv_a.bias is None)
@@ -287,9 +348,10 @@ class MLA(nn.Module):
         )
 
     def _check_geometry(self) -> None:
-        if (self.n_heads, self.kv_lora_rank, self.qk_rope_head_dim) != (kernels.H, kernels.R, kernels.P):
+        if ((self.n_heads, self.qk_rope_head_dim) != (kernels.H, kernels.P)
+                or not 1 <= self.kv_lora_rank <= kernels.MAX_RANK):
             raise NotImplementedError(
-                f"kernels are built for n_heads={kernels.H}, kv_lora_rank={kernels.R}, "
+                f"kernels are built for n_heads={kernels.H}, kv_lora_rank 1..{kernels.MAX_RANK}, "
                 f"qk_rope_head_dim={kernels.P}; got {self.n_heads}, {self.kv_lora_rank}, "
                 f"{self.qk_rope_head_dim}"
             )
@@ -318,8 +380,8 @@ class MLA(nn.Module):
         if n_splits <= 1:
             return None
         ws = self._workspace
-        if ws is None or not ws.fits(n_rows, n_splits) or ws.o_part.device != device:
-            ws = DecodeWorkspace.allocate(n_rows, n_splits, device)
+        if ws is None or not ws.fits(n_rows, n_splits, self.kv_lora_rank) or ws.o_part.device != device:
+            ws = DecodeWorkspace.allocate(n_rows, n_splits, device, rank=self.kv_lora_rank)
             self._workspace = ws
         return ws
 
@@ -365,12 +427,14 @@ class MLA(nn.Module):
         with torch.no_grad():
             _, kv = self.input_projections(x, need_q=False)
             cos, sin = self.rope.half_tables()
-            kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
+            ln_w, ln_b = self.kv_norm_params()
+            kernels.append(kv, cache, ln_w, ln_b, self.kv_norm.eps, cos, sin,
                            start_pos=sp, tokens_per_seq=T, rope_abs=self.rope_positions == "absolute")
 
     def input_projections(self, x: torch.Tensor, need_q: bool = True) -> tuple[Optional[torch.Tensor], torch.Tensor]:
-        """(q [B*T, H, 192] or None, kv [B*T, R + P]): the wkv_a rows that
-        forward feeds the append kernel (mla.py:281-288, :307-308).
+        """(q [B*T, H, 192] or None, kv [B*T, R_pad + P]): the wkv_a rows
+        that forward feeds the append kernel (mla.py:281-288, :307-308), with
+        zero latent padding up to R_pad.
         Decode-sized bf16 inputs take kv from the fused input product (and
         return no q: forward uses the absorbed query directly); other inputs
         use the ATen projections (q is skipped when not needed)."""
@@ -380,7 +444,11 @@ class MLA(nn.Module):
             if self._fused_step_ok(x, n):
                 _, _, kv = self._fused_projections(x)
                 return None, kv
-            kv = self.wkv_a(x).view(n, -1)
+            if self.rank_pad == self.kv_lora_rank:
+                kv = self.wkv_a(x).view(n, -1)
+            else:
+                w, b = self._wkv_a_padded()
+                kv = torch.nn.functional.linear(x, w, b).view(n, -1)
             if not need_q:
                 return None, kv
             if self.q_lora_rank == 0:
@@ -417,7 +485,7 @@ class MLA(nn.Module):
             max_len = (int(start_pos) + T) if not isinstance(start_pos, torch.Tensor) else cache.ckv.shape[1]
         else:
             # No cache (mla.py:419-423): attend over this call's tokens only.
-            cache = LatentCache.allocate(B, T, x.dtype, dev, fp8=self.fp8_cache)
+            cache = LatentCache.allocate(B, T, x.dtype, dev, fp8=self.fp8_cache, rank=R)
             sp = torch.zeros(B, dtype=torch.int32, device=dev)
             max_len = T
 
@@ -431,19 +499,20 @@ class MLA(nn.Module):
         # A one-token step appends inside the attention launch; longer chunks
         # append first (their rows attend to each other's new tokens).
         fold_append = fused and T == 1
+        ln_w, ln_b = self.kv_norm_params()
         if not fold_append:
-            kernels.append(kv, cache, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps, cos, sin,
+            kernels.append(kv, cache, ln_w, ln_b, self.kv_norm.eps, cos, sin,
                            start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
 
         n_splits, min_chunk, balance = self._decode_plan(
             n, max_len, dev, isinstance(start_pos, torch.Tensor) and self.inference_mode)
         # A chunk of many tokens per sequence: four queries share each cache
         # tile (no split-KV) instead of one row per workgroup.
-        prefill = x.dtype == torch.bfloat16 and kernels.use_prefill(B, T, self._num_cus)
+        prefill = x.dtype == torch.bfloat16 and kernels.use_prefill(B, T, self._num_cus, rank=R)
         if prefill:
             n_splits, balance = 1, 0
         if fused:
-            o_lat = torch.empty(n, H, R, dtype=x.dtype, device=dev)
+            o_lat = torch.empty(n, H, self.rank_pad, dtype=x.dtype, device=dev)
             ws = self._workspace_for(n, n_splits, dev)
             if prefill:
                 kernels.prefill_attention(q_abs, q_pe, cos, sin, cache, self.softmax_scale, start_pos=sp,
@@ -451,7 +520,7 @@ class MLA(nn.Module):
             else:
                 fa = None
                 if fold_append:
-                    fa = kernels.FusedAppend(kv, self.kv_norm.weight, self.kv_norm.bias, self.kv_norm.eps)
+                    fa = kernels.FusedAppend(kv, ln_w, ln_b, self.kv_norm.eps)
                 kernels.decode_attention(
                     q_abs, q_pe, cos, sin, cache, self.softmax_scale,
                     start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
@@ -459,7 +528,7 @@ class MLA(nn.Module):
                 )
             # o[r, h*Dv + d] = W_uv[h][d] . merged o_lat[r, h]: split merge and
             # read-out in one launch, written straight in wo's input layout
-            w_uv = self.wkv_b.weight.detach().view(H, Dn + Dv, R)[:, Dn:, :]
+            w_uv = self._w_uv()
             o = torch.empty(n, H * Dv, dtype=x.dtype, device=dev)
             kernels.merge_project(o_lat, w_uv, o.view(n, H, Dv), cache, n_splits=n_splits, min_chunk=min_chunk,
                                   workspace=ws, start_pos=sp, rows_per_seq=T, balanced=balance > 0)
@@ -473,8 +542,8 @@ class MLA(nn.Module):
 
         w_uk, w_uv_t = self.absorbed_weights()
         q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]
-        q_abs = torch.bmm(q_nope, w_uk)  # [H, n, R]
-        o_lat = torch.empty(H, n, R, dtype=x.dtype, device=dev)
+        q_abs = torch.bmm(q_nope, w_uk)  # [H, n, R_pad]
+        o_lat = torch.empty(H, n, self.rank_pad, dtype=x.dtype, device=dev)
         if prefill:
             kernels.prefill_attention(q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
                                       start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, out=o_lat.transpose(0, 1))

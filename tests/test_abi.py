@@ -59,7 +59,8 @@ def _decode(lib, **kw):
 @pytest.mark.parametrize(
     "kw,code",
     [
-        (dict(R=128), -2),
+        (dict(R=513), -2),  # kv_lora_rank 1..512
+        (dict(R=0), -2),
         (dict(P=32), -2),
         (dict(in_dt=0, c_dt=1), -2),
         (dict(in_dt=2, c_dt=2), -2),
@@ -68,6 +69,7 @@ def _decode(lib, **kw):
         (dict(seq=None), -1),
         (dict(c_dt=2), -1),  # fp8 without a scale buffer
         (dict(in_rs=100), -1),
+        (dict(R=200, in_rs=300), -1),  # rows hold R_pad = 256 latent channels + 64
         (dict(cs=0), -1),
         (dict(rope_len=0), -1),
         (dict(ckv=FAKE + 8), -3),
@@ -92,7 +94,7 @@ def test_append_zero_tokens_is_a_noop(lib):
     "kw,code",
     [
         (dict(H=8), -2),
-        (dict(R=512), -2),
+        (dict(R=520), -2),
         (dict(dt=1, c_dt=0), -2),
         (dict(n_rows=70000), -1),
         (dict(ns=0), -1),
@@ -103,6 +105,7 @@ def test_append_zero_tokens_is_a_noop(lib):
         (dict(sm=float("nan")), -1),
         (dict(o=None), -1),
         (dict(qa_hs=100), -1),
+        (dict(R=300, qa_hs=312, o_hs=320), -1),  # head strides cover R_pad = 320
         (dict(c_dt=2), -1),
         (dict(qa=FAKE + 4), -3),
         (dict(o_rs=4100), -3),
@@ -146,6 +149,8 @@ def _decode_append(lib, **kw):
         (dict(kv_in=FAKE + 4), -3),
         (dict(in_rs=322), -3),
         (dict(w=FAKE + 2), -3),
+        (dict(R=512, in_rs=576, qa_hs=512, o_hs=512, kv_in=FAKE + 8), -3),  # 8 channels a lane: 16-byte loads
+        (dict(R=512, in_rs=580, qa_hs=512, o_hs=512), -3),
         (dict(c_dt=2), -1),  # fp8 without a scale buffer
         (dict(ns=4), -1),
         (dict(o=None), -1),
@@ -205,7 +210,7 @@ def _merge(lib, **kw):
 
 def test_merge_rejects_and_noop(lib):
     assert _merge(lib, ns=1) == 0
-    assert _merge(lib, R=128) == -2
+    assert _merge(lib, R=1024) == -2
     assert _merge(lib, o_part=None) == -1
     assert _merge(lib, dt=2) == -2
     assert _merge(lib, o_part=FAKE + 4) == -3
@@ -294,7 +299,7 @@ def _merge_project(lib, **kw):
     [
         (dict(dt=0), -2),
         (dict(Dv=64), -2),
-        (dict(R=128), -2),
+        (dict(R=600), -2),
         (dict(ns=0), -1),
         (dict(o_part=None), -1),
         (dict(row_seq=None), -1),
@@ -318,8 +323,8 @@ def test_merge_project_single_split_needs_no_partials(lib):
 
 
 def test_python_check_raises_with_message(lib):
-    rc = _append(lib, R=128)
-    with pytest.raises(_abi.SwamlaError, match="UNSUPPORTED.*R=128"):
+    rc = _append(lib, R=640)
+    with pytest.raises(_abi.SwamlaError, match="UNSUPPORTED.*R=640"):
         _abi.check(rc)
     with pytest.raises(RuntimeError):
         _abi.check(rc)

@@ -39,20 +39,23 @@ def close(out, ref, rtol, atol):
 
 
 # ------------------------------------------------------------------ append
-def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0):
-    say(f"append case dtype={dtype} fp8={fp8} n_tok={n_tok}")
+def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0, rank=R):
+    say(f"append case dtype={dtype} fp8={fp8} n_tok={n_tok} rank={rank}")
+    rp = kernels.padded_rank(rank)
     g = torch.Generator().manual_seed(seed)
-    kv = torch.randn(n_tok, 336, generator=g) * 2 + 0.3  # row stride 336 > 320
+    # rows [R_pad latent | P rope] with 16 spare columns; the latent padding
+    # R .. R_pad-1 holds garbage the kernel must ignore
+    kv = torch.randn(n_tok, rp + P + 16, generator=g) * 2 + 0.3
     kv = kv.to(dtype)
-    w = (1 + 0.1 * torch.randn(R, generator=g)).to(dtype)
-    b = (0.1 * torch.randn(R, generator=g)).to(dtype)
+    w = (1 + 0.1 * torch.randn(rank, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(rank, generator=g)).to(dtype)
     seq = torch.randint(0, B, (n_tok,), generator=g, dtype=torch.int32)
     # distinct destination per token: a random permutation of the (b, pos) grid
     flat = torch.randperm(B * S, generator=g)[:n_tok]
     seq = (flat // S).to(torch.int32)
     dst = (flat % S).to(torch.int32)
-    rp = torch.randint(0, S, (n_tok,), generator=g, dtype=torch.int32)
-    cache = LatentCache.allocate(B, S, dtype, gpu, fp8=fp8)
+    rpos = torch.randint(0, S, (n_tok,), generator=g, dtype=torch.int32)
+    cache = LatentCache.allocate(B, S, dtype, gpu, fp8=fp8, rank=rank)
     canary_c = torch.randint(0, 255, cache.ckv.shape, generator=g).to(torch.uint8) if fp8 else \
         torch.randn(cache.ckv.shape, generator=g).to(dtype)
     canary_p = torch.randn(cache.kpe.shape, generator=g).to(dtype)
@@ -63,14 +66,16 @@ def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0):
     cos, sin = tables(dtype, S, gpu)
     kvg = kv.to(gpu)
     kernels.append(kvg, cache, w.to(gpu), b.to(gpu), 1e-5, cos, sin,
-                   seq_idx=seq.to(gpu), dst_pos=dst.to(gpu), rope_pos=rp.to(gpu))
+                   seq_idx=seq.to(gpu), dst_pos=dst.to(gpu), rope_pos=rpos.to(gpu))
     torch.cuda.synchronize()
 
-    # expected rows
-    y = lo.layernorm_exact(kv[:, :R].float().numpy(), w.float().numpy(), b.float().numpy(), 1e-5,
+    # expected rows: the exactly rounded LayerNorm over the R channels, zeros
+    # in the padding
+    y = lo.layernorm_exact(kv[:, :rank].float().numpy(), w.float().numpy(), b.float().numpy(), 1e-5,
                            torch.bfloat16 if fp8 else dtype)
+    y = torch.cat([y, torch.zeros(n_tok, rp - rank, dtype=y.dtype)], 1)
     cos_c, sin_c = cos.cpu(), sin.cpu()
-    kpe = lo.rope_interleaved(kv[:, R:R + P], cos_c[rp.long()], sin_c[rp.long()])
+    kpe = lo.rope_interleaved(kv[:, rp:rp + P], cos_c[rpos.long()], sin_c[rpos.long()])
     exp_c = canary_c.clone()
     exp_p = canary_p.clone()
     if fp8:
@@ -94,6 +99,14 @@ def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0):
 @pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.float32, False), (torch.bfloat16, True)])
 def test_append_bit_exact(gpu, dtype, fp8):
     _append_case(gpu, dtype, fp8)
+
+
+@pytest.mark.parametrize("rank", [1, 64, 100, 128, 173, 200, 320, 384, 449, 512])
+@pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.float32, False), (torch.bfloat16, True)])
+def test_append_bit_exact_any_rank(gpu, dtype, fp8, rank):
+    """kv_lora_rank other than 256 (the real model scales it per layer): rows
+    padded to a multiple of 64 channels, the padding written as zeros."""
+    _append_case(gpu, dtype, fp8, rank=rank, seed=rank)
 
 
 def test_append_many_tokens_bit_exact(gpu):
@@ -122,22 +135,26 @@ def test_append_out_of_range_is_skipped_and_flagged(gpu):
 
 # ------------------------------------------------------------------ decode
 def _decode_case(gpu, dtype, fp8, lens, n_splits, min_chunk, row_seq=None, B=None, S=None, seed=0,
-                 q_scale=1.0, rope_pos=None, rtol=2e-2, atol=1e-2):
+                 q_scale=1.0, rope_pos=None, rtol=2e-2, atol=1e-2, rank=R, balance=0):
     rows = len(lens)
     B = B or rows
     S = S or max(max(lens), 1)
+    rp_ = kernels.padded_rank(rank)
     say(f"decode case dtype={dtype} fp8={fp8} rows={rows} lens={lens[:6]}... splits={n_splits} "
-        f"chunk={min_chunk}")
+        f"chunk={min_chunk} rank={rank} balance={balance}")
     g = torch.Generator().manual_seed(seed)
     cdt = torch.bfloat16 if fp8 else dtype
-    ckv = (torch.randn(B, S, R, generator=g)).to(cdt)
+    # latent rows of R_pad channels, zero beyond the rank (as the append writes them)
+    ckv = torch.zeros(B, S, rp_, dtype=cdt)
+    ckv[..., :rank] = torch.randn(B, S, rank, generator=g).to(cdt)
     kpe = (torch.randn(B, S, P, generator=g)).to(dtype)
     if fp8:
-        codes, scale = lo.fp8_quantize(ckv.reshape(-1, R))
-        cache = LatentCache(codes.view(B, S, R).to(gpu), kpe.to(gpu), scale.view(B, S).to(gpu))
+        codes, scale = lo.fp8_quantize(ckv.reshape(-1, rp_))
+        cache = LatentCache(codes.view(B, S, rp_).to(gpu), kpe.to(gpu), scale.view(B, S).to(gpu), rank)
     else:
-        cache = LatentCache(ckv.to(gpu), kpe.to(gpu))
-    q_abs = (torch.randn(rows, H, R, generator=g) * q_scale).to(dtype)
+        cache = LatentCache(ckv.to(gpu), kpe.to(gpu), rank=rank)
+    # the query's padding channels hold garbage the kernel must ignore
+    q_abs = (torch.randn(rows, H, rp_, generator=g) * q_scale).to(dtype)
     q_pe = (torch.randn(rows, H, P, generator=g) * q_scale).to(dtype)
     rs = torch.arange(rows, dtype=torch.int32) if row_seq is None else torch.tensor(row_seq, dtype=torch.int32)
     kl = torch.tensor(lens, dtype=torch.int32)
@@ -145,14 +162,16 @@ def _decode_case(gpu, dtype, fp8, lens, n_splits, min_chunk, row_seq=None, B=Non
     cos, sin = tables(dtype, max(S, 64), gpu)
     out = kernels.decode_attention(
         q_abs.to(gpu), q_pe.to(gpu), cos, sin, cache, SCALE, row_seq=rs.to(gpu), kv_len=kl.to(gpu),
-        q_rope_pos=rp.to(gpu), n_splits=n_splits, min_chunk=min_chunk,
+        q_rope_pos=rp.to(gpu), n_splits=n_splits, min_chunk=min_chunk, balance=balance,
     )
     torch.cuda.synchronize()
     q_pe_rot = lo.rope_interleaved(q_pe, cos.cpu()[rp.long()][:, None], sin.cpu()[rp.long()][:, None])
     ref, _ = lo.absorbed_attention_f64(
-        q_abs, q_pe_rot, cache.ckv.cpu(), kpe, kl, rs, SCALE, cache.scale.cpu() if fp8 else None
+        q_abs[..., :rank], q_pe_rot, cache.ckv.cpu()[..., :rank], kpe, kl, rs, SCALE,
+        cache.scale.cpu() if fp8 else None
     )
-    close(out, ref, rtol, atol)
+    close(out[..., :rank], ref, rtol, atol)
+    assert bool((out[..., rank:].float() == 0).all()), "padding channels of o_lat must be 0"
     return out
 
 
@@ -162,6 +181,17 @@ def test_decode_short_rows(gpu, dtype, fp8):
     _decode_case(gpu, dtype, fp8, [1], 1, 256, **tol)
     _decode_case(gpu, dtype, fp8, [15, 64, 100, 17], 1, 256, seed=1, **tol)
     _decode_case(gpu, dtype, fp8, [130, 1, 63, 65], 4, 64, seed=2, **tol)
+
+
+@pytest.mark.parametrize("rank", [1, 64, 100, 128, 173, 200, 320, 384, 449, 512])
+@pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.bfloat16, True), (torch.float32, False)])
+def test_decode_any_rank(gpu, dtype, fp8, rank):
+    """kv_lora_rank other than 256: one split, split-KV with the merge, and
+    the balanced plan; the query padding is ignored and the output padding 0."""
+    tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else {}
+    _decode_case(gpu, dtype, fp8, [1, 70, 300], 1, 256, seed=rank, rank=rank, **tol)
+    _decode_case(gpu, dtype, fp8, [1000, 1, 513, 2100], 8, 64, seed=rank + 1, rank=rank, **tol)
+    _decode_case(gpu, dtype, fp8, [1000, 0, 513, 2100], 16, 64, seed=rank + 2, rank=rank, balance=256, **tol)
 
 
 @pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.bfloat16, True), (torch.float32, False)])

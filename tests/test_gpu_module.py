@@ -43,15 +43,17 @@ def expected_cache(m, xs, dtype, fp8=False):
     cos, sin = (t.cpu() for t in m.rope.half_tables())
     w = m.kv_norm.weight.detach().float().cpu().numpy()
     b = m.kv_norm.bias.detach().float().cpu().numpy()
+    rank, rpad = m.kv_lora_rank, m.rank_pad
     cs, ps, ss = [], [], []
     with torch.no_grad():
         for x in xs:
             B, T, _ = x.shape
             kv = m.input_projections(x)[1].cpu()  # the rows forward fed the append kernel
-            y = lo.layernorm_exact(kv[:, :256].float().numpy(), w, b, m.kv_norm.eps,
+            y = lo.layernorm_exact(kv[:, :rank].float().numpy(), w, b, m.kv_norm.eps,
                                    torch.bfloat16 if fp8 else dtype)
+            y = torch.cat([y, torch.zeros(y.shape[0], rpad - rank, dtype=y.dtype)], 1)  # zero padding
             rp = torch.arange(T).repeat(B)
-            kpe = lo.rope_interleaved(kv[:, 256:320], cos[rp], sin[rp])
+            kpe = lo.rope_interleaved(kv[:, rpad:rpad + 64], cos[rp], sin[rp])
             if fp8:
                 y, sc = lo.fp8_quantize(y)
                 ss.append(sc.view(B, T))
@@ -206,3 +208,31 @@ def test_no_cache_forward_matches_reference(gpu):
     x = torch.randn(2, 33, 512).to(dtype)
     with torch.no_grad():
         close(ours(x.to(gpu), 0), ref(x, 0), dtype)
+
+
+@pytest.mark.parametrize("rank,q_lora,dim", [
+    (128, 0, 256), (173, 0, 256), (320, 0, 256), (449, 0, 256), (512, 0, 256),
+    (256, 96, 256), (200, 160, 1024), (300, 0, 1024),
+])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_module_any_rank_and_q_lora(gpu, dtype, rank, q_lora, dim):
+    """kv_lora_rank other than 256 (the real model scales it per layer:
+    swa_mla_model.py:216-247) and the low-rank query path (mla.py:98-103):
+    a prefill chunk, then decode steps at batch 2, against the reference
+    restatement with the same weights; cache rows bit-exact."""
+    say(f"rank={rank} q_lora={q_lora} dim={dim} dtype={dtype}")
+    cfg = MLAConfig(n_embd=dim, max_batch_size=2, max_seq_len=192, kv_lora_rank=rank, q_lora_rank=q_lora)
+    ref, ours = make_pair(cfg, 31 + rank, dtype, gpu, ln_random=True)
+    assert ours.kv_cache.shape[-1] == 64 * -(-rank // 64)
+    g = torch.Generator().manual_seed(32 + rank)
+    x = torch.randn(2, 40, dim, generator=g).to(dtype)
+    xs = [x.to(gpu)]
+    with torch.no_grad():
+        close(ours(xs[0], 0), ref(x, 0), dtype)
+        for step in range(6):
+            xd = torch.randn(2, 1, dim, generator=g).to(dtype)
+            xs.append(xd.to(gpu))
+            close(ours(xs[-1], 40 + step), ref(xd, 40 + step), dtype)
+    torch.cuda.synchronize()
+    assert_cache_bits(ours, xs, dtype)
+    assert bool((ours.kv_cache[:2, :46, rank:].float() == 0).all())

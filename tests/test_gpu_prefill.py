@@ -32,13 +32,17 @@ def tables(S, device):
             sin.to(torch.bfloat16)[0, 0, :, :32].contiguous().to(device))
 
 
-def make_cache(B, S, fp8, gen, device):
+def make_cache(B, S, fp8, gen, device, rank=R):
+    """Latent rows of R_pad channels, zero beyond the rank (as the append writes them)."""
+    rp = kernels.padded_rank(rank)
+    c = torch.zeros(B * S, rp, device=device, dtype=torch.bfloat16)
+    c[:, :rank] = torch.randn(B * S, rank, generator=gen, device=device).to(torch.bfloat16)
     if fp8:
-        codes, scale = lo.fp8_quantize(torch.randn(B * S, R, generator=gen, device=device).to(torch.bfloat16))
-        return LatentCache(codes.view(B, S, R), torch.randn(B, S, P, generator=gen, device=device).to(torch.bfloat16),
-                           scale.view(B, S).float())
-    return LatentCache(torch.randn(B, S, R, generator=gen, device=device).to(torch.bfloat16),
-                       torch.randn(B, S, P, generator=gen, device=device).to(torch.bfloat16))
+        codes, scale = lo.fp8_quantize(c)
+        return LatentCache(codes.view(B, S, rp), torch.randn(B, S, P, generator=gen, device=device).to(torch.bfloat16),
+                           scale.view(B, S).float(), rank)
+    return LatentCache(c.view(B, S, rp), torch.randn(B, S, P, generator=gen, device=device).to(torch.bfloat16),
+                       rank=rank)
 
 
 def reference(q_abs, q_pe, cos, sin, cache, sp, T, rope_abs):
@@ -47,7 +51,8 @@ def reference(q_abs, q_pe, cos, sin, cache, sp, T, rope_abs):
     batch) are zero."""
     rows = q_abs.shape[0]
     Bc, S = cache.ckv.shape[0], cache.ckv.shape[1]
-    out = torch.zeros(rows, H, R, dtype=torch.float32, device=q_abs.device)
+    rk = cache.rank
+    out = torch.zeros(rows, H, cache.rank_pad, dtype=torch.float32, device=q_abs.device)
     cos_c, sin_c = cos.cpu(), sin.cpu()
     for r in range(rows):
         b, t = divmod(r, T)
@@ -63,7 +68,7 @@ def reference(q_abs, q_pe, cos, sin, cache, sp, T, rope_abs):
             c = lo.fp8_dequantize(cache.ckv[b, :L], cache.scale[b, :L])
         else:
             c = cache.ckv[b, :L].float()
-        s = (q_abs[r].float() @ c.T + qpe.to(q_abs.device).float() @ cache.kpe[b, :L].float().T) * SCALE
+        s = (q_abs[r, :, :rk].float() @ c[:, :rk].T + qpe.to(q_abs.device).float() @ cache.kpe[b, :L].float().T) * SCALE
         out[r] = torch.softmax(s, dim=-1) @ c
     return out
 
@@ -85,16 +90,28 @@ def check(out, ref):
 ])
 @pytest.mark.parametrize("rope_abs", [False, True], ids=["chunk", "abs"])
 def test_prefill_matches_fp32_reference(gpu, fp8, B, T, starts, rope_abs):
-    say(f"prefill fp8={fp8} B={B} T={T} starts={starts} rope_abs={rope_abs}")
-    gen = torch.Generator(device=gpu).manual_seed(100 + B * 7 + T)
+    _prefill_case(gpu, fp8, B, T, starts, rope_abs, R)
+
+
+@pytest.mark.parametrize("rank", [1, 64, 100, 173, 192])
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "fp8"])
+def test_prefill_any_rank(gpu, fp8, rank):
+    """kv_lora_rank up to 256 other than 256 (padded rows; query padding ignored)."""
+    _prefill_case(gpu, fp8, 2, 65, [63, 700], True, rank)
+
+
+def _prefill_case(gpu, fp8, B, T, starts, rope_abs, rank):
+    say(f"prefill fp8={fp8} B={B} T={T} starts={starts} rope_abs={rope_abs} rank={rank}")
+    gen = torch.Generator(device=gpu).manual_seed(100 + B * 7 + T + rank)
     S = 2304
-    cache = make_cache(B, S, fp8, gen, gpu)
+    rp = kernels.padded_rank(rank)
+    cache = make_cache(B, S, fp8, gen, gpu, rank)
     cos, sin = tables(S, gpu)
     rows = B * T
-    q_abs = (0.3 * torch.randn(rows, H, R, generator=gen, device=gpu)).to(torch.bfloat16)
+    q_abs = (0.3 * torch.randn(rows, H, rp, generator=gen, device=gpu)).to(torch.bfloat16)
     q_pe = (0.3 * torch.randn(rows, H, P, generator=gen, device=gpu)).to(torch.bfloat16)
     sp = torch.tensor(starts, dtype=torch.int32, device=gpu)
-    out = torch.full((rows, H, R), float("nan"), dtype=torch.bfloat16, device=gpu)
+    out = torch.full((rows, H, rp), float("nan"), dtype=torch.bfloat16, device=gpu)
     kernels.prefill_attention(q_abs, q_pe, cos, sin, cache, SCALE, start_pos=sp, rows_per_seq=T,
                               rope_abs=rope_abs, out=out)
     # the per-row decode kernel on the same rows (one split)

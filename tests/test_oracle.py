@@ -118,20 +118,47 @@ def test_e4m3_decoders_match_torch(lib):
 
 
 # ---------------------------------------------------------------- LayerNorm
+@pytest.mark.parametrize("rank", [256, 1, 64, 173, 200, 320, 512])
 @pytest.mark.parametrize("ln_random", [False, True])
-def test_layernorm_f64_statement(ln_random):
+def test_layernorm_f64_statement(ln_random, rank):
     g = torch.Generator().manual_seed(4)
-    c = torch.randn(512, 256, generator=g) * 3 + 0.5
-    w = 1 + 0.1 * torch.randn(256, generator=g) if ln_random else torch.ones(256)
-    b = 0.1 * torch.randn(256, generator=g) if ln_random else torch.zeros(256)
+    c = torch.randn(512, rank, generator=g) * 3 + 0.5
+    w = 1 + 0.1 * torch.randn(rank, generator=g) if ln_random else torch.ones(rank)
+    b = 0.1 * torch.randn(rank, generator=g) if ln_random else torch.zeros(rank)
     eps = 1e-5
     y = lo.layernorm_f64(c.numpy(), w.numpy(), b.numpy(), eps)
-    ref = F.layer_norm(c.double(), (256,), w.double(), b.double(), float(np.float32(eps))).numpy()
+    assert y.shape == (512, rank)
+    ref = F.layer_norm(c.double(), (rank,), w.double(), b.double(), float(np.float32(eps))).numpy()
+    if rank == 1:  # a single channel normalises to exactly b
+        assert np.array_equal(y, np.broadcast_to(b.double().numpy(), y.shape))
+        return
     assert np.max(np.abs(y - ref)) < 1e-13
     if not ln_random:  # invariants of the normalised rows
         assert np.max(np.abs(y.mean(axis=1))) < 1e-14
         var = y.var(axis=1)
         assert np.max(np.abs(var - 1.0 / (1.0 + eps / c.double().var(dim=1, unbiased=False).numpy()))) < 1e-12
+
+
+def test_layernorm_f64_lane_order_at_rank_256():
+    """At R = 256 the statement is the four-channels-per-lane order: a
+    plain restatement of that order gives identical fp64 bits."""
+    g = torch.Generator().manual_seed(6)
+    c = (torch.randn(64, 256, generator=g) * 3).double().numpy()
+    w = (1 + 0.1 * torch.randn(256, generator=g)).double().numpy()
+    b = (0.1 * torch.randn(256, generator=g)).double().numpy()
+    x = c.reshape(-1, 64, 4)
+    s = ((x[..., 0] + x[..., 1]) + x[..., 2]) + x[..., 3]
+    lanes = np.arange(64)
+    for m in (1, 2, 4, 8, 16, 32):
+        s = s + s[..., lanes ^ m]
+    mean = s[..., :1] * (1.0 / 256.0)
+    d = x - mean[..., None]
+    q = ((d[..., 0] * d[..., 0] + d[..., 1] * d[..., 1]) + d[..., 2] * d[..., 2]) + d[..., 3] * d[..., 3]
+    for m in (1, 2, 4, 8, 16, 32):
+        q = q + q[..., lanes ^ m]
+    rstd = 1.0 / np.sqrt(q[..., :1] * (1.0 / 256.0) + float(np.float32(1e-5)))
+    want = ((d * rstd[..., None]) * w.reshape(64, 4) + b.reshape(64, 4)).reshape(-1, 256)
+    assert np.array_equal(lo.layernorm_f64(c, w, b, 1e-5), want)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
