@@ -67,7 +67,7 @@ def layernorm_f64(c: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np
     order, for any rank R = c.shape[-1] up to 512: the row is padded with
     zeros to R_pad = 64 * ceil(R / 64), lane l holds channels K*l .. K*l+K-1
     (K = R_pad / 64) summed left to right (padding adds +0.0), then an xor
-    butterfly, divided by R; the variance sums only the R real channels.
+    butterfly, times fl64(1 / R); the variance sums only the R real channels.
     Returns unrounded fp64 y [N, R].  ``eps`` is used as its fp32 value, as
     torch's LayerNorm does.  Pinned against torch.nn.functional.layer_norm in
     fp64 (agreement ~1e-15) and the mean-0 / var-1 invariants; for R = 256
@@ -83,12 +83,13 @@ def layernorm_f64(c: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np
     s = x[..., 0].copy()
     for i in range(1, K):
         s = s + x[..., i]
-    mean = _butterfly(s)[..., :1] / float(Rr)  # [N, 1]
+    inv_r = 1.0 / float(Rr)  # fp64, as the kernels receive it
+    mean = _butterfly(s)[..., :1] * inv_r  # [N, 1]
     d = np.where(valid, x - mean[..., None], 0.0)
     q = d[..., 0] * d[..., 0]
     for i in range(1, K):
         q = q + d[..., i] * d[..., i]
-    var = _butterfly(q)[..., :1] / float(Rr)
+    var = _butterfly(q)[..., :1] * inv_r
     rstd = 1.0 / np.sqrt(var + float(np.float32(eps)))
     wp = np.zeros(rp, np.float64)
     bp = np.zeros(rp, np.float64)

@@ -87,10 +87,10 @@ __device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xo
 // is rounded on its own: the result must reproduce the fixed-order fp64
 // statement exactly.  Statistics in fp64; fixed order: in-lane left to
 // right, then xor butterfly 1,2,4,...,32 (every lane ends with the same total),
-// divided by R.
+// times inv_r = fl64(1 / R) (exactly 2^-8 for R = 256).
 template <int K>
 __device__ __forceinline__ void layernorm_lane(const double (&x)[K], const double (&wt)[K], const double (&bs)[K],
-                                               int R, int lane, float eps, double (&y)[K]) {
+                                               int R, double inv_r, int lane, float eps, double (&y)[K]) {
 #pragma clang fp contract(off)
   bool v[K];
 #pragma unroll
@@ -100,7 +100,7 @@ __device__ __forceinline__ void layernorm_lane(const double (&x)[K], const doubl
   for (int i = 1; i < K; ++i) s = s + (v[i] ? x[i] : 0.0);
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) s = s + shfl_xor_f64(s, m);
-  const double mean = s / static_cast<double>(R);
+  const double mean = s * inv_r;
   double d[K];
 #pragma unroll
   for (int i = 0; i < K; ++i) d[i] = v[i] ? x[i] - mean : 0.0;
@@ -109,7 +109,7 @@ __device__ __forceinline__ void layernorm_lane(const double (&x)[K], const doubl
   for (int i = 1; i < K; ++i) q = q + d[i] * d[i];
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) q = q + shfl_xor_f64(q, m);
-  const double var = q / static_cast<double>(R);
+  const double var = q * inv_r;
   // correctly rounded square root and IEEE division
   const double rstd = 1.0 / __dsqrt_rn(var + static_cast<double>(eps));
 #pragma unroll

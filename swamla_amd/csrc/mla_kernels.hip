@@ -54,7 +54,7 @@ __device__ __forceinline__ void append_token(const AppendArgs& a, int tok, int l
     wt[i] = static_cast<double>(E::ld(w, NB * lane + i));
     bs[i] = static_cast<double>(E::ld(bb, NB * lane + i));
   }
-  layernorm_lane<NB>(x, wt, bs, a.R, lane, a.eps, y);
+  layernorm_lane<NB>(x, wt, bs, a.R, a.inv_r, lane, a.eps, y);
 
   const int64_t crow = static_cast<int64_t>(b) * a.cache_s + pos;
   if constexpr (C_DT == 0) {
@@ -248,7 +248,8 @@ struct FusedTok {
 
 // Same arithmetic as append_token<1, C_DT, NB>.
 template <int C_DT, int NB>
-__device__ __forceinline__ FusedTok<C_DT, NB> fused_compute(const FusedIn<NB>& f, float eps, int R, int lane) {
+__device__ __forceinline__ FusedTok<C_DT, NB> fused_compute(const FusedIn<NB>& f, float eps, int R, double inv_r,
+                                                            int lane) {
   double x[NB], wt[NB], bs[NB], y[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
@@ -256,7 +257,7 @@ __device__ __forceinline__ FusedTok<C_DT, NB> fused_compute(const FusedIn<NB>& f
     wt[i] = static_cast<double>(bf16_to_f32(f.wt[i]));
     bs[i] = static_cast<double>(bf16_to_f32(f.bs[i]));
   }
-  layernorm_lane<NB>(x, wt, bs, R, lane, eps, y);
+  layernorm_lane<NB>(x, wt, bs, R, inv_r, lane, eps, y);
   FusedTok<C_DT, NB> t;
   t.scale = 1.f;
   if constexpr (C_DT == 1) {
@@ -463,7 +464,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) 
   // tiles load.
   FusedTok<C_DT, NB> ftok;
   if constexpr (FUSE)
-    if (fa_wave) ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, lane);
+    if (fa_wave) ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, a.fa.inv_r, lane);
 
   f32x4_t oacc[NB];
 #pragma unroll
