@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define SWAMLA_ABI_VERSION 2
+#define SWAMLA_ABI_VERSION 3
 
 enum {
   SWAMLA_OK = 0,
@@ -326,6 +326,19 @@ int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk);
 int32_t mla_balanced_chunk(const int32_t* lens, int32_t n_rows,
                            int32_t n_splits, int32_t min_chunk,
                            int32_t balance_blocks);
+
+/* Decode workgroups per CU that the kernel mla_decode_attn (fused = 0) or
+ * mla_decode_attn_append (fused = 1) launches for this dtype pair and rank
+ * is built for, capped by the HIP occupancy of that kernel on the current
+ * device: 1 for a bf16 cache and for fp32; 3 for an e4m3 cache at
+ * R <= 256, whose kernel shares each CU among three workgroups to hide its
+ * per-tile latency.  A
+ * host sizes n_splits (static plan) or balance_blocks (balanced plan) for
+ * CUs x this many workgroups.  Negative SWAMLA_ERR_* on an unsupported
+ * combination or a failed HIP query.  No reference counterpart (the
+ * reference does not split the KV range). */
+int32_t mla_decode_blocks_per_cu(int32_t dtype, int32_t cache_dtype,
+                                 int32_t R, int32_t fused);
 
 #ifdef __cplusplus
 }

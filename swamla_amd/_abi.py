@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libswamla_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_F32, DTYPE_BF16, DTYPE_FP8 = 0, 1, 2
 ERR_NAMES = {
     -1: "INVALID_ARG",
@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "mla_merge",
     "mla_split_count",
     "mla_balanced_chunk",
+    "mla_decode_blocks_per_cu",
     "mla_linear",
     "mla_pack_weight",
     "mla_linear_packed",
@@ -73,6 +74,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_split_count.argtypes = [_I32, _I32, _I32]
     lib.mla_balanced_chunk.restype = _I32
     lib.mla_balanced_chunk.argtypes = [_P, _I32, _I32, _I32, _I32]
+    lib.mla_decode_blocks_per_cu.restype = _I32
+    lib.mla_decode_blocks_per_cu.argtypes = [_I32, _I32, _I32, _I32]
     lib.mla_append.restype = ctypes.c_int
     lib.mla_append.argtypes = [
         _P, _I64, _I32, _P, _P, _P, _P, _I32, _I32, _P, _P, _F, _P, _P, _I64,

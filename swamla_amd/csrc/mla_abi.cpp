@@ -109,6 +109,22 @@ int32_t mla_split_count(int32_t L, int32_t n_splits, int32_t min_chunk) {
   return split_count_impl(L, n_splits, min_chunk);
 }
 
+int32_t mla_decode_blocks_per_cu(int32_t dtype, int32_t cache_dtype, int32_t R, int32_t fused) {
+  if (int e = check_geometry(16, R, 64)) return e;
+  if (int e = check_pair(dtype, cache_dtype)) return e;
+  if (fused != 0 && fused != 1) return fail(SWAMLA_ERR_INVALID_ARG, "mla_decode_blocks_per_cu: fused must be 0 or 1");
+  int n = 0;
+  const int rc = swamla::decode_blocks_per_cu(dtype, cache_dtype, R, fused != 0, &n);
+  if (rc == -1)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_blocks_per_cu: no decode kernel for model=%d cache=%d fused=%d",
+                dtype, cache_dtype, fused);
+  if (rc != 0) {
+    const hipError_t e = hipGetLastError();
+    return fail(SWAMLA_ERR_HIP, "mla_decode_blocks_per_cu: occupancy query failed: %s", hipGetErrorString(e));
+  }
+  return n;
+}
+
 int32_t mla_balanced_chunk(const int32_t* lens, int32_t n_rows, int32_t n_splits, int32_t min_chunk,
                            int32_t balance_blocks) {
   if (n_rows < 0 || n_rows > swamla::kBalanceMaxRows || (n_rows > 0 && !lens) || n_splits < 1 ||

@@ -125,6 +125,10 @@ struct MergeProjectArgs {
 
 int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s);
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s);
+// Workgroups of the decode launch one CU holds at once (HIP occupancy of the
+// instance launch_decode picks); -1 for a combination without a kernel, -2
+// when the HIP query fails.
+int decode_blocks_per_cu(int dt, int c_dt, int R, bool fuse, int* blocks);
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s);
 int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s);
 // Product with a packed weight (see mla_pack_weight): Y = X . W^T (+ bias).

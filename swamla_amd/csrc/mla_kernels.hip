@@ -286,8 +286,24 @@ __device__ __forceinline__ void fused_store(const AppendArgs& a, int64_t crow, c
   if (lane < kP / 2) reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.kpe) + crow * kP)[lane] = t.pe;
 }
 
+// Occupancy of the decode kernel by cache type.  A bf16 tile streams at the
+// HBM rate with one workgroup per CU (four waves, one per SIMD) and DEPTH 2
+// tiles of loads in flight per wave.  An e4m3 tile carries 40% fewer bytes
+// through the same LDS/MFMA/softmax chain (plus the e4m3 decode), so with
+// one wave per SIMD that chain's latency, not HBM, sets the tile rate; at
+// ranks up to 256 three workgroups share a CU instead (one tile of loads in
+// flight per wave, at most 168 VGPRs, 3 x 45.7 KB of LDS), and each wave's
+// waits hide under the other workgroups' work.  The split plan asks
+// mla_decode_blocks_per_cu how many workgroups a CU holds.
+template <int C_DT, int NB>
+struct DecodeShape {
+  static constexpr bool kShared = C_DT == 2 && NB <= 4;
+  static constexpr int kDepth = kShared ? 1 : 2;       // tiles of loads in flight per wave
+  static constexpr int kWavesPerEU = kShared ? 3 : 1;  // workgroups per CU
+};
+
 template <int C_DT, int DEPTH, bool FUSE, int NB>
-__global__ __launch_bounds__(kWaves * 64, 1) void mla_decode_mfma(DecodeArgs a) {
+__global__ __launch_bounds__(kWaves * 64, (DecodeShape<C_DT, NB>::kWavesPerEU)) void mla_decode_mfma(DecodeArgs a) {
   constexpr int RP = LatGeo<NB>::RP, kCRow = LatGeo<NB>::CRow;
   __shared__ __attribute__((aligned(16))) uint8_t c_lds[LatGeo<NB>::CBytes];
   __shared__ __attribute__((aligned(16))) uint8_t pe_lds[kPeBytes];
@@ -834,10 +850,19 @@ int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-#ifndef SWAMLA_DECODE_DEPTH
-#define SWAMLA_DECODE_DEPTH 2
-#endif
-constexpr int kDecodeDepth = SWAMLA_DECODE_DEPTH;  // tiles of loads in flight per wave
+// The decode kernel instance for (model dtype, cache dtype, rank, fused
+// append), as a host function pointer; nullptr for a combination without one.
+template <int NB>
+const void* decode_kernel(int dt, int c_dt, bool fuse) {
+  if (dt == 1 && c_dt == 1 && !fuse)
+    return reinterpret_cast<const void*>(&mla_decode_mfma<1, DecodeShape<1, NB>::kDepth, false, NB>);
+  if (dt == 1 && c_dt == 2 && !fuse)
+    return reinterpret_cast<const void*>(&mla_decode_mfma<2, DecodeShape<2, NB>::kDepth, false, NB>);
+  if (dt == 1 && c_dt == 1) return reinterpret_cast<const void*>(&mla_decode_mfma<1, DecodeShape<1, NB>::kDepth, true, NB>);
+  if (dt == 1 && c_dt == 2) return reinterpret_cast<const void*>(&mla_decode_mfma<2, DecodeShape<2, NB>::kDepth, true, NB>);
+  if (dt == 0 && c_dt == 0 && !fuse) return reinterpret_cast<const void*>(&mla_decode_f32<NB>);
+  return nullptr;
+}
 
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
@@ -845,21 +870,28 @@ int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   const bool fuse = a.fa.kv_in != nullptr;
   const int rc = with_nb(a.R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value;
-    if (dt == 1 && c_dt == 1 && !fuse)
-      hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, false, NB>), grid, dim3(256), 0, s, a);
-    else if (dt == 1 && c_dt == 2 && !fuse)
-      hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, false, NB>), grid, dim3(256), 0, s, a);
-    else if (dt == 1 && c_dt == 1)
-      hipLaunchKernelGGL((mla_decode_mfma<1, kDecodeDepth, true, NB>), grid, dim3(256), 0, s, a);
-    else if (dt == 1 && c_dt == 2)
-      hipLaunchKernelGGL((mla_decode_mfma<2, kDecodeDepth, true, NB>), grid, dim3(256), 0, s, a);
-    else if (dt == 0 && c_dt == 0 && !fuse)
-      hipLaunchKernelGGL((mla_decode_f32<NB>), grid, dim3(256), 0, s, a);
-    else return -1;
-    return 0;
+    const void* fn = decode_kernel<NB>(dt, c_dt, fuse);
+    if (!fn) return -1;
+    void* args[] = {const_cast<DecodeArgs*>(&a)};
+    return hipLaunchKernel(fn, grid, dim3(256), args, 0, s) == hipSuccess ? 0 : -2;
   });
   if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// The workgroups per CU each instance is tuned for (DecodeShape; the fp32
+// kernel one), capped by what the device's registers and LDS hold.
+int decode_blocks_per_cu(int dt, int c_dt, int R, bool fuse, int* blocks) {
+  return with_nb(R, [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    const void* fn = decode_kernel<NB>(dt, c_dt, fuse);
+    if (!fn) return -1;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, 0) != hipSuccess || n < 1) return -2;
+    const int tuned = dt == 0 ? 1 : (c_dt == 2 ? DecodeShape<2, NB>::kWavesPerEU : DecodeShape<1, NB>::kWavesPerEU);
+    *blocks = n < tuned ? n : tuned;
+    return 0;
+  });
 }
 
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s) {

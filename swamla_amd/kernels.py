@@ -224,19 +224,43 @@ def plan_splits(n_rows: int, max_len: int, num_cus: int = 256, blocks_per_cu: in
     return int(max(1, min(target, by_len, 1024))), int(min_chunk)
 
 
+_BLOCKS_PER_CU: dict = {}
+
+
+def decode_blocks_per_cu(model_dtype: torch.dtype, fp8_cache: bool, rank: int, fused: bool,
+                         device: torch.device) -> int:
+    """Decode workgroups one CU holds at once for this kernel instance
+    (mla_decode_blocks_per_cu; cached per device): 1 for a bf16 cache, 3 for
+    an e4m3 cache at ranks up to 256.  Split plans target CUs x this."""
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    cache = _abi.DTYPE_FP8 if fp8_cache else _abi.dtype_code(model_dtype)
+    key = (idx, _abi.dtype_code(model_dtype), cache, int(rank), bool(fused))
+    n = _BLOCKS_PER_CU.get(key)
+    if n is None:
+        with torch.cuda.device(idx):
+            n = _abi.lib().mla_decode_blocks_per_cu(key[1], cache, int(rank), int(bool(fused)))
+        if n < 1:
+            _abi.check(n)
+        _BLOCKS_PER_CU[key] = n
+    return n
+
+
 BALANCE_MAX_ROWS = 256  # rows a balanced plan covers (mla_decode_attn)
 
 
-def balanced_splits(n_rows: int, num_cus: int = 256) -> tuple[int, int]:
+def balanced_splits(n_rows: int, num_cus: int = 256, blocks_per_cu: int = 1) -> tuple[int, int]:
     """Host side of a length-balanced plan (ragged batches): returns
     (balance_blocks, n_splits) for decode_attention's ``balance`` and
-    ``n_splits``: one workgroup per CU, and a per-row split cap of
-    4 * ceil(num_cus / n_rows), so one row may take several times its share
-    while the partial buffers stay near 4 * num_cus splits.  (0, 0) when
-    the batch has more rows than a balanced plan covers."""
-    if n_rows <= 0 or n_rows > min(num_cus, BALANCE_MAX_ROWS):
+    ``n_splits``: one workgroup per slot (num_cus x blocks_per_cu slots), and
+    a per-row split cap of 4 * ceil(slots / n_rows), so one row may take
+    several times its share while the partial buffers stay near 4 * slots
+    splits.  (0, 0) when the batch has more rows than a balanced plan
+    covers."""
+    slots = num_cus * max(1, blocks_per_cu)
+    if n_rows <= 0 or n_rows > min(slots, BALANCE_MAX_ROWS):
         return 0, 0
-    return int(num_cus), int(min(1024, 4 * -(-num_cus // n_rows)))
+    return int(slots), int(min(1024, 4 * -(-slots // n_rows)))
 
 
 def balanced_chunk(lens, n_splits: int, min_chunk: int, balance_blocks: int) -> int:

@@ -356,22 +356,27 @@ class MLA(nn.Module):
                 f"{self.qk_rope_head_dim}"
             )
 
-    def _split_plan(self, n_rows: int, max_len: int, device) -> tuple[int, int]:
+    def _split_plan(self, n_rows: int, max_len: int, device, blocks_per_cu: int = 1) -> tuple[int, int]:
         if self._num_cus is None:
             self._num_cus = torch.cuda.get_device_properties(device).multi_processor_count
-        return kernels.plan_splits(n_rows, max_len, num_cus=self._num_cus)
+        return kernels.plan_splits(n_rows, max_len, num_cus=self._num_cus, blocks_per_cu=blocks_per_cu)
 
-    def _decode_plan(self, n_rows: int, max_len: int, device, per_row_positions: bool) -> tuple[int, int, int]:
-        """(n_splits, min_chunk, balance) of a decode launch.  With per-sequence
-        positions (a start_pos tensor: lengths unknown to the host, ragged in
-        general) the launch balances the rows' splits over the CUs from the
-        lengths on the device, so the plan follows them in a replayed graph;
+    def _decode_plan(self, n_rows: int, max_len: int, device, per_row_positions: bool,
+                     dtype: Optional[torch.dtype] = None) -> tuple[int, int, int]:
+        """(n_splits, min_chunk, balance) of a decode launch, sized for as many
+        workgroups as the CUs hold at once (one per CU for a bf16 cache, three
+        for an e4m3 cache at ranks up to 256).  With per-sequence positions (a
+        start_pos tensor: lengths unknown to the host, ragged in general) the
+        launch balances the rows' splits over those slots from the lengths on
+        the device, so the plan follows them in a replayed graph;
         ``split_plan`` overrides the choice."""
         if self.split_plan not in ("auto", "static", "balanced"):
             raise ValueError(f"split_plan must be 'auto', 'static' or 'balanced', got {self.split_plan!r}")
-        n_splits, min_chunk = self._split_plan(n_rows, max_len, device)
+        dt = dtype if dtype is not None else self.wkv_a.weight.dtype
+        bpc = kernels.decode_blocks_per_cu(dt, self.fp8_cache, self.kv_lora_rank, dt == torch.bfloat16, device)
+        n_splits, min_chunk = self._split_plan(n_rows, max_len, device, bpc)
         if self.split_plan == "balanced" or (self.split_plan == "auto" and per_row_positions):
-            bal, cap = kernels.balanced_splits(n_rows, self._num_cus)
+            bal, cap = kernels.balanced_splits(n_rows, self._num_cus, bpc)
             if bal:
                 return cap, min_chunk, bal
         return n_splits, min_chunk, 0
@@ -505,7 +510,7 @@ class MLA(nn.Module):
                            start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
 
         n_splits, min_chunk, balance = self._decode_plan(
-            n, max_len, dev, isinstance(start_pos, torch.Tensor) and self.inference_mode)
+            n, max_len, dev, isinstance(start_pos, torch.Tensor) and self.inference_mode, dtype=x.dtype)
         # A chunk of many tokens per sequence: four queries share each cache
         # tile (no split-KV) instead of one row per workgroup.
         prefill = x.dtype == torch.bfloat16 and kernels.use_prefill(B, T, self._num_cus, rank=R)

@@ -36,7 +36,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mla_abi_version() == _abi.ABI_VERSION == 2
+    assert lib.mla_abi_version() == _abi.ABI_VERSION == 3
 
 
 def _append(lib, **kw):
@@ -428,6 +428,17 @@ def test_balanced_chunk_matches_its_definition(seed):
         min_chunk = rng.choice([1, 64, 100, 256, 4096])
         want = _brute_balanced_chunk(lens, n_splits, min_chunk, target)
         assert kernels.balanced_chunk(lens, n_splits, min_chunk, target) == want, (lens, n_splits, min_chunk, target)
+
+
+def test_decode_blocks_per_cu_rejects(lib):
+    """Argument checks come before any HIP call."""
+    bf, f32, fp8 = _abi.DTYPE_BF16, _abi.DTYPE_F32, _abi.DTYPE_FP8
+    assert lib.mla_decode_blocks_per_cu(bf, bf, 0, 0) == -2
+    assert lib.mla_decode_blocks_per_cu(bf, bf, 513, 0) == -2
+    assert lib.mla_decode_blocks_per_cu(f32, fp8, 256, 0) == -2
+    assert lib.mla_decode_blocks_per_cu(fp8, fp8, 256, 0) == -2
+    assert lib.mla_decode_blocks_per_cu(bf, bf, 256, 2) == -1
+    assert "fused" in lib.mla_last_error().decode()
 
 
 def test_balanced_chunk_examples_and_rejects(lib):
