@@ -288,13 +288,13 @@ struct KTile<2, NB> {
   float4 sc;
 };
 
-// e4m3 x 4 (one dword) -> 4 bf16 with the hardware converter (exact: every
-// e4m3fn value is a bf16 value, so keeping the high halves is exact).
+// e4m3 x 4 (one dword) -> 4 bf16 with gfx950's packed converter, two codes
+// per instruction (scale 1: exact, since every e4m3fn value is a bf16 value).
+// Bit-identical, NaN codes included, to converting each pair to f32 and
+// keeping the high halves, over all 65,536 code pairs.
 __device__ __forceinline__ uint2 e4m3x4_to_bf16x4_hw(uint32_t w) {
-  const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
-  const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
-  const uint32_t a = __builtin_amdgcn_perm(f2u(lo[1]), f2u(lo[0]), 0x07060302u);
-  const uint32_t b = __builtin_amdgcn_perm(f2u(hi[1]), f2u(hi[0]), 0x07060302u);
+  const uint32_t a = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+  const uint32_t b = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
   return make_uint2(a, b);
 }
 

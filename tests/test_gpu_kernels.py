@@ -367,6 +367,40 @@ def test_balanced_plan_matches_oracle_and_host_chunk(gpu, dtype, fp8):
     assert bool((out[1].float() == 0).all()) and bool((out[10].float() == 0).all())
 
 
+def test_e4m3_decode_every_code_exact(gpu):
+    """The kernels' e4m3 -> bf16 conversion, bit for bit on every finite code.
+    A row whose single cached token has scale 1 gets one softmax weight of
+    exactly 1, so the output is the decoded latent row itself; 256 channels
+    hold the codes 0..255 (the NaN codes 0x7f and 0xff hold 0, and so does
+    -0, 0x80, which the accumulation 0 + 1 x -0 returns as +0).  The prefill
+    kernel is checked on the rows that attend to 1, 2, 4 or 8 identical tokens
+    (equal weights, exact 1/n)."""
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    codes[0x7F] = 0
+    codes[0xFF] = 0
+    codes[0x80] = 0
+    expect = codes.view(torch.float8_e4m3fn).to(torch.bfloat16).view(torch.int16)
+    B, S = 3, 16
+    cache = LatentCache(codes.repeat(B, S, 1).to(gpu), torch.zeros(B, S, P, dtype=torch.bfloat16, device=gpu),
+                        torch.ones(B, S, device=gpu))
+    g = torch.Generator().manual_seed(5)
+    cos, sin = tables(torch.bfloat16, 64, gpu)
+    q_abs = torch.randn(B, H, R, generator=g).to(torch.bfloat16).to(gpu)
+    q_pe = torch.randn(B, H, P, generator=g).to(torch.bfloat16).to(gpu)
+    one = torch.ones(B, dtype=torch.int32, device=gpu)
+    out = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE, row_seq=torch.arange(B, dtype=torch.int32, device=gpu),
+                                   kv_len=one, q_rope_pos=one * 0, n_splits=1, min_chunk=64)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu().view(torch.int16), expect.expand(B, H, R))
+    T = 8
+    qa = torch.randn(B * T, H, R, generator=g).to(torch.bfloat16).to(gpu)
+    qp = torch.randn(B * T, H, P, generator=g).to(torch.bfloat16).to(gpu)
+    out = kernels.prefill_attention(qa, qp, cos, sin, cache, SCALE, start_pos=one * 0, rows_per_seq=T)
+    torch.cuda.synchronize()
+    rows = [b * T + i for b in range(B) for i in (0, 1, 3, 7)]
+    assert torch.equal(out.cpu()[rows].view(torch.int16), expect.expand(len(rows), H, R))
+
+
 def test_decode_blocks_per_cu(gpu):
     """Workgroups per CU the split plans target: one for bf16 caches and fp32,
     three for e4m3 caches at ranks up to 256 (their kernel is built for three
