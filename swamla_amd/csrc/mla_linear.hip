@@ -162,28 +162,41 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
     const int r = r0 + rr;
     uint4 xv = make_uint4(0, 0, 0, 0);
     if (r < a.n_rows) {
+      const float* lp = a.lse_part + static_cast<int64_t>(r) * a.n_splits * H + h;
+      const float* op0 = a.o_part + (static_cast<int64_t>(r) * a.n_splits * H + h) * R + cc;
+      // Splits in groups of 8 with every load of a group issued before it is
+      // used; the running maximum moves per group (online log-sum-exp).
+      float ls[8];
+      float4 v[8][2];
+      auto load_group = [&](int s0, int last) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int s = min(s0 + k, last);
+          ls[k] = lp[s * H];
+          const float* op = op0 + static_cast<int64_t>(s) * H * R;
+          v[k][0] = *reinterpret_cast<const float4*>(op);
+          v[k][1] = *reinterpret_cast<const float4*>(op + 4);
+        }
+      };
+      // With n_splits > 1 (the partial buffers are then given, [n_rows,
+      // n_splits, H, R_pad]) the first group goes out before the row's split
+      // count is known; slots past the count may hold stale, even
+      // non-finite, values and are dropped by selects below, never
+      // multiplied in.  With n_splits == 1 the buffers may be null and are
+      // not touched: every row then reads o_lat.
+      const bool early = a.n_splits > 1;  // block-uniform
+      if (early) load_group(0, a.n_splits - 1);
       const int L = clamped_row_len(a.ad, r, a.cache_b, a.cache_s);
-      const int ns = row_splits(L, a.n_splits, a.min_chunk, a.plan ? *a.plan : 0).ns;
+      // at most n_splits (a plan word from another launch cannot send the
+      // reads past the row's slots)
+      const int ns = min(row_splits(L, a.n_splits, a.min_chunk, a.plan ? *a.plan : 0).ns, a.n_splits);
       if (ns <= 1) {
         xv = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.o_lat) + r * a.ol_rs + h * a.ol_hs + cc);
       } else {
-        const float* lp = a.lse_part + static_cast<int64_t>(r) * a.n_splits * H + h;
-        const float* op0 = a.o_part + (static_cast<int64_t>(r) * a.n_splits * H + h) * R + cc;
-        // Splits in groups of 8 with every load of a group issued before it is
-        // used; the running maximum moves per group (online log-sum-exp).
         float M = -INFINITY, tot = 0.f;
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         for (int s0 = 0; s0 < ns; s0 += 8) {
-          float ls[8];
-          float4 v[8][2];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const int s = min(s0 + k, ns - 1);  // surplus slots re-read the last split and get weight 0
-            ls[k] = lp[s * H];
-            const float* op = op0 + static_cast<int64_t>(s) * H * R;
-            v[k][0] = *reinterpret_cast<const float4*>(op);
-            v[k][1] = *reinterpret_cast<const float4*>(op + 4);
-          }
+          if (s0 > 0 || !early) load_group(s0, ns - 1);
           float mg = M;
 #pragma unroll
           for (int k = 0; k < 8; ++k)
@@ -195,10 +208,12 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
           M = mg;
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
-            const float ws = (s0 + k < ns && ls[k] != -INFINITY) ? __expf(ls[k] - M) : 0.f;
+            const bool in = s0 + k < ns;
+            const float ws = (in && ls[k] != -INFINITY) ? __expf(ls[k] - M) : 0.f;
             tot += ws;
-            acc[0] += ws * v[k][0].x; acc[1] += ws * v[k][0].y; acc[2] += ws * v[k][0].z; acc[3] += ws * v[k][0].w;
-            acc[4] += ws * v[k][1].x; acc[5] += ws * v[k][1].y; acc[6] += ws * v[k][1].z; acc[7] += ws * v[k][1].w;
+            const float t[8] = {v[k][0].x, v[k][0].y, v[k][0].z, v[k][0].w, v[k][1].x, v[k][1].y, v[k][1].z, v[k][1].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = in ? acc[i] + ws * t[i] : acc[i];
           }
         }
         const float inv = tot > 0.f ? 1.f / tot : 0.f;
