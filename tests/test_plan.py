@@ -1,0 +1,53 @@
+"""Host-side split planning (CPU): how many splits and balanced workgroups a
+decode launch asks for, given the workgroups per CU its kernel is built for
+(one for a bf16 cache, three for an e4m3 cache at ranks up to 256)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.mla_ref import MLAConfig
+from swamla_amd import kernels
+from swamla_amd.mla import MLA
+
+
+def test_plan_splits_fills_every_slot():
+    # config 2: 32 rows over 256 CUs, one workgroup per CU -> 8 splits
+    assert kernels.plan_splits(32, 4224, 256) == (8, 256)
+    # config 5: 128 rows; three workgroups per CU -> 6 splits, one -> 2
+    assert kernels.plan_splits(128, 8256, 256, blocks_per_cu=3) == (6, 256)
+    assert kernels.plan_splits(128, 8256, 256, blocks_per_cu=1) == (2, 256)
+    # short rows stop at one split per min_chunk tokens
+    assert kernels.plan_splits(4, 600, 256, blocks_per_cu=3) == (3, 256)
+    assert kernels.plan_splits(0, 100) == (1, 256)
+
+
+def test_balanced_splits_scale_with_slots():
+    assert kernels.balanced_splits(64, 256) == (256, 16)
+    assert kernels.balanced_splits(64, 256, blocks_per_cu=3) == (768, 48)
+    assert kernels.balanced_splits(200, 256) == (256, 8)
+    # more rows than a balanced plan covers, or more rows than slots
+    assert kernels.balanced_splits(257, 256, blocks_per_cu=3) == (0, 0)
+    assert kernels.balanced_splits(300, 256) == (0, 0)
+    assert kernels.balanced_splits(0, 256) == (0, 0)
+
+
+@pytest.mark.parametrize("cache_dtype,bpc", [(None, 1), ("fp8_e4m3", 3)])
+def test_module_plan_uses_workgroups_per_cu(monkeypatch, cache_dtype, bpc):
+    """MLA._decode_plan sizes both plans for CUs x the kernel's workgroups per
+    CU (the occupancy query needs a GPU, so it is stubbed here with the values
+    the GPU tests check)."""
+    seen = []
+
+    def fake(dtype, fp8, rank, fused, device):
+        seen.append((dtype, fp8, rank, fused))
+        return bpc
+
+    monkeypatch.setattr(kernels, "decode_blocks_per_cu", fake)
+    m = MLA(MLAConfig(max_batch_size=128, max_seq_len=64), cache_dtype=cache_dtype).to(torch.bfloat16)
+    m._num_cus = 256
+    ns, mc, bal = m._decode_plan(128, 8256, torch.device("cpu"), False, dtype=torch.bfloat16)
+    assert (ns, mc, bal) == (2 * bpc, 256, 0)
+    ns, mc, bal = m._decode_plan(64, 8256, torch.device("cpu"), True, dtype=torch.bfloat16)
+    assert (ns, bal) == (16 * bpc, 256 * bpc)
+    assert seen[0] == (torch.bfloat16, cache_dtype == "fp8_e4m3", 256, True)
