@@ -79,6 +79,10 @@ def parse():
     p.add_argument("--cpu-batch", type=int, default=4)
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run plain device copies of known size (calibrates FETCH_SIZE / WRITE_SIZE)")
+    p.add_argument("--prefill", type=int, default=0, metavar="T",
+                   help="only time the prompt pass: MLA.forward over T tokens per sequence at start_pos 0 "
+                        "(its own JSON line; the profiling workload for the prefill-side products)")
+    p.add_argument("--prefill-batch", type=int, default=4)
     args = p.parse_args()
     preset = CONFIGS[args.config]
     for k, v in preset.items():
@@ -340,6 +344,44 @@ def cpu_baseline(args, torch):
     }
 
 
+def run_prefill(args, dev, torch) -> int:
+    """One layer's prompt pass: the drop-in MLA.forward over args.prefill
+    tokens per sequence at start_pos 0, i.e. the input products and the
+    query absorption (ATen GEMMs above 128 rows), the append of every token,
+    causal attention over the latent cache (mla_prefill_attn), the W_uv
+    read-out and wo; timed over a few forwards after one warm-up."""
+    from swamla_amd import MLA, MLAConfig
+
+    B, T, reps = args.prefill_batch, args.prefill, 5
+    cfg = MLAConfig(n_embd=args.dim, max_batch_size=B, max_seq_len=(T + 63) // 64 * 64)
+    m = MLA(cfg, cache_dtype="fp8_e4m3" if args.cache == "fp8" else None)
+    init_linear_weights(m, 100, torch)
+    m.eval().to(torch.bfloat16).to(dev)
+    m.set_inference_mode(True)
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(B, T, args.dim, generator=g, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        y = m(x, 0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            y = m(x, 0)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+    pairs = B * T * (T + 1) // 2  # causal (query, cached token) pairs
+    attn_flop = pairs * H * (2 * (R + P) + 2 * R)
+    print(json.dumps({
+        "metric": "MLA prefill: prompt tokens/s through the drop-in MLA.forward at start_pos 0",
+        "value": B * T * reps / el, "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+        "ms_per_forward": el / reps * 1e3, "dtype": "bf16" if args.cache == "bf16" else "bf16+e4m3-cache",
+        "data": "synthetic: N(0,1) hidden states, N(0,0.02) random-init weights (no checkpoint)",
+        "config": {"workload": f"prompt pass, batch {B}, {T} tokens per sequence", "batch": B, "tokens": T,
+                   "n_embd": args.dim, "heads": H, "kv_lora_rank": R, "rope_dim": P, "cache": args.cache},
+        "attention_flop_per_forward": attn_flop, "finite": bool(torch.isfinite(y).all()),
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -365,6 +407,8 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2, "copies": 5}))
         return 0
+    if args.prefill:
+        return run_prefill(args, dev, torch)
     fp8 = args.cache == "fp8"
     log(f"building {args.layers} layers, batch {args.batch}, prefill {args.ctx} ({args.cache} cache)")
     layers = build_layers(args, dev, torch)
