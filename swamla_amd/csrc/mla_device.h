@@ -212,11 +212,16 @@ constexpr int kPeRow = 2 * kP + 16;        // 144 B per LDS rope row
 constexpr int kPeBytes = kTileTok * kPeRow;  // 9216 B
 
 // Latent geometry of an instance: R_pad = 64 NB channels, LDS latent rows of
-// 2 R_pad + 16 bytes (528 for NB = 4).
-template <int NB>
+// 2 R_pad + PAD bytes.  The decode kernel uses PAD = 16 (528 B for NB = 4:
+// the 16 rows of a 16-byte-per-lane operand read fall on distinct 16-byte
+// bank slots).  The prefill kernel, where every wave also reads the whole
+// tile transposed (32 bytes of each of 16 rows per instruction), uses
+// PAD = 32: measured 6-8 % faster there (B = 4 and 32 x 4096 tokens), and
+// no faster for decode.
+template <int NB, int PAD = 16>
 struct LatGeo {
   static constexpr int RP = 64 * NB;
-  static constexpr int CRow = 2 * RP + 16;
+  static constexpr int CRow = 2 * RP + PAD;
   static constexpr int CBytes = kTileTok * CRow;
 };
 constexpr int kPRow = 2 * kTileTok + 8;    // bytes per head row of P (128 + 8 pad: the 16 heads

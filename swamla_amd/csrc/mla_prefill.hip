@@ -56,10 +56,11 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
   constexpr int TPW = kTileTok / NW;  // tokens each wave loads per tile
   constexpr int RPL = TPW / 8;        // ... rows of 8 tokens per lane
   constexpr int SEG = C_DT == 2 ? (NB + 1) / 2 : NB;  // 128-byte latent segments per row
-  constexpr int RP = LatGeo<NB>::RP, kCRow = LatGeo<NB>::CRow;
+  using Geo = LatGeo<NB, 32>;
+  constexpr int RP = Geo::RP, kCRow = Geo::CRow;
   constexpr int CB = C_DT == 2 ? RP : 2 * RP;  // latent bytes per cached token
   constexpr int MB = 4 * NB;                   // 16-channel output blocks
-  __shared__ __attribute__((aligned(16))) uint8_t c_lds[LatGeo<NB>::CBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t c_lds[Geo::CBytes];
   __shared__ __attribute__((aligned(16))) uint8_t pe_lds[kPeBytes];
   __shared__ __attribute__((aligned(16))) float sc_lds[kTileTok];
 
