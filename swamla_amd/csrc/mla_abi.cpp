@@ -72,12 +72,10 @@ int mla_abi_version_impl() { return SWAMLA_ABI_VERSION; }
 
 const char* last_error_impl() { return g_err; }
 
+// The kernels' own plan (mla_plan.h), one definition for host and device.
 int32_t split_count_impl(int32_t L, int32_t n_splits, int32_t min_chunk) {
   if (n_splits < 1 || min_chunk < 1) return 0;
-  int c = (L + n_splits - 1) / n_splits;
-  if (c < min_chunk) c = min_chunk;
-  c = (c + 15) & ~15;
-  return L <= 0 ? 0 : (L + c - 1) / c;
+  return swamla::split_count(L, n_splits, min_chunk);
 }
 
 // Addressing: explicit per-entry arrays, or dense (start_pos[n / T]).
