@@ -94,8 +94,10 @@ const char* mla_last_error(void);
  * err_flag     optional device int32; a token whose cache row / position /
  *              RoPE row lies outside the buffers is skipped and sets it to 1.
  *
- * Numerics: LayerNorm statistics are reduced in fp64 in a fixed order and the
- * result is rounded once to the cache dtype (exactly-rounded LayerNorm).
+ * Numerics: the LayerNorm is PyTorch's CPU LayerNorm op for op (fp32 Welford
+ * statistics in ATen's vectorised order, fused multiply-adds where its
+ * compiled kernel fuses), so the latent rows equal the reference's
+ * kv_norm(kv) bit for bit for bf16 and fp32 rows.
  * RoPE rounds after every multiply and add in in_dtype, as eager PyTorch does.
  * FP8: scale = max(amax, 1e-12) / 448 in fp32, code = RNE(y / scale).
  */

@@ -10,7 +10,7 @@ Contents
                branch and ``RoPE`` (models/mla.py, models/positional_encoding.py);
                pinned bit-exactly to the real reference by tests/golden fixtures.
   latent_ops   numpy / fp64 statements of what each kernel must produce:
-               exactly-rounded LayerNorm (fixed fp64 reduction order), bf16 /
+               torch's CPU LayerNorm op for op (aten_layernorm.c), bf16 /
                e4m3 rounding, per-op-rounded RoPE, absorbed attention in fp64,
                split plan and log-sum-exp merge.  Each function's header says
                how it is pinned.

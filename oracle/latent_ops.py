@@ -6,7 +6,10 @@ in tests/test_oracle.py.
 """
 from __future__ import annotations
 
+import ctypes
 import math
+import os
+import subprocess
 
 import numpy as np
 import torch
@@ -54,59 +57,55 @@ def e4m3_codes_to_f32(c: np.ndarray) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- LayerNorm
-def _butterfly(s: np.ndarray) -> np.ndarray:
-    """xor-butterfly over the 64 lanes of the last axis, distances 1..32."""
-    lanes = np.arange(64)
-    for m in (1, 2, 4, 8, 16, 32):
-        s = s + s[..., lanes ^ m]
-    return s
+_HERE = os.path.dirname(os.path.abspath(__file__))
+ATEN_LN_SRC = os.path.join(_HERE, "aten_layernorm.c")
+ATEN_LN_LIB = os.path.join(_HERE, "libaten_layernorm.so")
+_aten_ln = None
 
 
-def layernorm_f64(c: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np.ndarray:
-    """kv_norm (mla.py:107, :409) in fp64 with the append kernel's reduction
-    order, for any rank R = c.shape[-1] up to 512: the row is padded with
-    zeros to R_pad = 64 * ceil(R / 64), lane l holds channels K*l .. K*l+K-1
-    (K = R_pad / 64) summed left to right (padding adds +0.0), then an xor
-    butterfly, times fl64(1 / R); the variance sums only the R real channels.
-    Returns unrounded fp64 y [N, R].  ``eps`` is used as its fp32 value, as
-    torch's LayerNorm does.  Pinned against torch.nn.functional.layer_norm in
-    fp64 (agreement ~1e-15) and the mean-0 / var-1 invariants; for R = 256
-    the order is lane l holding channels 4l..4l+3."""
-    x0 = np.asarray(c, dtype=np.float64)
-    Rr = x0.shape[-1]
-    K = -(-Rr // 64)
-    rp = 64 * K
-    x = np.zeros(x0.shape[:-1] + (rp,), dtype=np.float64)
-    x[..., :Rr] = x0
-    x = x.reshape(-1, 64, K)
-    valid = (np.arange(rp) < Rr).reshape(64, K)
-    s = x[..., 0].copy()
-    for i in range(1, K):
-        s = s + x[..., i]
-    inv_r = 1.0 / float(Rr)  # fp64, as the kernels receive it
-    mean = _butterfly(s)[..., :1] * inv_r  # [N, 1]
-    d = np.where(valid, x - mean[..., None], 0.0)
-    q = d[..., 0] * d[..., 0]
-    for i in range(1, K):
-        q = q + d[..., i] * d[..., i]
-    var = _butterfly(q)[..., :1] * inv_r
-    rstd = 1.0 / np.sqrt(var + float(np.float32(eps)))
-    wp = np.zeros(rp, np.float64)
-    bp = np.zeros(rp, np.float64)
-    wp[:Rr] = np.asarray(w, np.float64).reshape(-1)
-    bp[:Rr] = np.asarray(b, np.float64).reshape(-1)
-    y = np.where(valid, (d * rstd[..., None]) * wp.reshape(64, K) + bp.reshape(64, K), 0.0)
-    return y.reshape(-1, rp)[:, :Rr]
+def build_aten_layernorm(force: bool = False) -> str:
+    """Compile oracle/aten_layernorm.c (gcc, contraction off: every fused
+    multiply-add of the statement is an explicit fmaf) next to its source."""
+    if force or not os.path.exists(ATEN_LN_LIB) or os.path.getmtime(ATEN_LN_LIB) < os.path.getmtime(ATEN_LN_SRC):
+        tmp = ATEN_LN_LIB + f".tmp{os.getpid()}"
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", "-shared", "-fPIC", ATEN_LN_SRC,
+                        "-o", tmp, "-lm"], check=True, capture_output=True, text=True)
+        os.replace(tmp, ATEN_LN_LIB)
+    return ATEN_LN_LIB
 
 
-def layernorm_exact(c, w, b, eps: float, dtype: torch.dtype) -> torch.Tensor:
-    """Exactly-rounded LayerNorm output in ``dtype`` (what the cache holds)."""
-    y = layernorm_f64(c, w, b, eps)
-    if dtype == torch.bfloat16:
-        return torch.from_numpy(f64_to_bf16_bits(y).view(np.int16)).view(torch.bfloat16)
-    if dtype == torch.float32:
-        return torch.from_numpy(y.astype(np.float32))
-    raise TypeError(dtype)
+def _aten_ln_lib():
+    global _aten_ln
+    if _aten_ln is None:
+        lib = ctypes.CDLL(build_aten_layernorm())
+        vp, i64, i32, f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+        for name in ("aten_layernorm_bf16", "aten_layernorm_f32"):
+            fn = getattr(lib, name)
+            fn.argtypes = [vp, i64, i32, i32, vp, vp, f, vp, i64, vp, vp, i32]
+            fn.restype = None
+        _aten_ln = lib
+    return _aten_ln
+
+
+def layernorm_aten(c: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float, variant: int = 0):
+    """kv_norm (mla.py:107, :409) as PyTorch's CPU LayerNorm computes it, op
+    for op (oracle/aten_layernorm.c): c [M, N] bf16 or fp32 rows, w / b [N] in
+    the same dtype.  Returns (y [M, N] in c's dtype, mean [M], rstd [M] fp32).
+    ``variant`` plants single-site mistakes for the tests that pin it.
+    Pinned bit for bit against torch.nn.functional.layer_norm /
+    torch.native_layer_norm on CPU (tests/test_oracle.py)."""
+    lib = _aten_ln_lib()
+    c = c.detach().cpu().contiguous()
+    M, N = c.shape
+    w = w.detach().cpu().to(c.dtype).contiguous()
+    b = b.detach().cpu().to(c.dtype).contiguous()
+    y = torch.empty_like(c)
+    mean = torch.empty(M, dtype=torch.float32)
+    rstd = torch.empty(M, dtype=torch.float32)
+    fn = {torch.bfloat16: lib.aten_layernorm_bf16, torch.float32: lib.aten_layernorm_f32}[c.dtype]
+    fn(c.data_ptr(), N, M, N, w.data_ptr(), b.data_ptr(), float(np.float32(eps)), y.data_ptr(), N,
+       mean.data_ptr(), rstd.data_ptr(), int(variant))
+    return y, mean, rstd
 
 
 def fp8_quantize(y: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

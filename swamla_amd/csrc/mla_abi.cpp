@@ -169,7 +169,7 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const in
       !aligned(ln_w, es) || !aligned(ln_b, es) || !aligned(cos_tab, es) || !aligned(sin_tab, es) ||
       (ckv_scale && !aligned(ckv_scale, 4)))
     return fail(SWAMLA_ERR_MISALIGNED, "mla_append: ckv_cache must be 16-byte aligned, others element-aligned");
-  swamla::AppendArgs a{kv_in,    in_row_stride, n_tok,     R,           1.0 / R,   ad,      ln_w,    ln_b,    eps,
+  swamla::AppendArgs a{kv_in,    in_row_stride, n_tok,     R,           ad,        ln_w,    ln_b,    eps,
                        cos_tab,  sin_tab,       rope_len,  ckv_cache,   kpe_cache, ckv_scale,
                        cache_batch, cache_seq,  err_flag};
   const int rc = swamla::launch_append(a, in_dtype, cache_dtype, static_cast<hipStream_t>(stream));
@@ -313,7 +313,7 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
                 "%s: input rows and LayerNorm parameters need %d-byte aligned bases and a row stride that is a "
                 "multiple of %d elements", fn, static_cast<int>(la), static_cast<int>(la / 2));
   if (n_rows == 0) return ok();
-  a.fa = swamla::AppendArgs{kv_in,   in_row_stride, n_rows,      R,         1.0 / R,   a.ad,      ln_w,      ln_b,   eps,
+  a.fa = swamla::AppendArgs{kv_in,   in_row_stride, n_rows,      R,         a.ad,      ln_w,      ln_b,   eps,
                             cos_tab, sin_tab,       rope_len,    ckv_cache, kpe_cache, ckv_scale,
                             cache_batch, cache_seq, err_flag};
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));

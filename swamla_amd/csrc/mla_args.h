@@ -29,8 +29,7 @@ struct AppendArgs {
   const void* kv_in;  // rows [R_pad latent | P rope]
   int64_t in_rs;
   int n_tok;
-  int R;        // kv_lora_rank; rows are R_pad = 64 ceil(R / 64) channels
-  double inv_r;  // fl64(1 / R), the LayerNorm's mean / variance factor
+  int R;  // kv_lora_rank; rows are R_pad = 64 ceil(R / 64) channels
   Addressing ad;
   const void* ln_w;
   const void* ln_b;

@@ -81,58 +81,183 @@ __device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xo
 // The arithmetic below is shared by the append kernel and the decode kernel's
 // fused one-token append, so both write identical bits.
 
-// LayerNorm of one latent row held by a wavefront, lane owning the K = R_pad /
-// 64 channels K*lane .. K*lane + K - 1.  Channels >= R are padding: they take
-// no part in the statistics and come out as exactly 0.  Every multiply / add
-// is rounded on its own: the result must reproduce the fixed-order fp64
-// statement exactly.  Statistics in fp64; fixed order: in-lane left to
-// right, then xor butterfly 1,2,4,...,32 (every lane ends with the same total),
-// times inv_r = fl64(1 / R) (exactly 2^-8 for R = 256).
-template <int K>
-__device__ __forceinline__ void layernorm_lane(const double (&x)[K], const double (&wt)[K], const double (&bs)[K],
-                                               int R, double inv_r, int lane, float eps, double (&y)[K]) {
+// ---------------------------------------------------------------------------
+// kv_norm exactly as PyTorch's CPU LayerNorm computes it (the reference's
+// `self.kv_norm(kv)`, models/mla.py:107, :409).  The statistics are a
+// vectorised fp32 Welford pass, every product and sum rounded where ATen's
+// compiled CPU kernel rounds it (restated and pinned bit for bit against
+// torch on the host by the oracle's aten_layernorm.c):
+//   * input vectors of V values (16 for bf16 input, 8 for fp32) are HV = V/8
+//     float vectors of 8 lanes; n = R / V whole vectors in chunks of 16;
+//   * one Welford stream per (chunk, half, lane k) over the chunk's vectors j:
+//       d = x - m1;  m1 = fma(d, fl(1/(j+1)), m1);  m2 = fma(d, x - m1, m2)
+//   * the streams merge, chunk by chunk and half by half, into a binary-counter
+//     stack of 8-lane accumulators (depth ceil(log2(chunks)), at least 1):
+//       c = fl(cnt_add / cnt);  dc = d * c;  m1 += dc;
+//       m2 = fma(dc, d * fl(cnt_old), m2 + m2_add)
+//   * the R - nV tail values run a scalar Welford (m1 += d / cnt), and the 8
+//     lanes, n HV values each, merge into it one by one:
+//       m1 = fma(d, c, m1);  m2 = m2 + fma((d * d) * c, fl(cnt_old), m2_add)
+//   * var = m2 / R;  rstd = 1 / sqrt(var + eps).
+// One wavefront per row: lanes 0..31 run the streams (chunk / half / lane from
+// the lane index), the stack merges run in every lane for its k = lane % 8,
+// the tail and the lane merges run uniformly in all lanes.  Kernel ranks are
+// R <= 512: at most 2 chunks for bf16 (depth 1) and 4 for fp32 (depth 2).
+struct LnStats {
+  float mean, rstd;
+};
+
+// Correctly rounded fp32 square root.  On gfx950 the compiler lowers both
+// sqrtf and __fsqrt_rn to v_sqrt_f32, whose result is not always the nearest
+// float.  The estimate s is within an ulp or two of the root; the root lies
+// below s's lower midpoint iff x is below that midpoint's square (likewise
+// above), and a midpoint of two floats (25 significant bits) squares exactly
+// in fp64.  A float's root is never exactly a midpoint, so there are no ties.
+__device__ __forceinline__ float sqrt_rn_f32(float x) {
 #pragma clang fp contract(off)
-  bool v[K];
+  float s = __builtin_sqrtf(x);
+  if (!(x > 0.f) || !(x < INFINITY)) return s;  // 0, negative, NaN, inf: as the hardware gives
+  const double xd = static_cast<double>(x);
 #pragma unroll
-  for (int i = 0; i < K; ++i) v[i] = K * lane + i < R;
-  double s = v[0] ? x[0] : 0.0;
-#pragma unroll
-  for (int i = 1; i < K; ++i) s = s + (v[i] ? x[i] : 0.0);
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) s = s + shfl_xor_f64(s, m);
-  const double mean = s * inv_r;
-  double d[K];
-#pragma unroll
-  for (int i = 0; i < K; ++i) d[i] = v[i] ? x[i] - mean : 0.0;
-  double q = d[0] * d[0];
-#pragma unroll
-  for (int i = 1; i < K; ++i) q = q + d[i] * d[i];
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) q = q + shfl_xor_f64(q, m);
-  const double var = q * inv_r;
-  // correctly rounded square root and IEEE division
-  const double rstd = 1.0 / __dsqrt_rn(var + static_cast<double>(eps));
-#pragma unroll
-  for (int i = 0; i < K; ++i) y[i] = v[i] ? (d[i] * rstd) * wt[i] + bs[i] : 0.0;
+  for (int it = 0; it < 2; ++it) {
+    const float dn = u2f(f2u(s) - 1u), up = u2f(f2u(s) + 1u);
+    const double mlo = 0.5 * (static_cast<double>(dn) + static_cast<double>(s));
+    const double mhi = 0.5 * (static_cast<double>(s) + static_cast<double>(up));
+    s = xd < mlo * mlo ? dn : (xd > mhi * mhi ? up : s);
+  }
+  return s;
 }
 
-// bf16 cache: each channel rounded once from fp64.
-template <int K>
-__device__ __forceinline__ void encode_bf16_lane(const double (&y)[K], uint16_t (&o)[K]) {
+__device__ __forceinline__ void ln_stack_merge(int add_cnt, float a1, float a2, int& cnt, float& m1, float& m2) {
+#pragma clang fp contract(off)
+  const int tot = cnt + add_cnt;
+  const float c = tot == 0 ? 0.f : __fdiv_rn(static_cast<float>(add_cnt), static_cast<float>(tot));
+  const float d = a1 - m1;
+  const float dc = d * c;
+  const float base = m2 + a2;
+  m2 = __builtin_fmaf(dc, d * static_cast<float>(cnt), base);
+  m1 = m1 + dc;
+  cnt = tot;
+}
+
+template <int IN_DT>
+__device__ __forceinline__ LnStats aten_ln_stats(const typename Elem<IN_DT>::T* row, int R, float eps, int lane) {
+#pragma clang fp contract(off)
+  using E = Elem<IN_DT>;
+  constexpr int V = IN_DT == 1 ? 16 : 8;         // values per input vector
+  constexpr int HV = V / 8;                       // 8-lane float vectors per input vector
+  constexpr int kMaxChunks = IN_DT == 1 ? 2 : 4;  // R <= 512
+  const int n = R / V;
+  const int chunks = (n + 15) >> 4;
+  // --- streams (lanes 0..31; a lane past the chunks has none)
+  const int sc = lane / (8 * HV), sh = (lane >> 3) & (HV - 1), sk = lane & 7;
+  int scnt = n - 16 * sc;
+  scnt = scnt < 0 ? 0 : (scnt > 16 ? 16 : scnt);
+  const auto* sp = row + sc * 16 * V + 8 * sh + sk;
+  float xs[16];
 #pragma unroll
-  for (int i = 0; i < K; ++i) o[i] = f64_to_bf16(y[i]);
+  for (int j = 0; j < 16; ++j) xs[j] = j < scnt ? E::ld(sp, j * V) : 0.f;
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (j < scnt) {
+      const float c = __fdiv_rn(1.0f, static_cast<float>(j + 1));
+      const float d = xs[j] - s1;
+      s1 = __builtin_fmaf(d, c, s1);
+      s2 = __builtin_fmaf(d, xs[j] - s1, s2);
+    }
+  }
+  // --- stack merges (lane k = lane % 8 keeps lane k's accumulators)
+  const int k = lane & 7;
+  const int depth = chunks <= 2 ? 1 : 2;
+  int c0 = 0, c1 = 0;
+  float a1 = 0.f, a2 = 0.f, b1 = 0.f, b2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    if (i < chunks) {  // uniform
+      const int ci = (n - 16 * i) < 16 ? n - 16 * i : 16;
+#pragma unroll
+      for (int h = 0; h < HV; ++h) {
+        const int src = (i * HV + h) * 8 + k;
+        ln_stack_merge(ci, __shfl(s1, src, 64), __shfl(s2, src, 64), c0, a1, a2);
+      }
+      if (depth == 2 && ((i + 1) & 1) == 0) {
+        ln_stack_merge(c0, a1, a2, c1, b1, b2);
+        c0 = 0;
+        a1 = 0.f;
+        a2 = 0.f;
+      }
+    }
+  }
+  if (depth == 2) ln_stack_merge(c1, b1, b2, c0, a1, a2);
+  // --- scalar tail, then the 8 lanes (values uniform across the wave)
+  int cnt = 0;
+  float m1 = 0.f, m2 = 0.f;
+  for (int i = n * V; i < R; ++i) {
+    const float xv = E::ld(row, i);
+    const float d = xv - m1;
+    ++cnt;
+    m1 = m1 + __fdiv_rn(d, static_cast<float>(cnt));
+    m2 = __builtin_fmaf(d, xv - m1, m2);
+  }
+  const int per_lane = n * HV;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    const float l1 = u2f(__builtin_amdgcn_readlane(f2u(a1), kk));
+    const float l2 = u2f(__builtin_amdgcn_readlane(f2u(a2), kk));
+    const int tot = cnt + per_lane;
+    const float c = tot == 0 ? 0.f : __fdiv_rn(static_cast<float>(per_lane), static_cast<float>(tot));
+    const float d = l1 - m1;
+    m1 = __builtin_fmaf(d, c, m1);
+    const float t = (d * d) * c;
+    m2 = m2 + __builtin_fmaf(t, static_cast<float>(cnt), l2);
+    cnt = tot;
+  }
+  const float var = __fdiv_rn(m2, static_cast<float>(R));
+  return LnStats{m1, __fdiv_rn(1.0f, sqrt_rn_f32(var + eps))};
+}
+
+// The affine part per channel (fp32 result, before rounding to the cache
+// dtype): bf16 input y = fma(fma(x, rstd, -rstd * mean), w, b); fp32 input
+// y = fma((x - mean) * rstd, w, b).
+template <int IN_DT>
+__device__ __forceinline__ float aten_ln_affine(float x, float w, float b, const LnStats& st) {
+#pragma clang fp contract(off)
+  if constexpr (IN_DT == 1) {
+    const float bias = -st.rstd * st.mean;
+    return __builtin_fmaf(__builtin_fmaf(x, st.rstd, bias), w, b);
+  } else {
+    return __builtin_fmaf((x - st.mean) * st.rstd, w, b);
+  }
+}
+
+// LayerNorm of one latent row held by a wavefront, lane owning the K = R_pad /
+// 64 channels K*lane .. K*lane + K - 1 (x, w, b as loaded, in fp32).  Channels
+// >= R are padding and come out as exactly 0.
+template <int IN_DT, int K>
+__device__ __forceinline__ void layernorm_lane(const float (&x)[K], const float (&wt)[K], const float (&bs)[K],
+                                               int R, int lane, const LnStats& st, float (&y)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) y[i] = K * lane + i < R ? aten_ln_affine<IN_DT>(x[i], wt[i], bs[i], st) : 0.f;
+}
+
+// bf16 cache: each channel rounded once (RNE) from the fp32 result.
+template <int K>
+__device__ __forceinline__ void encode_bf16_lane(const float (&y)[K], uint16_t (&o)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) o[i] = f32_to_bf16(y[i]);
 }
 
 // e4m3 per token: y is first rounded to bf16 (the value a bf16 cache would
 // hold), amax over the token, scale = max(amax,1e-12)/448, code = RNE(y/scale).
 // Padding channels (y = 0) encode as 0.
 template <int K>
-__device__ __forceinline__ void encode_e4m3_lane(const double (&y)[K], uint8_t (&codes)[K], float& scale) {
+__device__ __forceinline__ void encode_e4m3_lane(const float (&y)[K], uint8_t (&codes)[K], float& scale) {
   float yb[K];
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < K; ++i) {
-    yb[i] = bf16_to_f32(f64_to_bf16(y[i]));
+    yb[i] = bf16_to_f32(f32_to_bf16(y[i]));
     amax = fmaxf(amax, fabsf(yb[i]));
   }
 #pragma unroll

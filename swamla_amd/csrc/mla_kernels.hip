@@ -45,22 +45,24 @@ __device__ __forceinline__ void append_token(const AppendArgs& a, int tok, int l
   const T* w = static_cast<const T*>(a.ln_w);
   const T* bb = static_cast<const T*>(a.ln_b);
 
-  // --- LayerNorm over c[0..R): lane owns channels NB*lane .. NB*lane+NB-1 of
+  // --- LayerNorm over c[0..R) in ATen's CPU order: statistics from the whole
+  // row, then the affine with lane owning channels NB*lane .. NB*lane+NB-1 of
   // the R_pad-channel input row and LayerNorm parameters (entries >= R unused).
-  double x[NB], wt[NB], bs[NB], y[NB];
+  const LnStats st = aten_ln_stats<IN_DT>(row, a.R, a.eps, lane);
+  float x[NB], wt[NB], bs[NB], y[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
-    x[i] = static_cast<double>(E::ld(row, NB * lane + i));
-    wt[i] = static_cast<double>(E::ld(w, NB * lane + i));
-    bs[i] = static_cast<double>(E::ld(bb, NB * lane + i));
+    x[i] = E::ld(row, NB * lane + i);
+    wt[i] = E::ld(w, NB * lane + i);
+    bs[i] = E::ld(bb, NB * lane + i);
   }
-  layernorm_lane<NB>(x, wt, bs, a.R, a.inv_r, lane, a.eps, y);
+  layernorm_lane<IN_DT, NB>(x, wt, bs, a.R, lane, st, y);
 
   const int64_t crow = static_cast<int64_t>(b) * a.cache_s + pos;
   if constexpr (C_DT == 0) {
     uint32_t o[NB];
 #pragma unroll
-    for (int i = 0; i < NB; ++i) o[i] = f2u(static_cast<float>(y[i]));
+    for (int i = 0; i < NB; ++i) o[i] = f2u(y[i]);
     store_lane<NB>(static_cast<uint32_t*>(a.ckv) + crow * RP + NB * lane, o);
   } else if constexpr (C_DT == 1) {
     uint16_t o[NB];
@@ -246,18 +248,20 @@ struct FusedTok {
   float scale;
 };
 
-// Same arithmetic as append_token<1, C_DT, NB>.
+// Same arithmetic as append_token<1, C_DT, NB>; `row` is the token's wkv_a
+// row (the statistics read it in their own order).
 template <int C_DT, int NB>
-__device__ __forceinline__ FusedTok<C_DT, NB> fused_compute(const FusedIn<NB>& f, float eps, int R, double inv_r,
-                                                            int lane) {
-  double x[NB], wt[NB], bs[NB], y[NB];
+__device__ __forceinline__ FusedTok<C_DT, NB> fused_compute(const FusedIn<NB>& f, const uint16_t* row, float eps,
+                                                            int R, int lane) {
+  const LnStats st = aten_ln_stats<1>(row, R, eps, lane);
+  float x[NB], wt[NB], bs[NB], y[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
-    x[i] = static_cast<double>(bf16_to_f32(f.x[i]));
-    wt[i] = static_cast<double>(bf16_to_f32(f.wt[i]));
-    bs[i] = static_cast<double>(bf16_to_f32(f.bs[i]));
+    x[i] = bf16_to_f32(f.x[i]);
+    wt[i] = bf16_to_f32(f.wt[i]);
+    bs[i] = bf16_to_f32(f.bs[i]);
   }
-  layernorm_lane<NB>(x, wt, bs, R, inv_r, lane, eps, y);
+  layernorm_lane<1, NB>(x, wt, bs, R, lane, st, y);
   FusedTok<C_DT, NB> t;
   t.scale = 1.f;
   if constexpr (C_DT == 1) {
@@ -480,7 +484,9 @@ __global__ __launch_bounds__(kWaves * 64, (DecodeShape<C_DT, NB>::kWavesPerEU)) 
   // tiles load.
   FusedTok<C_DT, NB> ftok;
   if constexpr (FUSE)
-    if (fa_wave) ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, a.fa.inv_r, lane);
+    if (fa_wave)
+      ftok = fused_compute<C_DT, NB>(
+          fin, static_cast<const uint16_t*>(a.fa.kv_in) + static_cast<int64_t>(r) * a.fa.in_rs, a.fa.eps, a.R, lane);
 
   f32x4_t oacc[NB];
 #pragma unroll

@@ -283,8 +283,8 @@ class MLA(nn.Module):
         re-associating mla.py:427), q_pe and the wkv_a rows (mla.py:281-288,
         :307).  The absorbed block is formed in fp32 and rounded once to the
         model dtype; rebuilt when any source weight changes."""
-        ws = (self.wq.weight, self.wkv_a.weight, self.wkv_b.weight)
-        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in ws)
+        ws = (self.wq.weight, self.wkv_a.weight, self.wkv_b.weight, self.wq.bias, self.wkv_a.bias)
+        key = tuple(None if t is None else (t.data_ptr(), t._version, t.dtype, t.device) for t in ws)
         if self._decode_w is None or self._decode_w[0] != key:
             H, Dn, R, rp = self.n_heads, self.qk_nope_head_dim, self.kv_lora_rank, self.rank_pad
             wq = self.wq.weight.detach().view(H, self.qk_head_dim, self.dim)

@@ -3,9 +3,9 @@ the golden fixtures written by the real reference, and the oracle's op-for-op
 restatement (oracle/mla_ref.py) on identical seeded inputs and weights.
 
 Bars: attention outputs within 2e-2 relative / 1e-2 absolute (bf16) and
-1e-4 / 1e-5 (fp32); k_pe cache rows bit-exact; latent rows exactly-rounded,
-which is within one bf16 ulp of torch's LayerNorm on a small fraction of
-elements (the reference reduces LayerNorm statistics in fp32)."""
+1e-4 / 1e-5 (fp32); cache rows bit-exact given the wkv_a rows: latent rows
+equal torch's CPU LayerNorm (the reference's kv_norm) bit for bit, k_pe rows
+the per-op-rounded RoPE."""
 import glob
 import hashlib
 import os
@@ -38,19 +38,21 @@ def close(out, ref, dtype):
 def expected_cache(m, xs, dtype, fp8=False):
     """Oracle cache contents for the append kernel's actual inputs: the wkv_a
     rows the GPU computed in forward (recomputed with the same GEMM), put
-    through the exactly-rounded LayerNorm, per-op RoPE at the call-local
+    through torch's CPU LayerNorm order, per-op RoPE at the call-local
     positions and, for e4m3, torch's cast.  Calls are contiguous from 0."""
     cos, sin = (t.cpu() for t in m.rope.half_tables())
-    w = m.kv_norm.weight.detach().float().cpu().numpy()
-    b = m.kv_norm.bias.detach().float().cpu().numpy()
+    w = m.kv_norm.weight.detach().cpu()
+    b = m.kv_norm.bias.detach().cpu()
     rank, rpad = m.kv_lora_rank, m.rank_pad
     cs, ps, ss = [], [], []
     with torch.no_grad():
         for x in xs:
             B, T, _ = x.shape
             kv = m.input_projections(x)[1].cpu()  # the rows forward fed the append kernel
-            y = lo.layernorm_exact(kv[:, :rank].float().numpy(), w, b, m.kv_norm.eps,
-                                   torch.bfloat16 if fp8 else dtype)
+            y = lo.layernorm_aten(kv[:, :rank], w, b, m.kv_norm.eps)[0]
+            # the oracle statement is torch's own CPU LayerNorm, bit for bit
+            ref_ln = torch.nn.functional.layer_norm(kv[:, :rank], (rank,), w, b, m.kv_norm.eps)
+            assert torch.equal(y.view(torch.uint8), ref_ln.view(torch.uint8))
             y = torch.cat([y, torch.zeros(y.shape[0], rpad - rank, dtype=y.dtype)], 1)  # zero padding
             rp = torch.arange(T).repeat(B)
             kpe = lo.rope_interleaved(kv[:, rpad:rpad + 64], cos[rp], sin[rp])

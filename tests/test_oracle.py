@@ -118,68 +118,93 @@ def test_e4m3_decoders_match_torch(lib):
 
 
 # ---------------------------------------------------------------- LayerNorm
-@pytest.mark.parametrize("rank", [256, 1, 64, 173, 200, 320, 512])
-@pytest.mark.parametrize("ln_random", [False, True])
-def test_layernorm_f64_statement(ln_random, rank):
-    g = torch.Generator().manual_seed(4)
-    c = torch.randn(512, rank, generator=g) * 3 + 0.5
-    w = 1 + 0.1 * torch.randn(rank, generator=g) if ln_random else torch.ones(rank)
-    b = 0.1 * torch.randn(rank, generator=g) if ln_random else torch.zeros(rank)
-    eps = 1e-5
-    y = lo.layernorm_f64(c.numpy(), w.numpy(), b.numpy(), eps)
-    assert y.shape == (512, rank)
-    ref = F.layer_norm(c.double(), (rank,), w.double(), b.double(), float(np.float32(eps))).numpy()
-    if rank == 1:  # a single channel normalises to exactly b
-        assert np.array_equal(y, np.broadcast_to(b.double().numpy(), y.shape))
-        return
-    assert np.max(np.abs(y - ref)) < 1e-13
-    if not ln_random:  # invariants of the normalised rows
-        assert np.max(np.abs(y.mean(axis=1))) < 1e-14
-        var = y.var(axis=1)
-        assert np.max(np.abs(var - 1.0 / (1.0 + eps / c.double().var(dim=1, unbiased=False).numpy()))) < 1e-12
+LN_RANKS = [1, 5, 16, 64, 100, 128, 173, 192, 200, 256, 300, 320, 384, 449, 512]
 
 
-def test_layernorm_f64_lane_order_at_rank_256():
-    """At R = 256 the statement is the four-channels-per-lane order: a
-    plain restatement of that order gives identical fp64 bits."""
-    g = torch.Generator().manual_seed(6)
-    c = (torch.randn(64, 256, generator=g) * 3).double().numpy()
-    w = (1 + 0.1 * torch.randn(256, generator=g)).double().numpy()
-    b = (0.1 * torch.randn(256, generator=g)).double().numpy()
-    x = c.reshape(-1, 64, 4)
-    s = ((x[..., 0] + x[..., 1]) + x[..., 2]) + x[..., 3]
-    lanes = np.arange(64)
-    for m in (1, 2, 4, 8, 16, 32):
-        s = s + s[..., lanes ^ m]
-    mean = s[..., :1] * (1.0 / 256.0)
-    d = x - mean[..., None]
-    q = ((d[..., 0] * d[..., 0] + d[..., 1] * d[..., 1]) + d[..., 2] * d[..., 2]) + d[..., 3] * d[..., 3]
-    for m in (1, 2, 4, 8, 16, 32):
-        q = q + q[..., lanes ^ m]
-    rstd = 1.0 / np.sqrt(q[..., :1] * (1.0 / 256.0) + float(np.float32(1e-5)))
-    want = ((d * rstd[..., None]) * w.reshape(64, 4) + b.reshape(64, 4)).reshape(-1, 256)
-    assert np.array_equal(lo.layernorm_f64(c, w, b, 1e-5), want)
+def _ln_rows(kind: str, M: int, N: int, g: torch.Generator) -> torch.Tensor:
+    z = torch.randn(M, N, generator=g)
+    if kind == "normal":
+        return z
+    if kind == "scaled":  # per-row scale over e^[-6, 6]
+        return z * torch.exp(2 * torch.randn(M, 1, generator=g))
+    if kind == "offset":  # large common offset: catastrophic-cancellation regime
+        return z + 30 * torch.randn(M, 1, generator=g)
+    if kind == "narrow":  # tiny spread around 1
+        return z * 1e-3 + 1.0
+    if kind == "heavy":  # heavy tails
+        return z ** 3
+    raise ValueError(kind)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_layernorm_exact_vs_torch_within_one_ulp(dtype):
-    """Exactly-rounded LN vs torch's fp32-statistics LN: at most 1 ulp, rarely."""
-    g = torch.Generator().manual_seed(5)
-    c = (torch.randn(4096, 256, generator=g) * 2).to(dtype)
-    w = (1 + 0.1 * torch.randn(256, generator=g)).to(dtype)
-    b = (0.1 * torch.randn(256, generator=g)).to(dtype)
-    ours = lo.layernorm_exact(c.float().numpy(), w.float().numpy(), b.float().numpy(), 1e-5, dtype)
-    ref = F.layer_norm(c, (256,), w, b, 1e-5)
-    if dtype == torch.bfloat16:
-        # torch's fp32 statistics carry ~1e-7 absolute error, so away from
-        # zero the two differ by at most one bf16 ulp, near zero by <= 2^-20.
-        ulp = (ours.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
-        big = ref.float().abs() >= 2.0 ** -12
-        assert int(ulp[big].max()) <= 1
-        assert float((ours.float() - ref.float()).abs()[~big].max()) <= 2.0 ** -20
-        assert float((ulp > 0).float().mean()) < 1e-3
-    else:
-        assert torch.allclose(ours, ref, rtol=2e-6, atol=2e-6)
+@pytest.mark.parametrize("rank", LN_RANKS)
+def test_aten_layernorm_bit_exact_vs_torch(dtype, rank):
+    """The oracle's LayerNorm (oracle/aten_layernorm.c) against the library
+    routine the reference calls (torch.nn.functional.layer_norm on CPU,
+    models/mla.py:107, :409): every output bit, plus torch's own per-row
+    mean and rstd, over row families from narrow to heavy-tailed, with unit
+    and random affine parameters."""
+    g = torch.Generator().manual_seed(1000 + rank)
+    for kind in ("normal", "scaled", "offset", "narrow", "heavy"):
+        x = _ln_rows(kind, 1500, rank, g).to(dtype)
+        for affine in (False, True):
+            if affine:
+                w = (1 + 0.5 * torch.randn(rank, generator=g)).to(dtype)
+                b = (0.3 * torch.randn(rank, generator=g)).to(dtype)
+            else:
+                w, b = torch.ones(rank, dtype=dtype), torch.zeros(rank, dtype=dtype)
+            y, mean, rstd = lo.layernorm_aten(x, w, b, 1e-5)
+            ref = F.layer_norm(x, (rank,), w, b, 1e-5)
+            assert torch.equal(y.view(torch.uint8), ref.view(torch.uint8)), f"{kind} affine={affine}: output bits"
+            # fp32 parameters make torch return its fp32 statistics for bf16 input
+            _, m_t, r_t = torch.native_layer_norm(x, [rank], w.float() if dtype == torch.bfloat16 else w,
+                                                  b.float() if dtype == torch.bfloat16 else b, 1e-5)
+            assert torch.equal(mean, m_t.view(-1)) and torch.equal(rstd, r_t.view(-1)), f"{kind}: statistics"
+
+
+@pytest.mark.parametrize("variant,dtype,rank", [
+    (1, torch.bfloat16, 256),   # Welford m1 update without its fused multiply-add
+    (2, torch.bfloat16, 512),   # stack merge m1 update fused (two chunks)
+    (2, torch.float32, 384),    # ... and for fp32 rows (three chunks at rank 384)
+    (4, torch.bfloat16, 256),   # lane merge m2 associated the other way
+    (8, torch.bfloat16, 256),   # affine without fused multiply-adds
+    (8, torch.float32, 256),
+])
+def test_aten_layernorm_planted_mistakes_are_caught(variant, dtype, rank):
+    """Each single-site change of the statement disagrees with torch on these
+    rows, so the bit-exact comparison above pins every site it touches."""
+    g = torch.Generator().manual_seed(77)
+    x = _ln_rows("scaled", 4000, rank, g).to(dtype)
+    w = (1 + 0.5 * torch.randn(rank, generator=g)).to(dtype)
+    b = (0.3 * torch.randn(rank, generator=g)).to(dtype)
+    ref = F.layer_norm(x, (rank,), w, b, 1e-5)
+    good = lo.layernorm_aten(x, w, b, 1e-5)[0]
+    bad = lo.layernorm_aten(x, w, b, 1e-5, variant=variant)[0]
+    assert torch.equal(good.view(torch.uint8), ref.view(torch.uint8))
+    assert not torch.equal(bad.view(torch.uint8), ref.view(torch.uint8))
+
+
+@pytest.mark.parametrize("rank", [1, 64, 173, 256, 512])
+def test_aten_layernorm_near_exact_mathematics(rank):
+    """Sanity against the mathematics: within 1 bf16 ulp of the fp64
+    LayerNorm, and a normalised row (unit affine) has mean ~0 and variance
+    ~1 in fp64.  A single channel normalises to the rounding error of
+    rstd * x (rstd = eps^-1/2), as in torch: tiny, not exactly 0."""
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(2000, rank, generator=g) * 3 + 0.5).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(rank, generator=g)).to(torch.bfloat16)
+    b = (0.1 * torch.randn(rank, generator=g)).to(torch.bfloat16)
+    y1 = lo.layernorm_aten(x, torch.ones(rank, dtype=torch.bfloat16), torch.zeros(rank, dtype=torch.bfloat16),
+                           1e-5)[0].double()
+    if rank == 1:
+        assert float(y1.abs().max()) <= 2.0 ** -10
+        return
+    y = lo.layernorm_aten(x, w, b, 1e-5)[0]
+    exact = F.layer_norm(x.double(), (rank,), w.double(), b.double(), float(np.float32(1e-5)))
+    ulp = torch.abs(exact).clamp(min=2.0 ** -10).log2().floor().exp2() * 2.0 ** -7
+    assert bool(((y.double() - exact).abs() <= ulp * 1.0001).all())
+    assert float(y1.mean(dim=1).abs().max()) < 2e-2
+    assert float((y1.var(dim=1, unbiased=False) - 1).abs().max()) < 2e-2
 
 
 # --------------------------------------------------------------------- RoPE
@@ -297,6 +322,28 @@ def test_fp8_emulation_error_bound():
     bound = torch.maximum(y.float().abs() * 2.0 ** -4, scale[:, None] * 2.0 ** -10)
     assert bool((err <= bound * (1 + 1e-6)).all())
     assert int(codes.max()) <= 0xFE and not bool(((codes & 0x7F) == 0x7F).any())
+
+
+def test_fp8_amax_encodes_to_e4m3_max():
+    """The saturation constant is e4m3fn's 448: each token's largest element
+    encodes to code 0x7E (+448) or 0xFE (-448) and dequantises back to exactly
+    that element up to fp32 rounding (an e4m3fnuz-style 240 divisor codes it
+    0x77 / 0xF7)."""
+    g = torch.Generator().manual_seed(12)
+    y = (torch.randn(512, 256, generator=g) * torch.exp(torch.randn(512, 1, generator=g))).to(torch.bfloat16)
+    codes, scale = lo.fp8_quantize(y)
+    yf = y.float()
+    idx = yf.abs().argmax(dim=1)
+    top = codes[torch.arange(512), idx]
+    sign = yf[torch.arange(512), idx] < 0
+    assert torch.equal(top, torch.where(sign, 0xFE, 0x7E).to(torch.uint8))
+    deq = lo.fp8_dequantize(codes, scale)
+    # 448 * fl(amax / 448) is amax up to the two fp32 roundings
+    assert torch.allclose(deq[torch.arange(512), idx], yf[torch.arange(512), idx], rtol=2.0 ** -22, atol=0)
+    # the same check rejects the fnuz-style divisor
+    bad_scale = yf.abs().amax(dim=1) / 240.0
+    bad = (yf / bad_scale[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert not torch.equal(bad[torch.arange(512), idx], top)
 
 
 def test_ref_module_decode_equals_recompute():
