@@ -111,7 +111,8 @@ def log(*a):
 
 # the decode kernel's translation unit (its traffic summary is keyed by these)
 KERNEL_SOURCES = [os.path.join(ROOT, "swamla_amd", "csrc", f)
-                  for f in ("mla_kernels.hip", "mla_device.h", "mla_plan.h", "mla_args.h", "numerics.h")]
+                  for f in ("mla_decode.hip", "mla_fused.h", "mla_kernels.hip", "mla_device.h", "mla_plan.h",
+                            "mla_args.h", "numerics.h")]
 
 
 def kernel_source_hash() -> str:
@@ -247,7 +248,7 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
                 cache.ckv.shape[0], cache.ckv.shape[1], sp.data_ptr(), 0,
                 B, H, R, P, float(m.softmax_scale), n_splits, min_chunk, balance, plan,
                 ws.o_part.data_ptr(), ws.lse_part.data_ptr(),
-                ol.data_ptr(), ol.stride(0), ol.stride(1), _abi.DTYPE_BF16, cache.cache_code, h,
+                ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16, cache.cache_code, h,
             )
             margs = (ws.o_part.data_ptr(), ws.lse_part.data_ptr(), None, None, sp.data_ptr(), 1,
                      cache.ckv.shape[0], cache.ckv.shape[1], B, H, R, n_splits, min_chunk, plan,
@@ -508,7 +509,7 @@ def main() -> int:
         },
         "hbm_gbs_step": step_bytes / (ms_per_step * 1e-3) / 1e9,
         "roofline": {
-            "kernel": "mla_decode_mfma, fused-append instance (mla_decode_attn_append: one-token append + "
+            "kernel": "mla_decode_dma, fused-append instance (mla_decode_attn_append: one-token append + "
                       "split-KV decode attention)",
             "bound": "hbm",
             "achieved": achieved,

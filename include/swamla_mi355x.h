@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define SWAMLA_ABI_VERSION 3
+#define SWAMLA_ABI_VERSION 4
 
 enum {
   SWAMLA_OK = 0,
@@ -144,6 +144,10 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok,
  * [n_rows, n_splits, H] (natural log of sum exp(s)) that mla_merge combines.
  * o_lat        row r, head h at o_lat + r*o_rs + h*o_hs, R_pad values (R..
  *              written 0), in dtype.
+ * lse_out      optional fp32 [n_rows, H] (may be NULL): the natural-log
+ *              log-sum-exp of the scaled scores of every row this launch
+ *              finishes (ns <= 1; -inf for an empty row); mla_merge writes the
+ *              others'.
  */
 int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
                     const void* q_pe, int64_t q_pe_rs, int64_t q_pe_hs,
@@ -157,8 +161,8 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs,
                     int32_t P, float sm_scale, int32_t n_splits,
                     int32_t min_chunk, int32_t balance_blocks, int32_t* plan,
                     float* o_part, float* lse_part, void* o_lat, int64_t o_rs,
-                    int64_t o_hs, int32_t dtype, int32_t cache_dtype,
-                    void* stream);
+                    int64_t o_hs, float* lse_out, int32_t dtype,
+                    int32_t cache_dtype, void* stream);
 
 /*
  * mla_decode_attn_append — one decode step (one new token per sequence) with
@@ -194,8 +198,8 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
                            int32_t n_splits, int32_t min_chunk,
                            int32_t balance_blocks, int32_t* plan, float* o_part,
                            float* lse_part, void* o_lat, int64_t o_rs,
-                           int64_t o_hs, int32_t dtype, int32_t cache_dtype,
-                           void* stream);
+                           int64_t o_hs, float* lse_out, int32_t dtype,
+                           int32_t cache_dtype, void* stream);
 
 /*
  * mla_prefill_attn — absorbed attention of a prefill chunk: T new query

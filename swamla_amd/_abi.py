@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libswamla_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_F32, DTYPE_BF16, DTYPE_FP8 = 0, 1, 2
 ERR_NAMES = {
     -1: "INVALID_ARG",
@@ -85,14 +85,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_decode_attn.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
         _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
-        _F, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
+        _F, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _P, _I32, _I32, _P,
     ]
     lib.mla_decode_attn_append.restype = ctypes.c_int
     lib.mla_decode_attn_append.argtypes = [
         _P, _I64, _P, _P, _F, _P,
         _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
         _P, _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _I32, _I32,
-        _F, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _P,
+        _F, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _P, _I32, _I32, _P,
     ]
     lib.mla_prefill_attn.restype = ctypes.c_int
     lib.mla_prefill_attn.argtypes = [

@@ -8,11 +8,13 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = [
     os.path.join(HERE, "csrc", "mla_kernels.hip"),
+    os.path.join(HERE, "csrc", "mla_decode.hip"),
     os.path.join(HERE, "csrc", "mla_prefill.hip"),
     os.path.join(HERE, "csrc", "mla_linear.hip"),
     os.path.join(HERE, "csrc", "mla_abi.cpp"),
@@ -28,30 +30,52 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build)")
 
 
-def compile_command(output: str = OUTPUT) -> list[str]:
+# Per-source options.  The decode kernel keeps its MFMA accumulators in
+# ordinary VGPRs (its softmax rescales them on the VALU every sub-tile, and
+# AGPR accumulators would be copied back and forth each time).
+EXTRA = {
+    "mla_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+BUILD_DIR = os.path.join(HERE, "_build")
+
+
+def base_flags() -> list[str]:
     return [
-        hipcc(),
         f"--offload-arch={ARCH}",
         "-O3",
         "-std=c++17",
         "-fPIC",
-        "-shared",
         # packed fp32 VALU ops are kept out of the generated code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(ROOT, "include"),
-        *SOURCES,
-        "-o", output,
     ]
 
 
+def compile_commands(output: str = OUTPUT) -> tuple[list[list[str]], list[str]]:
+    """(one compile command per source, the link command)."""
+    objs, cmds = [], []
+    for src in SOURCES:
+        obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
+        cmds.append([hipcc(), *base_flags(), *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj])
+        objs.append(obj)
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", output]
+    return cmds, link
+
+
 def build_library(verbose: bool = False) -> str:
+    os.makedirs(BUILD_DIR, exist_ok=True)
     tmp = OUTPUT + ".tmp"
-    cmd = compile_command(tmp)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+    cmds, link = compile_commands(tmp)
+    with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1, 8)) as ex:
+        results = list(ex.map(lambda c: subprocess.run(c, capture_output=True, text=True), cmds))
+    for cmd, res in zip(cmds, results):
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({res.returncode}) on {cmd[-3]}:\n{res.stderr[-4000:]}")
+        if verbose and res.stderr:
+            print(res.stderr)
+    res = subprocess.run(link, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
-    if verbose and res.stderr:
-        print(res.stderr)
+        raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr[-4000:]}")
     os.replace(tmp, OUTPUT)
     return OUTPUT
 

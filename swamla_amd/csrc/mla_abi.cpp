@@ -190,7 +190,8 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
                  const int32_t* start_pos, int32_t rows_per_seq, int32_t rope_abs, int32_t n_rows, int32_t H,
                  int32_t R, int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk, int32_t balance,
                  int32_t* plan, float* o_part, float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs,
-                 int32_t dtype, int32_t cache_dtype, swamla::DecodeArgs* a, int32_t max_rows = 65535) {
+                 float* lse_out, int32_t dtype, int32_t cache_dtype, swamla::DecodeArgs* a,
+                 int32_t max_rows = 65535) {
   if (int e = check_geometry(H, R, P)) return e;
   if (int e = check_pair(dtype, cache_dtype)) return e;
   if (n_rows < 0 || n_rows > max_rows)
@@ -241,14 +242,14 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
                   "multiples of 4", fn);
   }
   if ((o_part && !aligned(o_part, 16)) || (lse_part && !aligned(lse_part, 4)) ||
-      (ckv_scale && !aligned(ckv_scale, 4)))
-    return fail(SWAMLA_ERR_MISALIGNED, "%s: o_part must be 16-byte aligned", fn);
+      (ckv_scale && !aligned(ckv_scale, 4)) || (lse_out && !aligned(lse_out, 4)))
+    return fail(SWAMLA_ERR_MISALIGNED, "%s: o_part must be 16-byte aligned, lse / scale arrays 4-byte", fn);
   const float log2e = 1.4426950408889634f;
   *a = swamla::DecodeArgs{R,         q_abs,     q_abs_rs,  q_abs_hs,  q_pe,      q_pe_rs,     q_pe_hs,
                           cos_tab,   sin_tab,   rope_len,  ckv_cache, kpe_cache,   ckv_scale,
                           cache_batch, cache_seq, ad,      n_rows,    sm_scale * log2e, n_splits,
                           min_chunk, balance,   plan,      o_part,    lse_part,  o_lat,
-                          o_rs,      o_hs,      swamla::AppendArgs{}};
+                          o_rs,      o_hs,      lse_out,   swamla::AppendArgs{}};
   return SWAMLA_OK;
 }
 
@@ -264,14 +265,14 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const
                     const int32_t* start_pos, int32_t rows_per_seq, int32_t rope_abs, int32_t n_rows,
                     int32_t H, int32_t R, int32_t P, float sm_scale, int32_t n_splits,
                     int32_t min_chunk, int32_t balance_blocks, int32_t* plan, float* o_part,
-                    float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, int32_t dtype,
-                    int32_t cache_dtype, void* stream) {
+                    float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs, float* lse_out,
+                    int32_t dtype, int32_t cache_dtype, void* stream) {
   swamla::DecodeArgs a;
   if (int e = check_decode("mla_decode_attn", q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab,
                            sin_tab, rope_len, ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, row_seq,
                            kv_len, q_rope_pos, start_pos, rows_per_seq, rope_abs, n_rows, H, R, P, sm_scale,
-                           n_splits, min_chunk, balance_blocks, plan, o_part, lse_part, o_lat, o_rs, o_hs, dtype,
-                           cache_dtype, &a))
+                           n_splits, min_chunk, balance_blocks, plan, o_part, lse_part, o_lat, o_rs, o_hs, lse_out,
+                           dtype, cache_dtype, &a))
     return e;
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_attn: no kernel for this dtype pair");
@@ -287,7 +288,8 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
                            const int32_t* start_pos, int32_t rope_abs, int32_t n_rows, int32_t H, int32_t R,
                            int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk,
                            int32_t balance_blocks, int32_t* plan, float* o_part, float* lse_part, void* o_lat,
-                           int64_t o_rs, int64_t o_hs, int32_t dtype, int32_t cache_dtype, void* stream) {
+                           int64_t o_rs, int64_t o_hs, float* lse_out, int32_t dtype, int32_t cache_dtype,
+                           void* stream) {
   const char* fn = "mla_decode_attn_append";
   if (dtype != SWAMLA_DTYPE_BF16)
     return fail(SWAMLA_ERR_UNSUPPORTED, "%s: model dtype %d not built (bf16 only)", fn, dtype);
@@ -296,7 +298,8 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
   if (int e = check_decode(fn, q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab, sin_tab, rope_len,
                            ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, nullptr, nullptr, nullptr,
                            start_pos, 1, rope_abs, n_rows, H, R, P, sm_scale, n_splits, min_chunk,
-                           balance_blocks, plan, o_part, lse_part, o_lat, o_rs, o_hs, dtype, cache_dtype, &a))
+                           balance_blocks, plan, o_part, lse_part, o_lat, o_rs, o_hs, lse_out, dtype, cache_dtype,
+                           &a))
     return e;
   if (n_rows > 0 && !kv_in) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null input rows", fn);
   if (!ln_w || !ln_b) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null LayerNorm pointer", fn);
@@ -339,7 +342,7 @@ int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, cons
   if (int e = check_decode(fn, q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab, sin_tab, rope_len,
                            ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, nullptr, nullptr, nullptr,
                            start_pos, tokens_per_seq, rope_abs, n_rows, H, R, P, sm_scale, 1, 1, 0, nullptr,
-                           nullptr, nullptr, o_lat, o_rs, o_hs, dtype, cache_dtype, &a, 1 << 30))
+                           nullptr, nullptr, o_lat, o_rs, o_hs, nullptr, dtype, cache_dtype, &a, 1 << 30))
     return e;
   // grid: (ceil(T / 4), sequences)
   if (n_rows / tokens_per_seq > 65535)

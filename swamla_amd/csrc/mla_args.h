@@ -70,6 +70,7 @@ struct DecodeArgs {
   float* lse_part;
   void* o_lat;
   int64_t o_rs, o_hs;
+  float* lse_out;  // optional [rows, H]: log-sum-exp of the rows finished in this launch (one split)
   // Optional fused append of one new token per row (fa.kv_in == nullptr:
   // none): the block owning a row's last split appends row r's token r.
   // fa.ad is always this launch's `ad` (dense, T = 1): the kernel derives the

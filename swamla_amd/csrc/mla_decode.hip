@@ -1,0 +1,665 @@
+// mla_decode.hip — absorbed decode attention over the latent cache on gfx950
+// (bf16 model, bf16 or e4m3 cache), with the one-token append optionally
+// folded in.  Reference: models/mla.py:417-487 (cache gather, wkv_b
+// up-projection, SDPA), re-associated: s_t = scale (q_abs . c_t + q_pe . k_pe_t),
+// o_lat = sum_t softmax(s)_t c_t; with the fused append also :307-323, :409-414.
+//
+// One workgroup of four wavefronts per (query row, split).  The split's tokens
+// are cut into 16-token sub-tiles dealt round-robin to the waves (a short first
+// round of n_sub % 4 sub-tiles, then full rounds in which the four waves cover
+// 64 consecutive tokens; the last sub-tile lands on a least-loaded wave), and
+// every wave runs its own online softmax over its sub-tiles: no barrier or
+// exchange inside the loop.  Per sub-tile a wave
+//   * streams the 16 latent rows and 16 rope rows from HBM straight into its
+//     own LDS ring buffer with global_load_lds_dwordx4 (1 KB per instruction,
+//     whole 128-byte lines, non-temporal), NBUF sub-tiles in flight;
+//     16-byte chunks are XOR-swizzled within each 128-byte group of a row so
+//     that the operand reads below hit distinct banks;
+//   * S^T[16 tok x 16 heads] = K . Q^T: mfma_f32_16x16x32_bf16, K from LDS
+//     (16 tokens x 8 channels per instruction), Q^T in registers for the
+//     whole split;
+//   * per-head maxima over the sub-tile with two row-swap permutes, lazily
+//     moved softmax reference (log2 domain);
+//   * O^T[16 ch x 16 heads] += C^T . P^T per 16-channel block:
+//     mfma_f32_16x16x16_bf16 with C^T read transposed from LDS
+//     (ds_read_b64_tr_b16) and P^T straight from the score registers (the
+//     score accumulator's layout is the product's B operand).
+// An e4m3 cache is streamed as codes and decoded exactly (packed
+// cvt_scalef32_pk_bf16_fp8 at scale 1) into a per-wave bf16 staging tile;
+// its per-token scale multiplies the latent score and the token's weight.
+// At the end the four waves' (max, sum, O) meet in LDS and are combined in a
+// fixed order; a one-split row writes o_lat (and its log-sum-exp if asked),
+// otherwise the split writes fp32 partials and a natural-log LSE for the merge.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "mla_args.h"
+#include "mla_device.h"
+#include "mla_fused.h"
+#include "mla_plan.h"
+#include "numerics.h"
+
+namespace swamla {
+
+int launch_decode_f32(const DecodeArgs& a, hipStream_t s);
+int decode_f32_blocks_per_cu(int R, int* blocks);
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kSubTok = 16;   // tokens per wave sub-tile
+constexpr int kDecWaves = 4;  // waves per workgroup
+constexpr int kLdsMax = 160 * 1024;
+
+// Chunk swizzle: 16-byte chunk c of a sub-tile row t lives at c ^ swz(t)
+// (bits 0..2, so a chunk stays inside its 128-byte group).  The operand read
+// of 8 consecutive rows at one chunk hits 8 distinct 16-byte bank groups, and
+// the transposed read of 4 consecutive rows x 32 bytes hits 8 as well.
+__device__ __forceinline__ int swz(int t) { return ((t & 3) << 1) | ((t >> 2) & 1); }
+
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+// Geometry of one instance (cache dtype, R_pad = 64 NB).
+template <int C_DT, int NB>
+struct DecGeo {
+  static constexpr int RP = 64 * NB;
+  static constexpr int kLat = C_DT == 2 ? kSubTok * RP : kSubTok * 2 * RP;  // latent bytes of a sub-tile
+  static constexpr int kPe = kSubTok * 2 * kP;                                // 2 KB of rope rows
+  static constexpr int kSc = C_DT == 2 ? 256 : 0;                             // e4m3 scales (4 copies of 16)
+  static constexpr int kSub = kLat + kPe + kSc;
+  static constexpr int kStage = C_DT == 2 ? kSubTok * 2 * RP : 0;            // e4m3: decoded bf16 tile
+  static constexpr int kVm = (kLat + kPe) / 1024 + (C_DT == 2 ? 1 : 0);      // vm operations per sub-tile
+  static constexpr int kCap = 3;                                              // sub-tiles in flight, at most
+  static constexpr int NBUF = cmin(cmin(kCap + 1, (kLdsMax / kDecWaves - kStage) / kSub), 63 / kVm + 1);
+  static constexpr int kWave = NBUF * kSub + kStage;  // LDS bytes per wave
+  // epilogue: per wave, per head a row of RP fp32 (+4 pad), then max / sum
+  static constexpr int kCombRow = RP + 4;
+  static constexpr int kComb = kDecWaves * kH * kCombRow * 4;
+  static constexpr int kML = 2 * kDecWaves * kH * 4;
+  static constexpr int kLds = cmax(kDecWaves * kWave, kComb + kML);
+  static_assert(NBUF >= 2, "a sub-tile ring needs two buffers");
+  static_assert(ln_stage_bytes<1>() <= kSub, "the fused LayerNorm stages its row in a ring buffer");
+  static_assert(kLds <= kLdsMax, "LDS budget");
+};
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt / lgkmcnt not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Wait until at most `ahead` sub-tiles (of V vm operations each) are in flight.
+template <int V, int NBUF>
+__device__ __forceinline__ void wait_subtiles(int ahead) {
+  static_assert(NBUF <= 5, "extend the cases");
+  if constexpr (NBUF > 4) if (ahead >= 4) { wait_vm<4 * V>(); return; }
+  if constexpr (NBUF > 3) if (ahead >= 3) { wait_vm<3 * V>(); return; }
+  if constexpr (NBUF > 2) if (ahead >= 2) { wait_vm<2 * V>(); return; }
+  if (ahead >= 1) { wait_vm<V>(); return; }
+  wait_vm<0>();
+}
+
+// 16 bytes per lane from global memory into LDS at dst + 16 * lane
+// (non-temporal: the cache is streamed once).
+__device__ __forceinline__ void dma16(const void* src, lds_u8* dst) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 16, 0, 2);
+}
+__device__ __forceinline__ void dma4(const void* src, lds_u8* dst) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 4, 0, 2);
+}
+
+template <typename T>
+__device__ __forceinline__ void lds_st(lds_u8* p, const T& v) {
+  *reinterpret_cast<__attribute__((address_space(3))) T*>(p) = v;
+}
+typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void lds_st16(lds_u8* p, uint4 v) {
+  *reinterpret_cast<__attribute__((address_space(3))) u32x4v_t*>(p) = u32x4v_t{v.x, v.y, v.z, v.w};
+}
+// LDS byte address of an LDS pointer (32 bits on the device).
+__device__ __forceinline__ uint32_t lds_off(const lds_u8* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// Reads of the streamed tiles.  The compiler cannot tell an LDS read of one
+// ring buffer from the DMA still filling another, and would drain every load
+// in flight (s_waitcnt vmcnt(0)) before each LDS read; these reads are
+// therefore issued as inline assembly after the explicit vmcnt wait for the
+// buffer they read, and their results are released by lds_fence(): one
+// s_waitcnt lgkmcnt(0), then an empty asm that redefines each result so no
+// use can be scheduled above the wait.
+template <int OFF>
+__device__ __forceinline__ u32x4v_t ds_read16(uint32_t addr) {
+  u32x4v_t v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+template <int OFF>
+__device__ __forceinline__ s16x4_t ds_read_tr16(uint32_t addr) {
+  s16x4_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <typename T>
+__device__ __forceinline__ void tie(T& v) { asm volatile("" : "+v"(v)); }
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+}  // namespace
+
+template <int C_DT, bool FUSE, int NB>
+__global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a) {
+  using G = DecGeo<C_DT, NB>;
+  constexpr int RP = G::RP, NBUF = G::NBUF;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[G::kLds];
+  lds_u8* const lds = (lds_u8*)(lds_raw);  // the LDS address space, for the DMA and typed LDS access
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  if constexpr (FUSE) {
+    // The fused append's own arguments come in with the rest at entry: read
+    // first inside the owning wave's branch, they sit on kernel-argument lines
+    // no other wave touches, and that cold read would hold back the wave's
+    // first tile.
+    asm volatile("" ::"s"(a.fa.in_rs), "s"(a.fa.ln_w), "s"(a.fa.ln_b), "s"(a.fa.kv_in));
+  }
+
+  // ---- workgroup -> (row, split)
+  int r = blockIdx.y, split = blockIdx.x, bal_chunk = 0;
+  TokAddr ra;
+  if (a.balance > 0) {
+    const BalancedSlot bs =
+        balanced_slot(a.ad, a.n_rows, a.cache_b, a.cache_s, a.n_splits, a.min_chunk, a.balance, blockIdx.x);
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.plan) *a.plan = bs.chunk;
+    if (!bs.ok) return;
+    r = __builtin_amdgcn_readfirstlane(bs.r);
+    split = __builtin_amdgcn_readfirstlane(bs.split);
+    bal_chunk = bs.chunk;
+    ra = bs.addr;
+  } else {
+    ra = row_addr(a.ad, r);
+  }
+
+  // ---- query loads (Q^T as the B operand: lane holds head n, 8 channels at
+  // 32 kb + 8 g); issued before anything waits.  These and the other loads
+  // ahead of the first tile are vm_load()s, released after the explicit wait
+  // below.
+  const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + r * a.qa_rs + n * a.qa_hs;
+  uint32_t qraw[2 * NB][4];
+#pragma unroll
+  for (int s = 0; s < 2 * NB; ++s) vm_load<4>(qa + 32 * s + 8 * g, qraw[s]);
+  const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + r * a.qp_rs + n * a.qp_hs;
+  uint32_t praw[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) vm_load<4>(qp + 32 * s + 8 * g, praw[s]);
+
+  const int b = ra.b;
+  int L = ra.pos;
+  if (L > a.cache_s) L = static_cast<int>(a.cache_s);
+  if (b < 0 || b >= a.cache_b) L = 0;
+  const RowSplits rsp = row_splits(L, a.n_splits, a.min_chunk, bal_chunk);
+  const int ns = rsp.ns;
+  if (split >= ns && !(ns == 0 && split == 0)) return;
+  // Splits run last-first over blockIdx.x: the row's last split, the one that
+  // also appends the new token, gets the first workgroup id of the row and so
+  // the earliest start (workgroups are dealt to the XCDs in id order, and the
+  // later XCDs begin later).
+  if (a.balance <= 0 && ns > 0) split = ns - 1 - split;
+  const int t0 = split * rsp.chunk;  // a multiple of 16
+  const int t1 = min(L, t0 + rsp.chunk);
+  const int n_sub = t1 > t0 ? (t1 - t0 + kSubTok - 1) / kSubTok : 0;
+  // This wave's sub-tiles.  A short first round deals sub-tiles 0 .. rem - 1
+  // (rem = n_sub % 4) to waves 0 .. rem - 1, then full rounds follow: wave w's
+  // k-th sub-tile is w (w < rem, k = 0), else rem + w + 4 (k - [w < rem]).  So
+  // the split's last sub-tile, which holds the fused append's token, goes to
+  // wave 3, one of the waves with the fewest sub-tiles.
+  const int rem = n_sub % kDecWaves;
+  const int my_n = n_sub / kDecWaves + (w < rem ? 1 : 0);
+  const int j_base = rem + w - (w < rem ? kDecWaves : 0);  // j = j_base + 4 k, except (w < rem, k = 0): j = w
+  auto sub_of = [&](int k) { return (k == 0 && w < rem) ? w : j_base + kDecWaves * k; };
+  const int t_last = t1 > 0 ? t1 - 1 : 0;
+  const int64_t row0 = static_cast<int64_t>((b < 0 || b >= a.cache_b) ? 0 : b) * a.cache_s;
+
+  // RoPE row of the query (cos / sin loads go out before the tiles')
+  int rp = ra.rope;
+  rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
+  const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
+  const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
+  uint32_t cr[2][2], sr[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    vm_load<2>(ct + (32 * s + 8 * g) / 2, cr[s]);
+    vm_load<2>(st + (32 * s + 8 * g) / 2, sr[s]);
+  }
+
+  // ---- fused append: the split holding position L - 1 owns the new token
+  bool fa_own = false;  // workgroup-uniform
+  int fa_k = 0, fa_t = 0, fa_w = 0;
+  TokAddr fa_a{0, 0, 0};
+  if constexpr (FUSE) {
+    if (split == (ns > 0 ? ns - 1 : 0)) {
+      fa_a = TokAddr{ra.b, ra.pos - 1, ra.rope};
+      if (fa_a.b < 0 || fa_a.b >= a.fa.cache_b || fa_a.pos < 0 || fa_a.pos >= a.fa.cache_s || fa_a.rope < 0 ||
+          fa_a.rope >= a.fa.rope_len) {
+        if (threadIdx.x == 0 && a.fa.err_flag) a.fa.err_flag[0] = 1;  // skipped, as mla_append does
+      } else {
+        fa_own = true;  // then L = pos + 1 <= cache_s and t1 = L
+        const int j = (fa_a.pos - t0) / kSubTok;
+        if (j < rem) {
+          fa_w = j;
+          fa_k = 0;
+        } else {
+          fa_w = (j - rem) % kDecWaves;
+          fa_k = (j - rem) / kDecWaves + (fa_w < rem ? 1 : 0);
+        }
+        fa_t = (fa_a.pos - t0) % kSubTok;
+      }
+    }
+  }
+  const bool fa_wave = FUSE && fa_own && w == fa_w;  // wave-uniform
+  FusedIn<NB> fin;
+  if constexpr (FUSE)
+    if (fa_wave) fin = fused_load<NB>(a.fa, r, fa_a.rope, lane);
+
+  // ---- sub-tile ring: wave w's k-th sub-tile goes to buffer k % NBUF
+  lds_u8* const wave_lds = lds + w * G::kWave;
+  lds_u8* const stage = wave_lds + NBUF * G::kSub;  // e4m3 only
+  const uint8_t* const ckv = static_cast<const uint8_t*>(a.ckv);
+  const uint8_t* const kpe = static_cast<const uint8_t*>(a.kpe);
+
+  // Per-lane source offsets within a sub-tile (16 rows from its first token)
+  // for each DMA instruction; a sub-tile wholly inside the split then needs one
+  // add per instruction.  bf16 rows: lane's 16-byte slot s of row tt holds chunk
+  // s ^ swz(tt); e4m3 code rows are copied as they lie.
+  constexpr int kLatQ = G::kLat / 1024;
+  uint32_t lat_off[kLatQ], pe_off[2];
+#pragma unroll
+  for (int q = 0; q < kLatQ; ++q) {
+    const int o = 1024 * q + 16 * lane;
+    if constexpr (C_DT == 2) {
+      lat_off[q] = o;
+    } else {
+      const int tt = o / (2 * RP), sl = (o % (2 * RP)) >> 4;
+      lat_off[q] = tt * (2 * RP) + 16 * (sl ^ swz(tt));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int tt = 8 * q + (lane >> 3);
+    pe_off[q] = tt * (2 * kP) + 16 * ((lane & 7) ^ swz(tt));
+  }
+  constexpr int kLatRow = C_DT == 2 ? RP : 2 * RP;  // bytes of a latent cache row
+
+  auto issue = [&](int k) {
+    const int tb = t0 + kSubTok * sub_of(k);
+    lds_u8* const dst = wave_lds + (k % NBUF) * G::kSub;
+    if (tb + kSubTok - 1 <= t_last) {  // uniform: the whole sub-tile is in the split
+      const uint8_t* lb = ckv + (row0 + tb) * kLatRow;
+      const uint8_t* pb = kpe + (row0 + tb) * (2 * kP);
+#pragma unroll
+      for (int q = 0; q < kLatQ; ++q) dma16(lb + lat_off[q], dst + 1024 * q);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) dma16(pb + pe_off[q], dst + G::kLat + 1024 * q);
+      if constexpr (C_DT == 2) dma4(a.ckv_scale + row0 + tb + (lane & 15), dst + G::kLat + G::kPe);
+      return;
+    }
+    // the split's last, partial sub-tile: rows past its end re-read its last row
+#pragma unroll
+    for (int q = 0; q < kLatQ; ++q) {
+      const int tt = (1024 * q + 16 * lane) / kLatRow;
+      const int tok = min(tb + tt, t_last);
+      dma16(ckv + (row0 + tok) * kLatRow + (lat_off[q] - tt * kLatRow), dst + 1024 * q);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int tt = 8 * q + (lane >> 3);
+      const int tok = min(tb + tt, t_last);
+      dma16(kpe + (row0 + tok) * (2 * kP) + (pe_off[q] - tt * (2 * kP)), dst + G::kLat + 1024 * q);
+    }
+    if constexpr (C_DT == 2) {
+      const int tok = min(tb + (lane & 15), t_last);
+      dma4(a.ckv_scale + row0 + tok, dst + G::kLat + G::kPe);
+    }
+  };
+
+  // The first sub-tile goes out right behind the query loads; the rest of the
+  // ring follows once the query has landed (below), so the data every wave
+  // needs first sits at the front of the memory queues rather than behind
+  // everyone's whole ring.
+  // A wave without sub-tiles issues one as well (past the split's end, so it
+  // re-reads the split's last row): the wait below then holds for every wave.
+  issue(0);
+
+  // Everything issued before the first sub-tile (query, RoPE row, fused
+  // inputs) has landed.
+  wait_vm<G::kVm>();
+#pragma unroll
+  for (int s = 0; s < 2 * NB; ++s) vm_release(qraw[s]);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    vm_release(praw[s]);
+    vm_release(cr[s]);
+    vm_release(sr[s]);
+  }
+  if constexpr (FUSE) fused_release(fin);
+
+  // ---- Q^T registers: latent channels >= R zeroed, q_pe rotated (per-op rounded)
+  bf16x8_t qb[2 * NB + 2];
+#pragma unroll
+  for (int s = 0; s < 2 * NB; ++s)
+    qb[s] = as_bf16x8(mask_bf16x8(make_uint4(qraw[s][0], qraw[s][1], qraw[s][2], qraw[s][3]), a.R - (32 * s + 8 * g)));
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    uint32_t wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t cj = (j & 1) ? (cr[s][j >> 1] >> 16) : (cr[s][j >> 1] & 0xFFFF);
+      const uint32_t sj = (j & 1) ? (sr[s][j >> 1] >> 16) : (sr[s][j >> 1] & 0xFFFF);
+      float o1, o2;
+      rope_pair<1>(bf16_to_f32(praw[s][j] & 0xFFFF), bf16_to_f32(praw[s][j] >> 16), bf16_to_f32(cj), bf16_to_f32(sj),
+                   o1, o2);
+      wv[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+    }
+    qb[2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
+  }
+
+#pragma unroll
+  for (int k = 1; k < NBUF - 1; ++k)
+    if (k < my_n) issue(k);
+
+  f32x4_t oacc[4 * NB];
+#pragma unroll
+  for (int i = 0; i < 4 * NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_part = 0.f;
+  FusedTok<C_DT, NB> ftok;
+
+  // Operand addresses within a sub-tile (bytes).  QK (A = K): lane (n, g)
+  // reads row n, chunk (4 s + g) ^ swz(n) = 4 (s ^ b2) + ((g ^ swz(n)) & 3),
+  // b2 = swz(n) >> 2, i.e. +64 s from one base for even s and another for odd
+  // s.  PV (A = C^T, transposed read): lane s = n of group g reads row
+  // 4g + s/4 at channel 16 mb + 4 (s % 4), chunk (2 mb + (s % 4) / 2) ^ swz(row):
+  // with mb = 4 a + m that is a base per m plus 128 a.
+  const int sw_n = swz(n), b2 = sw_n >> 2;
+  const uint32_t qk_lo = n * (2 * RP) + 16 * ((g ^ sw_n) & 3);
+  const uint32_t qk_even = qk_lo + 64 * b2, qk_odd = qk_lo - 64 * b2;
+  const uint32_t pe_lo = n * (2 * kP) + 16 * ((g ^ sw_n) & 3);
+  const uint32_t pe_even = pe_lo + 64 * b2, pe_odd = pe_lo - 64 * b2;
+  const int pv_row = 4 * g + (n >> 2);
+  const int pv_sw = swz(pv_row);
+  uint32_t pv_m[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    pv_m[m] = pv_row * (2 * RP) + 8 * (n & 1) + 16 * ((((n & 3) >> 1)) ^ (pv_sw & 1)) + 32 * (m ^ (pv_sw >> 1));
+
+  auto process = [&](int k) {
+    const int tb = t0 + kSubTok * sub_of(k);
+    lds_u8* const sb = wave_lds + (k % NBUF) * G::kSub;
+    lds_u8* const pe = sb + G::kLat;
+    if constexpr (FUSE) {
+      if (fa_wave && k == fa_k) {
+        // The new token replaces the cache row the stream loaded (this wave's
+        // own buffer, after its loads landed).
+        if constexpr (C_DT == 2) {
+#pragma unroll
+          for (int i = 0; i < NB; ++i) sb[fa_t * RP + NB * lane + i] = ftok.codes[i];
+          if (lane == 0) lds_st<float>(sb + G::kLat + G::kPe + 4 * fa_t, ftok.scale);
+        } else {
+#pragma unroll
+          for (int i = 0; i < NB; ++i) {
+            const int ch = NB * lane + i;
+            lds_st<uint16_t>(sb + fa_t * (2 * RP) + 16 * ((ch >> 3) ^ swz(fa_t)) + 2 * (ch & 7), ftok.row[i]);
+          }
+        }
+        if (lane < kP / 2)
+          lds_st<uint32_t>(pe + fa_t * (2 * kP) + 16 * ((lane >> 2) ^ swz(fa_t)) + 4 * (lane & 3), ftok.pe);
+      }
+    }
+    float4 scv = make_float4(1.f, 1.f, 1.f, 1.f);
+    uint32_t lat = lds_off(sb);
+    if constexpr (C_DT == 2) {
+      // scales, and the codes decoded into the bf16 staging tile (swizzled as a bf16 tile)
+      u32x4v_t sc = ds_read16<0>(lds_off(sb + G::kLat + G::kPe) + 16 * g);
+      u32x4v_t cv[NB];
+      static_for<0, NB>([&](auto q) { cv[q] = ds_read16<1024 * decltype(q)::value>(lds_off(sb) + 16 * lane); });
+      lds_fence();
+      tie(sc);
+      scv = make_float4(u2f(sc.x), u2f(sc.y), u2f(sc.z), u2f(sc.w));
+#pragma unroll
+      for (int q = 0; q < NB; ++q) {
+        tie(cv[q]);
+        const int o = 1024 * q + 16 * lane;
+        const int tt = o / RP, c0 = (o % RP) >> 3;  // chunk of the bf16 row
+        const uint2 d0 = e4m3x4_to_bf16x4_hw(cv[q].x), d1 = e4m3x4_to_bf16x4_hw(cv[q].y);
+        const uint2 d2 = e4m3x4_to_bf16x4_hw(cv[q].z), d3 = e4m3x4_to_bf16x4_hw(cv[q].w);
+        lds_st16(stage + tt * (2 * RP) + 16 * (c0 ^ swz(tt)), make_uint4(d0.x, d0.y, d1.x, d1.y));
+        lds_st16(stage + tt * (2 * RP) + 16 * ((c0 + 1) ^ swz(tt)), make_uint4(d2.x, d2.y, d3.x, d3.y));
+      }
+      lat = lds_off(stage);
+    }
+    const uint32_t pe0 = lds_off(pe);
+
+    // operand reads: K (and rope) for S^T, then C^T for the product, whose
+    // latency hides under the score and softmax arithmetic
+    u32x4v_t kr[2 * NB + 2];
+    static_for<0, 2 * NB>([&](auto sI) {
+      constexpr int S = decltype(sI)::value;
+      kr[S] = ds_read16<64 * S>(lat + ((S & 1) ? qk_odd : qk_even));
+    });
+    kr[2 * NB] = ds_read16<0>(pe0 + pe_even);
+    kr[2 * NB + 1] = ds_read16<64>(pe0 + pe_odd);
+    lds_fence();
+#pragma unroll
+    for (int i = 0; i < 2 * NB + 2; ++i) tie(kr[i]);
+    s16x4_t ctr[4 * NB];
+    static_for<0, 4 * NB>([&](auto mI) {
+      constexpr int MB = decltype(mI)::value;
+      ctr[MB] = ds_read_tr16<128 * (MB >> 2)>(lat + pv_m[MB & 3]);
+    });
+
+    // S^T = K . Q^T
+    f32x4_t s_c = {0.f, 0.f, 0.f, 0.f}, s_p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 2 * NB; ++i)
+      s_c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[i], s_c, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const bf16x8_t kp = __builtin_bit_cast(bf16x8_t, kr[2 * NB + i]);
+      if constexpr (C_DT == 2) s_p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp, qb[2 * NB + i], s_p, 0, 0, 0);
+      else s_c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp, qb[2 * NB + i], s_c, 0, 0, 0);
+    }
+
+    const float sc4[4] = {scv.x, scv.y, scv.z, scv.w};
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float sv = (C_DT == 2) ? (sc4[i] * s_c[i] + s_p[i]) : s_c[i];
+      x[i] = tb + 4 * g + i < t1 ? sv * a.scale_log2 : -INFINITY;
+    }
+    float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    mt = wave_max_rows(mt);  // head n's maximum over the sub-tile (finite: token tb is valid)
+    if (__any(mt > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = exp2f(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4 * NB; ++i) oacc[i] = oacc[i] * alpha;
+    }
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = exp2f(x[i] - m_run);
+    // bf16 weights (hardware RNE); l sums exactly those values, so a constant
+    // latent row is reproduced exactly
+    const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
+    l_part += (u2f(w01 << 16) + u2f(w01 & 0xFFFF0000u)) + (u2f(w23 << 16) + u2f(w23 & 0xFFFF0000u));
+    uint2 pw = make_uint2(w01, w23);
+    if constexpr (C_DT == 2) {
+      pw.x = pack_bf16x2(u2f(w01 << 16) * sc4[0], u2f(w01 & 0xFFFF0000u) * sc4[1]);
+      pw.y = pack_bf16x2(u2f(w23 << 16) * sc4[2], u2f(w23 & 0xFFFF0000u) * sc4[3]);
+    }
+    const s16x4_t pb = __builtin_bit_cast(s16x4_t, pw);
+
+    // O^T[16 mb + ., head] += C^T . P^T
+    lds_fence();
+#pragma unroll
+    for (int mb = 0; mb < 4 * NB; ++mb) {
+      tie(ctr[mb]);
+      oacc[mb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ctr[mb], pb, oacc[mb], 0, 0, 0);
+    }
+  };
+
+  // The new token's cache row, computed while the first tiles stream in (its
+  // inputs were loaded ahead of them).
+  if constexpr (FUSE)
+    if (fa_wave) {
+      ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, lane, wave_lds + (NBUF - 1) * G::kSub);
+    }
+
+  for (int k = 0; k < my_n; ++k) {  // uniform
+    if (k + NBUF - 1 < my_n) issue(k + NBUF - 1);
+    wait_subtiles<G::kVm, NBUF>(min(NBUF - 1, my_n - 1 - k));
+    process(k);
+  }
+  if constexpr (FUSE)
+    if (fa_wave) fused_store<C_DT, NB>(a.fa, static_cast<int64_t>(fa_a.b) * a.fa.cache_s + fa_a.pos, ftok, lane);
+
+  // ---- combine the four waves: per head max, sum and O (fixed order)
+  float l_w = l_part + shfl_xor_f32(l_part, 16);
+  l_w += shfl_xor_f32(l_w, 32);
+  wait_vm<0>();      // (a wave without sub-tiles still has its first one in flight)
+  __syncthreads();  // every wave is done with its ring; the LDS is reused below
+  float* const comb = reinterpret_cast<float*>(lds_raw);
+  float* const mls = comb + kDecWaves * kH * G::kCombRow;  // [2][waves][heads]
+  if (g == 0) {
+    mls[w * kH + n] = m_run;
+    mls[kDecWaves * kH + w * kH + n] = l_w;
+  }
+  // lane (n, g) holds O^T[16 mb + 4 g + i][head n]
+#pragma unroll
+  for (int mb = 0; mb < 4 * NB; ++mb)
+    *reinterpret_cast<float4*>(comb + (w * kH + n) * G::kCombRow + 16 * mb + 4 * g) =
+        make_float4(oacc[mb][0], oacc[mb][1], oacc[mb][2], oacc[mb][3]);
+  __syncthreads();
+
+  // wave w finishes heads 4w .. 4w + 3: lane -> head 4w + g, channels
+  // 64 i + 4 n .. +4 for i < NB (the 16 lanes of a head read and write
+  // consecutive 16-byte pieces)
+  const int h = kDecWaves * w + g;
+  float mw[kDecWaves], lw[kDecWaves];
+  float M = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < kDecWaves; ++v) {
+    mw[v] = mls[v * kH + h];
+    lw[v] = mls[kDecWaves * kH + v * kH + h];
+    M = fmaxf(M, mw[v]);
+  }
+  float sc[kDecWaves], Ltot = 0.f;
+#pragma unroll
+  for (int v = 0; v < kDecWaves; ++v) {
+    sc[v] = mw[v] == -INFINITY ? 0.f : exp2f(mw[v] - M);
+    Ltot += sc[v] * lw[v];
+  }
+  const float inv = Ltot > 0.f ? 1.f / Ltot : 0.f;
+  const int c0 = 4 * n;
+  float o[4 * NB];
+#pragma unroll
+  for (int i = 0; i < 4 * NB; ++i) o[i] = 0.f;
+#pragma unroll
+  for (int v = 0; v < kDecWaves; ++v) {
+    const float* src = comb + (v * kH + h) * G::kCombRow + c0;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const float4 t = *reinterpret_cast<const float4*>(src + 64 * i);
+      o[4 * i + 0] += sc[v] * t.x;
+      o[4 * i + 1] += sc[v] * t.y;
+      o[4 * i + 2] += sc[v] * t.z;
+      o[4 * i + 3] += sc[v] * t.w;
+    }
+  }
+  const float lse2 = Ltot > 0.f ? M + __log2f(Ltot) : -INFINITY;  // log2 domain
+  if (ns <= 1) {
+    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + h * a.o_hs + c0;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      uint2 pk;
+      pk.x = pack_bf16x2(o[4 * i] * inv, o[4 * i + 1] * inv);
+      pk.y = pack_bf16x2(o[4 * i + 2] * inv, o[4 * i + 3] * inv);
+      *reinterpret_cast<uint2*>(op + 64 * i) = pk;
+    }
+    if (a.lse_out && n == 0) a.lse_out[static_cast<int64_t>(r) * kH + h] = lse2 * kLn2;
+    return;
+  }
+  const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * kH + h;
+  float* op = a.o_part + pidx * RP + c0;
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+    *reinterpret_cast<float4*>(op + 64 * i) =
+        make_float4(o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv);
+  if (n == 0) a.lse_part[pidx] = lse2 * kLn2;
+}
+
+// ===========================================================================
+// Launchers behind the C-ABI (argument validation lives in mla_abi.cpp).
+// ===========================================================================
+namespace {
+template <int NB>
+const void* decode_kernel(int c_dt, bool fuse) {
+  if (c_dt == 1 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<1, false, NB>);
+  if (c_dt == 2 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<2, false, NB>);
+  if (c_dt == 1) return reinterpret_cast<const void*>(&mla_decode_dma<1, true, NB>);
+  if (c_dt == 2) return reinterpret_cast<const void*>(&mla_decode_dma<2, true, NB>);
+  return nullptr;
+}
+}  // namespace
+
+int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
+  if (a.n_rows == 0) return 0;
+  if (dt == 0) {
+    if (c_dt != 0 || a.fa.kv_in != nullptr) return -1;
+    return launch_decode_f32(a, s);
+  }
+  if (dt != 1) return -1;
+  const dim3 grid = a.balance > 0 ? dim3(a.balance, 1) : dim3(a.n_splits, a.n_rows);
+  const bool fuse = a.fa.kv_in != nullptr;
+  const int rc = with_nb(a.R, [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    const void* fn = decode_kernel<NB>(c_dt, fuse);
+    if (!fn) return -1;
+    void* args[] = {const_cast<DecodeArgs*>(&a)};
+    return hipLaunchKernel(fn, grid, dim3(kDecWaves * 64), args, 0, s) == hipSuccess ? 0 : -2;
+  });
+  if (rc != 0) return rc;
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// Workgroups of a decode launch one CU holds at once: the MFMA kernel takes a
+// whole CU (its LDS ring), the fp32 kernel's own count.
+int decode_blocks_per_cu(int dt, int c_dt, int R, bool fuse, int* blocks) {
+  if (dt == 0) return (c_dt == 0 && !fuse) ? decode_f32_blocks_per_cu(R, blocks) : -1;
+  if (dt != 1) return -1;
+  return with_nb(R, [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    const void* fn = decode_kernel<NB>(c_dt, fuse);
+    if (!fn) return -1;
+    int nblk = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nblk, fn, kDecWaves * 64, 0) != hipSuccess || nblk < 1)
+      return -2;
+    *blocks = 1;
+    return 0;
+  });
+}
+
+}  // namespace swamla

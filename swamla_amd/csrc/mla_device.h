@@ -140,31 +140,155 @@ __device__ __forceinline__ void ln_stack_merge(int add_cnt, float a1, float a2, 
   cnt = tot;
 }
 
+// The row's values as the statistics read them: lane l < 32 holds its
+// stream's (up to 16) values, lane i < R - nV the i-th tail value, as raw bits
+// (bf16 in the low half, or fp32).
+struct LnRow {
+  uint32_t xs[16];
+  uint32_t xt;
+};
+
 template <int IN_DT>
-__device__ __forceinline__ LnStats aten_ln_stats(const typename Elem<IN_DT>::T* row, int R, float eps, int lane) {
+__device__ __forceinline__ float ln_val(uint32_t raw) {
+  if constexpr (IN_DT == 1) return u2f(raw << 16);
+  else return u2f(raw);
+}
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// Vector-memory loads as inline assembly, for kernels that keep count of their
+// loads in flight themselves: the compiler's wait insertion does not see these,
+// so it neither waits for them nor (missing the global_load_lds tile copies
+// issued after them) drains every copy in flight before their first use.  The
+// caller waits with an explicit s_waitcnt vmcnt and then passes the results
+// through vm_release(), which keeps every use below that wait.
+typedef uint32_t vm_u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t vm_u32x3_t __attribute__((ext_vector_type(3)));
+typedef uint32_t vm_u32x4_t __attribute__((ext_vector_type(4)));
+template <int W>
+__device__ __forceinline__ void vm_load(const void* p, uint32_t (&v)[W]) {
+  static_assert(W >= 1 && W <= 4, "1 to 4 words");
+  if constexpr (W == 1) {
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v[0]) : "v"(p));
+  } else if constexpr (W == 2) {
+    vm_u32x2_t t;
+    asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(t) : "v"(p));
+    v[0] = t[0], v[1] = t[1];
+  } else if constexpr (W == 3) {
+    vm_u32x3_t t;
+    asm volatile("global_load_dwordx3 %0, %1, off" : "=v"(t) : "v"(p));
+    v[0] = t[0], v[1] = t[1], v[2] = t[2];
+  } else {
+    vm_u32x4_t t;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(t) : "v"(p));
+    v[0] = t[0], v[1] = t[1], v[2] = t[2], v[3] = t[3];
+  }
+}
+__device__ __forceinline__ uint32_t vm_load_u16(const void* p) {
+  uint32_t v;
+  asm volatile("global_load_ushort %0, %1, off" : "=v"(v) : "v"(p));
+  return v;
+}
+template <int W>
+__device__ __forceinline__ void vm_release(uint32_t (&v)[W]) {
+#pragma unroll
+  for (int i = 0; i < W; ++i) asm volatile("" : "+v"(v[i]));
+}
+
+// LDS bytes ln_gather needs: the row (64 K elements) and the spans its
+// reads touch (16 vectors past each lane's stream start, values unused).
+template <int IN_DT>
+constexpr int ln_stage_bytes() {
+  return IN_DT == 1 ? 2048 : 4096;
+}
+
+namespace ln_detail {
+// The LDS traffic is inline assembly so that the compiler, which cannot tell
+// this area from a ring buffer still being filled by global_load_lds in the
+// decode kernel, does not drain every load in flight before it.
+template <int ES, int OFF>
+__device__ __forceinline__ void write(uint32_t addr, uint32_t v) {
+  if constexpr (ES == 2) asm volatile("ds_write_b16 %0, %1 offset:%2" ::"v"(addr), "v"(v), "i"(OFF) : "memory");
+  else asm volatile("ds_write_b32 %0, %1 offset:%2" ::"v"(addr), "v"(v), "i"(OFF) : "memory");
+}
+template <int ES, int OFF>
+__device__ __forceinline__ uint32_t read(uint32_t addr) {
+  uint32_t v;
+  if constexpr (ES == 2) asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  else asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+template <int ES, int K, int W, int M>
+__device__ __forceinline__ void write_lane(uint32_t addr, const uint32_t (&xw)[W]) {
+  if constexpr (M < K) {
+    if constexpr (ES == 4) write<4, 4 * M>(addr, xw[M]);
+    else if constexpr (K % 2 == 0 && M % 2 == 0) write<4, 2 * M>(addr, xw[M / 2]);  // a pair per word
+    else if constexpr (K % 2 != 0) write<2, 2 * M>(addr, (M & 1) ? (xw[M / 2] >> 16) : xw[M / 2]);
+    write_lane<ES, K, W, M + 1>(addr, xw);
+  }
+}
+template <int ES, int STEP, int J>
+__device__ __forceinline__ void read_stream(uint32_t addr, uint32_t (&xs)[16]) {
+  if constexpr (J < 16) {
+    xs[J] = read<ES, J * STEP>(addr);
+    read_stream<ES, STEP, J + 1>(addr, xs);
+  }
+}
+}  // namespace ln_detail
+
+// Builds the statistics' layout from the row as the wavefront already holds
+// it — lane l owning channels K l .. K l + K - 1 as raw words (K bf16 values
+// packed two per word, or K fp32 words) — by staging the row in `buf`
+// (ln_stage_bytes<IN_DT>() bytes of LDS that only this wavefront touches
+// while this runs), so the LayerNorm reads the row from memory once.  A
+// wavefront's LDS operations complete in order, so the reads see the writes.
+template <int IN_DT, int K>
+__device__ __forceinline__ LnRow ln_gather(const uint32_t (&xw)[IN_DT == 1 ? (K + 1) / 2 : K], int R, int lane,
+                                           lds_u8* buf) {
+  constexpr int V = IN_DT == 1 ? 16 : 8;
+  constexpr int HV = V / 8;
+  constexpr int ES = IN_DT == 1 ? 2 : 4;  // bytes per element
+  constexpr int W = IN_DT == 1 ? (K + 1) / 2 : K;
+  static_assert(64 * K * ES <= ln_stage_bytes<IN_DT>(), "staging area");
+  const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(buf));
+  ln_detail::write_lane<ES, K, W, 0>(base + ES * K * lane, xw);
+  // the lane of stream (chunk sc, half sh, lane sk) reads elements s0 + j V,
+  // j = 0..15, s0 = 16 V sc + 8 sh + sk (those past the stream's count, and
+  // every read of a lane without a stream, land in the staging area and are
+  // ignored); lane i reads tail value n V + i
+  const int n = R / V;
+  const int sc = lane / (8 * HV), sh = (lane >> 3) & (HV - 1), sk = lane & 7;
+  LnRow x;
+  ln_detail::read_stream<ES, ES * V, 0>(base + ES * (sc * 16 * V + 8 * sh + sk), x.xs);
+  x.xt = ln_detail::read<ES, 0>(base + ES * (n * V + lane));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < 16; ++j) asm volatile("" : "+v"(x.xs[j]));
+  asm volatile("" : "+v"(x.xt));
+  return x;
+}
+
+template <int IN_DT>
+__device__ __forceinline__ LnStats aten_ln_stats(const LnRow& x, int R, float eps, int lane) {
 #pragma clang fp contract(off)
-  using E = Elem<IN_DT>;
   constexpr int V = IN_DT == 1 ? 16 : 8;         // values per input vector
   constexpr int HV = V / 8;                       // 8-lane float vectors per input vector
   constexpr int kMaxChunks = IN_DT == 1 ? 2 : 4;  // R <= 512
   const int n = R / V;
   const int chunks = (n + 15) >> 4;
   // --- streams (lanes 0..31; a lane past the chunks has none)
-  const int sc = lane / (8 * HV), sh = (lane >> 3) & (HV - 1), sk = lane & 7;
+  const int sc = lane / (8 * HV);
   int scnt = n - 16 * sc;
   scnt = scnt < 0 ? 0 : (scnt > 16 ? 16 : scnt);
-  const auto* sp = row + sc * 16 * V + 8 * sh + sk;
-  float xs[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) xs[j] = j < scnt ? E::ld(sp, j * V) : 0.f;
   float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     if (j < scnt) {
+      const float xv = ln_val<IN_DT>(x.xs[j]);
       const float c = __fdiv_rn(1.0f, static_cast<float>(j + 1));
-      const float d = xs[j] - s1;
+      const float d = xv - s1;
       s1 = __builtin_fmaf(d, c, s1);
-      s2 = __builtin_fmaf(d, xs[j] - s1, s2);
+      s2 = __builtin_fmaf(d, xv - s1, s2);
     }
   }
   // --- stack merges (lane k = lane % 8 keeps lane k's accumulators)
@@ -193,8 +317,8 @@ __device__ __forceinline__ LnStats aten_ln_stats(const typename Elem<IN_DT>::T* 
   // --- scalar tail, then the 8 lanes (values uniform across the wave)
   int cnt = 0;
   float m1 = 0.f, m2 = 0.f;
-  for (int i = n * V; i < R; ++i) {
-    const float xv = E::ld(row, i);
+  for (int i = 0; i < R - n * V; ++i) {  // uniform, < V
+    const float xv = ln_val<IN_DT>(__builtin_amdgcn_readlane(x.xt, i));
     const float d = xv - m1;
     ++cnt;
     m1 = m1 + __fdiv_rn(d, static_cast<float>(cnt));
@@ -387,6 +511,7 @@ __device__ __forceinline__ float wave_max_rows(float v) {
 }
 
 constexpr float kLazy = 8.0f;  // log2 headroom before the softmax reference moves
+constexpr float kLn2 = 0.6931471805599453f;
 
 // Workgroup barrier that orders LDS only: global loads stay in flight across
 // it (a full fence would also wait for them).  The release half completes

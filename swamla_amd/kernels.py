@@ -342,8 +342,9 @@ def decode_attention(
     explicit (row_seq, kv_len, q_rope_pos) or dense (start_pos [rows /
     rows_per_seq], causal).  Returns o_lat [rows, H, R_pad], whose padding
     channels are 0 (``out`` may be a strided view, e.g. a transpose of a
-    [H, rows, R_pad] buffer).  With more than one split, mla_merge runs after the decode
-    kernel (and writes the log-sum-exp to ``lse_out`` if given) unless
+    [H, rows, R_pad] buffer).  ``lse_out`` [rows, H] fp32, if given, receives
+    every row's log-sum-exp (natural log; -inf for an empty row).  With more
+    than one split, mla_merge runs after the decode kernel unless
     ``merge`` is False: then rows with several splits leave their partials in
     ``workspace`` for merge_project.  With ``append`` (bf16, dense
     addressing, one row per sequence) the step's new tokens are appended in
@@ -404,7 +405,7 @@ def decode_attention(
                 rows, H, rk, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
                 _abi.ptr(workspace.o_part if workspace else None),
                 _abi.ptr(workspace.lse_part if workspace else None),
-                out.data_ptr(), out.stride(0), out.stride(1),
+                out.data_ptr(), out.stride(0), out.stride(1), _abi.ptr(lse_out),
                 _abi.dtype_code(dt), cache.cache_code, stream,
             )
         )
@@ -420,7 +421,7 @@ def decode_attention(
                 rows, H, rk, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
                 _abi.ptr(workspace.o_part if workspace else None),
                 _abi.ptr(workspace.lse_part if workspace else None),
-                out.data_ptr(), out.stride(0), out.stride(1),
+                out.data_ptr(), out.stride(0), out.stride(1), _abi.ptr(lse_out),
                 _abi.dtype_code(dt), cache.cache_code, stream,
             )
         )

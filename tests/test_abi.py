@@ -36,7 +36,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mla_abi_version() == _abi.ABI_VERSION == 3
+    assert lib.mla_abi_version() == _abi.ABI_VERSION == 4
 
 
 def _append(lib, **kw):
@@ -51,7 +51,7 @@ def _decode(lib, **kw):
     args = dict(qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, cos=FAKE, sin=FAKE,
                 rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, row_seq=FAKE, kv_len=FAKE, qrp=FAKE,
                 sp=None, T=1, rope_abs=0, n_rows=2, H=16, R=256, P=64, sm=0.07, ns=1, mc=64, bal=0, plan=None,
-                o_part=None, lse=None, o=FAKE, o_rs=4096, o_hs=256, dt=1, c_dt=1, stream=None)
+                o_part=None, lse=None, o=FAKE, o_rs=4096, o_hs=256, lse_out=None, dt=1, c_dt=1, stream=None)
     args.update(kw)
     return lib.mla_decode_attn(*args.values())
 
@@ -119,6 +119,7 @@ def test_append_zero_tokens_is_a_noop(lib):
         (dict(bal=300, n_rows=257), -1),  # a balanced plan covers at most 256 rows
         (dict(bal=256, plan=FAKE + 2), -3),
         (dict(bal=256, cs=(1 << 24) + 1), -2),  # balanced plans cover caches up to 2^24 positions
+        (dict(lse_out=FAKE + 2), -3),
     ],
 )
 def test_decode_rejects(lib, kw, code):
@@ -131,7 +132,7 @@ def _decode_append(lib, **kw):
                 qa=FAKE, qa_rs=4096, qa_hs=256, qp=FAKE, qp_rs=3072, qp_hs=192, cos=FAKE, sin=FAKE,
                 rope_len=16, ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=16, sp=FAKE, rope_abs=0, n_rows=2,
                 H=16, R=256, P=64, sm=0.07, ns=1, mc=64, bal=0, plan=None, o_part=None, lse=None, o=FAKE,
-                o_rs=4096, o_hs=256, dt=1, c_dt=1, stream=None)
+                o_rs=4096, o_hs=256, lse_out=None, dt=1, c_dt=1, stream=None)
     args.update(kw)
     return lib.mla_decode_attn_append(*args.values())
 

@@ -349,9 +349,9 @@ def test_balanced_plan_matches_oracle_and_host_chunk(gpu, dtype, fp8):
     rp = torch.zeros(rows, dtype=torch.int32)
     cos, sin = tables(dtype, S, gpu)
     seq_t, len_t = torch.tensor(seqs, dtype=torch.int32), torch.tensor(lens, dtype=torch.int32)
-    # as many workgroups as the CUs hold (three per CU for the e4m3 cache)
+    # as many workgroups as the CUs hold (one per CU: a workgroup's tile ring takes the CU's LDS)
     bal, cap = kernels.balanced_splits(rows, 256, kernels.decode_blocks_per_cu(dtype, fp8, R, False, gpu))
-    assert bal == (768 if fp8 else 256)
+    assert bal == 256
     ws = DecodeWorkspace.allocate(rows, cap, gpu)
     ws.plan.fill_(-7)
     out = kernels.decode_attention(q_abs.to(gpu), q_pe.to(gpu), cos, sin, cache, SCALE, row_seq=seq_t.to(gpu),
@@ -404,14 +404,13 @@ def test_e4m3_decode_every_code_exact(gpu):
 
 
 def test_decode_blocks_per_cu(gpu):
-    """Workgroups per CU the split plans target: one for bf16 caches and fp32,
-    three for e4m3 caches at ranks up to 256 (their kernel is built for three
-    per CU), the same for the fused-append instance."""
+    """Workgroups per CU the split plans target: one for every cache type and
+    rank (a decode workgroup's tile ring takes the CU's LDS), the fused-append
+    instance included, and one for fp32."""
     for rank in (64, 128, 200, 256, 320, 512):
         for fused in (False, True):
             assert kernels.decode_blocks_per_cu(torch.bfloat16, False, rank, fused, gpu) == 1
-            n8 = kernels.decode_blocks_per_cu(torch.bfloat16, True, rank, fused, gpu)
-            assert n8 == 3 if rank <= 256 else n8 == 1
+            assert kernels.decode_blocks_per_cu(torch.bfloat16, True, rank, fused, gpu) == 1
         assert kernels.decode_blocks_per_cu(torch.float32, False, rank, False, gpu) == 1
     lib = _abi.lib()
     assert lib.mla_decode_blocks_per_cu(_abi.DTYPE_F32, _abi.DTYPE_F32, 256, 1) == -2  # no fused fp32 kernel

@@ -1,6 +1,6 @@
 """Host-side split planning (CPU): how many splits and balanced workgroups a
 decode launch asks for, given the workgroups per CU its kernel is built for
-(one for a bf16 cache, three for an e4m3 cache at ranks up to 256)."""
+(one per CU for the MFMA decode kernel; other counts exercise the formula)."""
 from __future__ import annotations
 
 import pytest
