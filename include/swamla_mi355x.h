@@ -3,8 +3,10 @@
  *
  * Every entry point replaces one piece of the absorb branch of the reference
  * `MLA.forward` (Orolol/swamla, models/mla.py).  The library allocates no
- * memory, keeps no pointer after it returns and holds no device state: the
- * caller owns caches, partial buffers and outputs.  Work is enqueued on the
+ * memory and keeps no pointer after it returns; its only device state is the
+ * fixed scratch area of mla_decode_attn_noalloc (one per GPU, part of the
+ * loaded code object).  The caller owns caches, partial buffers and outputs.
+ * Work is enqueued on the
  * caller's HIP stream (`stream` is a hipStream_t; NULL = default stream) and
  * nothing synchronises the host.  All entry points are graph-capturable.
  *
@@ -200,6 +202,39 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
                            float* lse_part, void* o_lat, int64_t o_rs,
                            int64_t o_hs, float* lse_out, int32_t dtype,
                            int32_t cache_dtype, void* stream);
+
+/*
+ * mla_decode_attn_noalloc — mla_decode_attn followed by mla_merge, with the
+ * split partials, their log-sum-exps and the balanced plan kept in a fixed
+ * scratch area inside the library instead of caller buffers.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc); it calls no allocating routine.
+ * Arguments: those of mla_decode_attn without plan / o_part / lse_part;
+ * o_lat and lse_out receive every row's merged result.  Limit: n_rows x
+ * n_splits x H x R_pad x 4 bytes of partials at most 16 MiB (n_splits == 1
+ * needs none); larger calls return SWAMLA_ERR_UNSUPPORTED.  There is one
+ * scratch area per GPU, shared by every call on it: calls that overlap on
+ * one GPU (other streams, other threads) race and must be serialised by the
+ * caller.  Nothing in the area needs clearing between calls (each launch
+ * writes every partial it reads back).
+ */
+int mla_decode_attn_noalloc(const void* q_abs, int64_t q_abs_rs,
+                            int64_t q_abs_hs, const void* q_pe,
+                            int64_t q_pe_rs, int64_t q_pe_hs,
+                            const void* cos_tab, const void* sin_tab,
+                            int64_t rope_len, const void* ckv_cache,
+                            const void* kpe_cache, const float* ckv_scale,
+                            int64_t cache_batch, int64_t cache_seq,
+                            const int32_t* row_seq, const int32_t* kv_len,
+                            const int32_t* q_rope_pos,
+                            const int32_t* start_pos, int32_t rows_per_seq,
+                            int32_t rope_abs, int32_t n_rows, int32_t H,
+                            int32_t R, int32_t P, float sm_scale,
+                            int32_t n_splits, int32_t min_chunk,
+                            int32_t balance_blocks, void* o_lat, int64_t o_rs,
+                            int64_t o_hs, float* lse_out, int32_t dtype,
+                            int32_t cache_dtype, void* stream);
 
 /*
  * mla_prefill_attn — absorbed attention of a prefill chunk: T new query

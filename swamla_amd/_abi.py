@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "mla_append",
     "mla_decode_attn",
     "mla_decode_attn_append",
+    "mla_decode_attn_noalloc",
     "mla_prefill_attn",
     "mla_merge",
     "mla_split_count",
@@ -93,6 +94,12 @@ def _declare(lib: ctypes.CDLL) -> None:
         _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
         _P, _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _I32, _I32,
         _F, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _P, _I32, _I32, _P,
+    ]
+    lib.mla_decode_attn_noalloc.restype = ctypes.c_int
+    lib.mla_decode_attn_noalloc.argtypes = [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64,
+        _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
+        _F, _I32, _I32, _I32, _P, _I64, _I64, _P, _I32, _I32, _P,
     ]
     lib.mla_prefill_attn.restype = ctypes.c_int
     lib.mla_prefill_attn.argtypes = [

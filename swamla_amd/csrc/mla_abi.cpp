@@ -10,6 +10,7 @@
 #include "../../include/swamla_mi355x_testing.h"
 #include "mla_args.h"
 #include "mla_plan.h"
+#include "mla_scratch.h"
 #include "numerics.h"
 
 namespace {
@@ -321,6 +322,63 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
                             cache_batch, cache_seq, err_flag};
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair", fn);
+  if (rc != 0) return hip_fail(fn);
+  return ok();
+}
+
+int mla_decode_attn_noalloc(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const void* q_pe,
+                            int64_t q_pe_rs, int64_t q_pe_hs, const void* cos_tab, const void* sin_tab,
+                            int64_t rope_len, const void* ckv_cache, const void* kpe_cache,
+                            const float* ckv_scale, int64_t cache_batch, int64_t cache_seq,
+                            const int32_t* row_seq, const int32_t* kv_len, const int32_t* q_rope_pos,
+                            const int32_t* start_pos, int32_t rows_per_seq, int32_t rope_abs, int32_t n_rows,
+                            int32_t H, int32_t R, int32_t P, float sm_scale, int32_t n_splits,
+                            int32_t min_chunk, int32_t balance_blocks, void* o_lat, int64_t o_rs, int64_t o_hs,
+                            float* lse_out, int32_t dtype, int32_t cache_dtype, void* stream) {
+  const char* fn = "mla_decode_attn_noalloc";
+  if (int e = check_geometry(H, R, P)) return e;
+  if (n_rows < 0 || n_rows > 65535 || n_splits < 1 || n_splits > 1024)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_rows=%d / n_splits=%d outside [0, 65535] / [1, 1024]", fn, n_rows,
+                n_splits);
+  // partials of every (row, split, head): R_pad fp32 values and one log-sum-exp
+  const int64_t part = n_splits > 1 ? int64_t(n_rows) * n_splits * H * swamla::padded_rank(R) * 4 : 0;
+  if (part > static_cast<int64_t>(swamla::kScratchPartBytes))
+    return fail(SWAMLA_ERR_UNSUPPORTED,
+                "%s: %d rows x %d splits need %lld bytes of split partials, above this entry point's fixed "
+                "scratch of %lld bytes (use fewer splits or rows per call, or mla_decode_attn with a workspace)",
+                fn, n_rows, n_splits, (long long)part, (long long)swamla::kScratchPartBytes);
+  // Validate everything first (no GPU call), with stand-ins for the
+  // scratch pointers: 256-aligned, as the real area is.
+  float* const stand_in = reinterpret_cast<float*>(uintptr_t(256));
+  swamla::DecodeArgs a;
+  if (int e = check_decode(fn, q_abs, q_abs_rs, q_abs_hs, q_pe, q_pe_rs, q_pe_hs, cos_tab, sin_tab, rope_len,
+                           ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, row_seq, kv_len, q_rope_pos,
+                           start_pos, rows_per_seq, rope_abs, n_rows, H, R, P, sm_scale, n_splits, min_chunk,
+                           balance_blocks, nullptr, stand_in, stand_in, o_lat, o_rs, o_hs, lse_out, dtype,
+                           cache_dtype, &a))
+    return e;
+  void* area = nullptr;
+  if (const int rc = swamla::scratch_area(&area)) {
+    if (rc == -2) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: device ordinal beyond the scratch table", fn);
+    return fail(SWAMLA_ERR_HIP, "%s: scratch address lookup failed: %s", fn, hipGetErrorString(hipGetLastError()));
+  }
+  uint8_t* const base = static_cast<uint8_t*>(area);
+  float* const o_part = reinterpret_cast<float*>(base);
+  float* const lse_part = reinterpret_cast<float*>(base + swamla::kScratchPartBytes);
+  int32_t* const plan = balance_blocks > 0 ? reinterpret_cast<int32_t*>(base + swamla::kScratchPlanOffset) : nullptr;
+  a.o_part = o_part;
+  a.lse_part = lse_part;
+  a.plan = plan;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = swamla::launch_decode(a, dtype, cache_dtype, st);
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair", fn);
+  if (rc != 0) return hip_fail(fn);
+  if (n_splits == 1 || n_rows == 0) return ok();
+  // every partial the merge reads was written by the launch above
+  swamla::MergeArgs m{o_part, lse_part, a.ad, cache_batch, cache_seq, n_rows, n_splits,
+                      min_chunk, plan, R, o_lat, o_rs, o_hs, lse_out};
+  rc = swamla::launch_merge(m, dtype, st);
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no merge kernel for dtype %d", fn, dtype);
   if (rc != 0) return hip_fail(fn);
   return ok();
 }
