@@ -142,23 +142,46 @@ class RefMLA(nn.Module):
         q_pe = q_pe.transpose(1, 2).contiguous()
         q_pe = self.rope(q_pe)
         q_pe = q_pe.transpose(1, 2).contiguous()
+        kv, k_pe = self.project_kv(x)
+        return q_nope, q_pe, kv, k_pe
+
+    def project_kv(self, x: torch.Tensor):
+        """mla.py:307-323: raw c (split view) and RoPE'd k_pe."""
+        bsz, seqlen, _ = x.size()
         kv = self.wkv_a(x)
         kv, k_pe = torch.split(kv, [self.kv_lora_rank, self.qk_rope_head_dim], dim=-1)
         k_pe = k_pe.view(bsz, seqlen, 1, -1).transpose(1, 2)
         k_pe = self.rope(k_pe.contiguous()).squeeze(1)
-        return q_nope, q_pe, kv, k_pe
+        return kv, k_pe
 
-    def forward(self, x: torch.Tensor, start_pos: int) -> torch.Tensor:
-        bsz, seqlen, _ = x.size()
-        end_pos = start_pos + seqlen
-        q_nope, q_pe, kv, k_pe = self.project(x)
-        wkv_b = self.wkv_b.weight.view(self.n_heads, -1, self.kv_lora_rank)  # :404-406
-        kv_norm_tensor = self.kv_norm(kv)  # :409
+    def cache_rows(self, kv: torch.Tensor) -> torch.Tensor:
+        """mla.py:409 (kv_norm), plus the e4m3 round trip of the emulated
+        fp8 cache."""
+        kv_norm_tensor = self.kv_norm(kv)
         if self.fp8_cache:
             from .latent_ops import fp8_dequantize, fp8_quantize
 
             codes, scale = fp8_quantize(kv_norm_tensor.reshape(-1, self.kv_lora_rank))
             kv_norm_tensor = fp8_dequantize(codes, scale).to(kv.dtype).view_as(kv_norm_tensor)
+        return kv_norm_tensor
+
+    def fill_cache(self, x: torch.Tensor, start_pos: int) -> None:
+        """The cache writes of forward (mla.py:307-323, :409-414) without the
+        query projection or attention: what a prompt pass leaves in
+        kv_cache / pe_cache."""
+        bsz, seqlen, _ = x.size()
+        kv, k_pe = self.project_kv(x)
+        self.kv_cache[:bsz, start_pos:start_pos + seqlen] = self.cache_rows(kv)
+        self.pe_cache[:bsz, start_pos:start_pos + seqlen] = k_pe
+
+    def forward(self, x: torch.Tensor, start_pos: int, freqs_cis=None, mask=None) -> torch.Tensor:
+        """``mask``: additive [S, T] mask, expanded and cast to the query
+        dtype as mla.py:473-478 does (is_causal is then off, :483)."""
+        bsz, seqlen, _ = x.size()
+        end_pos = start_pos + seqlen
+        q_nope, q_pe, kv, k_pe = self.project(x)
+        wkv_b = self.wkv_b.weight.view(self.n_heads, -1, self.kv_lora_rank)  # :404-406
+        kv_norm_tensor = self.cache_rows(kv)  # :409
         if self.inference_mode:
             self.kv_cache[:bsz, start_pos:end_pos] = kv_norm_tensor  # :413-414
             self.pe_cache[:bsz, start_pos:end_pos] = k_pe
@@ -174,9 +197,12 @@ class RefMLA(nn.Module):
         q_sdpa = q_full.transpose(1, 2).contiguous()  # :466-468
         k_sdpa = k_full.transpose(1, 2).contiguous()
         v_sdpa = v.transpose(1, 2).contiguous()
+        attn_mask = None
+        if mask is not None:  # :474-478
+            attn_mask = mask.unsqueeze(0).unsqueeze(0).expand(bsz, self.n_heads, -1, -1).to(q_sdpa.dtype)
         attn = F.scaled_dot_product_attention(  # :581-595 (no cuDNN, dropout 0 in eval)
-            q_sdpa, k_sdpa, v_sdpa, attn_mask=None, dropout_p=0.0,
-            is_causal=seqlen > 1, scale=self.softmax_scale,
+            q_sdpa, k_sdpa, v_sdpa, attn_mask=attn_mask, dropout_p=0.0,
+            is_causal=mask is None and seqlen > 1, scale=self.softmax_scale,
         )
         x = attn.transpose(1, 2).contiguous().reshape(bsz, seqlen, -1)
         return self.wo(x)

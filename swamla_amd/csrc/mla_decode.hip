@@ -79,7 +79,7 @@ struct DecGeo {
   // epilogue: per wave, per head a row of RP fp32 (+4 pad), then max / sum
   static constexpr int kCombRow = RP + 4;
   static constexpr int kComb = kDecWaves * kH * kCombRow * 4;
-  static constexpr int kML = 2 * kDecWaves * kH * 4;
+  static constexpr int kML = 3 * kDecWaves * kH * 4;
   static constexpr int kLds = cmax(kDecWaves * kWave, kComb + kML);
   static_assert(NBUF >= 2, "a sub-tile ring needs two buffers");
   static_assert(ln_stage_bytes<1>() <= kSub, "the fused LayerNorm stages its row in a ring buffer");
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   f32x4_t oacc[4 * NB];
 #pragma unroll
   for (int i = 0; i < 4 * NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_part = 0.f;
+  float m_run = -INFINITY, l_part = 0.f, e_part = 0.f;
   FusedTok<C_DT, NB> ftok;
 
   // Operand addresses within a sub-tile (bytes).  QK (A = K): lane (n, g)
@@ -495,6 +495,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
       const float alpha = exp2f(m_run - m_new);
       m_run = m_new;
       l_part *= alpha;
+      e_part *= alpha;
 #pragma unroll
       for (int i = 0; i < 4 * NB; ++i) oacc[i] = oacc[i] * alpha;
     }
@@ -502,9 +503,11 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
 #pragma unroll
     for (int i = 0; i < 4; ++i) p[i] = exp2f(x[i] - m_run);
     // bf16 weights (hardware RNE); l sums exactly those values, so a constant
-    // latent row is reproduced exactly
+    // latent row is reproduced exactly; e sums the fp32 weights for the
+    // log-sum-exp (the bf16 roundings would move it by up to 2^-9 relative)
     const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
     l_part += (u2f(w01 << 16) + u2f(w01 & 0xFFFF0000u)) + (u2f(w23 << 16) + u2f(w23 & 0xFFFF0000u));
+    e_part += (p[0] + p[1]) + (p[2] + p[3]);
     uint2 pw = make_uint2(w01, w23);
     if constexpr (C_DT == 2) {
       pw.x = pack_bf16x2(u2f(w01 << 16) * sc4[0], u2f(w01 & 0xFFFF0000u) * sc4[1]);
@@ -539,13 +542,16 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   // ---- combine the four waves: per head max, sum and O (fixed order)
   float l_w = l_part + shfl_xor_f32(l_part, 16);
   l_w += shfl_xor_f32(l_w, 32);
+  float e_w = e_part + shfl_xor_f32(e_part, 16);
+  e_w += shfl_xor_f32(e_w, 32);
   wait_vm<0>();      // (a wave without sub-tiles still has its first one in flight)
   __syncthreads();  // every wave is done with its ring; the LDS is reused below
   float* const comb = reinterpret_cast<float*>(lds_raw);
-  float* const mls = comb + kDecWaves * kH * G::kCombRow;  // [2][waves][heads]
+  float* const mls = comb + kDecWaves * kH * G::kCombRow;  // [3][waves][heads]: max, l, e
   if (g == 0) {
     mls[w * kH + n] = m_run;
     mls[kDecWaves * kH + w * kH + n] = l_w;
+    mls[2 * kDecWaves * kH + w * kH + n] = e_w;
   }
   // lane (n, g) holds O^T[16 mb + 4 g + i][head n]
 #pragma unroll
@@ -558,19 +564,21 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   // 64 i + 4 n .. +4 for i < NB (the 16 lanes of a head read and write
   // consecutive 16-byte pieces)
   const int h = kDecWaves * w + g;
-  float mw[kDecWaves], lw[kDecWaves];
+  float mw[kDecWaves], lw[kDecWaves], ew[kDecWaves];
   float M = -INFINITY;
 #pragma unroll
   for (int v = 0; v < kDecWaves; ++v) {
     mw[v] = mls[v * kH + h];
     lw[v] = mls[kDecWaves * kH + v * kH + h];
+    ew[v] = mls[2 * kDecWaves * kH + v * kH + h];
     M = fmaxf(M, mw[v]);
   }
-  float sc[kDecWaves], Ltot = 0.f;
+  float sc[kDecWaves], Ltot = 0.f, Etot = 0.f;
 #pragma unroll
   for (int v = 0; v < kDecWaves; ++v) {
     sc[v] = mw[v] == -INFINITY ? 0.f : exp2f(mw[v] - M);
     Ltot += sc[v] * lw[v];
+    Etot += sc[v] * ew[v];
   }
   const float inv = Ltot > 0.f ? 1.f / Ltot : 0.f;
   const int c0 = 4 * n;
@@ -589,7 +597,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
       o[4 * i + 3] += sc[v] * t.w;
     }
   }
-  const float lse2 = Ltot > 0.f ? M + __log2f(Ltot) : -INFINITY;  // log2 domain
+  const float lse2 = Etot > 0.f ? M + __log2f(Etot) : -INFINITY;  // log2 domain
   if (ns <= 1) {
     uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + h * a.o_hs + c0;
 #pragma unroll

@@ -10,15 +10,10 @@
 
 namespace swamla {
 
-#ifndef SWAMLA_PREFILL_QPW
-#define SWAMLA_PREFILL_QPW 1  // prefill queries per wave
-#endif
-#ifndef SWAMLA_PREFILL_WAVES
-#define SWAMLA_PREFILL_WAVES 8  // prefill waves (= query groups) per workgroup
-#endif
-#ifndef SWAMLA_PREFILL_DEPTH
-#define SWAMLA_PREFILL_DEPTH 1  // prefill tiles of loads in flight per wave
-#endif
+constexpr int kPrefillQpw = 1;    // queries per wave
+constexpr int kPrefillWaves = 8;  // waves (= query groups) per workgroup
+constexpr int kPrefillDepth = 1;  // tiles of loads in flight per wave
+constexpr int kPrefillOcc = 1;    // workgroups per CU the registers must allow
 
 // ---------------------------------------------------------------------------
 // Prefill attention (a chunk of T > 1 new tokens per sequence, dense
@@ -26,7 +21,7 @@ namespace swamla {
 // cache positions [0, start_pos[b] + t + 1) (bottom-right).  A block of NW
 // waves takes NW * QPW consecutive query tokens of one sequence, QPW per
 // wave, so each 64-token tile of the cache is loaded once for all of them x
-// 16 heads.  The tile is staged in LDS as in mla_decode_mfma (each wave loads
+// 16 heads.  The tile is staged in LDS (each wave loads
 // 64 / NW of its tokens as whole lines); every wave then scores all 64 tokens for its own
 // queries (S^T = K . Q^T: each K operand read from LDS feeds QPW MFMAs),
 // keeps its own online softmax per (query, head) and accumulates O^T for all
@@ -37,13 +32,10 @@ namespace swamla {
 // directly.  Built with NW = 8 waves of one query each (QPW = 1) and one tile
 // of loads in flight: 178 VGPRs, two waves per SIMD.
 // ---------------------------------------------------------------------------
-#ifndef SWAMLA_PREFILL_OCC
-#define SWAMLA_PREFILL_OCC 1  // prefill workgroups per CU the registers must allow
-#endif
 // One wave's share of a prefill tile: RPL rows of 8 tokens (lane: token l%8,
 // 16 bytes at 16(l/8) of each 128-byte segment), plus the rows' e4m3 scales.
 // Latent rows of R_pad = 64 NB channels are NB segments (bf16) or ceil(NB / 2)
-// (e4m3; for odd NB the last one is half a row, as in mla_decode_mfma).
+// (e4m3; for odd NB the last one is half a row).
 template <int C_DT, int RPL, int NB>
 struct PTile {
   uint4 c[RPL * (C_DT == 2 ? (NB + 1) / 2 : NB)];
@@ -52,7 +44,7 @@ struct PTile {
 };
 
 template <int C_DT, int DEPTH, int QPW, int NW, int NB>
-__global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(DecodeArgs a) {
+__global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeArgs a) {
   constexpr int TPW = kTileTok / NW;  // tokens each wave loads per tile
   constexpr int RPL = TPW / 8;        // ... rows of 8 tokens per lane
   constexpr int SEG = C_DT == 2 ? (NB + 1) / 2 : NB;  // 128-byte latent segments per row
@@ -108,7 +100,7 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
     }
   };
 
-  // ---- Q^T operands of this wave's queries (as in mla_decode_mfma).
+  // ---- Q^T operands of this wave's queries (lane: head n, 8 channels at 32 kb + 8 g).
   PTile<C_DT, RPL, NB> kt[DEPTH];
   bf16x8_t qb[QPW][2 * NB + 2];
 #pragma unroll
@@ -249,19 +241,22 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
       mt = wave_max_rows(mt);  // this query's tile maximum for head n
       if (__any(mt > m_run[qi] + kLazy)) {
         const float m_new = fmaxf(m_run[qi], mt);
-        const float alpha = exp2f(m_run[qi] - m_new);  // m_new is finite: tile 0 holds token 0
+        const float alpha = exp2f(m_run[qi] - m_new);  // m_new is finite: mt is
         m_run[qi] = m_new;
         l_part[qi] *= alpha;
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) oacc[qi][mb] = oacc[qi][mb] * alpha;
       }
       // bf16 weights (fp8: times the token's scale) in the PV operand order.
+      // A query with no valid token yet (m_run still -inf: only a negative
+      // start position gives one) takes weight 0 for every token, not NaN.
+      const float mref = m_run[qi] == -INFINITY ? 0.f : m_run[qi];
       uint2 pw[4];
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         float pr[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pr[i] = exp2f(x[qi][tb][i] - m_run[qi]);
+        for (int i = 0; i < 4; ++i) pr[i] = exp2f(x[qi][tb][i] - mref);
         const uint32_t w01 = pack_bf16x2(pr[0], pr[1]), w23 = pack_bf16x2(pr[2], pr[3]);
         l_part[qi] += (u2f(w01 << 16) + u2f(w01 & 0xFFFF0000u)) + (u2f(w23 << 16) + u2f(w23 & 0xFFFF0000u));
         if constexpr (C_DT == 2) {
@@ -322,12 +317,11 @@ __global__ __launch_bounds__(NW * 64, SWAMLA_PREFILL_OCC) void mla_prefill_mfma(
   }
 }
 
-constexpr int kPrefillDepth = SWAMLA_PREFILL_DEPTH;
 
 int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
   const int T = a.ad.T;
-  constexpr int kQpw = SWAMLA_PREFILL_QPW, kNw = SWAMLA_PREFILL_WAVES;
+  constexpr int kQpw = kPrefillQpw, kNw = kPrefillWaves;
   const dim3 grid((T + kNw * kQpw - 1) / (kNw * kQpw), a.n_rows / T), block(kNw * 64);
   // Each wave accumulates all R_pad output channels of its query: built for
   // R_pad <= 256 (larger ranks take the per-row decode path).

@@ -30,9 +30,15 @@ Differences from the reference, all deliberate:
   * ``clear_cache()`` also leaves inference mode, so the next
     ``set_inference_mode(True)`` reallocates (the reference leaves None
     caches behind and its next forward fails);
-  * the training / autograd path, ``mask``, ``position_ids`` and
-    ``cu_seqlens`` backends and ``attn_impl="naive"`` are not part of this
-    path and raise ``NotImplementedError``.
+  * ``mask``: the additive causal mask SWAMLAModel builds for a prompt at
+    start_pos 0 is accepted (it equals the causal attention the kernels
+    run); any other mask raises ``NotImplementedError``;
+  * positions outside the cache raise: at once when known on the host (int
+    or CPU tensor ``start_pos``), else from the kernels' error flag at the
+    next eager call or ``check_cache_errors()``;
+  * the training / autograd path, ``position_ids`` and ``cu_seqlens``
+    backends and ``attn_impl="naive"`` are not part of this path and raise
+    ``NotImplementedError``.
 """
 from __future__ import annotations
 
@@ -114,6 +120,12 @@ class MLA(nn.Module):
         self._padded_w = {}  # name -> (key, zero-padded copy to R_pad): kv_norm, wkv_a, W_uv
         self._workspace: Optional[DecodeWorkspace] = None
         self._num_cus: Optional[int] = None
+        # Out-of-range appends: the kernels skip a token whose cache position
+        # or RoPE row is outside the tables and set this device flag; an eager
+        # call reads it back asynchronously (pinned copy + event) and the next
+        # eager call raises, as would mla.py:413's slice assignment.
+        self._err: Optional[list] = None  # [device flag int32[1], pinned host copy, event or None]
+        self._mask_ok = None  # (key, tensor) of the last mask verified as the prompt's causal mask
         # Split-KV plan of decode launches: "auto" balances the rows' splits
         # over the CUs on the device when positions come as a tensor (ragged
         # batches), "static" always cuts each row by its own length (the plan
@@ -193,6 +205,58 @@ class MLA(nn.Module):
                 moved = fn(scale)
                 self._buffers["kv_scale"] = scale.to(device=moved.device)
         return out
+
+    # ------------------------------------------------------------ errors
+    def _err_flag(self, device) -> Optional[torch.Tensor]:
+        if self._err is None or self._err[0].device != device:
+            if self._capturing():  # created by an eager call only (a captured zero-fill would rerun)
+                return None
+            flag = torch.zeros(1, dtype=torch.int32, device=device)
+            self._err = [flag, torch.zeros(1, dtype=torch.int32, pin_memory=True), None]
+        return self._err[0]
+
+    @staticmethod
+    def _capturing() -> bool:
+        return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+    def _raise_cache_error(self) -> None:
+        flag, host, _ = self._err
+        flag.zero_()
+        host.zero_()
+        self._err[2] = None
+        raise RuntimeError(
+            "an earlier call appended a token outside the latent cache or the RoPE table "
+            "(start_pos + seqlen > max_seq_len, a negative start_pos, or a batch row past max_batch_size); "
+            "those tokens were not written (mla.py:413 raises for the same input)")
+
+    def _poll_cache_errors(self) -> None:
+        """Raise for a flag an earlier eager call left set, if its read-back
+        has landed (no synchronisation; skipped under graph capture)."""
+        if self._err is None or self._capturing():
+            return
+        ev = self._err[2]
+        if ev is not None and ev.query() and int(self._err[1][0]) != 0:
+            self._raise_cache_error()
+
+    def _read_back_cache_errors(self) -> None:
+        if self._err is None or self._capturing():
+            return
+        flag, host, _ = self._err
+        host.copy_(flag, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._err[2] = ev
+
+    def check_cache_errors(self) -> None:
+        """Synchronising check: raise RuntimeError if any append since the
+        last check skipped an out-of-range token (including appends replayed
+        from a captured HIP graph), and clear the flag."""
+        if self._err is None:
+            return
+        if int(self._err[0].item()) != 0:
+            self._raise_cache_error()
+        self._err[1].zero_()
+        self._err[2] = None
 
     def latent_cache(self) -> LatentCache:
         """The module's cache buffers as a kernel-level ``LatentCache``."""
@@ -405,8 +469,12 @@ class MLA(nn.Module):
         in the reference's RoPE call (positional_encoding.py:30-34)."""
         if self.training and self.inference_mode:  # mla.py:274-275
             self.set_inference_mode(False)
-        if mask is not None or position_ids is not None or cu_seqlens is not None:
-            raise NotImplementedError("mask / position_ids / cu_seqlens backends are not part of this path")
+        if position_ids is not None or cu_seqlens is not None:
+            raise NotImplementedError("position_ids / cu_seqlens backends are not part of this path")
+        if mask is not None and not self._is_causal_prompt_mask(mask, x.size(1), start_pos):
+            raise NotImplementedError(
+                "only the additive causal mask of a prompt at start_pos 0 (swa_mla_model.py:384-387) is "
+                "supported; other masks are not part of this path")
         if self.attn_impl != "absorb":
             raise NotImplementedError(f"attn_impl={self.attn_impl!r} is not built")
         if torch.is_grad_enabled() and x.requires_grad:
@@ -414,8 +482,35 @@ class MLA(nn.Module):
         if x.device.type != "cuda":
             raise RuntimeError("swamla_amd.MLA runs on the GPU only (no CPU fallback)")
         self._check_geometry()
+        self._poll_cache_errors()
         with torch.no_grad():
-            return self._forward_kernels(x, start_pos)
+            out = self._forward_kernels(x, start_pos)
+        self._read_back_cache_errors()
+        return out
+
+    def _is_causal_prompt_mask(self, mask: torch.Tensor, T: int, start_pos) -> bool:
+        """True for the mask SWAMLAModel passes with a prompt
+        (swa_mla_model.py:207-211, :384-387: triu(full(-inf), 1)[:T, :T],
+        additive) when the call starts at position 0, where the reference's
+        SDPA with that mask (mla.py:473-485) equals the causal attention the
+        kernels run.  Verified once per mask tensor (a device comparison,
+        so not under graph capture)."""
+        if isinstance(start_pos, torch.Tensor) or int(start_pos) != 0:
+            return False
+        if mask.dim() != 2 or tuple(mask.shape) != (T, T) or not mask.is_floating_point():
+            return False
+        # the verified tensor is kept alive with its key, so an equal pointer is
+        # the same storage and an equal version means it was not written since
+        key = (mask.data_ptr(), mask.device, mask.dtype, tuple(mask.stride()), mask._version, T)
+        if self._mask_ok is not None and self._mask_ok[0] == key:
+            return True
+        if self._capturing():
+            return False
+        want = torch.full((T, T), float("-inf"), dtype=mask.dtype, device=mask.device).triu(1)
+        if not torch.equal(mask, want):
+            return False
+        self._mask_ok = (key, mask)
+        return True
 
     def prefill_cache(self, x: torch.Tensor, start_pos: Union[int, torch.Tensor] = 0) -> None:
         """Append path only (wkv_a GEMM + fused append kernel), no attention:
@@ -427,6 +522,7 @@ class MLA(nn.Module):
             raise RuntimeError("swamla_amd.MLA runs on the GPU only (no CPU fallback)")
         self._check_geometry()
         B, T, _ = x.size()
+        self._poll_cache_errors()
         cache = self.latent_cache()
         sp = self._start_positions(B, T, start_pos, cache, x.device)
         with torch.no_grad():
@@ -434,7 +530,9 @@ class MLA(nn.Module):
             cos, sin = self.rope.half_tables()
             ln_w, ln_b = self.kv_norm_params()
             kernels.append(kv, cache, ln_w, ln_b, self.kv_norm.eps, cos, sin,
-                           start_pos=sp, tokens_per_seq=T, rope_abs=self.rope_positions == "absolute")
+                           start_pos=sp, tokens_per_seq=T, rope_abs=self.rope_positions == "absolute",
+                           err_flag=self._err_flag(x.device))
+        self._read_back_cache_errors()
 
     def input_projections(self, x: torch.Tensor, need_q: bool = True) -> tuple[Optional[torch.Tensor], torch.Tensor]:
         """(q [B*T, H, 192] or None, kv [B*T, R_pad + P]): the wkv_a rows
@@ -468,9 +566,15 @@ class MLA(nn.Module):
         if B > cache.ckv.shape[0]:
             raise ValueError(f"batch {B} exceeds max_batch_size {cache.ckv.shape[0]}")
         if isinstance(start_pos, torch.Tensor):
+            if start_pos.numel() != B:
+                raise ValueError(f"start_pos tensor has {start_pos.numel()} entries for batch {B}")
+            if start_pos.device.type == "cpu":  # values known on the host: check them now
+                lo_, hi_ = int(start_pos.min()), int(start_pos.max())
+                if lo_ < 0 or hi_ + T > cache.ckv.shape[1]:
+                    raise ValueError(f"start_pos in [{lo_}, {hi_}] + seqlen {T} is outside max_seq_len "
+                                     f"{cache.ckv.shape[1]}")
+            # device values are checked by the kernels (the module's error flag)
             sp = start_pos.to(device=device, dtype=torch.int32).reshape(-1)
-            if sp.numel() != B:
-                raise ValueError(f"start_pos tensor has {sp.numel()} entries for batch {B}")
             return sp if sp.is_contiguous() else sp.contiguous()
         start_pos = int(start_pos)
         if start_pos < 0 or start_pos + T > cache.ckv.shape[1]:
@@ -490,6 +594,11 @@ class MLA(nn.Module):
             max_len = (int(start_pos) + T) if not isinstance(start_pos, torch.Tensor) else cache.ckv.shape[1]
         else:
             # No cache (mla.py:419-423): attend over this call's tokens only.
+            if T > self.rope.cos_cached.shape[2]:
+                # the reference grows its table in fp32 here (positional_encoding.py:44-46, :64-86), which
+                # also turns its rotation into fp32 arithmetic; this path does not reproduce that
+                raise ValueError(f"seqlen {T} exceeds the RoPE table ({self.rope.cos_cached.shape[2]} positions, "
+                                 f"max_seq_len)")
             cache = LatentCache.allocate(B, T, x.dtype, dev, fp8=self.fp8_cache, rank=R)
             sp = torch.zeros(B, dtype=torch.int32, device=dev)
             max_len = T
@@ -505,9 +614,10 @@ class MLA(nn.Module):
         # append first (their rows attend to each other's new tokens).
         fold_append = fused and T == 1
         ln_w, ln_b = self.kv_norm_params()
+        err = self._err_flag(dev)
         if not fold_append:
             kernels.append(kv, cache, ln_w, ln_b, self.kv_norm.eps, cos, sin,
-                           start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs)
+                           start_pos=sp, tokens_per_seq=T, rope_abs=rope_abs, err_flag=err)
 
         n_splits, min_chunk, balance = self._decode_plan(
             n, max_len, dev, isinstance(start_pos, torch.Tensor) and self.inference_mode, dtype=x.dtype)
@@ -525,7 +635,7 @@ class MLA(nn.Module):
             else:
                 fa = None
                 if fold_append:
-                    fa = kernels.FusedAppend(kv, ln_w, ln_b, self.kv_norm.eps)
+                    fa = kernels.FusedAppend(kv, ln_w, ln_b, self.kv_norm.eps, err_flag=err)
                 kernels.decode_attention(
                     q_abs, q_pe, cos, sin, cache, self.softmax_scale,
                     start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,

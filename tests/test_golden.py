@@ -31,7 +31,8 @@ def build_ref(meta):
 
 
 def test_fixtures_present():
-    assert len(GOLDEN) == 4
+    assert len(GOLDEN) == 6
+    assert sum("masked" in os.path.basename(p) for p in GOLDEN) == 2
 
 
 @pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p) for p in GOLDEN])
@@ -47,8 +48,9 @@ def test_restatement_matches_reference_bitwise(path):
     m.to(dtype)
     pos = 0
     with torch.no_grad():
-        for x, ref_out in zip(blob["inputs"], blob["outputs"]):
-            out = m(x, pos)
+        masks = blob.get("masks") or [None] * len(blob["inputs"])
+        for x, ref_out, mask in zip(blob["inputs"], blob["outputs"], masks):
+            out = m(x, pos, None, mask)
             assert out.dtype == ref_out.dtype
             assert torch.equal(out, ref_out), f"output mismatch at start_pos={pos}"
             pos += x.shape[1]

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+from attn_ref import check_lse
 from oracle import latent_ops as lo
 from swamla_amd import _abi, kernels
 from swamla_amd.kernels import DecodeWorkspace, LatentCache
@@ -162,17 +163,19 @@ def _decode_case(gpu, dtype, fp8, lens, n_splits, min_chunk, row_seq=None, B=Non
     kl = torch.tensor(lens, dtype=torch.int32)
     rp = torch.zeros(rows, dtype=torch.int32) if rope_pos is None else torch.tensor(rope_pos, dtype=torch.int32)
     cos, sin = tables(dtype, max(S, 64), gpu)
+    lse = torch.full((rows, H), float("nan"), device=gpu)
     out = kernels.decode_attention(
         q_abs.to(gpu), q_pe.to(gpu), cos, sin, cache, SCALE, row_seq=rs.to(gpu), kv_len=kl.to(gpu),
-        q_rope_pos=rp.to(gpu), n_splits=n_splits, min_chunk=min_chunk, balance=balance,
+        q_rope_pos=rp.to(gpu), n_splits=n_splits, min_chunk=min_chunk, balance=balance, lse_out=lse,
     )
     torch.cuda.synchronize()
     q_pe_rot = lo.rope_interleaved(q_pe, cos.cpu()[rp.long()][:, None], sin.cpu()[rp.long()][:, None])
-    ref, _ = lo.absorbed_attention_f64(
+    ref, ref_lse = lo.absorbed_attention_f64(
         q_abs[..., :rank], q_pe_rot, cache.ckv.cpu()[..., :rank], kpe, kl, rs, SCALE,
         cache.scale.cpu() if fp8 else None
     )
     close(out[..., :rank], ref, rtol, atol)
+    check_lse(lse, ref_lse)
     assert bool((out[..., rank:].float() == 0).all()), "padding channels of o_lat must be 0"
     return out
 
@@ -256,7 +259,8 @@ def test_decode_constant_latent_rows(gpu):
 
 
 def test_decode_headline_shape(gpu):
-    """Config-2 shape: 32 rows over 4097 cached tokens, graph-style split plan."""
+    """Config-2 shape: 32 rows over 4097 cached tokens, graph-style split
+    plan; o_lat and the log-sum-exp against the fp64 oracle."""
     lens = [4097] * 32
     n_splits, mc = kernels.plan_splits(32, 4097)
     _decode_case(gpu, torch.bfloat16, False, lens, n_splits, mc, seed=11, q_scale=0.5)

@@ -106,9 +106,10 @@ def test_module_matches_reference_fixtures(gpu, path):
     m.set_inference_mode(True)
     pos = 0
     xs = [x.to(gpu) for x in blob["inputs"]]
+    masks = blob.get("masks") or [None] * len(xs)
     with torch.no_grad():
-        for x, ref_out in zip(xs, blob["outputs"]):
-            out = m(x, pos)
+        for x, ref_out, mask in zip(xs, blob["outputs"], masks):
+            out = m(x, pos, None, None if mask is None else mask.to(gpu))
             close(out, ref_out, dtype)
             pos += x.shape[1]
     torch.cuda.synchronize()
@@ -238,3 +239,73 @@ def test_module_any_rank_and_q_lora(gpu, dtype, rank, q_lora, dim):
     torch.cuda.synchronize()
     assert_cache_bits(ours, xs, dtype)
     assert bool((ours.kv_cache[:2, :46, rank:].float() == 0).all())
+
+
+def test_out_of_range_positions_raise(gpu):
+    """Positions outside the cache raise, as mla.py:413's slice assignment
+    does: at once when they are known on the host (int or CPU tensor); for a
+    device tensor the kernels skip the token and flag it, check_cache_errors()
+    raises, and so does the next eager call once the flag has been read back.
+    A no-cache call longer than the RoPE table raises."""
+    say("out-of-range positions")
+    dtype = torch.bfloat16
+    cfg = MLAConfig(n_embd=256, max_batch_size=2, max_seq_len=64)
+    _, ours = make_pair(cfg, 41, dtype, gpu)
+    g = torch.Generator().manual_seed(42)
+    step = torch.randn(2, 1, 256, generator=g).to(dtype).to(gpu)
+    chunk = torch.randn(2, 8, 256, generator=g).to(dtype).to(gpu)
+    with torch.no_grad():
+        with pytest.raises(ValueError):
+            ours(step, 64)
+        with pytest.raises(ValueError):
+            ours(step, torch.tensor([3, 64], dtype=torch.int32))
+        with pytest.raises(ValueError):
+            ours(chunk, torch.tensor([-1, 0], dtype=torch.int32))
+        ours(step, torch.tensor([3, 5], dtype=torch.int32, device=gpu))
+        ours.check_cache_errors()  # in range: nothing flagged
+        # one-token step (append folded into the attention launch)
+        ours(step, torch.tensor([3, 64], dtype=torch.int32, device=gpu))
+        with pytest.raises(RuntimeError):
+            ours.check_cache_errors()
+        ours.check_cache_errors()  # the flag was cleared
+        # multi-token chunk (separate append), negative start
+        out = ours(chunk, torch.tensor([-3, 0], dtype=torch.int32, device=gpu))
+        assert bool(torch.isfinite(out.float()).all())
+        torch.cuda.synchronize()
+        with pytest.raises(RuntimeError):  # the next eager call raises
+            ours(step, torch.tensor([9, 9], dtype=torch.int32, device=gpu))
+        ours.check_cache_errors()
+        ours.set_inference_mode(False)
+        ours(torch.randn(1, 64, 256, generator=g).to(dtype).to(gpu), 0)
+        with pytest.raises(ValueError):
+            ours(torch.randn(1, 65, 256, generator=g).to(dtype).to(gpu), 0)
+
+
+def test_causal_prompt_mask_equals_unmasked(gpu):
+    """SWAMLAModel passes triu(full(-inf), 1)[:T, :T] with every prompt
+    (swa_mla_model.py:207-211, :384-387): accepted at start_pos 0 and
+    bit-identical to mask=None; any other mask (or a start_pos > 0) raises."""
+    say("causal prompt mask")
+    dtype = torch.bfloat16
+    cfg = MLAConfig(n_embd=512, max_batch_size=2, max_seq_len=96)
+    g = torch.Generator().manual_seed(43)
+    x = torch.randn(2, 40, 512, generator=g).to(dtype).to(gpu)
+    step = torch.randn(2, 1, 512, generator=g).to(dtype).to(gpu)
+    mask = torch.triu(torch.full((40, 40), float("-inf")), diagonal=1).to(gpu)
+    outs = []
+    for use_mask in (False, True):
+        _, ours = make_pair(cfg, 44, dtype, gpu)
+        with torch.no_grad():
+            outs.append((ours(x, 0, None, mask if use_mask else None), ours(step, 40)))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    _, ours = make_pair(cfg, 44, dtype, gpu)
+    with torch.no_grad():
+        bad = mask.clone()
+        bad[5, 3] = float("-inf")
+        with pytest.raises(NotImplementedError):
+            ours(x, 0, None, bad)
+        with pytest.raises(NotImplementedError):
+            ours(x[:, :8], 40, None, mask[:8, :8])
+        ours.set_inference_mode(False)  # no cache: the call's own tokens, causal
+        ref = ours(x, 0)
+        assert torch.equal(ours(x, 0, None, mask), ref)

@@ -145,6 +145,25 @@ def test_prefill_edges_clamp_negative_and_past_batch(gpu):
     assert bool((out[T:].float() == 0).all())  # negative start and past-batch rows
 
 
+def test_prefill_partly_empty_query_group_has_no_nan(gpu):
+    """A start position of -3: the first three queries of the sequence see no
+    token while the others in their workgroup do; they come out zero (not
+    NaN), as the decode kernel gives."""
+    gen = torch.Generator(device=gpu).manual_seed(8)
+    Bc, S, T = 2, 128, 12
+    cache = make_cache(Bc, S, False, gen, gpu)
+    cos, sin = tables(S, gpu)
+    sp = torch.tensor([-3, 10], dtype=torch.int32, device=gpu)
+    rows = Bc * T
+    q_abs = (0.3 * torch.randn(rows, H, R, generator=gen, device=gpu)).to(torch.bfloat16)
+    q_pe = (0.3 * torch.randn(rows, H, P, generator=gen, device=gpu)).to(torch.bfloat16)
+    out = kernels.prefill_attention(q_abs, q_pe, cos, sin, cache, SCALE, start_pos=sp, rows_per_seq=T)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all())
+    assert bool((out[:3].float() == 0).all())
+    check(out, reference(q_abs, q_pe, cos, sin, cache, sp.cpu(), T, False))
+
+
 def test_module_prefill_chunk_uses_prefill_kernel_and_matches_row_path(gpu, monkeypatch):
     """A 2 x 512-token bf16 prefill through MLA.forward runs mla_prefill_attn
     and agrees with the same module forced onto the per-row decode path."""
