@@ -335,51 +335,14 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
     }
   };
 
-  // The first sub-tile goes out right behind the query loads; the rest of the
-  // ring follows once the query has landed (below), so the data every wave
-  // needs first sits at the front of the memory queues rather than behind
-  // everyone's whole ring.
-  // A wave without sub-tiles issues one as well (past the split's end, so it
-  // re-reads the split's last row): the wait below then holds for every wave.
-  issue(0);
+  // The ring fills at once: the first sub-tile right behind the query loads,
+  // then the next ones.  Every wave issues all NBUF - 1 of them, also past its
+  // own sub-tiles (they then re-read the split's last row, in bounds), so one
+  // fixed wait below covers the loads issued before them.
+#pragma unroll
+  for (int k = 0; k < NBUF - 1; ++k) issue(k);
 
-  // Everything issued before the first sub-tile (query, RoPE row, fused
-  // inputs) has landed.
-  wait_vm<G::kVm>();
-#pragma unroll
-  for (int s = 0; s < 2 * NB; ++s) vm_release(qraw[s]);
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    vm_release(praw[s]);
-    vm_release(cr[s]);
-    vm_release(sr[s]);
-  }
-  if constexpr (FUSE) fused_release(fin);
-
-  // ---- Q^T registers: latent channels >= R zeroed, q_pe rotated (per-op rounded)
-  bf16x8_t qb[2 * NB + 2];
-#pragma unroll
-  for (int s = 0; s < 2 * NB; ++s)
-    qb[s] = as_bf16x8(mask_bf16x8(make_uint4(qraw[s][0], qraw[s][1], qraw[s][2], qraw[s][3]), a.R - (32 * s + 8 * g)));
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    uint32_t wv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t cj = (j & 1) ? (cr[s][j >> 1] >> 16) : (cr[s][j >> 1] & 0xFFFF);
-      const uint32_t sj = (j & 1) ? (sr[s][j >> 1] >> 16) : (sr[s][j >> 1] & 0xFFFF);
-      float o1, o2;
-      rope_pair<1>(bf16_to_f32(praw[s][j] & 0xFFFF), bf16_to_f32(praw[s][j] >> 16), bf16_to_f32(cj), bf16_to_f32(sj),
-                   o1, o2);
-      wv[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
-    }
-    qb[2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
-  }
-
-#pragma unroll
-  for (int k = 1; k < NBUF - 1; ++k)
-    if (k < my_n) issue(k);
-
+  bf16x8_t qb[2 * NB + 2];  // Q^T, set once the query has landed
   f32x4_t oacc[4 * NB];
 #pragma unroll
   for (int i = 0; i < 4 * NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -404,12 +367,16 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   for (int m = 0; m < 4; ++m)
     pv_m[m] = pv_row * (2 * RP) + 8 * (n & 1) + 16 * ((((n & 3) >> 1)) ^ (pv_sw & 1)) + 32 * (m ^ (pv_sw >> 1));
 
-  auto process = [&](int k) {
+  // process(k, dry): sub-tile k of this wave.  A dry pass (k = 0) runs the
+  // loop body on whatever buffer 0 holds and its results are thrown away: it
+  // brings the body into the instruction cache while the first tiles are on
+  // their way (a cold first pass costs over a microsecond).
+  auto process = [&](int k, bool dry) {
     const int tb = t0 + kSubTok * sub_of(k);
     lds_u8* const sb = wave_lds + (k % NBUF) * G::kSub;
     lds_u8* const pe = sb + G::kLat;
     if constexpr (FUSE) {
-      if (fa_wave && k == fa_k) {
+      if (fa_wave && k == fa_k && !dry) {
         // The new token replaces the cache row the stream loaded (this wave's
         // own buffer, after its loads landed).
         if constexpr (C_DT == 2) {
@@ -524,6 +491,38 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
     }
   };
 
+  // Everything issued before the first sub-tile (query, RoPE row, fused
+  // inputs) has landed; the ring's sub-tiles may still be in flight.
+  wait_vm<(NBUF - 1) * G::kVm>();
+#pragma unroll
+  for (int s = 0; s < 2 * NB; ++s) vm_release(qraw[s]);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    vm_release(praw[s]);
+    vm_release(cr[s]);
+    vm_release(sr[s]);
+  }
+  if constexpr (FUSE) fused_release(fin);
+
+  // ---- Q^T registers: latent channels >= R zeroed, q_pe rotated (per-op rounded)
+#pragma unroll
+  for (int s = 0; s < 2 * NB; ++s)
+    qb[s] = as_bf16x8(mask_bf16x8(make_uint4(qraw[s][0], qraw[s][1], qraw[s][2], qraw[s][3]), a.R - (32 * s + 8 * g)));
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    uint32_t wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t cj = (j & 1) ? (cr[s][j >> 1] >> 16) : (cr[s][j >> 1] & 0xFFFF);
+      const uint32_t sj = (j & 1) ? (sr[s][j >> 1] >> 16) : (sr[s][j >> 1] & 0xFFFF);
+      float o1, o2;
+      rope_pair<1>(bf16_to_f32(praw[s][j] & 0xFFFF), bf16_to_f32(praw[s][j] >> 16), bf16_to_f32(cj), bf16_to_f32(sj),
+                   o1, o2);
+      wv[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+    }
+    qb[2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
+  }
+
   // The new token's cache row, computed while the first tiles stream in (its
   // inputs were loaded ahead of them).
   if constexpr (FUSE)
@@ -531,10 +530,23 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
       ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, lane, wave_lds + (NBUF - 1) * G::kSub);
     }
 
-  for (int k = 0; k < my_n; ++k) {  // uniform
-    if (k + NBUF - 1 < my_n) issue(k + NBUF - 1);
-    wait_subtiles<G::kVm, NBUF>(min(NBUF - 1, my_n - 1 - k));
-    process(k);
+  // k = -1 is the dry pass: the loop body's first run, on buffer 0 while
+  // its data may still be arriving, with the results discarded.
+  for (int k = -1; k < my_n; ++k) {  // uniform
+    const bool dry = k < 0;
+    const int kk = dry ? 0 : k;
+    if (!dry) {
+      if (kk + NBUF - 1 < my_n) issue(kk + NBUF - 1);
+      wait_subtiles<G::kVm, NBUF>(min(NBUF - 1, my_n - 1 - kk));
+    }
+    process(kk, dry);
+    if (dry) {
+#pragma unroll
+      for (int i = 0; i < 4 * NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      m_run = -INFINITY;
+      l_part = 0.f;
+      e_part = 0.f;
+    }
   }
   if constexpr (FUSE)
     if (fa_wave) fused_store<C_DT, NB>(a.fa, static_cast<int64_t>(fa_a.b) * a.fa.cache_s + fa_a.pos, ftok, lane);
@@ -610,13 +622,15 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
     if (a.lse_out && n == 0) a.lse_out[static_cast<int64_t>(r) * kH + h] = lse2 * kLn2;
     return;
   }
+  // partials: non-temporal stores (every workgroup writes at its end, and the
+  // merge reads them in the next launch, from another XCD's view of memory)
   const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * kH + h;
   float* op = a.o_part + pidx * RP + c0;
 #pragma unroll
   for (int i = 0; i < NB; ++i)
-    *reinterpret_cast<float4*>(op + 64 * i) =
-        make_float4(o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv);
-  if (n == 0) a.lse_part[pidx] = lse2 * kLn2;
+    __builtin_nontemporal_store(f32x4_t{o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv},
+                                reinterpret_cast<f32x4_t*>(op + 64 * i));
+  if (n == 0) __builtin_nontemporal_store(lse2 * kLn2, a.lse_part + pidx);
 }
 
 // ===========================================================================
