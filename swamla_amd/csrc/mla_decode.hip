@@ -76,14 +76,15 @@ struct DecGeo {
   static constexpr int kCap = 3;                                              // sub-tiles in flight, at most
   static constexpr int NBUF = cmin(cmin(kCap + 1, (kLdsMax / kDecWaves - kStage) / kSub), 63 / kVm + 1);
   static constexpr int kWave = NBUF * kSub + kStage;  // LDS bytes per wave
-  // epilogue: per wave, per head a row of RP fp32 (+4 pad), then max / sum
+  // epilogue: each wave stashes, in its own ring, per head a row of RP fp32
+  // (+4 pad) and then its max / l / e per head
   static constexpr int kCombRow = RP + 4;
-  static constexpr int kComb = kDecWaves * kH * kCombRow * 4;
-  static constexpr int kML = 3 * kDecWaves * kH * 4;
-  static constexpr int kLds = cmax(kDecWaves * kWave, kComb + kML);
+  static constexpr int kStash = (kH * kCombRow + 3 * kH) * 4;
+  static constexpr int kLds = kDecWaves * kWave;
   static_assert(NBUF >= 2, "a sub-tile ring needs two buffers");
   static_assert(ln_stage_bytes<1>() <= kSub, "the fused LayerNorm stages its row in a ring buffer");
   static_assert(kLds <= kLdsMax, "LDS budget");
+  static_assert(kStash <= kWave, "a wave's epilogue stash fits its ring");
 };
 
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt / lgkmcnt not waited for).
@@ -556,21 +557,22 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   l_w += shfl_xor_f32(l_w, 32);
   float e_w = e_part + shfl_xor_f32(e_part, 16);
   e_w += shfl_xor_f32(e_w, 32);
-  wait_vm<0>();      // (a wave without sub-tiles still has its first one in flight)
-  __syncthreads();  // every wave is done with its ring; the LDS is reused below
-  float* const comb = reinterpret_cast<float*>(lds_raw);
-  float* const mls = comb + kDecWaves * kH * G::kCombRow;  // [3][waves][heads]: max, l, e
+  // The wave's ring is free once its own loads have landed: it stashes its
+  // O^T rows and per-head max / l / e there, without waiting for the others.
+  wait_vm<0>();  // (the ring's loads past the wave's own sub-tiles included)
+  auto stash_of = [&](int v) { return reinterpret_cast<float*>(lds_raw + v * G::kWave); };
+  float* const mine = stash_of(w);
   if (g == 0) {
-    mls[w * kH + n] = m_run;
-    mls[kDecWaves * kH + w * kH + n] = l_w;
-    mls[2 * kDecWaves * kH + w * kH + n] = e_w;
+    mine[kH * G::kCombRow + n] = m_run;
+    mine[kH * G::kCombRow + kH + n] = l_w;
+    mine[kH * G::kCombRow + 2 * kH + n] = e_w;
   }
   // lane (n, g) holds O^T[16 mb + 4 g + i][head n]
 #pragma unroll
   for (int mb = 0; mb < 4 * NB; ++mb)
-    *reinterpret_cast<float4*>(comb + (w * kH + n) * G::kCombRow + 16 * mb + 4 * g) =
+    *reinterpret_cast<float4*>(mine + n * G::kCombRow + 16 * mb + 4 * g) =
         make_float4(oacc[mb][0], oacc[mb][1], oacc[mb][2], oacc[mb][3]);
-  __syncthreads();
+  __syncthreads();  // every wave's stash is written
 
   // wave w finishes heads 4w .. 4w + 3: lane -> head 4w + g, channels
   // 64 i + 4 n .. +4 for i < NB (the 16 lanes of a head read and write
@@ -580,9 +582,10 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   float M = -INFINITY;
 #pragma unroll
   for (int v = 0; v < kDecWaves; ++v) {
-    mw[v] = mls[v * kH + h];
-    lw[v] = mls[kDecWaves * kH + v * kH + h];
-    ew[v] = mls[2 * kDecWaves * kH + v * kH + h];
+    const float* ml = stash_of(v) + kH * G::kCombRow;
+    mw[v] = ml[h];
+    lw[v] = ml[kH + h];
+    ew[v] = ml[2 * kH + h];
     M = fmaxf(M, mw[v]);
   }
   float sc[kDecWaves], Ltot = 0.f, Etot = 0.f;
@@ -599,7 +602,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   for (int i = 0; i < 4 * NB; ++i) o[i] = 0.f;
 #pragma unroll
   for (int v = 0; v < kDecWaves; ++v) {
-    const float* src = comb + (v * kH + h) * G::kCombRow + c0;
+    const float* src = stash_of(v) + h * G::kCombRow + c0;
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const float4 t = *reinterpret_cast<const float4*>(src + 64 * i);
