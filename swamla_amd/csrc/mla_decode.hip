@@ -54,11 +54,28 @@ constexpr int kSubTok = 16;   // tokens per wave sub-tile
 constexpr int kDecWaves = 4;  // waves per workgroup
 constexpr int kLdsMax = 160 * 1024;
 
-// Chunk swizzle: 16-byte chunk c of a sub-tile row t lives at c ^ swz(t)
-// (bits 0..2, so a chunk stays inside its 128-byte group).  The operand read
-// of 8 consecutive rows at one chunk hits 8 distinct 16-byte bank groups, and
-// the transposed read of 4 consecutive rows x 32 bytes hits 8 as well.
-__device__ __forceinline__ int swz(int t) { return ((t & 3) << 1) | ((t >> 2) & 1); }
+// Chunk swizzles for gfx950's LDS (64 banks of 4 bytes: a 16-byte-per-lane
+// read serves 16 lanes per cycle from one 256-byte window, an 8-byte read 32
+// lanes).  16-byte chunk c of latent row t (a sub-tile's 16 rows) lives at
+// c ^ swz<NB>(t); rope row t's at c ^ swp(t).  The XOR stays inside aligned
+// groups of kSwG chunks, which divide the row.
+//  * rows of a multiple of 256 bytes (NB even): 16-chunk groups, swz = (2t |
+//    t >> 3) & 15.  The K read of one chunk from all 16 rows hits 16 distinct
+//    slots of a window; the transposed C^T read (4 rows x 32 bytes per 16
+//    lanes) puts rows 0..7 on the 8 even slot pairs, rows 8..15 on the odd.
+//  * rows of an odd multiple of 128 bytes (NB odd; consecutive rows alternate
+//    window halves): 8-chunk groups, swz = ((t & 14) | t >> 3) & 7: each
+//    parity's 8 rows take distinct slots, and the transposed read's rows
+//    distinct slot pairs.
+//  * rope rows (128 bytes): swp = t >> 1 (each parity's rows distinct).
+template <int NB>
+constexpr int kSwG = NB % 2 == 0 ? 16 : 8;
+template <int NB>
+__device__ __forceinline__ int swz(int t) {
+  if constexpr (NB % 2 == 0) return ((t << 1) | (t >> 3)) & 15;
+  else return ((t & 14) | (t >> 3)) & 7;
+}
+__device__ __forceinline__ int swp(int t) { return (t >> 1) & 7; }
 
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
@@ -284,7 +301,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   // Per-lane source offsets within a sub-tile (16 rows from its first token)
   // for each DMA instruction; a sub-tile wholly inside the split then needs one
   // add per instruction.  bf16 rows: lane's 16-byte slot s of row tt holds chunk
-  // s ^ swz(tt); e4m3 code rows are copied as they lie.
+  // s ^ swz(tt) (rope rows: ^ swp(tt)); e4m3 code rows are copied as they lie.
   constexpr int kLatQ = G::kLat / 1024;
   uint32_t lat_off[kLatQ], pe_off[2];
 #pragma unroll
@@ -294,13 +311,13 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
       lat_off[q] = o;
     } else {
       const int tt = o / (2 * RP), sl = (o % (2 * RP)) >> 4;
-      lat_off[q] = tt * (2 * RP) + 16 * (sl ^ swz(tt));
+      lat_off[q] = tt * (2 * RP) + 16 * (sl ^ swz<NB>(tt));
     }
   }
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int tt = 8 * q + (lane >> 3);
-    pe_off[q] = tt * (2 * kP) + 16 * ((lane & 7) ^ swz(tt));
+    pe_off[q] = tt * (2 * kP) + 16 * ((lane & 7) ^ swp(tt));
   }
   constexpr int kLatRow = C_DT == 2 ? RP : 2 * RP;  // bytes of a latent cache row
 
@@ -350,23 +367,26 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   float m_run = -INFINITY, l_part = 0.f, e_part = 0.f;
   FusedTok<C_DT, NB> ftok;
 
-  // Operand addresses within a sub-tile (bytes).  QK (A = K): lane (n, g)
-  // reads row n, chunk (4 s + g) ^ swz(n) = 4 (s ^ b2) + ((g ^ swz(n)) & 3),
-  // b2 = swz(n) >> 2, i.e. +64 s from one base for even s and another for odd
-  // s.  PV (A = C^T, transposed read): lane s = n of group g reads row
-  // 4g + s/4 at channel 16 mb + 4 (s % 4), chunk (2 mb + (s % 4) / 2) ^ swz(row):
-  // with mb = 4 a + m that is a base per m plus 128 a.
-  const int sw_n = swz(n), b2 = sw_n >> 2;
-  const uint32_t qk_lo = n * (2 * RP) + 16 * ((g ^ sw_n) & 3);
-  const uint32_t qk_even = qk_lo + 64 * b2, qk_odd = qk_lo - 64 * b2;
-  const uint32_t pe_lo = n * (2 * kP) + 16 * ((g ^ sw_n) & 3);
-  const uint32_t pe_even = pe_lo + 64 * b2, pe_odd = pe_lo - 64 * b2;
-  const int pv_row = 4 * g + (n >> 2);
-  const int pv_sw = swz(pv_row);
-  uint32_t pv_m[4];
+  // Operand addresses within a sub-tile (bytes), K = kSwG chunks per swizzle
+  // group.  QK (A = K): lane (n, g) reads latent row n, chunk (4 s + g) ^ sw,
+  // sw = swz(n): a base per s % (K / 4) plus 16 K (s / (K / 4)); rope chunk
+  // 4 i + g of row n likewise with swp(n), a base per i.  PV (A = C^T,
+  // transposed read): lane s = n of group g reads row 4g + s/4 at channel
+  // 16 mb + 4 (s % 4), chunk (2 mb + (s % 4) / 2) ^ swz(row): a base per
+  // mb % (K / 2) plus 16 K (mb / (K / 2)).
+  constexpr int kGrp = kSwG<NB>, kQkB = kGrp / 4, kPvM = kGrp / 2;
+  const int sw_n = swz<NB>(n), sp_n = swp(n);
+  uint32_t qk_b[kQkB], pe_b[2];
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
-    pv_m[m] = pv_row * (2 * RP) + 8 * (n & 1) + 16 * ((((n & 3) >> 1)) ^ (pv_sw & 1)) + 32 * (m ^ (pv_sw >> 1));
+  for (int j = 0; j < kQkB; ++j) qk_b[j] = n * (2 * RP) + 16 * ((4 * j + g) ^ sw_n);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) pe_b[i] = n * (2 * kP) + 16 * ((4 * i + g) ^ sp_n);
+  const int pv_row = 4 * g + (n >> 2);
+  const int pv_sw = swz<NB>(pv_row);
+  uint32_t pv_m[kPvM];
+#pragma unroll
+  for (int m = 0; m < kPvM; ++m)
+    pv_m[m] = pv_row * (2 * RP) + 16 * ((2 * m + ((n & 3) >> 1)) ^ pv_sw) + 8 * (n & 1);
 
   // process(k, dry): sub-tile k of this wave.  A dry pass (k = 0) runs the
   // loop body on whatever buffer 0 holds and its results are thrown away: it
@@ -388,11 +408,11 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
 #pragma unroll
           for (int i = 0; i < NB; ++i) {
             const int ch = NB * lane + i;
-            lds_st<uint16_t>(sb + fa_t * (2 * RP) + 16 * ((ch >> 3) ^ swz(fa_t)) + 2 * (ch & 7), ftok.row[i]);
+            lds_st<uint16_t>(sb + fa_t * (2 * RP) + 16 * ((ch >> 3) ^ swz<NB>(fa_t)) + 2 * (ch & 7), ftok.row[i]);
           }
         }
         if (lane < kP / 2)
-          lds_st<uint32_t>(pe + fa_t * (2 * kP) + 16 * ((lane >> 2) ^ swz(fa_t)) + 4 * (lane & 3), ftok.pe);
+          lds_st<uint32_t>(pe + fa_t * (2 * kP) + 16 * ((lane >> 2) ^ swp(fa_t)) + 4 * (lane & 3), ftok.pe);
       }
     }
     float4 scv = make_float4(1.f, 1.f, 1.f, 1.f);
@@ -412,8 +432,8 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
         const int tt = o / RP, c0 = (o % RP) >> 3;  // chunk of the bf16 row
         const uint2 d0 = e4m3x4_to_bf16x4_hw(cv[q].x), d1 = e4m3x4_to_bf16x4_hw(cv[q].y);
         const uint2 d2 = e4m3x4_to_bf16x4_hw(cv[q].z), d3 = e4m3x4_to_bf16x4_hw(cv[q].w);
-        lds_st16(stage + tt * (2 * RP) + 16 * (c0 ^ swz(tt)), make_uint4(d0.x, d0.y, d1.x, d1.y));
-        lds_st16(stage + tt * (2 * RP) + 16 * ((c0 + 1) ^ swz(tt)), make_uint4(d2.x, d2.y, d3.x, d3.y));
+        lds_st16(stage + tt * (2 * RP) + 16 * (c0 ^ swz<NB>(tt)), make_uint4(d0.x, d0.y, d1.x, d1.y));
+        lds_st16(stage + tt * (2 * RP) + 16 * ((c0 + 1) ^ swz<NB>(tt)), make_uint4(d2.x, d2.y, d3.x, d3.y));
       }
       lat = lds_off(stage);
     }
@@ -424,17 +444,17 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
     u32x4v_t kr[2 * NB + 2];
     static_for<0, 2 * NB>([&](auto sI) {
       constexpr int S = decltype(sI)::value;
-      kr[S] = ds_read16<64 * S>(lat + ((S & 1) ? qk_odd : qk_even));
+      kr[S] = ds_read16<16 * kGrp * (S / kQkB)>(lat + qk_b[S % kQkB]);
     });
-    kr[2 * NB] = ds_read16<0>(pe0 + pe_even);
-    kr[2 * NB + 1] = ds_read16<64>(pe0 + pe_odd);
+    kr[2 * NB] = ds_read16<0>(pe0 + pe_b[0]);
+    kr[2 * NB + 1] = ds_read16<0>(pe0 + pe_b[1]);
     lds_fence();
 #pragma unroll
     for (int i = 0; i < 2 * NB + 2; ++i) tie(kr[i]);
     s16x4_t ctr[4 * NB];
     static_for<0, 4 * NB>([&](auto mI) {
       constexpr int MB = decltype(mI)::value;
-      ctr[MB] = ds_read_tr16<128 * (MB >> 2)>(lat + pv_m[MB & 3]);
+      ctr[MB] = ds_read_tr16<16 * kGrp * (MB / kPvM)>(lat + pv_m[MB % kPvM]);
     });
 
     // S^T = K . Q^T
