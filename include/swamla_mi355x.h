@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SWAMLA_ABI_VERSION 4
+#define SWAMLA_ABI_VERSION 5
 
 enum {
   SWAMLA_OK = 0,
@@ -354,6 +354,27 @@ int mla_merge_project(const float* o_part, const float* lse_part,
                       int32_t min_chunk, const int32_t* plan, const void* w,
                       int64_t w_rs, int64_t w_hs, int32_t Dv, void* y,
                       int64_t y_rs, int64_t y_hs, int32_t dtype, void* stream);
+
+/*
+ * mla_head_product — the per-head products of the prompt pass (prefill-side
+ * absorption): y[m][h][n] = sum_k x[m][h][k] * w[h][n][k] for m < M, h < H,
+ * n < N, k < K; bf16 in / out, fp32 accumulation, one round-to-nearest-even
+ * rounding per output.  Replaces, for prompt-sized inputs, the einsums of
+ * models/mla.py:427 and :433 in their re-associated (absorbed) form:
+ *   q_abs = q_nope . W_uk   x = the wq output [M, H, 192] read in place,
+ *                           w = W_uk^T [H, R_pad, 128], y = q_abs [M, H, R_pad];
+ *   o = o_lat . W_uv^T      x = o_lat [M, H, R_pad], w = W_uv [H, 128, R_pad],
+ *                           y = [M, H * 128], wo's input (mla.py:490-491).
+ * Element strides: x row x_rs / head x_hs, w row (n) w_rs / head w_hs, y row
+ * y_rs / head y_hs; k and n contiguous.
+ * Limits: K a multiple of 64 up to 512, N a multiple of 4, H <= 65535; x and
+ * w 16-byte aligned with strides that are multiples of 8, y 8-byte aligned
+ * with strides that are multiples of 4.
+ */
+int mla_head_product(const void* x, int64_t x_rs, int64_t x_hs,
+                     const void* w, int64_t w_rs, int64_t w_hs, void* y,
+                     int64_t y_rs, int64_t y_hs, int32_t M, int32_t N,
+                     int32_t K, int32_t H, int32_t dtype, void* stream);
 
 /* Split plan used by both kernels, exported so hosts and tests can size the
  * partial buffers: number of splits of a row of length L (0 for L <= 0). */

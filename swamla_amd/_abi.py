@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libswamla_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPE_F32, DTYPE_BF16, DTYPE_FP8 = 0, 1, 2
 ERR_NAMES = {
     -1: "INVALID_ARG",
@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "mla_pack_weight",
     "mla_linear_packed",
     "mla_merge_project",
+    "mla_head_product",
     "mla_host_f32_to_e4m3",
     "mla_host_e4m3_to_f32",
     "mla_host_e4m3x4_to_bf16",
@@ -124,6 +125,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         _P, _P, _P, _I64, _I64, _P, _P, _P, _I32, _I64, _I64, _I32, _I32, _I32, _I32, _I32,
         _P, _P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P,
     ]
+    lib.mla_head_product.restype = ctypes.c_int
+    lib.mla_head_product.argtypes = [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P]
     lib.mla_host_f32_to_e4m3.restype = None
     lib.mla_host_f32_to_e4m3.argtypes = [_P, _P, _I64]
     lib.mla_host_e4m3_to_f32.restype = None

@@ -17,6 +17,7 @@ SOURCES = [
     os.path.join(HERE, "csrc", "mla_decode.hip"),
     os.path.join(HERE, "csrc", "mla_prefill.hip"),
     os.path.join(HERE, "csrc", "mla_linear.hip"),
+    os.path.join(HERE, "csrc", "mla_absorb.hip"),
     os.path.join(HERE, "csrc", "mla_scratch.hip"),
     os.path.join(HERE, "csrc", "mla_abi.cpp"),
 ]

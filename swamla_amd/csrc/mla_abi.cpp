@@ -545,6 +545,35 @@ int mla_merge_project(const float* o_part, const float* lse_part, const void* o_
   return ok();
 }
 
+int mla_head_product(const void* x, int64_t x_rs, int64_t x_hs, const void* w, int64_t w_rs, int64_t w_hs,
+                     void* y, int64_t y_rs, int64_t y_hs, int32_t M, int32_t N, int32_t K, int32_t H,
+                     int32_t dtype, void* stream) {
+  const char* fn = "mla_head_product";
+  if (dtype != SWAMLA_DTYPE_BF16) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: dtype %d not built (bf16 only)", fn, dtype);
+  if (M < 0 || N < 0 || H < 0 || H > 65535)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: M=%d N=%d H=%d out of range", fn, M, N, H);
+  if (K < 64 || K > 512 || K % 64 != 0)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "%s: K=%d (built: multiples of 64 up to 512)", fn, K);
+  if (N % 4 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: N=%d is not a multiple of 4", fn, N);
+  if (M == 0 || N == 0 || H == 0) return ok();
+  if (!x || !w || !y) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null x / w / y", fn);
+  if (x_rs < 0 || x_hs < 0 || w_hs < 0 || y_rs < 0 || y_hs < 0 || w_rs < K)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: negative strides, or a w row stride below K", fn);
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 8) || (x_rs | x_hs | w_rs | w_hs) % 8 != 0 ||
+      (y_rs | y_hs) % 4 != 0)
+    return fail(SWAMLA_ERR_MISALIGNED, "%s: x and w need 16-byte aligned bases and strides that are multiples of "
+                "8, y an 8-byte aligned base and strides that are multiples of 4", fn);
+  int dev = 0, n_cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cus < 1)
+    return hip_fail(fn);
+  swamla::HeadProductArgs a{x, x_rs, x_hs, w, w_rs, w_hs, y, y_rs, y_hs, M, N, K};
+  const int rc = swamla::launch_head_product(a, H, n_cus, static_cast<hipStream_t>(stream));
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for K=%d", fn, K);
+  if (rc != 0) return hip_fail(fn);
+  return ok();
+}
+
 // ---- host-side test hooks: the kernels' bit-level conversions run on the CPU.
 void mla_host_f32_to_e4m3(const float* x, uint8_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = swamla::f32_to_e4m3(x[i]);

@@ -149,9 +149,23 @@ struct PackWeightArgs {
   int N, K;
 };
 
+// Per-head product of the prompt pass: y[m, h, n] = sum_k x[m, h, k] w[h, n, k]
+// (strides in elements; m < M, n < N, k < K).
+struct HeadProductArgs {
+  const void* x;
+  int64_t x_rs, x_hs;
+  const void* w;
+  int64_t w_rs, w_hs;
+  void* y;
+  int64_t y_rs, y_hs;
+  int M, N, K;
+};
+
 int launch_linear(const LinearArgs& a, int batch, hipStream_t s);
 int launch_linear_packed(const PackedLinearArgs& a, hipStream_t s);
 int launch_pack_weight(const PackWeightArgs& a, hipStream_t s);
 int launch_merge_project(const MergeProjectArgs& a, hipStream_t s);
+// -1: no kernel for this K; -2: launch error.
+int launch_head_product(const HeadProductArgs& a, int H, int n_cus, hipStream_t s);
 
 }  // namespace swamla

@@ -548,6 +548,42 @@ def linear(
     return out[0] if squeeze else out
 
 
+def head_product_ok(K: int, N: int) -> bool:
+    """Whether mla_head_product covers a per-head product of this shape."""
+    return 64 <= K <= 512 and K % 64 == 0 and N > 0 and N % 4 == 0
+
+
+def head_product(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[m, h, n] = x[m, h, :] . w[h, n, :] in bf16 with fp32 accumulation
+    and one rounding (mla_head_product), for prompt-sized row counts: the
+    absorbed products q_nope . W_uk and o_lat . W_uv^T that re-associate the
+    einsums of models/mla.py:427 and :433.  x [M, H, K], w [H, N, K] and out
+    [M, H, N] may be strided views with a unit last stride (x read in place,
+    e.g. the q_nope columns of the wq output)."""
+    dev = _need_gpu(x, w, out)
+    if x.dim() != 3 or w.dim() != 3 or x.shape[1] != w.shape[0] or x.shape[2] != w.shape[2]:
+        raise ValueError(f"x {tuple(x.shape)} and w {tuple(w.shape)} must be [M, H, K] / [H, N, K]")
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError("head_product: bf16 inputs only")
+    M, Hx, K = x.shape
+    N = w.shape[1]
+    if out is None:
+        out = torch.empty(M, Hx, N, dtype=x.dtype, device=dev)
+    if tuple(out.shape) != (M, Hx, N) or out.dtype != x.dtype:
+        raise ValueError(f"out must be [{M}, {Hx}, {N}] bf16")
+    for t, name in ((x, "x"), (w, "w"), (out, "out")):
+        if t.stride(2) != 1:
+            raise ValueError(f"{name} needs a unit last stride")
+    _abi.check(
+        _abi.lib().mla_head_product(
+            x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), w.stride(1), w.stride(0),
+            out.data_ptr(), out.stride(0), out.stride(1), M, N, K, Hx,
+            _abi.DTYPE_BF16, _abi.stream_handle(dev),
+        )
+    )
+    return out
+
+
 PACKED_K = (512, 1024, 1536, 2048)
 
 

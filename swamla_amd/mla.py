@@ -324,6 +324,19 @@ class MLA(nn.Module):
             return view()
         return self._padded("w_uv", self.wkv_b.weight, lambda: kernels.pad_rank(view(), R))
 
+    def _w_uk_t(self) -> torch.Tensor:
+        """W_uk^T [H, R_pad, nope] for mla_head_product (its rows are the
+        latent channels; zero beyond kv_lora_rank)."""
+        w = self.wkv_b.weight
+        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        hit = self._padded_w.get("w_uk_t")
+        if hit is None or hit[0] != key:
+            H, Dn, R = self.n_heads, self.qk_nope_head_dim, self.kv_lora_rank
+            w_uk = kernels.pad_rank(w.detach().view(H, -1, R)[:, :Dn], R)  # [H, Dn, R_pad]
+            hit = (key, w_uk.transpose(1, 2).contiguous())
+            self._padded_w["w_uk_t"] = hit
+        return hit[1]
+
     # ------------------------------------------------------------- weights
     def absorbed_weights(self) -> tuple[torch.Tensor, torch.Tensor]:
         """W_uk [H, nope, R_pad] and W_uv^T [H, R_pad, v] from wkv_b
@@ -654,6 +667,27 @@ class MLA(nn.Module):
             else:
                 out = kernels.linear(o, self.wo.weight.detach(), bias=wo_b).view(B, T, self.dim)
             return self.resid_dropout(out)  # mla.py:490-495
+
+        if x.dtype == torch.bfloat16 and kernels.head_product_ok(Dn, self.rank_pad) \
+                and kernels.head_product_ok(self.rank_pad, Dv):
+            # prompt-sized bf16 calls: the absorbed products as per-head MFMA
+            # products that read q and o_lat in place and write q_abs in the
+            # attention kernels' layout and o in wo's (re-associating
+            # mla.py:427, :433)
+            q_abs = kernels.head_product(q[:, :, :Dn], self._w_uk_t())  # [n, H, R_pad]
+            o_lat = torch.empty(n, H, self.rank_pad, dtype=x.dtype, device=dev)
+            if prefill:
+                kernels.prefill_attention(q_abs, q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
+                                          start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, out=o_lat)
+            else:
+                kernels.decode_attention(
+                    q_abs, q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
+                    start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
+                    out=o_lat, workspace=self._workspace_for(n, n_splits, dev), balance=balance,
+                )
+            o = torch.empty(n, H * Dv, dtype=x.dtype, device=dev)
+            kernels.head_product(o_lat, self._w_uv(), out=o.view(n, H, Dv))
+            return self.resid_dropout(self.wo(o.view(B, T, H * Dv)))  # mla.py:490-495
 
         w_uk, w_uv_t = self.absorbed_weights()
         q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]

@@ -36,7 +36,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mla_abi_version() == _abi.ABI_VERSION == 4
+    assert lib.mla_abi_version() == _abi.ABI_VERSION == 5
 
 
 def _append(lib, **kw):
