@@ -6,11 +6,20 @@ parameter names (``wq`` | ``wq_a``/``q_norm``/``wq_b``, ``wkv_a``,
 ``set_inference_mode`` and ``clear_cache`` follow the reference so state
 dicts load unchanged and callers need no edits.
 
-What runs where (per forward):
-  ATen GEMMs   wq / wkv_a / wo and the two per-head absorption products
-               q_abs = q_nope . W_uk   and   o = o_lat . W_uv^T
-  HIP kernels  mla_append (kv_norm + RoPE(k_pe) + e4m3 + scatter) and
-               mla_decode_attn + mla_merge (attention over the latent cache)
+What runs where (per forward, bf16 model):
+  decode-sized calls (<= 128 query rows, the one-token step):
+    mla_linear_packed  x . [W_uk^T wq_nope | wq_pe | wkv_a]^T (q_abs, q_pe, kv)
+    mla_decode_attn_append  append (kv_norm + RoPE(k_pe) + e4m3 + scatter)
+                       folded into the split-KV attention launch (T = 1;
+                       longer chunks run mla_append first)
+    mla_merge_project  split merge + o = o_lat . W_uv^T in wo's layout
+    mla_linear_packed  wo
+  prompt-sized calls:
+    ATen GEMMs         wq / wkv_a / wo
+    mla_head_product   q_abs = q_nope . W_uk and o = o_lat . W_uv^T
+    mla_append, then mla_prefill_attn (or mla_decode_attn + mla_merge)
+  fp32 models use the ATen products and batched absorption around mla_append
+  and the fp32 decode kernel.
 
 Differences from the reference, all deliberate:
   * attention is absorbed: the reference re-projects the whole cache through
