@@ -19,7 +19,9 @@ What runs where (per forward, bf16 model):
     mla_head_product   q_abs = q_nope . W_uk and o = o_lat . W_uv^T
     mla_append, then mla_prefill_attn (or mla_decode_attn + mla_merge)
   fp32 models use the ATen products and batched absorption around mla_append
-  and the fp32 decode kernel.
+  and the fp32 decode kernel.  The attention launches take 16 heads each:
+  other head counts run as ceil(H / 16) launches over zero-padded query heads
+  (the fused decode step is built for 16 heads).
 
 Differences from the reference, all deliberate:
   * attention is absorbed: the reference re-projects the whole cache through
@@ -420,10 +422,11 @@ class MLA(nn.Module):
         return q_abs, q_pe, y[:, H * (R + P):]
 
     def _fused_step_ok(self, x: torch.Tensor, n: int) -> bool:
-        """The decode-step kernels cover bf16 modules with at most 128 query
-        rows, no q low-rank path and 128-aligned model widths."""
+        """The decode-step kernels cover bf16 modules with 16 heads, at most
+        128 query rows, no q low-rank path and 128-aligned model widths."""
         return (
-            self.q_lora_rank == 0
+            self.n_heads == kernels.H
+            and self.q_lora_rank == 0
             and x.dtype == torch.bfloat16
             and self.wq.weight.dtype == torch.bfloat16
             and 0 < n <= kernels.LINEAR_MAX_ROWS
@@ -434,12 +437,12 @@ class MLA(nn.Module):
         )
 
     def _check_geometry(self) -> None:
-        if ((self.n_heads, self.qk_rope_head_dim) != (kernels.H, kernels.P)
+        if (self.n_heads < 1 or self.qk_rope_head_dim != kernels.P
                 or not 1 <= self.kv_lora_rank <= kernels.MAX_RANK):
             raise NotImplementedError(
-                f"kernels are built for n_heads={kernels.H}, kv_lora_rank 1..{kernels.MAX_RANK}, "
-                f"qk_rope_head_dim={kernels.P}; got {self.n_heads}, {self.kv_lora_rank}, "
-                f"{self.qk_rope_head_dim}"
+                f"kernels are built for qk_rope_head_dim={kernels.P} and kv_lora_rank 1..{kernels.MAX_RANK} "
+                f"(any n_heads); got n_heads={self.n_heads}, kv_lora_rank={self.kv_lora_rank}, "
+                f"qk_rope_head_dim={self.qk_rope_head_dim}"
             )
 
     def _split_plan(self, n_rows: int, max_len: int, device, blocks_per_cu: int = 1) -> tuple[int, int]:
@@ -677,40 +680,47 @@ class MLA(nn.Module):
                 out = kernels.linear(o, self.wo.weight.detach(), bias=wo_b).view(B, T, self.dim)
             return self.resid_dropout(out)  # mla.py:490-495
 
-        if x.dtype == torch.bfloat16 and kernels.head_product_ok(Dn, self.rank_pad) \
-                and kernels.head_product_ok(self.rank_pad, Dv):
-            # prompt-sized bf16 calls: the absorbed products as per-head MFMA
-            # products that read q and o_lat in place and write q_abs in the
-            # attention kernels' layout and o in wo's (re-associating
-            # mla.py:427, :433)
-            q_abs = kernels.head_product(q[:, :, :Dn], self._w_uk_t())  # [n, H, R_pad]
-            o_lat = torch.empty(n, H, self.rank_pad, dtype=x.dtype, device=dev)
+        # Other calls: the absorbed products, then attention.  The attention
+        # kernels take 16 heads per launch, so H heads run as ceil(H / 16)
+        # launches over query rows padded with zero heads (whose outputs are
+        # dropped).
+        rp, HK = self.rank_pad, kernels.H
+        Hp = -(-H // HK) * HK
+        # prompt-sized bf16 calls: per-head MFMA products that read q and o_lat
+        # in place and write q_abs in the attention kernels' layout and o in
+        # wo's (re-associating mla.py:427, :433); fp32 modules use ATen's
+        # batched products
+        use_hp = (x.dtype == torch.bfloat16 and kernels.head_product_ok(Dn, rp)
+                  and kernels.head_product_ok(rp, Dv))
+        if Hp == H:
+            q_abs = torch.empty(n, H, rp, dtype=x.dtype, device=dev)
+            q_pe = q[:, :, Dn:]
+        else:
+            q_abs = torch.zeros(n, Hp, rp, dtype=x.dtype, device=dev)
+            q_pe = torch.zeros(n, Hp, self.qk_rope_head_dim, dtype=x.dtype, device=dev)
+            q_pe[:, :H] = q[:, :, Dn:]
+        if use_hp:
+            kernels.head_product(q[:, :, :Dn], self._w_uk_t(), out=q_abs[:, :H])  # [n, H, R_pad]
+        else:
+            w_uk, w_uv_t = self.absorbed_weights()
+            q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]
+            q_abs[:, :H] = torch.bmm(q_nope, w_uk).transpose(0, 1)  # [n, H, R_pad]
+        o_lat = torch.empty(n, Hp, rp, dtype=x.dtype, device=dev)
+        ws = None if prefill else self._workspace_for(n, n_splits, dev)
+        for h0 in range(0, Hp, HK):
+            hs = slice(h0, h0 + HK)
             if prefill:
-                kernels.prefill_attention(q_abs, q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
-                                          start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, out=o_lat)
+                kernels.prefill_attention(q_abs[:, hs], q_pe[:, hs], cos, sin, cache, self.softmax_scale,
+                                          start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, out=o_lat[:, hs])
             else:
                 kernels.decode_attention(
-                    q_abs, q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
+                    q_abs[:, hs], q_pe[:, hs], cos, sin, cache, self.softmax_scale,
                     start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
-                    out=o_lat, workspace=self._workspace_for(n, n_splits, dev), balance=balance,
+                    out=o_lat[:, hs], workspace=ws, balance=balance,
                 )
+        if use_hp:
             o = torch.empty(n, H * Dv, dtype=x.dtype, device=dev)
-            kernels.head_product(o_lat, self._w_uv(), out=o.view(n, H, Dv))
-            return self.resid_dropout(self.wo(o.view(B, T, H * Dv)))  # mla.py:490-495
-
-        w_uk, w_uv_t = self.absorbed_weights()
-        q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]
-        q_abs = torch.bmm(q_nope, w_uk)  # [H, n, R_pad]
-        o_lat = torch.empty(H, n, self.rank_pad, dtype=x.dtype, device=dev)
-        if prefill:
-            kernels.prefill_attention(q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
-                                      start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, out=o_lat.transpose(0, 1))
+            kernels.head_product(o_lat[:, :H], self._w_uv(), out=o.view(n, H, Dv))
         else:
-            kernels.decode_attention(
-                q_abs.transpose(0, 1), q[:, :, Dn:], cos, sin, cache, self.softmax_scale,
-                start_pos=sp, rows_per_seq=T, rope_abs=rope_abs, n_splits=n_splits, min_chunk=min_chunk,
-                out=o_lat.transpose(0, 1), workspace=self._workspace_for(n, n_splits, dev), balance=balance,
-            )
-        o = torch.bmm(o_lat, w_uv_t)  # [H, n, Dv]
-        out = o.transpose(0, 1).reshape(B, T, H * Dv)
-        return self.resid_dropout(self.wo(out))  # mla.py:490-495
+            o = torch.bmm(o_lat[:, :H].transpose(0, 1), w_uv_t).transpose(0, 1).reshape(n, H * Dv)  # [n, H*Dv]
+        return self.resid_dropout(self.wo(o.view(B, T, H * Dv)))  # mla.py:490-495

@@ -241,6 +241,33 @@ def test_module_any_rank_and_q_lora(gpu, dtype, rank, q_lora, dim):
     assert bool((ours.kv_cache[:2, :46, rank:].float() == 0).all())
 
 
+@pytest.mark.parametrize("n_head,dim,nope,rank", [(12, 1024, 128, 256), (32, 1024, 128, 256), (8, 512, 128, 173),
+                                                  (32, 1024, 64, 256)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_module_other_head_counts(gpu, dtype, n_head, dim, nope, rank):
+    """The reference presets' head counts (moe-1b: 12, xl: 32,
+    swa_mla_model.py:618-640; 32 heads of 64 nope channels is the
+    cudnn-compatible layout, :697-698), run as 16-head launches over
+    zero-padded query heads: a 160-token prompt (the prompt-sized products),
+    then decode steps at batch 2, against the reference restatement with the
+    same weights; cache rows bit-exact."""
+    say(f"n_head={n_head} dim={dim} nope={nope} rank={rank} dtype={dtype}")
+    cfg = MLAConfig(n_embd=dim, n_head=n_head, max_batch_size=2, max_seq_len=192, kv_lora_rank=rank,
+                    qk_nope_head_dim=nope)
+    ref, ours = make_pair(cfg, 41 + n_head, dtype, gpu, ln_random=True)
+    g = torch.Generator().manual_seed(42 + n_head)
+    x = torch.randn(2, 160, dim, generator=g).to(dtype)
+    xs = [x.to(gpu)]
+    with torch.no_grad():
+        close(ours(xs[0], 0), ref(x, 0), dtype)
+        for step in range(6):
+            xd = torch.randn(2, 1, dim, generator=g).to(dtype)
+            xs.append(xd.to(gpu))
+            close(ours(xs[-1], 160 + step), ref(xd, 160 + step), dtype)
+    torch.cuda.synchronize()
+    assert_cache_bits(ours, xs, dtype)
+
+
 def test_out_of_range_positions_raise(gpu):
     """Positions outside the cache raise, as mla.py:413's slice assignment
     does: at once when they are known on the host (int or CPU tensor); for a
