@@ -6,6 +6,7 @@ log-sum-exp merge as hand-written HIP kernels behind a C-ABI
 (include/swamla_mi355x.h), driven from PyTorch-ROCm host code.
 """
 from .config import MLAConfig
+from .generate import IncrementalDecoder
 from .kernels import DecodeWorkspace, LatentCache, append, decode_attention, plan_splits
 from .mla import MLA
 from .rope import RoPE, rope_tables
@@ -13,6 +14,7 @@ from .rope import RoPE, rope_tables
 __all__ = [
     "MLA",
     "MLAConfig",
+    "IncrementalDecoder",
     "RoPE",
     "rope_tables",
     "LatentCache",
