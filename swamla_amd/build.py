@@ -47,7 +47,11 @@ def base_flags() -> list[str]:
         "-O3",
         "-std=c++17",
         "-fPIC",
-        # packed fp32 VALU ops are kept out of the generated code
+        # packed fp32 VALU ops are kept out of the generated code (without
+        # this the device compiler emits thousands of v_pk_{add,mul,fma}_f32
+        # in the attention kernels; tests/test_codegen.py checks the built
+        # code objects).  The host pass does not know the feature and warns
+        # that it ignores it; -Xarch_device cannot forward -Xclang options.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(ROOT, "include"),
     ]
