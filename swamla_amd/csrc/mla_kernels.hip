@@ -106,82 +106,6 @@ __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-KV merge of one (row, head) by one wavefront; lane owns 4 channels of
-// each 256-channel chunk of the R_pad-channel rows.
-//   o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M),  M = max_s lse_s
-// Splits are consumed 8 at a time with all their loads in flight, merged
-// online across chunks (the reference moves with each chunk's maximum).
-// ---------------------------------------------------------------------------
-
-// Channels c0 .. c0+3 of one (row, head); lse_out (lane 0 of the first chunk
-// only) receives the merged log-sum-exp.
-template <int DT>
-__device__ __forceinline__ void merge_chunk(const float* __restrict__ o_part, const float* __restrict__ lse_part,
-                                            int64_t base, int c0, int r, int h, int ns, int rp, void* o_lat,
-                                            int64_t o_rs, int64_t o_hs, float* lse_out) {
-  float M = -INFINITY, wsum = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = 0; s0 < ns; s0 += 8) {
-    float ls[8];
-    float4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int s = min(s0 + j, ns - 1);  // in range; duplicates are masked below
-      const int64_t pi = base + static_cast<int64_t>(s) * kH;
-      ls[j] = lse_part[pi];
-      v[j] = *reinterpret_cast<const float4*>(o_part + pi * rp + c0);
-    }
-    float mc = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (s0 + j >= ns) ls[j] = -INFINITY;
-      mc = fmaxf(mc, ls[j]);
-    }
-    const float m_new = fmaxf(M, mc);
-    if (m_new == -INFINITY) continue;  // every split so far empty
-    const float alpha = (M == -INFINITY) ? 0.f : __expf(M - m_new);
-    wsum *= alpha;
-    acc.x *= alpha;
-    acc.y *= alpha;
-    acc.z *= alpha;
-    acc.w *= alpha;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float wgt = (ls[j] == -INFINITY) ? 0.f : __expf(ls[j] - m_new);
-      wsum += wgt;
-      acc.x += wgt * v[j].x;
-      acc.y += wgt * v[j].y;
-      acc.z += wgt * v[j].z;
-      acc.w += wgt * v[j].w;
-    }
-    M = m_new;
-  }
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  if constexpr (DT == 0) {
-    float* op = static_cast<float*>(o_lat) + r * o_rs + h * o_hs;
-    *reinterpret_cast<float4*>(op + c0) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-  } else {
-    uint16_t* op = static_cast<uint16_t*>(o_lat) + r * o_rs + h * o_hs;
-    uint2 pk;
-    pk.x = f32_to_bf16(acc.x * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.y * inv)) << 16);
-    pk.y = f32_to_bf16(acc.z * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.w * inv)) << 16);
-    *reinterpret_cast<uint2*>(op + c0) = pk;
-  }
-  if (lse_out) lse_out[static_cast<int64_t>(r) * kH + h] = M + __logf(wsum);
-}
-
-template <int DT>
-__device__ __forceinline__ void merge_head(const float* __restrict__ o_part, const float* __restrict__ lse_part,
-                                           int r, int h, int ns, int n_splits, int rp, void* o_lat, int64_t o_rs,
-                                           int64_t o_hs, float* lse_out) {
-  const int lane = threadIdx.x & 63;
-  const int64_t base = static_cast<int64_t>(r) * n_splits * kH + h;  // lse index of split 0
-  for (int c0 = 4 * lane; c0 < rp; c0 += 256) merge_chunk<DT>(o_part, lse_part, base, c0, r, h, ns, rp, o_lat,
-                                                              o_rs, o_hs, lse_out && c0 == 0 ? lse_out : nullptr);
-}
-
-
-// ---------------------------------------------------------------------------
 // Kernel 2 (fp32 models): the same maths on the VALU in fp32.  One block of
 // 256 threads per (row, split); 16-token tiles staged in LDS.
 // ---------------------------------------------------------------------------
@@ -311,16 +235,110 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 3: split-KV merge, one wavefront per (row, head).
+// Kernel 3: split-KV merge, one wavefront per (row r, head h):
+//   o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M),  M = max_s lse_s
+// The statistics are wavefront reductions: lane l takes splits l, l + 64, ...,
+// M is the wave max of their log-sum-exps, each lane forms its splits'
+// weights once and their sum is a wave sum.  The weighted sum of the partial
+// rows then runs over the splits in order (lane: 4 channels of each
+// 256-channel chunk; TWO: the padded row, at most 512 channels, spans a
+// second chunk), split s's weight broadcast from lane s % 64 (readlane).
+// The partial rows' loads go out 8 splits at a time.  Latency: the row's
+// length, lane l's log-sum-exp and the first 8 partial rows are all issued
+// before the row's split count is known (slots past the count, up to
+// n_splits - 1, are in the buffers but may hold stale, even non-finite,
+// values: they are dropped by selects, never multiplied in).  An empty split
+// (lse -inf) has weight 0; rows of at most one split were written by the
+// decode kernel itself.
 // ---------------------------------------------------------------------------
-template <int DT>
+template <int DT, bool TWO>
 __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
-  const int h = blockIdx.x, r = blockIdx.y;
-  const int ns = row_splits(clamped_row_len(a.ad, r, a.cache_b, a.cache_s), a.n_splits, a.min_chunk,
-                            a.plan ? *a.plan : 0).ns;
-  if (ns <= 1) return;  // written by the decode kernel
-  merge_head<DT>(a.o_part, a.lse_part, r, h, ns, a.n_splits, 64 * ((a.R + 63) / 64), a.o_lat, a.o_rs, a.o_hs,
-                 a.lse_out);
+  const int h = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
+  const int rp = 64 * ((a.R + 63) / 64);
+  const int64_t base = static_cast<int64_t>(r) * a.n_splits * kH + h;  // (row, split 0, head) slot
+  const int plan = a.plan ? *a.plan : 0;
+  const int L = clamped_row_len(a.ad, r, a.cache_b, a.cache_s);
+  const int last = a.n_splits - 1;
+  const float le = a.lse_part[base + static_cast<int64_t>(min(lane, last)) * kH];
+  const int c0 = 4 * lane, c1 = c0 + 256;
+  const bool on0 = c0 < rp, on1 = c1 < rp;
+  // channels read: a lane past the row re-reads channel 0 (its sums are not stored)
+  const int c0r = on0 ? c0 : 0, c1r = on1 ? c1 : 0;
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 v[8], u[8];
+  auto load_group = [&](int g, int s_max) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float* p = a.o_part + (base + static_cast<int64_t>(min(g + j, s_max)) * kH) * rp;
+      v[j] = *reinterpret_cast<const float4*>(p + c0r);
+      u[j] = z;
+      if constexpr (TWO) u[j] = *reinterpret_cast<const float4*>(p + c1r);
+    }
+  };
+  load_group(0, last);
+  // at most n_splits (a plan word from another launch cannot send the reads
+  // past the row's slots)
+  const int ns = min(row_splits(L, a.n_splits, a.min_chunk, plan).ns, a.n_splits);
+  if (ns <= 1) return;
+
+  auto lse_of = [&](int s) { return s < ns ? a.lse_part[base + static_cast<int64_t>(s) * kH] : -INFINITY; };
+  const float l0 = lane < ns ? le : -INFINITY;
+  float M = l0;
+  for (int s = lane + 64; s < ns; s += 64) M = fmaxf(M, lse_of(s));
+  M = lane_group_max<64>(M);
+  // all splits empty: M = -inf, every weight 0, output 0 and lse -inf
+  const float w0 = l0 == -INFINITY ? 0.f : __expf(l0 - M);
+  float tot = w0;
+  for (int s = lane + 64; s < ns; s += 64) {
+    const float l = lse_of(s);
+    tot += l == -INFINITY ? 0.f : __expf(l - M);
+  }
+  tot = lane_group_sum<64>(tot);
+  const float inv = tot > 0.f ? 1.f / tot : 0.f;
+
+  float4 a0 = z, a1 = z;
+  float wl = w0;  // weight of split (g & ~63) + lane
+  for (int g = 0; g < ns; g += 8) {
+    if (g > 0) {
+      load_group(g, ns - 1);
+      if ((g & 63) == 0) {
+        const float l = lse_of(g + lane);
+        wl = l == -INFINITY ? 0.f : __expf(l - M);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool in = g + j < ns;  // uniform
+      const float wj = u2f(__builtin_amdgcn_readlane(f2u(wl), (g & 63) + j));
+      if (in) {
+        a0.x += wj * v[j].x;
+        a0.y += wj * v[j].y;
+        a0.z += wj * v[j].z;
+        a0.w += wj * v[j].w;
+        if constexpr (TWO) {
+          a1.x += wj * u[j].x;
+          a1.y += wj * u[j].y;
+          a1.z += wj * u[j].z;
+          a1.w += wj * u[j].w;
+        }
+      }
+    }
+  }
+  auto store = [&](int c, const float4& acc) {
+    if constexpr (DT == 0) {
+      float* op = static_cast<float*>(a.o_lat) + r * a.o_rs + h * a.o_hs;
+      *reinterpret_cast<float4*>(op + c) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    } else {
+      uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + h * a.o_hs;
+      uint2 pk;
+      pk.x = f32_to_bf16(acc.x * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.y * inv)) << 16);
+      pk.y = f32_to_bf16(acc.z * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.w * inv)) << 16);
+      *reinterpret_cast<uint2*>(op + c) = pk;
+    }
+  };
+  if (on0) store(c0, a0);
+  if (TWO && on1) store(c1, a1);
+  if (a.lse_out && lane == 0) a.lse_out[static_cast<int64_t>(r) * kH + h] = M + __logf(tot);
 }
 
 }  // namespace swamla
@@ -374,8 +392,11 @@ int decode_f32_blocks_per_cu(int R, int* blocks) {
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s) {
   if (a.n_rows == 0 || a.n_splits <= 1) return 0;
   const dim3 grid(kH, a.n_rows), block(64);
-  if (dt == 1) hipLaunchKernelGGL((mla_merge_kernel<1>), grid, block, 0, s, a);
-  else if (dt == 0) hipLaunchKernelGGL((mla_merge_kernel<0>), grid, block, 0, s, a);
+  const bool two = a.R > 256;  // the padded row spans a second 256-channel chunk
+  if (dt == 1 && two) hipLaunchKernelGGL((mla_merge_kernel<1, true>), grid, block, 0, s, a);
+  else if (dt == 1) hipLaunchKernelGGL((mla_merge_kernel<1, false>), grid, block, 0, s, a);
+  else if (dt == 0 && two) hipLaunchKernelGGL((mla_merge_kernel<0, true>), grid, block, 0, s, a);
+  else if (dt == 0) hipLaunchKernelGGL((mla_merge_kernel<0, false>), grid, block, 0, s, a);
   else return -1;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }

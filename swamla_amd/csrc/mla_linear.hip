@@ -129,8 +129,6 @@ __global__ __launch_bounds__(NW * 64) void mla_linear_kernel(LinearArgs a) {
 // split partials into bf16 rows in LDS (thread t < 32*ROWS: row t/32,
 // channels 8(t%32) + 256k ..+8; one split: the decode kernel's o_lat row),
 // then multiplies: y[r, h, d] = sum_c W_uv[h][d][c] x[r][c].
-// The merge is o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M) with
-// M = max_s lse_s, accumulated over groups of 8 splits in order.
 // ---------------------------------------------------------------------------
 template <int DV, int ROWS, int NB>
 __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs a) {
@@ -154,77 +152,103 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
     for (int s = 0; s < 2 * NB; ++s) wb[j][s] = *reinterpret_cast<const uint4*>(wp + 32 * s);
   }
 
-  // Merge: thread -> (row rr, 8 channels cc per 256-channel chunk); threads
-  // past ROWS rows idle.
-  if (threadIdx.x < ROWS * 32)
-  for (int cc = 8 * (threadIdx.x & 31); cc < R; cc += 256) {
-    const int rr = threadIdx.x >> 5;
+  // Merge: thread -> (row rr, 8 channels cc per 256-channel chunk), one row
+  // per half-wave; threads past ROWS rows idle.
+  if (threadIdx.x < ROWS * 32) {
+    const int rr = threadIdx.x >> 5, cl = threadIdx.x & 31;
+    const bool hi = (threadIdx.x & 32) != 0;  // this row's lanes are 32 hi .. 32 hi + 31
     const int r = r0 + rr;
-    uint4 xv = make_uint4(0, 0, 0, 0);
-    if (r < a.n_rows) {
-      const float* lp = a.lse_part + static_cast<int64_t>(r) * a.n_splits * H + h;
-      const float* op0 = a.o_part + (static_cast<int64_t>(r) * a.n_splits * H + h) * R + cc;
-      // Splits in groups of 8 with every load of a group issued before it is
-      // used; the running maximum moves per group (online log-sum-exp).
-      float ls[8];
-      float4 v[8][2];
-      auto load_group = [&](int s0, int last) {
+    const bool live = r < a.n_rows;  // uniform over the half-wave
+    const float* lp = a.lse_part + static_cast<int64_t>(r) * a.n_splits * H + h;
+    const float* op0 = a.o_part + (static_cast<int64_t>(r) * a.n_splits * H + h) * R;
+    float4 v[8][2];
+    auto load_group = [&](int s0, int last, int cc) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int s = min(s0 + k, last);
-          ls[k] = lp[s * H];
-          const float* op = op0 + static_cast<int64_t>(s) * H * R;
-          v[k][0] = *reinterpret_cast<const float4*>(op);
-          v[k][1] = *reinterpret_cast<const float4*>(op + 4);
-        }
-      };
-      // With n_splits > 1 (the partial buffers are then given, [n_rows,
-      // n_splits, H, R_pad]) the first group goes out before the row's split
-      // count is known; slots past the count may hold stale, even
-      // non-finite, values and are dropped by selects below, never
-      // multiplied in.  With n_splits == 1 the buffers may be null and are
-      // not touched: every row then reads o_lat.
-      const bool early = a.n_splits > 1;  // block-uniform
-      if (early) load_group(0, a.n_splits - 1);
-      const int L = clamped_row_len(a.ad, r, a.cache_b, a.cache_s);
-      // at most n_splits (a plan word from another launch cannot send the
-      // reads past the row's slots)
-      const int ns = min(row_splits(L, a.n_splits, a.min_chunk, a.plan ? *a.plan : 0).ns, a.n_splits);
-      if (ns <= 1) {
-        xv = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.o_lat) + r * a.ol_rs + h * a.ol_hs + cc);
-      } else {
-        float M = -INFINITY, tot = 0.f;
+      for (int k = 0; k < 8; ++k) {
+        const float* op = op0 + static_cast<int64_t>(min(s0 + k, last)) * H * R + cc;
+        v[k][0] = *reinterpret_cast<const float4*>(op);
+        v[k][1] = *reinterpret_cast<const float4*>(op + 4);
+      }
+    };
+    // With n_splits > 1 (the partial buffers are then given, [n_rows,
+    // n_splits, H, R_pad]) the first 8 splits' partial rows and this lane's
+    // split's log-sum-exp go out before the row's split count is known;
+    // slots past the count may hold stale, even non-finite, values and are
+    // dropped by selects below, never multiplied in.  With n_splits == 1 the
+    // buffers may be null and are not touched: every row then reads o_lat.
+    const bool early = a.n_splits > 1;  // block-uniform
+    const int plan = a.plan ? *a.plan : 0;
+    const int L = live ? clamped_row_len(a.ad, r, a.cache_b, a.cache_s) : 0;
+    float l0 = -INFINITY;
+    if (live && early) {
+      l0 = lp[min(cl, a.n_splits - 1) * H];
+      load_group(0, a.n_splits - 1, 8 * cl);
+    }
+    // at most n_splits (a plan word from another launch cannot send the
+    // reads past the row's slots)
+    const int ns = live ? min(row_splits(L, a.n_splits, a.min_chunk, plan).ns, a.n_splits) : 0;
+    if (ns == 1) {
+      for (int cc = 8 * cl; cc < R; cc += 256)
+        *reinterpret_cast<uint4*>(x_lds + rr * kMpXRow + 2 * cc) =
+            *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.o_lat) + r * a.ol_rs + h * a.ol_hs + cc);
+    } else if (ns == 0) {
+      for (int cc = 8 * cl; cc < R; cc += 256)
+        *reinterpret_cast<uint4*>(x_lds + rr * kMpXRow + 2 * cc) = make_uint4(0, 0, 0, 0);
+    } else {
+      // o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M), M = max_s lse_s.
+      // Statistics as half-wave reductions: lane cl takes splits cl, cl + 32,
+      // ..., the max and the weight sum are butterflies over the row's 32
+      // lanes, and each split's weight is formed once, by its lane.
+      if (cl >= ns) l0 = -INFINITY;
+      float M = l0;
+      for (int s = cl + 32; s < ns; s += 32) M = fmaxf(M, lp[s * H]);
+      M = lane_group_max<32>(M);
+      const float w0 = l0 == -INFINITY ? 0.f : __expf(l0 - M);
+      float tot = w0;
+      for (int s = cl + 32; s < ns; s += 32) {
+        const float l = lp[s * H];
+        tot += l == -INFINITY ? 0.f : __expf(l - M);
+      }
+      tot = lane_group_sum<32>(tot);
+      const float inv = tot > 0.f ? 1.f / tot : 0.f;
+      // Weighted sum over the splits in order, 8 at a time; split s's weight
+      // comes from lane s % 32 of the row's half (readlane of both halves,
+      // then a select).  Every lane of the half runs every chunk, so the
+      // lanes read are active.
+      for (int cb = 0; cb < R; cb += 256) {
+        const int cc = cb + 8 * cl;
+        const bool on = cc < R;  // false only in a partial last chunk
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float wl = w0;  // weight of split (s0 & ~31) + cl
         for (int s0 = 0; s0 < ns; s0 += 8) {
-          if (s0 > 0 || !early) load_group(s0, ns - 1);
-          float mg = M;
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            if (s0 + k < ns) mg = fmaxf(mg, ls[k]);
-          const float alpha = (M == -INFINITY) ? 0.f : __expf(M - mg);
-          tot *= alpha;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-          M = mg;
+          if (s0 > 0 || cb > 0) {
+            if (on) load_group(s0, ns - 1, cc);
+            if (s0 > 0 && (s0 & 31) == 0) {
+              const float l = s0 + cl < ns ? lp[(s0 + cl) * H] : -INFINITY;
+              wl = l == -INFINITY ? 0.f : __expf(l - M);
+            }
+          }
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
+            const int j = (s0 & 31) + k;
+            const float w_lo = u2f(__builtin_amdgcn_readlane(f2u(wl), j));
+            const float w_hi = u2f(__builtin_amdgcn_readlane(f2u(wl), 32 + j));
             const bool in = s0 + k < ns;
-            const float ws = (in && ls[k] != -INFINITY) ? __expf(ls[k] - M) : 0.f;
-            tot += ws;
+            const float ws = hi ? w_hi : w_lo;
             const float t[8] = {v[k][0].x, v[k][0].y, v[k][0].z, v[k][0].w, v[k][1].x, v[k][1].y, v[k][1].z, v[k][1].w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[i] = in ? acc[i] + ws * t[i] : acc[i];
           }
         }
-        const float inv = tot > 0.f ? 1.f / tot : 0.f;
-        uint32_t pk[4];
+        if (on) {
+          uint32_t pk[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pk[i] = f32_to_bf16(acc[2 * i] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[2 * i + 1] * inv)) << 16);
-        xv = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+          for (int i = 0; i < 4; ++i)
+            pk[i] = f32_to_bf16(acc[2 * i] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[2 * i + 1] * inv)) << 16);
+          *reinterpret_cast<uint4*>(x_lds + rr * kMpXRow + 2 * cc) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        }
       }
     }
-    *reinterpret_cast<uint4*>(x_lds + rr * kMpXRow + 2 * cc) = xv;
   }
   __syncthreads();
 

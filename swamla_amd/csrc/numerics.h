@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #define SW_HD __host__ __device__ __forceinline__
 
 namespace swamla {
@@ -28,6 +30,42 @@ SW_HD uint16_t f32_to_bf16(float f) {
 }
 
 SW_HD float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Max / sum over each aligned group of W lanes of a wavefront (W = 16, 32
+// or 64), every lane of the group receiving the result.  Butterflies without
+// the LDS crossbar: DPP quad_perm [1,0,3,2] and [2,3,0,1] (lane ^ 1, ^ 2),
+// row_half_mirror (lane i of 8 <-> 7 - i: the other quad) and row_mirror
+// (i of 16 <-> 15 - i: the other half-row), then the gfx950 row swaps: after
+// permlane16_swap(v, v) the pair holds v[l] and v[l ^ 16] in some order,
+// after permlane32_swap v[l] and v[l ^ 32], so max and sum are order-free
+// and every lane of a group ends with the same bits.  All W lanes of a
+// group must be active.
+template <int W, bool MAX>
+__device__ __forceinline__ float lane_group_reduce(float v) {
+  static_assert(W == 16 || W == 32 || W == 64, "lane group width");
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  auto dpp = [](float x, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value,
+                                                                 0xf, 0xf, false));
+  };
+  v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  v = op(v, dpp(v, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  v = op(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+  if constexpr (W >= 32) {
+    const auto p = __builtin_amdgcn_permlane16_swap(f2u(v), f2u(v), false, false);
+    v = op(u2f(p[0]), u2f(p[1]));
+  }
+  if constexpr (W >= 64) {
+    const auto p = __builtin_amdgcn_permlane32_swap(f2u(v), f2u(v), false, false);
+    v = op(u2f(p[0]), u2f(p[1]));
+  }
+  return v;
+}
+template <int W>
+__device__ __forceinline__ float lane_group_max(float v) { return lane_group_reduce<W, true>(v); }
+template <int W>
+__device__ __forceinline__ float lane_group_sum(float v) { return lane_group_reduce<W, false>(v); }
 
 // fp64 -> bf16 with a single rounding: round to fp32 with round-to-odd (no
 // double-rounding hazard because 24 >= 8 + 2 bits), then RNE to bf16.

@@ -204,6 +204,8 @@ def test_decode_split_kv_merge(gpu, dtype, fp8):
     tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else {}
     _decode_case(gpu, dtype, fp8, [1000, 1, 513, 4096], 8, 64, seed=3, **tol)
     _decode_case(gpu, dtype, fp8, [4096, 4096], 64, 64, seed=4, **tol)
+    # more splits than a wavefront's lanes: 100 for the long rows
+    _decode_case(gpu, dtype, fp8, [7000, 6500, 3, 5000], 100, 64, seed=14, **tol)
 
 
 def test_decode_ragged_row_mapping_and_rope(gpu):

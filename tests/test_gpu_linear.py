@@ -92,31 +92,35 @@ def test_linear_rows_beyond_m_untouched(gpu):
     assert_within_ulp(buf[:5], ref_linear(x.cpu(), w.cpu()))
 
 
-@pytest.mark.parametrize("n_splits,min_chunk", [(1, 64), (8, 64), (47, 64)])
-def test_merge_project_equals_merge_then_product(gpu, n_splits, min_chunk):
+@pytest.mark.parametrize("n_splits,min_chunk,R", [(1, 64, 256), (8, 64, 256), (47, 64, 256), (100, 64, 256),
+                                                  (8, 64, 320), (47, 64, 512)])
+def test_merge_project_equals_merge_then_product(gpu, n_splits, min_chunk, R):
     """mla_merge_project == mla_merge followed by the W_uv product, on ragged
-    rows (empty, single-split and multi-split rows in one call)."""
+    rows (empty, single-split and multi-split rows in one call); up to 100
+    splits per row (more than the 32 lanes that hold a row's statistics) and
+    latent widths past one 256-channel chunk."""
     from swamla_amd.kernels import DecodeWorkspace, LatentCache
     from swamla_amd.rope import rope_tables
 
-    say(f"merge_project n_splits={n_splits}")
-    g = torch.Generator().manual_seed(20 + n_splits)
-    B, S, H, R = 5, 3000, 16, 256
+    say(f"merge_project n_splits={n_splits} R={R}")
+    g = torch.Generator().manual_seed(20 + n_splits + R)
+    B, H = 5, 16
+    S = 7000 if n_splits > 64 else 3000
     dt = torch.bfloat16
     cache = LatentCache(torch.randn(B, S, R, generator=g).to(dt).to(gpu),
-                        torch.randn(B, S, 64, generator=g).to(dt).to(gpu))
+                        torch.randn(B, S, 64, generator=g).to(dt).to(gpu), rank=R)
     cos, sin = rope_tables(64, S)
     cos = cos.to(dt)[0, 0, :, :32].contiguous().to(gpu)
     sin = sin.to(dt)[0, 0, :, :32].contiguous().to(gpu)
     rows = 11
     row_seq = torch.tensor([0, 1, 2, 3, 4, 0, 1, 2, 3, 4, 1], dtype=torch.int32, device=gpu)
-    kv_len = torch.tensor([2999, 1, 64, 65, 0, 777, 3000, 1500, 130, 17, 2048], dtype=torch.int32, device=gpu)
+    kv_len = torch.tensor([S - 1, 1, 64, 65, 0, 777, S, 1500, 130, 17, 2048], dtype=torch.int32, device=gpu)
     qrp = torch.zeros(rows, dtype=torch.int32, device=gpu)
     q_abs = (torch.randn(rows, H, R, generator=g) * 0.3).to(dt).to(gpu)
     q_pe = (torch.randn(rows, H, 64, generator=g) * 0.3).to(dt).to(gpu)
     wkv_b = (torch.randn(H * 256, R, generator=g) * 0.05).to(dt).to(gpu)
     w_uv = wkv_b.view(H, 256, R)[:, 128:, :]
-    ws = DecodeWorkspace.allocate(rows, n_splits, gpu) if n_splits > 1 else None
+    ws = DecodeWorkspace.allocate(rows, n_splits, gpu, rank=R) if n_splits > 1 else None
     o_lat = torch.empty(rows, H, R, dtype=dt, device=gpu)
     kernels.decode_attention(q_abs, q_pe, cos, sin, cache, 0.0721, row_seq=row_seq, kv_len=kv_len,
                              q_rope_pos=qrp, n_splits=n_splits, min_chunk=min_chunk, out=o_lat,
