@@ -310,9 +310,18 @@ __global__ __launch_bounds__(kPkWaves * 64) void mla_linear_packed_kernel(Packed
   constexpr int K = kPkWaves * 64 * KQ;
   constexpr int XS = 2 * K + 16;  // LDS row pitch (bytes): 8 rows of a read pass hit distinct banks
   constexpr int MT = MS / 16;
-  constexpr int RS = 16 * OPB;    // partial-sum row pitch (floats)
-  constexpr int kLds = MS * XS > kPkWaves * MS * RS * 4 ? MS * XS : kPkWaves * MS * RS * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t xl[kLds];  // X, then the partial sums
+  // Partial-sum row pitch (floats): 16 OPB + 4, so the four row groups of a
+  // store (rows 4g + i, lanes 16g .. 16g + 15) start 16 banks apart and the
+  // 64 lanes hit 64 distinct banks (a multiple of 64 would put all four
+  // groups on the same 16 banks).
+  constexpr int RS = 16 * OPB + 4;
+  constexpr int kXBytes = MS * XS, kPartBytes = kPkWaves * MS * RS * 4;
+  // The partial sums get LDS of their own when both fit in 160 KB (no
+  // barrier between the last X read and the first partial store); else they
+  // reuse X's.
+  constexpr bool kApart = kXBytes + kPartBytes <= 160 * 1024;
+  constexpr int kLds = kApart ? kXBytes + kPartBytes : (kXBytes > kPartBytes ? kXBytes : kPartBytes);
+  __shared__ __attribute__((aligned(16))) uint8_t xl[kLds];  // X, and the partial sums
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int slab = blockIdx.y;
@@ -374,12 +383,12 @@ __global__ __launch_bounds__(kPkWaves * 64) void mla_linear_packed_kernel(Packed
           acc[o][mt][h] =
               __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[mt][h]), as_bf16x8(wv[o][q]), acc[o][mt][h], 0, 0, 0);
   }
-  __syncthreads();  // X is no longer read: its LDS takes the partial sums
+  if constexpr (!kApart) __syncthreads();  // X is no longer read: its LDS takes the partial sums
 
   // part[w][row][16o + j]: lanes j < 8 keep the even half of output column
   // 8o + j, lanes j >= 8 the odd half of column 8o + j - 8 (D lane layout:
   // column j, rows 4g + i).
-  float* part = reinterpret_cast<float*>(xl);
+  float* part = reinterpret_cast<float*>(xl + (kApart ? kXBytes : 0));
 #pragma unroll
   for (int o = 0; o < OPB; ++o)
 #pragma unroll
