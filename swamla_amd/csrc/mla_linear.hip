@@ -137,7 +137,15 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
   constexpr int kTilesPerWave = DV / 16 / 4;
   static_assert(ROWS == 2 || ROWS == 4 || ROWS == 8, "rows per block");
   __shared__ __attribute__((aligned(16))) uint8_t x_lds[ROWS * kMpXRow];
-  const int h = blockIdx.y, r0 = blockIdx.x * ROWS;
+  // XCD-aware block order: workgroups go to the 8 XCDs round-robin by linear
+  // id, so id -> (XCD id % 8, slot id / 8) -> head-major index m gives each
+  // XCD the blocks of 2 whole heads, and each XCD's L2 fetches only those
+  // heads' W_uv (instead of every head's: 8 MB of fetches at 16 heads).
+  // The grid has 16 gx blocks, a multiple of 8.
+  const int gx = gridDim.x;
+  const int id = blockIdx.y * gx + blockIdx.x;
+  const int m = (id & 7) * (2 * gx) + (id >> 3);
+  const int h = m / gx, r0 = (m - h * gx) * ROWS;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
