@@ -52,9 +52,12 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
   constexpr int RP = Geo::RP, kCRow = Geo::CRow;
   constexpr int CB = C_DT == 2 ? RP : 2 * RP;  // latent bytes per cached token
   constexpr int MB = 4 * NB;                   // 16-channel output blocks
-  __shared__ __attribute__((aligned(16))) uint8_t c_lds[Geo::CBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t pe_lds[kPeBytes];
-  __shared__ __attribute__((aligned(16))) float sc_lds[kTileTok];
+  static_assert(DEPTH == 1, "one tile of loads in flight (the LDS tile is double-buffered)");
+  // Two LDS tiles: tile j + 1 is stored into one while tile j is read from
+  // the other, so one barrier per tile orders both.
+  __shared__ __attribute__((aligned(16))) uint8_t c_lds2[2][Geo::CBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t pe_lds2[2][kPeBytes];
+  __shared__ __attribute__((aligned(16))) float sc_lds2[2][kTileTok];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -160,16 +163,12 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
     l_part[qi] = 0.f;
   }
 
-  uint8_t* const c_st = c_lds + (TPW * w + lt) * kCRow + 16 * lc;
-  uint8_t* const pe_st = pe_lds + (TPW * w + lt) * kPeRow + 16 * lc;
-  // operand reads of token block tb: token 16tb + n, 8 channels at 32s + 8g
-  const uint8_t* const c_op = c_lds + n * kCRow + 2 * (8 * g);
-  const uint8_t* const pe_op = pe_lds + n * kPeRow + 2 * (8 * g);
-  // C^T reads: token row 4g + n/4 of each 16-token block, channel 4(n%4) (+16 mb)
-  const uint8_t* const c_tr = c_lds + (4 * g + (n >> 2)) * kCRow + 8 * (n & 3);
-
-  auto process = [&](int j, PTile<C_DT, RPL, NB>& kt) {
-    // This wave's rows (e4m3 decoded to bf16, with their scales) into the tile.
+  // This wave's rows of a loaded tile (e4m3 decoded to bf16, with their
+  // scales) into LDS buffer bf.
+  auto store_tile = [&](int bf, const PTile<C_DT, RPL, NB>& kt) {
+    uint8_t* const c_st = c_lds2[bf] + (TPW * w + lt) * kCRow + 16 * lc;
+    uint8_t* const pe_st = pe_lds2[bf] + (TPW * w + lt) * kPeRow + 16 * lc;
+    float* const sc_lds = sc_lds2[bf];
 #pragma unroll
     for (int rr = 0; rr < RPL; ++rr) {
       if constexpr (C_DT == 2) {
@@ -194,8 +193,18 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
       const uint4 pv = kt.p[rr];
       *reinterpret_cast<uint4*>(pe_st + 8 * rr * kPeRow) = make_uint4(pv.x, pv.y, pv.z, pv.w);
     }
-    load_tile(j + DEPTH, kt);
-    lds_barrier();  // the whole tile is visible
+  };
+
+  // process(j): tile j, read from LDS buffer j % 2.
+  auto process = [&](int j) {
+    const uint8_t* const c_lds = c_lds2[j & 1];
+    const uint8_t* const pe_lds = pe_lds2[j & 1];
+    const float* const sc_lds = sc_lds2[j & 1];
+    // operand reads of token block tb: token 16tb + n, 8 channels at 32s + 8g
+    const uint8_t* const c_op = c_lds + n * kCRow + 2 * (8 * g);
+    const uint8_t* const pe_op = pe_lds + n * kPeRow + 2 * (8 * g);
+    // C^T reads: token row 4g + n/4 of each 16-token block, channel 4(n%4) (+16 mb)
+    const uint8_t* const c_tr = c_lds + (4 * g + (n >> 2)) * kCRow + 8 * (n & 3);
 
     // Scores of all 64 tokens for this wave's queries: token 16tb + 4g + i, head n.
     float x[QPW][4][4];
@@ -286,17 +295,26 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
           oacc[qi][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cv, pb[qi][kb], oacc[qi][mb], 0, 0, 0);
       }
     }
-    lds_barrier();  // every wave is done with the tile's rows
   };
 
-  int it = 0;
-  for (; it + DEPTH <= n_tiles; it += DEPTH) {
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) process(it + d, kt[d]);
+  // Tile 0 into buffer 0, tile 1's loads in flight.  Iteration j stores tile
+  // j + 1 (loaded during iteration j - 1) into buffer (j + 1) % 2, issues
+  // tile j + 2's loads, processes tile j, and ends with the barrier that
+  // makes tile j + 1 visible and frees buffer j % 2 for tile j + 2.  Loads
+  // past the last tile re-read its last rows (in bounds, never stored).
+  if (n_tiles > 0) {
+    store_tile(0, kt[0]);
+    load_tile(1, kt[0]);
+    lds_barrier();
   }
-#pragma unroll
-  for (int d = 0; d < DEPTH - 1; ++d)
-    if (it + d < n_tiles) process(it + d, kt[d]);
+  for (int j = 0; j < n_tiles; ++j) {  // block-uniform
+    if (j + 1 < n_tiles) {
+      store_tile((j + 1) & 1, kt[0]);
+      load_tile(j + 2, kt[0]);
+    }
+    process(j);
+    lds_barrier();
+  }
 
 #pragma unroll
   for (int qi = 0; qi < QPW; ++qi) {
