@@ -30,7 +30,8 @@ constexpr int kPrefillOcc = 1;    // workgroups per CU the registers must allow
 // product are tokens 32kb + 4g + {0..3} and 32kb + 16 + 4g + {0..3}, exactly
 // the tokens whose scores the lane holds.  No split-KV: the output is o_lat
 // directly.  Built with NW = 8 waves of one query each (QPW = 1) and one tile
-// of loads in flight: 178 VGPRs, two waves per SIMD.
+// of loads in flight: 190 VGPRs, two waves per SIMD; the LDS tiles rotate
+// over three buffers so the loop can be software-pipelined (below).
 // ---------------------------------------------------------------------------
 // One wave's share of a prefill tile: RPL rows of 8 tokens (lane: token l%8,
 // 16 bytes at 16(l/8) of each 128-byte segment), plus the rows' e4m3 scales.
@@ -52,12 +53,15 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
   constexpr int RP = Geo::RP, kCRow = Geo::CRow;
   constexpr int CB = C_DT == 2 ? RP : 2 * RP;  // latent bytes per cached token
   constexpr int MB = 4 * NB;                   // 16-channel output blocks
-  static_assert(DEPTH == 1, "one tile of loads in flight (the LDS tile is double-buffered)");
-  // Two LDS tiles: tile j + 1 is stored into one while tile j is read from
-  // the other, so one barrier per tile orders both.
-  __shared__ __attribute__((aligned(16))) uint8_t c_lds2[2][Geo::CBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t pe_lds2[2][kPeBytes];
-  __shared__ __attribute__((aligned(16))) float sc_lds2[2][kTileTok];
+  static_assert(DEPTH == 1, "one tile of loads in flight (the LDS tiles rotate over three buffers)");
+  // Three LDS tiles: in iteration j tile j + 1 is stored into one, QK reads
+  // it after the iteration's barrier, and PV still reads tile j from another
+  // (the third was tile j - 1's, which every wave finished before the
+  // barrier).
+  constexpr int kBufs = 3;
+  __shared__ __attribute__((aligned(16))) uint8_t c_lds2[kBufs][Geo::CBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t pe_lds2[kBufs][kPeBytes];
+  __shared__ __attribute__((aligned(16))) float sc_lds2[kBufs][kTileTok];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -195,19 +199,19 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
     }
   };
 
-  // process(j): tile j, read from LDS buffer j % 2.
-  auto process = [&](int j) {
-    const uint8_t* const c_lds = c_lds2[j & 1];
-    const uint8_t* const pe_lds = pe_lds2[j & 1];
-    const float* const sc_lds = sc_lds2[j & 1];
+  // Tile j lives in LDS buffer j % 3.
+  // qk(j, x): scores of all 64 tokens of tile j for this wave's queries
+  // (token 16tb + 4g + i, head n), masked and scaled to the log2 domain.
+  float x[QPW][4][4];
+  bf16x8_t pb[QPW][2];
+  auto qk = [&](int j) {
+    const int bf = j % kBufs;
+    const uint8_t* const c_lds = c_lds2[bf];
+    const uint8_t* const pe_lds = pe_lds2[bf];
+    const float* const sc_lds = sc_lds2[bf];
     // operand reads of token block tb: token 16tb + n, 8 channels at 32s + 8g
     const uint8_t* const c_op = c_lds + n * kCRow + 2 * (8 * g);
     const uint8_t* const pe_op = pe_lds + n * kPeRow + 2 * (8 * g);
-    // C^T reads: token row 4g + n/4 of each 16-token block, channel 4(n%4) (+16 mb)
-    const uint8_t* const c_tr = c_lds + (4 * g + (n >> 2)) * kCRow + 8 * (n & 3);
-
-    // Scores of all 64 tokens for this wave's queries: token 16tb + 4g + i, head n.
-    float x[QPW][4][4];
     const int tile0 = j * kTileTok;
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -239,7 +243,13 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
           x[qi][tb][i] = tok < Lq[qi] ? sv * a.scale_log2 : -INFINITY;
         }
     }
-    bf16x8_t pb[QPW][2];
+  };
+  // softmax(j): the online-softmax step of tile j's scores x: running max
+  // (rescaling O when it moves), weight sums, and the bf16 weights pb in the
+  // PV operand order.
+  auto softmax = [&](int j) {
+    const float* const sc_lds = sc_lds2[j % kBufs];
+    (void)sc_lds;
 #pragma unroll
     for (int qi = 0; qi < QPW; ++qi) {
       float mt = -INFINITY;
@@ -280,7 +290,11 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
       for (int kb = 0; kb < 2; ++kb)
         pb[qi][kb] = as_bf16x8(make_uint4(pw[2 * kb].x, pw[2 * kb].y, pw[2 * kb + 1].x, pw[2 * kb + 1].y));
     }
-    // O^T[16mb + ., head] += C^T . P^T over the tile's two 32-token halves.
+  };
+  // pv(j): O^T[16mb + ., head] += C^T . P^T over tile j's two 32-token halves.
+  auto pv = [&](int j) {
+    // C^T reads: token row 4g + n/4 of each 16-token block, channel 4(n%4) (+16 mb)
+    const uint8_t* const c_tr = c_lds2[j % kBufs] + (4 * g + (n >> 2)) * kCRow + 8 * (n & 3);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -297,23 +311,31 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
     }
   };
 
-  // Tile 0 into buffer 0, tile 1's loads in flight.  Iteration j stores tile
-  // j + 1 (loaded during iteration j - 1) into buffer (j + 1) % 2, issues
-  // tile j + 2's loads, processes tile j, and ends with the barrier that
-  // makes tile j + 1 visible and frees buffer j % 2 for tile j + 2.  Loads
-  // past the last tile re-read its last rows (in bounds, never stored).
+  // Software-pipelined over tiles: the prologue stores tile 0, issues tile
+  // 1's loads and runs tile 0's scores and softmax.  Iteration j stores tile
+  // j + 1 (loaded during iteration j - 1) into its buffer and issues tile
+  // j + 2's loads; after the barrier (tile j + 1 visible, tile j - 1's buffer
+  // free) the wave issues tile j + 1's QK MFMAs and tile j's PV MFMAs back to
+  // back, then tile j + 1's softmax, whose VALU work overlaps the PV MFMAs
+  // still in flight.  Loads past the last tile re-read its last rows (in
+  // bounds, never stored).
   if (n_tiles > 0) {
     store_tile(0, kt[0]);
     load_tile(1, kt[0]);
     lds_barrier();
+    qk(0);
+    softmax(0);
   }
   for (int j = 0; j < n_tiles; ++j) {  // block-uniform
-    if (j + 1 < n_tiles) {
-      store_tile((j + 1) & 1, kt[0]);
+    const bool more = j + 1 < n_tiles;
+    if (more) {
+      store_tile((j + 1) % kBufs, kt[0]);
       load_tile(j + 2, kt[0]);
     }
-    process(j);
     lds_barrier();
+    if (more) qk(j + 1);
+    pv(j);
+    if (more) softmax(j + 1);
   }
 
 #pragma unroll
