@@ -151,18 +151,24 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
   const int n = lane & 15, g = lane >> 4;
 
   // W_uv[h] rows of this wave's output tiles (B operand: lane = output d).
+  // A merging wave issues them right behind its split loads (the merge waits
+  // only for those), the other waves at once.
   uint4 wb[kTilesPerWave][2 * NB];
+  auto load_w = [&]() {
 #pragma unroll
-  for (int j = 0; j < kTilesPerWave; ++j) {
-    const int d = 16 * (w + 4 * j) + n;
-    const uint16_t* wp = static_cast<const uint16_t*>(a.w) + h * a.w_hs + static_cast<int64_t>(d) * a.w_rs + 8 * g;
+    for (int j = 0; j < kTilesPerWave; ++j) {
+      const int d = 16 * (w + 4 * j) + n;
+      const uint16_t* wp = static_cast<const uint16_t*>(a.w) + h * a.w_hs + static_cast<int64_t>(d) * a.w_rs + 8 * g;
 #pragma unroll
-    for (int s = 0; s < 2 * NB; ++s) wb[j][s] = *reinterpret_cast<const uint4*>(wp + 32 * s);
-  }
+      for (int s = 0; s < 2 * NB; ++s) wb[j][s] = *reinterpret_cast<const uint4*>(wp + 32 * s);
+    }
+  };
+  const bool merger = threadIdx.x < ROWS * 32;  // wave-uniform: ROWS * 32 is a multiple of 64
+  if (!merger) load_w();
 
   // Merge: thread -> (row rr, 8 channels cc per 256-channel chunk), one row
   // per half-wave; threads past ROWS rows idle.
-  if (threadIdx.x < ROWS * 32) {
+  if (merger) {
     const int rr = threadIdx.x >> 5, cl = threadIdx.x & 31;
     const bool hi = (threadIdx.x & 32) != 0;  // this row's lanes are 32 hi .. 32 hi + 31
     const int r = r0 + rr;
@@ -192,6 +198,7 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
       l0 = lp[min(cl, a.n_splits - 1) * H];
       load_group(0, a.n_splits - 1, 8 * cl);
     }
+    load_w();
     // at most n_splits (a plan word from another launch cannot send the
     // reads past the row's slots)
     const int ns = live ? min(row_splits(L, a.n_splits, a.min_chunk, plan).ns, a.n_splits) : 0;
