@@ -602,6 +602,25 @@ def packed_ok(M: int, N: int, K: int) -> bool:
     return 0 < M <= LINEAR_MAX_ROWS and N > 0 and N % 8 == 0 and K in PACKED_K
 
 
+def packed_blocks(M: int, N: int, K: int) -> int:
+    """Workgroups mla_linear_packed launches for an [M, K] x [N, K]^T product
+    (packed_ok shapes).  Mirrors the C++ launcher's grid (launch_linear_packed
+    and packed_slab_rows in mla_linear.hip): slabs of 16 / 32 / 64 rows, about
+    256 workgroups, at most four 8-row output octets each.  Every workgroup
+    takes a CU to itself (its LDS), so a count above the CUs means a second
+    round."""
+    if K <= 1024 and M > 32:
+        ms = 64
+    elif K <= 1024 or (K <= 2048 and N // 8 >= 256):
+        ms = 32 if M > 16 else 16
+    else:
+        ms = 16
+    slabs = (M + ms - 1) // ms
+    n_oct = N // 8
+    gx = max((256 + slabs - 1) // slabs, (n_oct + 3) // 4)
+    return slabs * min(gx, n_oct)
+
+
 def pack_weight(w: torch.Tensor) -> PackedWeight:
     """Re-lay a [N, K] bf16 weight (unit last stride) for linear_packed."""
     dev = _need_gpu(w)

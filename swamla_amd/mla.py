@@ -9,6 +9,8 @@ dicts load unchanged and callers need no edits.
 What runs where (per forward, bf16 model):
   decode-sized calls (<= 128 query rows, the one-token step):
     mla_linear_packed  x . [W_uk^T wq_nope | wq_pe | wkv_a]^T (q_abs, q_pe, kv)
+                       (the library GEMM when its grid would need a second
+                       round of workgroups, e.g. 128 rows)
     mla_decode_attn_append  append (kv_norm + RoPE(k_pe) + e4m3 + scatter)
                        folded into the split-KV attention launch (T = 1;
                        longer chunks run mla_append first)
@@ -408,15 +410,25 @@ class MLA(nn.Module):
 
     def _fused_projections(self, x: torch.Tensor):
         """q_abs [n, H, R_pad], q_pe [n, H, P] and kv [n, R_pad+P] from one
-        product over decode_weights() (mla_linear_packed with its packed copy,
-        else mla_linear; column views of one [n, H*(R_pad+P)+R_pad+P] buffer)."""
+        product over decode_weights() (column views of one
+        [n, H*(R_pad+P)+R_pad+P] buffer): mla_linear_packed with its packed
+        copy while its grid fits the CUs in one round; past that (config 5's
+        128 rows: 340 workgroups) the library GEMM (hipBLASLt through
+        torch.nn.functional.linear) is faster, 9.4 against 15.1 us at 128 x 5440 x 1024; else
+        mla_linear."""
         n, H, R, P = x.shape[0] * x.shape[1], self.n_heads, self.rank_pad, self.qk_rope_head_dim
         w_in, b_in = self.decode_weights()
         wp = self._decode_w[3]
+        xf = x.reshape(n, self.dim)
         if wp is not None and kernels.packed_ok(n, wp.N, wp.K):
-            y = kernels.linear_packed(x.reshape(n, self.dim), wp, bias=b_in)
+            if self._num_cus is None:
+                self._num_cus = torch.cuda.get_device_properties(x.device).multi_processor_count
+            if kernels.packed_blocks(n, wp.N, wp.K) <= self._num_cus:
+                y = kernels.linear_packed(xf, wp, bias=b_in)
+            else:
+                y = torch.nn.functional.linear(xf, w_in, b_in)
         else:
-            y = kernels.linear(x.reshape(n, self.dim), w_in, bias=b_in)
+            y = kernels.linear(xf, w_in, bias=b_in)
         q_abs = y[:, : H * R].view(n, H, R)
         q_pe = y[:, H * R: H * (R + P)].view(n, H, P)
         return q_abs, q_pe, y[:, H * (R + P):]

@@ -196,6 +196,36 @@ def test_fp8_cache_against_emulation(gpu):
     assert_cache_bits(ours, xs, dtype, fp8=True)
 
 
+def test_module_decode_batch_128(gpu):
+    """128 query rows per decode step (config 5's batch): mla_linear_packed
+    would need a second round of workgroups for the stacked input product, so
+    the module runs that product on the library GEMM, and wo still on
+    mla_linear_packed.  Against the reference restatement; cache rows
+    bit-exact."""
+    from swamla_amd import kernels
+
+    say("module, batch 128 decode")
+    dtype = torch.bfloat16
+    B = 128
+    cfg = MLAConfig(n_embd=1024, max_batch_size=B, max_seq_len=96)
+    ref, ours = make_pair(cfg, 31, dtype, gpu, ln_random=True)
+    ours.decode_weights()
+    wp = ours._decode_w[3]  # the packed stacked weight
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    assert kernels.packed_blocks(B, wp.N, wp.K) > cus  # the routing this test covers
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(B, 40, 1024, generator=g).to(dtype)
+    xs = [x.to(gpu)]
+    with torch.no_grad():
+        close(ours(xs[0], 0), ref(x, 0), dtype)
+        for s in range(3):
+            xd = torch.randn(B, 1, 1024, generator=g).to(dtype)
+            xs.append(xd.to(gpu))
+            close(ours(xs[-1], 40 + s), ref(xd, 40 + s), dtype)
+    torch.cuda.synchronize()
+    assert_cache_bits(ours, xs, dtype)
+
+
 def test_no_cache_forward_matches_reference(gpu):
     """Outside inference mode the reference attends over the call's own
     tokens with a causal mask (mla.py:419-423, :483)."""

@@ -51,3 +51,18 @@ def test_module_plan_uses_workgroups_per_cu(monkeypatch, cache_dtype, bpc):
     ns, mc, bal = m._decode_plan(64, 8256, torch.device("cpu"), True, dtype=torch.bfloat16)
     assert (ns, bal) == (16 * bpc, 256 * bpc)
     assert seen[0] == (torch.bfloat16, cache_dtype == "fp8_e4m3", 256, True)
+
+
+def test_packed_blocks_mirrors_the_launcher():
+    """kernels.packed_blocks restates launch_linear_packed's grid
+    (mla_linear.hip): the decode step's shapes at batch 32 fill the 256 CUs
+    once; the stacked input product at 128 rows needs 340 workgroups (two
+    slabs of 64 rows x 170 blocks of four octets), wo at 128 rows 256."""
+    from swamla_amd import kernels
+
+    assert kernels.packed_blocks(32, 5440, 1024) == 256
+    assert kernels.packed_blocks(32, 1024, 2048) == 256
+    assert kernels.packed_blocks(64, 5440, 1024) == 256
+    assert kernels.packed_blocks(128, 5440, 1024) == 340
+    assert kernels.packed_blocks(128, 1024, 2048) == 256
+    assert kernels.packed_blocks(1, 8, 512) == 1
