@@ -130,13 +130,16 @@ __global__ __launch_bounds__(NW * 64) void mla_linear_kernel(LinearArgs a) {
 // channels 8(t%32) + 256k ..+8; one split: the decode kernel's o_lat row),
 // then multiplies: y[r, h, d] = sum_c W_uv[h][d][c] x[r][c].
 // ---------------------------------------------------------------------------
-template <int DV, int ROWS, int NB>
+template <int DV, int ROWS, int NB, int G>
 __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs a) {
   constexpr int R = 64 * NB, H = 16;  // R: the padded latent width R_pad
   constexpr int kMpXRow = 2 * R + 16;  // LDS bytes per merged row (padded)
   constexpr int kTilesPerWave = DV / 16 / 4;
   static_assert(ROWS == 2 || ROWS == 4 || ROWS == 8, "rows per block");
   __shared__ __attribute__((aligned(16))) uint8_t x_lds[ROWS * kMpXRow];
+  // group states of the split merge (8 = groups x rows): M, T and A per channel
+  __shared__ float comb_m[8], comb_t[8];
+  __shared__ __attribute__((aligned(16))) float comb_a[G > 1 ? G * ROWS * R : 4];
   // XCD-aware block order: workgroups go to the 8 XCDs round-robin by linear
   // id, so id -> (XCD id % 8, slot id / 8) -> head-major index m gives each
   // XCD the blocks of 2 whole heads, and each XCD's L2 fetches only those
@@ -150,9 +153,8 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
 
-  // W_uv[h] rows of this wave's output tiles (B operand: lane = output d).
-  // A merging wave issues them right behind its split loads (the merge waits
-  // only for those), the other waves at once.
+  // W_uv[h] rows of this wave's output tiles (B operand: lane = output d),
+  // issued right behind the wave's split loads.
   uint4 wb[kTilesPerWave][2 * NB];
   auto load_w = [&]() {
 #pragma unroll
@@ -163,45 +165,128 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
       for (int s = 0; s < 2 * NB; ++s) wb[j][s] = *reinterpret_cast<const uint4*>(wp + 32 * s);
     }
   };
-  const bool merger = threadIdx.x < ROWS * 32;  // wave-uniform: ROWS * 32 is a multiple of 64
-  if (!merger) load_w();
-
-  // Merge: thread -> (row rr, 8 channels cc per 256-channel chunk), one row
-  // per half-wave; threads past ROWS rows idle.
-  if (merger) {
-    const int rr = threadIdx.x >> 5, cl = threadIdx.x & 31;
-    const bool hi = (threadIdx.x & 32) != 0;  // this row's lanes are 32 hi .. 32 hi + 31
-    const int r = r0 + rr;
-    const bool live = r < a.n_rows;  // uniform over the half-wave
-    const float* lp = a.lse_part + static_cast<int64_t>(r) * a.n_splits * H + h;
-    const float* op0 = a.o_part + (static_cast<int64_t>(r) * a.n_splits * H + h) * R;
-    float4 v[8][2];
-    auto load_group = [&](int s0, int last, int cc) {
+  // Merge.  The block's threads form 8 / ROWS groups of ROWS * 32 (whole
+  // waves), of which the first G merge: group grp takes splits grp, grp + G,
+  // grp + 2G, ... of every row (G > 1 when rows may have more than 8 splits,
+  // so their loads go out from several waves at once instead of in rounds of
+  // 8; with few splits the extra barrier costs more than it saves).  Within
+  // a group: thread -> (row rr, 8 channels cc per 256-channel chunk), one row
+  // per half-wave.  Each group forms its own state (max M_g, weight sum T_g,
+  // weighted sum A_g); with G > 1 the states meet in LDS and group 0 folds
+  // them in group order:
+  //   o = sum_g e^(M_g - M) A_g / sum_g e^(M_g - M) T_g,  M = max_g M_g.
+  static_assert(G >= 1 && G * ROWS <= 8, "merge groups");
+  constexpr int kGT = ROWS * 32;
+  const int grp = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kGT);  // wave-uniform
+  const bool merging = grp < G;
+  const int tg = threadIdx.x - grp * kGT;
+  const int rr = tg >> 5, cl = tg & 31;
+  const bool hi = (tg & 32) != 0;  // this row's lanes are 32 hi .. 32 hi + 31 of the wave
+  const int r = r0 + rr;
+  const bool live = r < a.n_rows;  // uniform over the half-wave
+  const float* lp = a.lse_part + static_cast<int64_t>(r) * a.n_splits * H + h;
+  const float* op0 = a.o_part + (static_cast<int64_t>(r) * a.n_splits * H + h) * R;
+  float4 v[8][2];
+  // this group's splits j0 .. j0 + 7 of its sequence (split grp + G j)
+  auto load_group = [&](int j0, int last, int cc) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float* op = op0 + static_cast<int64_t>(min(s0 + k, last)) * H * R + cc;
-        v[k][0] = *reinterpret_cast<const float4*>(op);
-        v[k][1] = *reinterpret_cast<const float4*>(op + 4);
-      }
-    };
-    // With n_splits > 1 (the partial buffers are then given, [n_rows,
-    // n_splits, H, R_pad]) the first 8 splits' partial rows and this lane's
-    // split's log-sum-exp go out before the row's split count is known;
-    // slots past the count may hold stale, even non-finite, values and are
-    // dropped by selects below, never multiplied in.  With n_splits == 1 the
-    // buffers may be null and are not touched: every row then reads o_lat.
-    const bool early = a.n_splits > 1;  // block-uniform
-    const int plan = a.plan ? *a.plan : 0;
-    const int L = live ? clamped_row_len(a.ad, r, a.cache_b, a.cache_s) : 0;
-    float l0 = -INFINITY;
-    if (live && early) {
-      l0 = lp[min(cl, a.n_splits - 1) * H];
-      load_group(0, a.n_splits - 1, 8 * cl);
+    for (int k = 0; k < 8; ++k) {
+      const float* op = op0 + static_cast<int64_t>(min(grp + G * (j0 + k), last)) * H * R + cc;
+      v[k][0] = *reinterpret_cast<const float4*>(op);
+      v[k][1] = *reinterpret_cast<const float4*>(op + 4);
     }
-    load_w();
-    // at most n_splits (a plan word from another launch cannot send the
-    // reads past the row's slots)
-    const int ns = live ? min(row_splits(L, a.n_splits, a.min_chunk, plan).ns, a.n_splits) : 0;
+  };
+  // With n_splits > 1 (the partial buffers are then given, [n_rows, n_splits,
+  // H, R_pad]) the group's first 8 splits' partial rows and this lane's
+  // split's log-sum-exp go out before the row's split count is known; slots
+  // past the count may hold stale, even non-finite, values and are dropped by
+  // selects below, never multiplied in.  With n_splits == 1 the buffers may
+  // be null and are not touched: every row then reads o_lat.  The W_uv loads
+  // go out right behind them (the merge waits only for its own loads).
+  const bool early = a.n_splits > 1;  // block-uniform
+  const int plan = a.plan ? *a.plan : 0;
+  const int L = live ? clamped_row_len(a.ad, r, a.cache_b, a.cache_s) : 0;
+  float l0 = -INFINITY;
+  if (merging && live && early) {
+    l0 = lp[min(grp + G * cl, a.n_splits - 1) * H];
+    load_group(0, a.n_splits - 1, 8 * cl);
+  }
+  load_w();
+  // at most n_splits (a plan word from another launch cannot send the reads
+  // past the row's slots)
+  const int ns = live ? min(row_splits(L, a.n_splits, a.min_chunk, plan).ns, a.n_splits) : 0;
+  const int nm = merging && ns > grp ? (ns - grp + G - 1) / G : 0;  // this group's splits of the row
+  constexpr int kChunks = (R + 255) / 256;
+  float M = -INFINITY, tot = 0.f;
+  float macc[kChunks][8];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) macc[c][i] = 0.f;
+  if (ns >= 2 && nm > 0) {
+    // Statistics as half-wave reductions: lane cl takes the group's splits
+    // cl, cl + 32, ...; max and weight sum are butterflies over the row's 32
+    // lanes, and each split's weight is formed once, by its lane.
+    if (cl >= nm) l0 = -INFINITY;
+    M = l0;
+    for (int j = cl + 32; j < nm; j += 32) M = fmaxf(M, lp[(grp + G * j) * H]);
+    M = lane_group_max<32>(M);
+    const float w0 = l0 == -INFINITY ? 0.f : __expf(l0 - M);
+    tot = w0;
+    for (int j = cl + 32; j < nm; j += 32) {
+      const float l = lp[(grp + G * j) * H];
+      tot += l == -INFINITY ? 0.f : __expf(l - M);
+    }
+    tot = lane_group_sum<32>(tot);
+    // Weighted sum over the group's splits in order, 8 at a time; split j's
+    // weight comes from lane j % 32 of the row's half (readlane of both
+    // halves, then a select).  Every lane of the half runs every chunk, so
+    // the lanes read are active.
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const int cc = 256 * c + 8 * cl;
+      const bool on = cc < R;  // false only in a partial last chunk
+      float wl = w0;  // weight of split (j0 & ~31) + cl
+      for (int j0 = 0; j0 < nm; j0 += 8) {
+        if (j0 > 0 || c > 0) {
+          if (on) load_group(j0, ns - 1, cc);
+          if (j0 > 0 && (j0 & 31) == 0) {
+            const float l = j0 + cl < nm ? lp[(grp + G * (j0 + cl)) * H] : -INFINITY;
+            wl = l == -INFINITY ? 0.f : __expf(l - M);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int jj = (j0 & 31) + k;
+          const float w_lo = u2f(__builtin_amdgcn_readlane(f2u(wl), jj));
+          const float w_hi = u2f(__builtin_amdgcn_readlane(f2u(wl), 32 + jj));
+          const bool in = j0 + k < nm;
+          const float ws = hi ? w_hi : w_lo;
+          const float t[8] = {v[k][0].x, v[k][0].y, v[k][0].z, v[k][0].w, v[k][1].x, v[k][1].y, v[k][1].z, v[k][1].w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) macc[c][i] = in ? macc[c][i] + ws * t[i] : macc[c][i];
+        }
+      }
+    }
+  }
+  if constexpr (G > 1) {
+    // group states into LDS: per (group, row) M and T, and A per channel
+    if (merging && cl == 0) {
+      comb_m[grp * ROWS + rr] = M;
+      comb_t[grp * ROWS + rr] = tot;
+    }
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const int cc = 256 * c + 8 * cl;
+      if (merging && cc < R) {
+        float* dst = comb_a + (grp * ROWS + rr) * R + cc;
+        *reinterpret_cast<float4*>(dst) = make_float4(macc[c][0], macc[c][1], macc[c][2], macc[c][3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(macc[c][4], macc[c][5], macc[c][6], macc[c][7]);
+      }
+    }
+    __syncthreads();
+  }
+  if (grp == 0) {
     if (ns == 1) {
       for (int cc = 8 * cl; cc < R; cc += 256)
         *reinterpret_cast<uint4*>(x_lds + rr * kMpXRow + 2 * cc) =
@@ -210,56 +295,44 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
       for (int cc = 8 * cl; cc < R; cc += 256)
         *reinterpret_cast<uint4*>(x_lds + rr * kMpXRow + 2 * cc) = make_uint4(0, 0, 0, 0);
     } else {
-      // o = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M), M = max_s lse_s.
-      // Statistics as half-wave reductions: lane cl takes splits cl, cl + 32,
-      // ..., the max and the weight sum are butterflies over the row's 32
-      // lanes, and each split's weight is formed once, by its lane.
-      if (cl >= ns) l0 = -INFINITY;
-      float M = l0;
-      for (int s = cl + 32; s < ns; s += 32) M = fmaxf(M, lp[s * H]);
-      M = lane_group_max<32>(M);
-      const float w0 = l0 == -INFINITY ? 0.f : __expf(l0 - M);
-      float tot = w0;
-      for (int s = cl + 32; s < ns; s += 32) {
-        const float l = lp[s * H];
-        tot += l == -INFINITY ? 0.f : __expf(l - M);
+      float scale[G];  // e^(M_g - M) per group
+      float den = tot;
+      if constexpr (G > 1) {
+        float Mx = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < G; ++q) Mx = fmaxf(Mx, comb_m[q * ROWS + rr]);
+        den = 0.f;
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+          const float mq = comb_m[q * ROWS + rr];
+          scale[q] = mq == -INFINITY ? 0.f : __expf(mq - Mx);
+          den += scale[q] * comb_t[q * ROWS + rr];
+        }
       }
-      tot = lane_group_sum<32>(tot);
-      const float inv = tot > 0.f ? 1.f / tot : 0.f;
-      // Weighted sum over the splits in order, 8 at a time; split s's weight
-      // comes from lane s % 32 of the row's half (readlane of both halves,
-      // then a select).  Every lane of the half runs every chunk, so the
-      // lanes read are active.
-      for (int cb = 0; cb < R; cb += 256) {
-        const int cc = cb + 8 * cl;
-        const bool on = cc < R;  // false only in a partial last chunk
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        float wl = w0;  // weight of split (s0 & ~31) + cl
-        for (int s0 = 0; s0 < ns; s0 += 8) {
-          if (s0 > 0 || cb > 0) {
-            if (on) load_group(s0, ns - 1, cc);
-            if (s0 > 0 && (s0 & 31) == 0) {
-              const float l = s0 + cl < ns ? lp[(s0 + cl) * H] : -INFINITY;
-              wl = l == -INFINITY ? 0.f : __expf(l - M);
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c) {
+        const int cc = 256 * c + 8 * cl;
+        if (cc < R) {
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = macc[c][i];
+          if constexpr (G > 1) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+            for (int q = 0; q < G; ++q) {
+              const float* src = comb_a + (q * ROWS + rr) * R + cc;
+              const float4 p0 = *reinterpret_cast<const float4*>(src), p1 = *reinterpret_cast<const float4*>(src + 4);
+              const float t[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+              for (int i = 0; i < 8; ++i) o[i] += scale[q] * t[i];
             }
           }
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const int j = (s0 & 31) + k;
-            const float w_lo = u2f(__builtin_amdgcn_readlane(f2u(wl), j));
-            const float w_hi = u2f(__builtin_amdgcn_readlane(f2u(wl), 32 + j));
-            const bool in = s0 + k < ns;
-            const float ws = hi ? w_hi : w_lo;
-            const float t[8] = {v[k][0].x, v[k][0].y, v[k][0].z, v[k][0].w, v[k][1].x, v[k][1].y, v[k][1].z, v[k][1].w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = in ? acc[i] + ws * t[i] : acc[i];
-          }
-        }
-        if (on) {
           uint32_t pk[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            pk[i] = f32_to_bf16(acc[2 * i] * inv) | (static_cast<uint32_t>(f32_to_bf16(acc[2 * i + 1] * inv)) << 16);
+            pk[i] = f32_to_bf16(o[2 * i] * inv) | (static_cast<uint32_t>(f32_to_bf16(o[2 * i + 1] * inv)) << 16);
           *reinterpret_cast<uint4*>(x_lds + rr * kMpXRow + 2 * cc) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         }
       }
@@ -529,9 +602,13 @@ int launch_merge_project(const MergeProjectArgs& a, hipStream_t s) {
   const dim3 grid((a.n_rows + rows - 1) / rows, 16), block(256);
   const int rc = with_nb(a.R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value;
-    if (rows == 2) hipLaunchKernelGGL((mla_merge_project_kernel<128, 2, NB>), grid, block, 0, s, a);
-    else if (rows == 4) hipLaunchKernelGGL((mla_merge_project_kernel<128, 4, NB>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((mla_merge_project_kernel<128, 8, NB>), grid, block, 0, s, a);
+    // more than 8 splits per row: every wave of the block takes a share of them
+    const bool many = a.n_splits > 8;
+    if (rows == 2 && many) hipLaunchKernelGGL((mla_merge_project_kernel<128, 2, NB, 4>), grid, block, 0, s, a);
+    else if (rows == 2) hipLaunchKernelGGL((mla_merge_project_kernel<128, 2, NB, 1>), grid, block, 0, s, a);
+    else if (rows == 4 && many) hipLaunchKernelGGL((mla_merge_project_kernel<128, 4, NB, 2>), grid, block, 0, s, a);
+    else if (rows == 4) hipLaunchKernelGGL((mla_merge_project_kernel<128, 4, NB, 1>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((mla_merge_project_kernel<128, 8, NB, 1>), grid, block, 0, s, a);
     return 0;
   });
   if (rc != 0) return rc;
