@@ -12,7 +12,8 @@ line, including their quirks:
     ``is_causal = mask is None and seqlen > 1`` (mla.py:402-487);
   * ``softmax_scale = qk_head_dim ** -0.5`` (mla.py:118).
 Pinned by tests/golden (fixtures written by importing the real reference in
-the survey container): outputs and caches must match bit-exactly.
+the build container, tests/golden/make_golden.py): outputs and caches must
+match bit-exactly.
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 """
