@@ -251,47 +251,6 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   const int t_last = t1 > 0 ? t1 - 1 : 0;
   const int64_t row0 = static_cast<int64_t>((b < 0 || b >= a.cache_b) ? 0 : b) * a.cache_s;
 
-  // RoPE row of the query (cos / sin loads go out before the tiles')
-  int rp = ra.rope;
-  rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
-  const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
-  const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
-  uint32_t cr[2][2], sr[2][2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    vm_load<2>(ct + (32 * s + 8 * g) / 2, cr[s]);
-    vm_load<2>(st + (32 * s + 8 * g) / 2, sr[s]);
-  }
-
-  // ---- fused append: the split holding position L - 1 owns the new token
-  bool fa_own = false;  // workgroup-uniform
-  int fa_k = 0, fa_t = 0, fa_w = 0;
-  TokAddr fa_a{0, 0, 0};
-  if constexpr (FUSE) {
-    if (split == (ns > 0 ? ns - 1 : 0)) {
-      fa_a = TokAddr{ra.b, ra.pos - 1, ra.rope};
-      if (fa_a.b < 0 || fa_a.b >= a.fa.cache_b || fa_a.pos < 0 || fa_a.pos >= a.fa.cache_s || fa_a.rope < 0 ||
-          fa_a.rope >= a.fa.rope_len) {
-        if (threadIdx.x == 0 && a.fa.err_flag) a.fa.err_flag[0] = 1;  // skipped, as mla_append does
-      } else {
-        fa_own = true;  // then L = pos + 1 <= cache_s and t1 = L
-        const int j = (fa_a.pos - t0) / kSubTok;
-        if (j < rem) {
-          fa_w = j;
-          fa_k = 0;
-        } else {
-          fa_w = (j - rem) % kDecWaves;
-          fa_k = (j - rem) / kDecWaves + (fa_w < rem ? 1 : 0);
-        }
-        fa_t = (fa_a.pos - t0) % kSubTok;
-      }
-    }
-  }
-  const bool fa_wave = FUSE && fa_own && w == fa_w;  // wave-uniform
-  FusedIn<NB> fin;
-  if constexpr (FUSE)
-    if (fa_wave) fin = fused_load<NB>(a.fa, r, fa_a.rope, lane);
-
   // ---- sub-tile ring: wave w's k-th sub-tile goes to buffer k % NBUF
   lds_u8* const wave_lds = lds + w * G::kWave;
   lds_u8* const stage = wave_lds + NBUF * G::kSub;  // e4m3 only
@@ -354,11 +313,55 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   };
 
   // The ring fills at once: the first sub-tile right behind the query loads,
-  // then the next ones.  Every wave issues all NBUF - 1 of them, also past its
-  // own sub-tiles (they then re-read the split's last row, in bounds), so one
-  // fixed wait below covers the loads issued before them.
+  // then (after the RoPE-row and fused-append loads) the next ones.  Every
+  // wave issues all NBUF - 1 of them, also past its own sub-tiles (they then
+  // re-read the split's last row, in bounds), so one fixed wait below covers
+  // the loads issued before the second.
+  issue(0);
+
+  // RoPE row of the query (cos / sin loads go out before the later tiles')
+  int rp = ra.rope;
+  rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
+  const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
+  const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
+  uint32_t cr[2][2], sr[2][2];
 #pragma unroll
-  for (int k = 0; k < NBUF - 1; ++k) issue(k);
+  for (int s = 0; s < 2; ++s) {
+    vm_load<2>(ct + (32 * s + 8 * g) / 2, cr[s]);
+    vm_load<2>(st + (32 * s + 8 * g) / 2, sr[s]);
+  }
+
+  // ---- fused append: the split holding position L - 1 owns the new token
+  bool fa_own = false;  // workgroup-uniform
+  int fa_k = 0, fa_t = 0, fa_w = 0;
+  TokAddr fa_a{0, 0, 0};
+  if constexpr (FUSE) {
+    if (split == (ns > 0 ? ns - 1 : 0)) {
+      fa_a = TokAddr{ra.b, ra.pos - 1, ra.rope};
+      if (fa_a.b < 0 || fa_a.b >= a.fa.cache_b || fa_a.pos < 0 || fa_a.pos >= a.fa.cache_s || fa_a.rope < 0 ||
+          fa_a.rope >= a.fa.rope_len) {
+        if (threadIdx.x == 0 && a.fa.err_flag) a.fa.err_flag[0] = 1;  // skipped, as mla_append does
+      } else {
+        fa_own = true;  // then L = pos + 1 <= cache_s and t1 = L
+        const int j = (fa_a.pos - t0) / kSubTok;
+        if (j < rem) {
+          fa_w = j;
+          fa_k = 0;
+        } else {
+          fa_w = (j - rem) % kDecWaves;
+          fa_k = (j - rem) / kDecWaves + (fa_w < rem ? 1 : 0);
+        }
+        fa_t = (fa_a.pos - t0) % kSubTok;
+      }
+    }
+  }
+  const bool fa_wave = FUSE && fa_own && w == fa_w;  // wave-uniform
+  FusedIn<NB> fin;
+  if constexpr (FUSE)
+    if (fa_wave) fin = fused_load<NB>(a.fa, r, fa_a.rope, lane);
+
+#pragma unroll
+  for (int k = 1; k < NBUF - 1; ++k) issue(k);
 
   bf16x8_t qb[2 * NB + 2];  // Q^T, set once the query has landed
   f32x4_t oacc[4 * NB];
@@ -512,9 +515,23 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
     }
   };
 
-  // Everything issued before the first sub-tile (query, RoPE row, fused
-  // inputs) has landed; the ring's sub-tiles may still be in flight.
-  wait_vm<(NBUF - 1) * G::kVm>();
+  // The dry pass: the loop body's first run, on buffer 0 while its data (and
+  // the query) may still be arriving, with zero queries and the results
+  // discarded.  It brings the body into the instruction cache (a cold first
+  // pass costs over a microsecond) while the loads are in flight.
+#pragma unroll
+  for (int i = 0; i < 2 * NB + 2; ++i) qb[i] = as_bf16x8(make_uint4(0u, 0u, 0u, 0u));
+  process(0, true);
+#pragma unroll
+  for (int i = 0; i < 4 * NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  m_run = -INFINITY;
+  l_part = 0.f;
+  e_part = 0.f;
+
+  // Everything issued before the second sub-tile (query, first sub-tile,
+  // RoPE row, fused inputs) has landed; the later sub-tiles may still be in
+  // flight.
+  wait_vm<(NBUF - 2) * G::kVm>();
 #pragma unroll
   for (int s = 0; s < 2 * NB; ++s) vm_release(qraw[s]);
 #pragma unroll
@@ -551,23 +568,10 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
       ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, lane, wave_lds + (NBUF - 1) * G::kSub);
     }
 
-  // k = -1 is the dry pass: the loop body's first run, on buffer 0 while
-  // its data may still be arriving, with the results discarded.
-  for (int k = -1; k < my_n; ++k) {  // uniform
-    const bool dry = k < 0;
-    const int kk = dry ? 0 : k;
-    if (!dry) {
-      if (kk + NBUF - 1 < my_n) issue(kk + NBUF - 1);
-      wait_subtiles<G::kVm, NBUF>(min(NBUF - 1, my_n - 1 - kk));
-    }
-    process(kk, dry);
-    if (dry) {
-#pragma unroll
-      for (int i = 0; i < 4 * NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      m_run = -INFINITY;
-      l_part = 0.f;
-      e_part = 0.f;
-    }
+  for (int k = 0; k < my_n; ++k) {  // uniform
+    if (k + NBUF - 1 < my_n) issue(k + NBUF - 1);
+    wait_subtiles<G::kVm, NBUF>(min(NBUF - 1, my_n - 1 - k));
+    process(k, false);
   }
   if constexpr (FUSE)
     if (fa_wave) fused_store<C_DT, NB>(a.fa, static_cast<int64_t>(fa_a.b) * a.fa.cache_s + fa_a.pos, ftok, lane);
