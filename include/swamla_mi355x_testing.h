@@ -19,8 +19,6 @@ void mla_host_f32_to_e4m3(const float* x, uint8_t* out, int64_t n);
 void mla_host_e4m3_to_f32(const uint8_t* c, float* out, int64_t n);
 /* packed 4 x e4m3 words -> 4 x bf16 each (the decode kernel's dequantiser). */
 void mla_host_e4m3x4_to_bf16(const uint32_t* w, uint16_t* out, int64_t n_words);
-/* fp64 -> bf16 with one rounding (the LayerNorm output rounding). */
-void mla_host_f64_to_bf16(const double* x, uint16_t* out, int64_t n);
 /* fp32 -> bf16 RNE (eager PyTorch's per-op rounding). */
 void mla_host_f32_to_bf16(const float* x, uint16_t* out, int64_t n);
 

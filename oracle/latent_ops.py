@@ -32,19 +32,6 @@ def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
     return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
-def f64_to_bf16_bits(d: np.ndarray) -> np.ndarray:
-    """One rounding fp64 -> bf16 (round-to-odd to fp32, then RNE to bf16).
-    Pinned against exact rational rounding (fractions) on random samples."""
-    d = np.asarray(d, dtype=np.float64)
-    f = d.astype(np.float32)
-    inexact = (f.astype(np.float64) != d) & np.isfinite(d)
-    u = f.view(np.uint32).copy()
-    away = np.abs(f.astype(np.float64)) > np.abs(d)
-    u = np.where(inexact & away, u - 1, u)
-    u = np.where(inexact, u | 1, u)
-    return f32_to_bf16_bits(u.view(np.float32))
-
-
 def f32_to_e4m3_codes(x: np.ndarray) -> np.ndarray:
     """fp32 -> e4m3fn codes through torch's own cast (RNE, NaN at >= 464)."""
     t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32))

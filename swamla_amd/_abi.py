@@ -47,7 +47,6 @@ EXPORTED_SYMBOLS = (
     "mla_host_f32_to_e4m3",
     "mla_host_e4m3_to_f32",
     "mla_host_e4m3x4_to_bf16",
-    "mla_host_f64_to_bf16",
     "mla_host_f32_to_bf16",
 )
 
@@ -133,8 +132,6 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_host_e4m3_to_f32.argtypes = [_P, _P, _I64]
     lib.mla_host_e4m3x4_to_bf16.restype = None
     lib.mla_host_e4m3x4_to_bf16.argtypes = [_P, _P, _I64]
-    lib.mla_host_f64_to_bf16.restype = None
-    lib.mla_host_f64_to_bf16.argtypes = [_P, _P, _I64]
     lib.mla_host_f32_to_bf16.restype = None
     lib.mla_host_f32_to_bf16.argtypes = [_P, _P, _I64]
 

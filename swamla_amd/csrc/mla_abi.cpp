@@ -591,9 +591,6 @@ void mla_host_e4m3x4_to_bf16(const uint32_t* w, uint16_t* out, int64_t n_words) 
     out[4 * i + 3] = hi >> 16;
   }
 }
-void mla_host_f64_to_bf16(const double* x, uint16_t* out, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) out[i] = swamla::f64_to_bf16(x[i]);
-}
 void mla_host_f32_to_bf16(const float* x, uint16_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = swamla::f32_to_bf16(x[i]);
 }

@@ -24,7 +24,9 @@
 // buffers (global_load_lds, 48-64 KB ahead) and, once tile i has landed,
 // meets the four compute waves at one barrier per tile.  The loader issues
 // no stores and the compute waves no loads after their prologue, so each
-// wave's vmcnt counts one kind of operation and its waits are exact.
+// wave's vmcnt counts one kind of operation; every tile, the last partial one
+// included, issues the same number of DMAs, so the loader's count-based waits
+// are exact.
 // Compute wave w keeps the W rows of its 16 NBK columns for all K in
 // registers for the whole walk.  MFMA (16x16x32 bf16): A = W rows (lane l:
 // row l % 16, k 8 (l / 16) .. + 8), B = x rows read from LDS (lane l: row
@@ -120,10 +122,15 @@ __global__ __launch_bounds__(320) void mla_head_product_kernel(HeadProductArgs a
   if (w == 4) {
     // --- loader.  Tile i of this block goes to buffer i % NBUF.  The DMA of
     // LDS slot p = 64 q + lane (q = 0 .. kDma - 1): row r = p / kChunks,
-    // slot s = p % kChunks, which holds chunk c = (s & ~15) | ((s ^ r) & 15);
-    // lanes whose chunk lies in the row's padding or whose row lies past M
-    // load nothing.
+    // slot s = p % kChunks, which holds chunk c = (s & ~15) | ((s ^ r) & 15).
+    // Every tile issues exactly kDma DMAs, which the count-based waits below
+    // rely on: rows past M re-read row M - 1 (in bounds; their results are
+    // never stored), and only lanes whose chunk lies in the row's padding
+    // load nothing — at most half of a row, so no DMA loses all 64 lanes
+    // (an instruction whose lanes are all masked off would be branched over
+    // and never counted).
     const uint16_t* X = static_cast<const uint16_t*>(a.x) + h * a.x_hs;
+    const int64_t last_row = static_cast<int64_t>(a.M) - 1;
     auto issue = [&](int i) {
       const int64_t row0 = static_cast<int64_t>(t0 + i * stride) * ROWS;
       lds_u8* dst = ring_p + (i % NBUF) * G::kTileBytes;
@@ -132,7 +139,8 @@ __global__ __launch_bounds__(320) void mla_head_product_kernel(HeadProductArgs a
         const int p = 64 * q + lane;
         const int r = p / G::kChunks, s = p % G::kChunks;
         const int c = (s & ~15) | ((s ^ r) & 15);
-        if (c < K / 8 && row0 + r < a.M) hp_dma16(X + (row0 + r) * a.x_rs + 8 * c, dst + 1024 * q);
+        const int64_t row = row0 + r < last_row ? row0 + r : last_row;
+        if (c < K / 8) hp_dma16(X + row * a.x_rs + 8 * c, dst + 1024 * q);
       }
     };
     for (int i = 0; i < NBUF - 1 && i < my_n; ++i) issue(i);

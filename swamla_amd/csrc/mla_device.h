@@ -27,7 +27,6 @@ struct Elem<0> {  // fp32
   using T = float;
   static __device__ __forceinline__ float ld(const T* p, int64_t i) { return p[i]; }
   static __device__ __forceinline__ T from_f32(float f) { return f; }
-  static __device__ __forceinline__ T from_f64(double d) { return static_cast<float>(d); }
   // op-by-op rounding of eager fp32 math: contraction into a fused
   // multiply-add is switched off (HIP's __fmul_rn is a plain multiply that
   // the compiler may otherwise fuse with the following add).
@@ -49,7 +48,6 @@ struct Elem<1> {  // bf16
   using T = uint16_t;
   static __device__ __forceinline__ float ld(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
   static __device__ __forceinline__ T from_f32(float f) { return f32_to_bf16(f); }
-  static __device__ __forceinline__ T from_f64(double d) { return f64_to_bf16(d); }
   // eager bf16 math: compute in fp32, round to bf16 after every op
   static __device__ __forceinline__ float mul(float a, float b) {
 #pragma clang fp contract(off)
@@ -75,7 +73,6 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
   o2 = E::add(E::mul(x2, c), E::mul(x1, s));
 }
 
-__device__ __forceinline__ double shfl_xor_f64(double v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ float shfl_xor_f32(float v, int m) { return __shfl_xor(v, m, 64); }
 
 // The arithmetic below is shared by the append kernel and the decode kernel's
@@ -473,8 +470,6 @@ struct LatGeo {
   static constexpr int CRow = 2 * RP + PAD;
   static constexpr int CBytes = kTileTok * CRow;
 };
-constexpr int kPRow = 2 * kTileTok + 8;    // bytes per head row of P (128 + 8 pad: the 16 heads
-                                           // of an 8-byte access fall on distinct banks)
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 __device__ __forceinline__ bf16x8_t cat_bf16x8(s16x4_t lo, s16x4_t hi) {
@@ -521,27 +516,6 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
-
-// Registers of one in-flight tile (this wave's 16 tokens), loaded as whole
-// lines: element s of c covers tokens 8(s&1)..+8, bytes 128(s>>1)..+128 of
-// the latent rows (lane: token l%8, 16 B at 16(l/8)); p[j] the same for
-// rope rows, tokens 8j..+8.  bf16 rows of R_pad = 64 NB channels are NB
-// segments; e4m3 rows are ceil(NB / 2) segments of codes (for odd NB the last
-// one is half a row: its upper lanes re-read the row's first bytes, unused),
-// plus the 4 scales this lane's scores need.
-template <int C_DT, int NB>
-struct KTile;
-template <int NB>
-struct KTile<1, NB> {
-  uint4 c[2 * NB];
-  uint4 p[2];
-};
-template <int NB>
-struct KTile<2, NB> {
-  uint4 c[2 * ((NB + 1) / 2)];
-  uint4 p[2];
-  float4 sc;
-};
 
 // e4m3 x 4 (one dword) -> 4 bf16 with gfx950's packed converter, two codes
 // per instruction (scale 1: exact, since every e4m3fn value is a bf16 value).

@@ -67,22 +67,6 @@ __device__ __forceinline__ float lane_group_max(float v) { return lane_group_red
 template <int W>
 __device__ __forceinline__ float lane_group_sum(float v) { return lane_group_reduce<W, false>(v); }
 
-// fp64 -> bf16 with a single rounding: round to fp32 with round-to-odd (no
-// double-rounding hazard because 24 >= 8 + 2 bits), then RNE to bf16.
-SW_HD uint16_t f64_to_bf16(double d) {
-  float f = static_cast<float>(d);  // RNE
-  if (f == f && static_cast<double>(f) != d) {
-    // Step toward zero if RNE rounded away from zero, then mark inexact.
-    uint32_t u = f2u(f);
-    double af = d < 0 ? -static_cast<double>(f) : static_cast<double>(f);
-    double ad = d < 0 ? -d : d;
-    if (af > ad) u -= 1u;
-    u |= 1u;
-    f = u2f(u);
-  }
-  return f32_to_bf16(f);
-}
-
 // fp32 -> e4m3fn code, round-to-nearest-even.  |x| > 464 (past the half-way
 // point between 448, the largest finite value, and the next step) and NaN/inf
 // give NaN (0x7F | sign); 464 itself ties to even (448).  This is how torch's

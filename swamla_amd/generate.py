@@ -22,10 +22,19 @@ same results up to summation order).
 The model is used through the attributes SWAMLAModel has
 (``transformer.wte / drop / h / ln_f``, ``lm_head``, ``config.block_size``)
 and each block through its call ``block(x, start_pos, freqs_cis, mask)``
-(models/mla_block.py:81).  The MLA modules are switched to absolute RoPE
-positions: a new token at position p must be rotated by p, which is what the
-reference's full-context recompute does (its chunk-local convention rotates a
-one-token call by 0).
+(models/mla_block.py:81).
+
+Side effects on the model's MLA modules, undone by ``close()`` (or by leaving
+a ``with IncrementalDecoder(model) as dec:`` block): they are switched to
+absolute RoPE positions — a new token at position p must be rotated by p,
+which is what the reference's full-context recompute does (its chunk-local
+convention rotates a one-token call by 0) — and, for graph replays, to the
+per-row split plan.  Their caches stay allocated (``MLA.clear_cache`` frees
+them).
+
+Positions are checked on the host against the smaller of ``block_size`` and
+every MLA's cache length before each step, eager or replayed; after
+``generate`` the modules' device-side append flags are read back as well.
 """
 from __future__ import annotations
 
@@ -56,15 +65,36 @@ class IncrementalDecoder:
                                           "history; not part of this path")
             self.mlas.append(attn)
         self.block_size = int(model.config.block_size)
+        self.limit = self.block_size  # positions available: block_size and every cache length
         self.pos = 0
+        # the attributes prefill() / the graph capture change, restored by close()
+        self._saved = [(m, m.rope_positions, m.split_plan) for m in self.mlas]
+
+    def close(self) -> None:
+        """Restore each MLA's RoPE convention and split plan as they were
+        before this decoder touched them, and drop the captured graph."""
+        for m, rope_positions, split_plan in self._saved:
+            m.rope_positions = rope_positions
+            m.split_plan = split_plan
+        self._g = None
+
+    def __enter__(self) -> "IncrementalDecoder":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    def _check_room(self, t: int) -> None:
+        if self.pos + t > self.limit:
+            what = "block_size" if self.limit == self.block_size else "the smallest MLA cache length"
+            raise ValueError(f"position {self.pos + t} exceeds {what} ({self.limit})")
 
     def _run(self, idx: torch.Tensor, start_pos) -> torch.Tensor:
         """Logits of the last position after running ``idx`` [B, T] from
         ``start_pos`` (an int, or an int32 device tensor [B] of positions;
         swa_mla_model.py:365-406 with start_pos threaded)."""
         t = idx.shape[1]
-        if self.pos + t > self.block_size:
-            raise ValueError(f"position {self.pos + t} exceeds block_size {self.block_size}")
+        self._check_room(t)
         tr = self.model.transformer
         x = tr.drop(tr.wte(idx))
         # the prompt's additive causal mask, as the model builds it (:384-387);
@@ -86,6 +116,7 @@ class IncrementalDecoder:
             if m.inference_mode and m.kv_cache is not None and m.kv_cache.shape[0] < idx.shape[0]:
                 m.clear_cache()
             m.set_inference_mode(True)
+        self.limit = min([self.block_size] + [int(m.kv_cache.shape[1]) for m in self.mlas])
         self.pos = 0
         self._g = None
         logits = self._run(idx, 0)
@@ -103,8 +134,7 @@ class IncrementalDecoder:
             return logits
         if self._g is not None:
             graph, tok, sp, out = self._g
-            if self.pos + 1 > self.block_size:
-                raise ValueError(f"position {self.pos + 1} exceeds block_size {self.block_size}")
+            self._check_room(1)  # the replay's positions come from the device
             tok.copy_(idx_next)
             graph.replay()
             self.pos += 1
@@ -150,4 +180,6 @@ class IncrementalDecoder:
             out = torch.cat((out, idx_next), dim=1)
             if i + 1 < max_new_tokens:
                 logits = self.step(idx_next)
+        for m in self.mlas:
+            m.check_cache_errors()  # appends skipped on the device (e.g. in graph replays) raise here
         return out

@@ -52,10 +52,13 @@ def _operands(M, H, K, N, seed, x_cols=None):
     return xb, xb[:, :, :K], w
 
 
-@pytest.mark.parametrize("M", [1, 15, 64, 65, 1000, 4099])
+@pytest.mark.parametrize("M", [1, 15, 64, 65, 1000, 2000, 3001, 4099])
 def test_query_absorption_shapes(gpu, M):
     """q_abs = q_nope . W_uk: x read in place from [M, 16, 192] rows, K = 128,
-    N = R_pad = 256, ragged last row tile."""
+    N = R_pad = 256, ragged last row tile.  At 16 heads the grid has 16 blocks
+    per head, so M = 2000, 3001 and 4099 give blocks two to five row tiles of
+    64 whose last one is partial (down to 3 valid rows): the loader must still
+    count every tile's DMAs alike."""
     say(f"head_product q-side M={M}")
     xb, x, w = _operands(M, 16, 128, 256, M, x_cols=192)
     out = kernels.head_product(xb.to(gpu)[:, :, :128], w.to(gpu))
@@ -64,10 +67,11 @@ def test_query_absorption_shapes(gpu, M):
     check(out, ref_head_product(x, w))
 
 
-@pytest.mark.parametrize("M", [1, 33, 64, 777, 4097])
+@pytest.mark.parametrize("M", [1, 33, 64, 777, 2100, 3000, 4097])
 def test_value_readout_shapes(gpu, M):
     """o = o_lat . W_uv^T: x = o_lat [M, 16, 256], K = 256, N = 128, written
-    into wo's input layout [M, 16 * 128]."""
+    into wo's input layout [M, 16 * 128].  M = 2100 and 3000 give blocks two
+    or three row tiles with a partial last one."""
     say(f"head_product o-side M={M}")
     _, x, w = _operands(M, 16, 256, 128, 100 + M)
     out = torch.full((M, 16 * 128), float("nan"), dtype=torch.bfloat16, device=gpu)
