@@ -14,7 +14,7 @@ layer decoded back to back would be served from there, not from HBM.  The
 bench therefore rotates ``--layers`` independent layers (own weights, own
 cache: 8 x 86.5 MB by default), like a decoder stack, and counts each token
 once per layer it passes: value = batch * steps * layers / seconds
-("layer-token decodes per second"); ms_per_step is per layer-step.
+("layer-token decodes per second").
 
 roofline: the step's attention launch (mla_decode_attn_append: the decode
 kernel with the one-token append folded in, split-KV), timed with HIP events
@@ -25,6 +25,17 @@ achieved = algorithmic bytes per launch /
 average launch duration, with bytes = sum_b L_b*(R+P)*2 (latent + rope
 cache) + B*H*(R+P)*2 (queries) + B*H*R*2 (latent outputs) + the append's
 B*(R+P)*2 read and B*(R+P)*2 written (+ LayerNorm parameters).
+
+Ceiling legs beside it (measurement kernels, not the product path):
+roofline.ceiling_gbs is the plain HBM read rate of the GPU
+(mla_probe_read over 1 GiB per launch, regions alternated so the Infinity
+Cache serves nothing), and roofline.stream_only_us the same decode launches'
+cache stream with the arithmetic left out (mla_probe_cache_stream), timed the
+same way as avg_launch_us.
+
+Every figure is the median of 5 timed repetitions.  ms_per_step is per
+graph replay of the whole stack (ms_per_step x steps = the timed region);
+us_per_layer_step divides it by the layers.
 
 cpu_baseline: the oracle's op-for-op CPU restatement of the reference MLA
 (oracle/mla_ref.py, which re-projects the cache and runs SDPA exactly as
@@ -44,6 +55,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 R, P, H = 256, 64, 16
+TIMING_REPS = 5  # every figure is the median of this many timed repetitions
 
 
 CONFIGS = {
@@ -269,16 +281,85 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (reps * len(indices))  # us
 
-    def run_graph(indices, reps):
-        """The same launches captured once in a HIP graph (as the decode step
-        runs them) and replayed: no host launch work between them."""
+    def run_graph(launch_one, indices, reps):
+        """Launches captured once in a HIP graph (as the decode step runs
+        them) and replayed: no host launch work between them.  Median over
+        TIMING_REPS timed repetitions of ``reps`` replays."""
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             hc = torch.cuda.current_stream(dev).cuda_stream
             for i in indices:
-                _abi.check(lib.mla_decode_attn_append(*(preps[i][0][:-1] + (hc,))))
+                launch_one(i, hc)
         graph.replay()
         torch.cuda.synchronize()
+        times = []
+        for _ in range(TIMING_REPS):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / (reps * len(indices)))  # us
+        return median(times)
+
+    def attn(i, hc):
+        _abi.check(lib.mla_decode_attn_append(*(preps[i][0][:-1] + (hc,))))
+
+    # the stream probe: the same launches' cache stream with no arithmetic
+    sinks = [torch.empty(p[4] * p[3] * 256, dtype=torch.int32, device=dev) for p in preps]
+
+    def probe(i, hc):
+        cache = layers[i].latent_cache()
+        dargs = preps[i][0]
+        _abi.check(lib.mla_probe_cache_stream(
+            cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale), cache.ckv.shape[0],
+            cache.ckv.shape[1], preps[i][1][3].data_ptr(), preps[i][3], R, preps[i][4], dargs[28],
+            cache.cache_code, sinks[i].data_ptr(), hc))
+
+    run(range(len(preps)), 3)  # warm-up
+    cold_us = median([run(range(len(preps)), args.kernel_reps) for _ in range(TIMING_REPS)])
+    graph_us = run_graph(attn, range(len(preps)), args.kernel_reps)
+    stream_us = None
+    if max(p[6] for p in preps) == 0:  # the probe runs the static plan only
+        stream_us = run_graph(probe, range(len(preps)), args.kernel_reps)
+    warm_us = median([run([0], args.kernel_reps * len(preps)) for _ in range(TIMING_REPS)])
+    merge_us = median([run(range(len(preps)), args.kernel_reps, which=1) for _ in range(TIMING_REPS)])
+    L, B, n_splits = preps[0][2], preps[0][3], preps[0][4]
+    return cold_us, graph_us, warm_us, merge_us, L, B, n_splits, preps[0][6], stream_us
+
+
+def median(xs):
+    xs = sorted(xs)
+    n = len(xs)
+    return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+
+
+def read_ceiling(dev, torch, gib: int = 1):
+    """HBM read ceiling of this GPU: mla_probe_read streaming ``gib`` GiB per
+    launch with 16-byte non-temporal loads, alternating between two disjoint
+    regions (each far above the 256 MB Infinity Cache), replayed from a HIP
+    graph; median GB/s over TIMING_REPS repetitions."""
+    from swamla_amd import _abi
+
+    lib = _abi.lib()
+    nbytes = gib << 30
+    buf = torch.empty(2 * nbytes, dtype=torch.uint8, device=dev)
+    buf.view(torch.int32).random_(0, 1 << 30)
+    grid = 256 * 8
+    sink = torch.empty(grid * 256, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        hc = torch.cuda.current_stream(dev).cuda_stream
+        for i in range(2):
+            _abi.check(lib.mla_probe_read(buf.data_ptr() + i * nbytes, nbytes, sink.data_ptr(), grid, hc))
+    graph.replay()
+    torch.cuda.synchronize()
+    rates = []
+    reps = 5
+    for _ in range(TIMING_REPS):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
@@ -286,15 +367,9 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
             graph.replay()
         e1.record(stream)
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (reps * len(indices))  # us
-
-    run(range(len(preps)), 3)  # warm-up
-    cold_us = run(range(len(preps)), args.kernel_reps)
-    graph_us = run_graph(range(len(preps)), args.kernel_reps)
-    warm_us = run([0], args.kernel_reps * len(preps))
-    merge_us = run(range(len(preps)), args.kernel_reps, which=1)
-    L, B, n_splits = preps[0][2], preps[0][3], preps[0][4]
-    return cold_us, graph_us, warm_us, merge_us, L, B, n_splits, preps[0][6]
+        rates.append(2 * reps * nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    del buf
+    return median(rates)
 
 
 def cpu_baseline(args, torch):
@@ -302,7 +377,7 @@ def cpu_baseline(args, torch):
     of decode steps over a bf16 cache of length ctx."""
     from oracle.mla_ref import MLAConfig, RefMLA, enable_cache, init_weights
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     B = args.cpu_batch
     cfg = MLAConfig(n_embd=args.dim, max_batch_size=B, max_seq_len=args.ctx + 1024)
@@ -444,29 +519,38 @@ def main() -> int:
         sp.copy_(sp0)
         for _ in range(args.warmup):
             graph.replay()
-        sp.copy_(sp0)  # timed steps decode positions start .. start+K-1
         log("timing")
-        if torch.distributed.is_available() and torch.distributed.is_initialized():
-            torch.distributed.barrier()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            graph.replay()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        if torch.distributed.is_available() and torch.distributed.is_initialized():
-            torch.distributed.barrier()
+        dist = torch.distributed.is_available() and torch.distributed.is_initialized()
+        elapsed_reps = []
+        for _ in range(TIMING_REPS):
+            sp.copy_(sp0)  # each repetition decodes positions start .. start+K-1
+            if dist:
+                torch.distributed.barrier()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                graph.replay()
+            torch.cuda.synchronize()
+            elapsed_reps.append(time.perf_counter() - t0)
+            if dist:
+                torch.distributed.barrier()
+        elapsed = median(elapsed_reps)
         ok = all(bool(torch.isfinite(o).all()) for o in outs)
 
     layer_steps = args.steps * len(layers)
     value = args.batch * layer_steps / elapsed
-    ms_per_step = elapsed / layer_steps * 1e3
-    log(f"decode: {value:.0f} layer-token/s, {ms_per_step * 1e3:.1f} us per layer-step, finite={ok}")
+    ms_per_step = elapsed / args.steps * 1e3  # one stack step: every layer once
+    us_per_layer_step = elapsed / layer_steps * 1e6
+    log(f"decode: {value:.0f} layer-token/s, {us_per_layer_step:.2f} us per layer-step, finite={ok}")
 
     lens = lens0 + args.canonical_steps  # the configuration's end lengths (config 2: 4224)
-    cold_us, graph_us, warm_us, merge_us, L, B, n_splits, balance = time_decode_kernel(layers, xs, lens, args, dev,
-                                                                                   torch)
+    cold_us, graph_us, warm_us, merge_us, L, B, n_splits, balance, stream_us = time_decode_kernel(
+        layers, xs, lens, args, dev, torch)
+    ceiling = read_ceiling(dev, torch)
+    log(f"read ceiling {ceiling:.0f} GB/s; cache stream alone "
+        + (f"{stream_us:.2f} us" if stream_us is not None else "n/a (balanced plan)"))
     abytes = attention_bytes_rows(lens, fp8) + append_bytes(B, fp8)
+    stream_bytes = int(lens.sum()) * (R * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0))
     traffic, traffic_src = measured_traffic(B, L, args.cache) if not args.ragged else (None, None)
     achieved = abytes / (graph_us * 1e-6) / 1e9
     warm = abytes / (warm_us * 1e-6) / 1e9
@@ -492,6 +576,9 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms_per_step,
+        "us_per_layer_step": us_per_layer_step,
+        "timed_reps": TIMING_REPS,
+        "elapsed_s_reps": elapsed_reps,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -503,6 +590,9 @@ def main() -> int:
             "heads": H, "kv_lora_rank": R, "rope_dim": P, "cache": args.cache,
             "layers_rotated": len(layers),
             "value_counts": "tokens x layers per second (each token counted once per MLA layer)",
+            "step_unit": (f"one step = one graph replay of the {len(layers)}-layer stack (ms_per_step x steps = "
+                          f"the timed region; us_per_layer_step = ms_per_step / {len(layers)}); figures are "
+                          f"medians of {TIMING_REPS} timed repetitions of the K steps"),
             "step": "full drop-in MLA.forward as one HIP graph per layer-step: stacked input product "
                     "(wq with W_uk absorbed, wkv_a), append + decode attention, split merge + W_uv, wo "
                     "(four launches)",
@@ -530,6 +620,17 @@ def main() -> int:
                             + (f"splits balanced over {balance} workgroups (per-row cap {n_splits})" if balance
                                else f"splits<={n_splits}")
                             + f", caches rotated over {len(layers)} layers"),
+            "ceiling_gbs": ceiling,
+            "ceiling_source": ("mla_probe_read: 1 GiB per launch with 16-byte non-temporal loads, alternating "
+                               "over two disjoint 1 GiB regions, graph-replayed (the plain HBM read rate of "
+                               "this GPU)"),
+            "frac_of_ceiling": achieved / ceiling,
+            "stream_only_us": stream_us,
+            "stream_only_gbs": (stream_bytes / (stream_us * 1e-6) / 1e9) if stream_us else None,
+            "stream_only_source": ("mla_probe_cache_stream: this launch's cache stream alone (same grid, split "
+                                   "plan, LDS ring, DMA instructions and waits; no query, arithmetic or epilogue), "
+                                   f"{stream_bytes} cache bytes, timed as avg_launch_us"),
+            "above_stream_only_us": (graph_us - stream_us) if stream_us else None,
             "warm_mall_achieved": warm,
             "warm_mall_avg_launch_us": warm_us,
             "merge_avg_launch_us": merge_us,

@@ -48,6 +48,8 @@ EXPORTED_SYMBOLS = (
     "mla_host_e4m3_to_f32",
     "mla_host_e4m3x4_to_bf16",
     "mla_host_f32_to_bf16",
+    "mla_probe_read",
+    "mla_probe_cache_stream",
 )
 
 _P = ctypes.c_void_p
@@ -134,6 +136,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_host_e4m3x4_to_bf16.argtypes = [_P, _P, _I64]
     lib.mla_host_f32_to_bf16.restype = None
     lib.mla_host_f32_to_bf16.argtypes = [_P, _P, _I64]
+    lib.mla_probe_read.restype = _I32
+    lib.mla_probe_read.argtypes = [_P, _I64, _P, _I32, _P]
+    lib.mla_probe_cache_stream.restype = _I32
+    lib.mla_probe_cache_stream.argtypes = [_P, _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _I32, _I32, _P, _P]
 
 
 def lib() -> ctypes.CDLL:

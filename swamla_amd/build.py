@@ -19,6 +19,7 @@ SOURCES = [
     os.path.join(HERE, "csrc", "mla_linear.hip"),
     os.path.join(HERE, "csrc", "mla_absorb.hip"),
     os.path.join(HERE, "csrc", "mla_scratch.hip"),
+    os.path.join(HERE, "csrc", "mla_probe.hip"),
     os.path.join(HERE, "csrc", "mla_abi.cpp"),
 ]
 OUTPUT = os.path.join(HERE, "libswamla_mi355x.so")

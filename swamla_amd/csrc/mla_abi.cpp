@@ -595,4 +595,47 @@ void mla_host_f32_to_bf16(const float* x, uint16_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = swamla::f32_to_bf16(x[i]);
 }
 
+int mla_probe_read(const void* src, int64_t bytes, uint32_t* sink, int32_t grid, void* stream) {
+  if (!src || !sink || bytes < 0 || bytes % 16 != 0 || grid < 1 || grid > 65535)
+    return fail(SWAMLA_ERR_INVALID_ARG, "mla_probe_read: bad arguments (bytes=%lld, grid=%d)", (long long)bytes, grid);
+  if (!aligned(src, 16) || !aligned(sink, 4))
+    return fail(SWAMLA_ERR_MISALIGNED, "mla_probe_read: src must be 16-byte aligned, sink 4-byte");
+  if (swamla::launch_read_probe(src, bytes / 16, sink, grid, static_cast<hipStream_t>(stream)) != 0)
+    return hip_fail("mla_probe_read");
+  return ok();
+}
+
+int mla_probe_cache_stream(const void* ckv_cache, const void* kpe_cache, const float* ckv_scale,
+                           int64_t cache_batch, int64_t cache_seq, const int32_t* start_pos, int32_t n_rows,
+                           int32_t R, int32_t n_splits, int32_t min_chunk, int32_t cache_dtype, uint32_t* sink,
+                           void* stream) {
+  const char* fn = "mla_probe_cache_stream";
+  if (int e = check_geometry(16, R, 64)) return e;
+  if (cache_dtype != SWAMLA_DTYPE_BF16 && cache_dtype != SWAMLA_DTYPE_FP8)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "%s: cache dtype %d (bf16 or fp8 caches of a bf16 model)", fn, cache_dtype);
+  if (!ckv_cache || !kpe_cache || !start_pos || !sink || (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale))
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: null pointer", fn);
+  if (n_rows < 0 || n_rows > 65535 || n_splits < 1 || n_splits > 1024 || min_chunk < 1 || cache_batch < 1 ||
+      cache_seq < 1 || cache_seq > (int64_t(1) << 31) - 1)
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: bad arguments (n_rows=%d, n_splits=%d, min_chunk=%d)", fn, n_rows,
+                n_splits, min_chunk);
+  if (!aligned(ckv_cache, 16) || !aligned(kpe_cache, 16) || !aligned(sink, 4) ||
+      (ckv_scale && !aligned(ckv_scale, 4)))
+    return fail(SWAMLA_ERR_MISALIGNED, "%s: caches must be 16-byte aligned", fn);
+  swamla::DecodeArgs a{};
+  a.R = R;
+  a.ckv = ckv_cache;
+  a.kpe = kpe_cache;
+  a.ckv_scale = ckv_scale;
+  a.cache_b = cache_batch;
+  a.cache_s = cache_seq;
+  a.ad = swamla::Addressing{nullptr, nullptr, nullptr, start_pos, 1, 0};
+  a.n_rows = n_rows;
+  a.n_splits = n_splits;
+  a.min_chunk = min_chunk;
+  if (swamla::launch_stream_probe(a, cache_dtype, sink, static_cast<hipStream_t>(stream)) != 0)
+    return hip_fail(fn);
+  return ok();
+}
+
 }  // extern "C"

@@ -161,6 +161,12 @@ struct HeadProductArgs {
   int M, N, K;
 };
 
+// Measurement kernels (bench.py's roofline ceiling legs): a decode launch's
+// cache stream alone (static plan; sink: n_splits * n_rows * 256 words) and
+// a plain non-temporal read of n16 16-byte words (sink: grid * 256 words).
+int launch_stream_probe(const DecodeArgs& a, int c_dt, uint32_t* sink, hipStream_t s);
+int launch_read_probe(const void* src, int64_t n16, uint32_t* sink, int grid, hipStream_t s);
+
 int launch_linear(const LinearArgs& a, int batch, hipStream_t s);
 int launch_linear_packed(const PackedLinearArgs& a, hipStream_t s);
 int launch_pack_weight(const PackWeightArgs& a, hipStream_t s);

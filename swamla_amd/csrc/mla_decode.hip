@@ -175,6 +175,91 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// One wave's share of a split's sub-tile stream.  The split [t0, t1) is cut
+// into n_sub 16-token sub-tiles dealt to the four waves: a short first round
+// deals sub-tiles 0 .. rem - 1 (rem = n_sub % 4) to waves 0 .. rem - 1, then
+// full rounds follow: wave w's k-th sub-tile is w (w < rem, k = 0), else
+// rem + w + 4 (k - [w < rem]).  So the split's last sub-tile goes to wave 3,
+// one of the waves with the fewest sub-tiles.  issue(k) streams the wave's
+// k-th sub-tile (16 latent rows, 16 rope rows, e4m3: 16 scales) from HBM into
+// ring buffer k % NBUF of the wave's LDS with G::kVm vector-memory
+// instructions: bf16 rows with their 16-byte chunks swizzled (slot s of row
+// tt holds chunk s ^ swz(tt), rope rows ^ swp(tt)), e4m3 code rows as they
+// lie.  A sub-tile past the split's end re-reads its last row (in bounds).
+template <int C_DT, int NB>
+struct SubStream {
+  using G = DecGeo<C_DT, NB>;
+  static constexpr int kLatQ = G::kLat / 1024;
+  static constexpr int kLatRow = C_DT == 2 ? G::RP : 2 * G::RP;  // bytes of a latent cache row
+  int t0, t_last, rem, my_n, j_base, w;
+  int64_t row0;
+  const uint8_t* ckv;
+  const uint8_t* kpe;
+  const float* scale;
+  lds_u8* wave_lds;
+  // per-lane source offsets within a sub-tile (16 rows from its first
+  // token) for each DMA instruction
+  uint32_t lat_off[kLatQ], pe_off[2];
+
+  __device__ __forceinline__ SubStream(int t0_, int t1, int w_, int lane, int64_t row0_, const void* ckv_,
+                                       const void* kpe_, const float* scale_, lds_u8* wave_lds_)
+      : t0(t0_), w(w_), row0(row0_), ckv(static_cast<const uint8_t*>(ckv_)),
+        kpe(static_cast<const uint8_t*>(kpe_)), scale(scale_), wave_lds(wave_lds_) {
+    const int n_sub = t1 > t0 ? (t1 - t0 + kSubTok - 1) / kSubTok : 0;
+    rem = n_sub % kDecWaves;
+    my_n = n_sub / kDecWaves + (w < rem ? 1 : 0);
+    j_base = rem + w - (w < rem ? kDecWaves : 0);  // j = j_base + 4 k, except (w < rem, k = 0): j = w
+    t_last = t1 > 0 ? t1 - 1 : 0;
+#pragma unroll
+    for (int q = 0; q < kLatQ; ++q) {
+      const int o = 1024 * q + 16 * lane;
+      if constexpr (C_DT == 2) {
+        lat_off[q] = o;
+      } else {
+        const int tt = o / (2 * G::RP), sl = (o % (2 * G::RP)) >> 4;
+        lat_off[q] = tt * (2 * G::RP) + 16 * (sl ^ swz<NB>(tt));
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int tt = 8 * q + (lane >> 3);
+      pe_off[q] = tt * (2 * kP) + 16 * ((lane & 7) ^ swp(tt));
+    }
+  }
+  __device__ __forceinline__ int sub_of(int k) const { return (k == 0 && w < rem) ? w : j_base + kDecWaves * k; }
+  __device__ __forceinline__ void issue(int k, int lane) const {
+    const int tb = t0 + kSubTok * sub_of(k);
+    lds_u8* const dst = wave_lds + (k % G::NBUF) * G::kSub;
+    if (tb + kSubTok - 1 <= t_last) {  // uniform: the whole sub-tile is in the split
+      const uint8_t* lb = ckv + (row0 + tb) * kLatRow;
+      const uint8_t* pb = kpe + (row0 + tb) * (2 * kP);
+#pragma unroll
+      for (int q = 0; q < kLatQ; ++q) dma16(lb + lat_off[q], dst + 1024 * q);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) dma16(pb + pe_off[q], dst + G::kLat + 1024 * q);
+      if constexpr (C_DT == 2) dma4(scale + row0 + tb + (lane & 15), dst + G::kLat + G::kPe);
+      return;
+    }
+    // the split's last, partial sub-tile: rows past its end re-read its last row
+#pragma unroll
+    for (int q = 0; q < kLatQ; ++q) {
+      const int tt = (1024 * q + 16 * lane) / kLatRow;
+      const int tok = min(tb + tt, t_last);
+      dma16(ckv + (row0 + tok) * kLatRow + (lat_off[q] - tt * kLatRow), dst + 1024 * q);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int tt = 8 * q + (lane >> 3);
+      const int tok = min(tb + tt, t_last);
+      dma16(kpe + (row0 + tok) * (2 * kP) + (pe_off[q] - tt * (2 * kP)), dst + G::kLat + 1024 * q);
+    }
+    if constexpr (C_DT == 2) {
+      const int tok = min(tb + (lane & 15), t_last);
+      dma4(scale + row0 + tok, dst + G::kLat + G::kPe);
+    }
+  }
+};
+
 }  // namespace
 
 template <int C_DT, bool FUSE, int NB>
@@ -238,79 +323,15 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   if (a.balance <= 0 && ns > 0) split = ns - 1 - split;
   const int t0 = split * rsp.chunk;  // a multiple of 16
   const int t1 = min(L, t0 + rsp.chunk);
-  const int n_sub = t1 > t0 ? (t1 - t0 + kSubTok - 1) / kSubTok : 0;
-  // This wave's sub-tiles.  A short first round deals sub-tiles 0 .. rem - 1
-  // (rem = n_sub % 4) to waves 0 .. rem - 1, then full rounds follow: wave w's
-  // k-th sub-tile is w (w < rem, k = 0), else rem + w + 4 (k - [w < rem]).  So
-  // the split's last sub-tile, which holds the fused append's token, goes to
-  // wave 3, one of the waves with the fewest sub-tiles.
-  const int rem = n_sub % kDecWaves;
-  const int my_n = n_sub / kDecWaves + (w < rem ? 1 : 0);
-  const int j_base = rem + w - (w < rem ? kDecWaves : 0);  // j = j_base + 4 k, except (w < rem, k = 0): j = w
-  auto sub_of = [&](int k) { return (k == 0 && w < rem) ? w : j_base + kDecWaves * k; };
-  const int t_last = t1 > 0 ? t1 - 1 : 0;
   const int64_t row0 = static_cast<int64_t>((b < 0 || b >= a.cache_b) ? 0 : b) * a.cache_s;
 
-  // ---- sub-tile ring: wave w's k-th sub-tile goes to buffer k % NBUF
+  // ---- this wave's sub-tiles; wave w's k-th goes to ring buffer k % NBUF
   lds_u8* const wave_lds = lds + w * G::kWave;
   lds_u8* const stage = wave_lds + NBUF * G::kSub;  // e4m3 only
-  const uint8_t* const ckv = static_cast<const uint8_t*>(a.ckv);
-  const uint8_t* const kpe = static_cast<const uint8_t*>(a.kpe);
-
-  // Per-lane source offsets within a sub-tile (16 rows from its first token)
-  // for each DMA instruction; a sub-tile wholly inside the split then needs one
-  // add per instruction.  bf16 rows: lane's 16-byte slot s of row tt holds chunk
-  // s ^ swz(tt) (rope rows: ^ swp(tt)); e4m3 code rows are copied as they lie.
-  constexpr int kLatQ = G::kLat / 1024;
-  uint32_t lat_off[kLatQ], pe_off[2];
-#pragma unroll
-  for (int q = 0; q < kLatQ; ++q) {
-    const int o = 1024 * q + 16 * lane;
-    if constexpr (C_DT == 2) {
-      lat_off[q] = o;
-    } else {
-      const int tt = o / (2 * RP), sl = (o % (2 * RP)) >> 4;
-      lat_off[q] = tt * (2 * RP) + 16 * (sl ^ swz<NB>(tt));
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int tt = 8 * q + (lane >> 3);
-    pe_off[q] = tt * (2 * kP) + 16 * ((lane & 7) ^ swp(tt));
-  }
-  constexpr int kLatRow = C_DT == 2 ? RP : 2 * RP;  // bytes of a latent cache row
-
-  auto issue = [&](int k) {
-    const int tb = t0 + kSubTok * sub_of(k);
-    lds_u8* const dst = wave_lds + (k % NBUF) * G::kSub;
-    if (tb + kSubTok - 1 <= t_last) {  // uniform: the whole sub-tile is in the split
-      const uint8_t* lb = ckv + (row0 + tb) * kLatRow;
-      const uint8_t* pb = kpe + (row0 + tb) * (2 * kP);
-#pragma unroll
-      for (int q = 0; q < kLatQ; ++q) dma16(lb + lat_off[q], dst + 1024 * q);
-#pragma unroll
-      for (int q = 0; q < 2; ++q) dma16(pb + pe_off[q], dst + G::kLat + 1024 * q);
-      if constexpr (C_DT == 2) dma4(a.ckv_scale + row0 + tb + (lane & 15), dst + G::kLat + G::kPe);
-      return;
-    }
-    // the split's last, partial sub-tile: rows past its end re-read its last row
-#pragma unroll
-    for (int q = 0; q < kLatQ; ++q) {
-      const int tt = (1024 * q + 16 * lane) / kLatRow;
-      const int tok = min(tb + tt, t_last);
-      dma16(ckv + (row0 + tok) * kLatRow + (lat_off[q] - tt * kLatRow), dst + 1024 * q);
-    }
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int tt = 8 * q + (lane >> 3);
-      const int tok = min(tb + tt, t_last);
-      dma16(kpe + (row0 + tok) * (2 * kP) + (pe_off[q] - tt * (2 * kP)), dst + G::kLat + 1024 * q);
-    }
-    if constexpr (C_DT == 2) {
-      const int tok = min(tb + (lane & 15), t_last);
-      dma4(a.ckv_scale + row0 + tok, dst + G::kLat + G::kPe);
-    }
-  };
+  const SubStream<C_DT, NB> ss(t0, t1, w, lane, row0, a.ckv, a.kpe, a.ckv_scale, wave_lds);
+  const int rem = ss.rem, my_n = ss.my_n;
+  auto sub_of = [&](int k) { return ss.sub_of(k); };
+  auto issue = [&](int k) { ss.issue(k, lane); };
 
   // The ring fills at once: the first sub-tile right behind the query loads,
   // then (after the RoPE-row and fused-append loads) the next ones.  Every
@@ -661,6 +682,55 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
 }
 
 // ===========================================================================
+// Measurement kernels (no reference counterpart; used by bench.py's ceiling
+// legs, never by the module).
+// ===========================================================================
+// mla_stream_probe: a decode launch's cache stream alone.  The same grid,
+// workgroup shape, LDS ring, split plan (static), sub-tile deal, DMA
+// instructions and count-based waits as mla_decode_dma, with no query loads,
+// no arithmetic and no epilogue.  Each wave folds one 16-byte word of every
+// sub-tile it receives into a checksum stored at sink[workgroup * 256 +
+// thread], so the stream is observable.  Its duration is the floor of any
+// decode launch with this access pattern on this GPU.
+template <int C_DT, int NB>
+__global__ __launch_bounds__(kDecWaves * 64, 1) void mla_stream_probe(DecodeArgs a, uint32_t* sink) {
+  using G = DecGeo<C_DT, NB>;
+  constexpr int NBUF = G::NBUF;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[G::kLds];
+  lds_u8* const lds = (lds_u8*)(lds_raw);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.y;
+  const TokAddr ra = row_addr(a.ad, r);
+  const int b = ra.b;
+  int L = ra.pos;
+  if (L > a.cache_s) L = static_cast<int>(a.cache_s);
+  if (b < 0 || b >= a.cache_b) L = 0;
+  const RowSplits rsp = row_splits(L, a.n_splits, a.min_chunk, 0);
+  uint32_t acc = 0;
+  if (static_cast<int>(blockIdx.x) < rsp.ns) {  // uniform
+    const int split = rsp.ns - 1 - static_cast<int>(blockIdx.x);
+    const int t0 = split * rsp.chunk;
+    const int t1 = min(L, t0 + rsp.chunk);
+    const int64_t row0 = static_cast<int64_t>(b) * a.cache_s;
+    lds_u8* const wave_lds = lds + w * G::kWave;
+    const SubStream<C_DT, NB> ss(t0, t1, w, lane, row0, a.ckv, a.kpe, a.ckv_scale, wave_lds);
+#pragma unroll
+    for (int k = 0; k < NBUF - 1; ++k) ss.issue(k, lane);
+    for (int k = 0; k < ss.my_n; ++k) {  // uniform
+      if (k + NBUF - 1 < ss.my_n) ss.issue(k + NBUF - 1, lane);
+      wait_subtiles<G::kVm, NBUF>(min(NBUF - 1, ss.my_n - 1 - k));
+      u32x4v_t v = ds_read16<0>(lds_off(wave_lds + (k % NBUF) * G::kSub) + 16 * lane);
+      lds_fence();
+      tie(v);
+      acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    wait_vm<0>();
+  }
+  sink[(static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * (kDecWaves * 64) + threadIdx.x] = acc;
+}
+
+// ===========================================================================
 // Launchers behind the C-ABI (argument validation lives in mla_abi.cpp).
 // ===========================================================================
 namespace {
@@ -689,6 +759,21 @@ int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
     if (!fn) return -1;
     void* args[] = {const_cast<DecodeArgs*>(&a)};
     return hipLaunchKernel(fn, grid, dim3(kDecWaves * 64), args, 0, s) == hipSuccess ? 0 : -2;
+  });
+  if (rc != 0) return rc;
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// The stream probe over a decode launch's rows (bf16 model; static plan).
+int launch_stream_probe(const DecodeArgs& a, int c_dt, uint32_t* sink, hipStream_t s) {
+  if (a.n_rows == 0) return 0;
+  if (a.balance > 0 || (c_dt != 1 && c_dt != 2)) return -1;
+  const int rc = with_nb(a.R, [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    const void* fn = c_dt == 1 ? reinterpret_cast<const void*>(&mla_stream_probe<1, NB>)
+                               : reinterpret_cast<const void*>(&mla_stream_probe<2, NB>);
+    void* args[] = {const_cast<DecodeArgs*>(&a), &sink};
+    return hipLaunchKernel(fn, dim3(a.n_splits, a.n_rows), dim3(kDecWaves * 64), args, 0, s) == hipSuccess ? 0 : -2;
   });
   if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;

@@ -1,7 +1,8 @@
 """Shared fp32 restatement of the absorbed attention for the tests (the
 oracle's statement, oracle/latent_ops.absorbed_attention_f64, in fp32 and
 row by row so it runs at the BASELINE configurations' sizes; pinned to the
-fp64 one in tests/test_oracle.py).  Reference: models/mla.py:417-487."""
+fp64 one, output and log-sum-exp, in tests/test_attn_ref.py).  Reference:
+models/mla.py:417-487."""
 import torch
 
 H = 16

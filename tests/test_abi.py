@@ -458,3 +458,26 @@ def test_balanced_chunk_examples_and_rejects(lib):
     big = (ctypes.c_int32 * 2)(1 << 24, (1 << 24) + 1)
     assert lib.mla_balanced_chunk(big, 1, 8, 64, 8) > 0
     assert lib.mla_balanced_chunk(big, 2, 8, 64, 8) == -1
+
+
+def test_probes_reject(lib):
+    """The measurement kernels behind bench.py's ceiling legs validate like
+    the product entry points (no HIP call on a bad argument)."""
+    E_ARG, E_UNS, E_MIS = -1, -2, -3  # SWAMLA_ERR_INVALID_ARG / _UNSUPPORTED / _MISALIGNED
+    assert lib.mla_probe_read(None, 1024, FAKE, 8, None) == E_ARG
+    assert lib.mla_probe_read(FAKE, 1000, FAKE, 8, None) == E_ARG  # not a multiple of 16
+    assert lib.mla_probe_read(FAKE, 1024, FAKE, 0, None) == E_ARG
+    assert lib.mla_probe_read(FAKE + 8, 1024, FAKE, 8, None) == E_MIS
+
+    def stream(**kw):
+        a = dict(ckv=FAKE, kpe=FAKE, scale=None, cb=2, cs=64, sp=FAKE, n_rows=2, R=256, ns=4, mc=16, c_dt=1,
+                 sink=FAKE, stream=None)
+        a.update(kw)
+        return lib.mla_probe_cache_stream(*a.values())
+
+    assert stream(R=600) == E_UNS
+    assert stream(c_dt=0) == E_UNS
+    assert stream(c_dt=2) == E_ARG  # fp8 without scales
+    assert stream(sp=None) == E_ARG
+    assert stream(ns=0) == E_ARG
+    assert stream(ckv=FAKE + 8) == E_MIS

@@ -3,7 +3,7 @@
 The fp64 oracle is too slow at these sizes, so the attention kernels are
 checked against a torch fp32 restatement of the same absorbed attention
 computed on the GPU, row by row (tests/attn_ref.py; the oracle's statement,
-pinned to the fp64 one at small sizes in tests/test_oracle.py).  Bars: the
+pinned to the fp64 one at small sizes in tests/test_attn_ref.py).  Bars: the
 north-star bf16 tolerance, 2e-2 relative / 1e-2 absolute, on o_lat; 1e-4
 absolute on the log-sum-exp, which, unlike o_lat, moves with the number of
 tokens attended (one 64-token tile of a 131073-token row shifts it by 4.9e-4;
@@ -14,7 +14,9 @@ distinct term, and rows with a zero query must give log-sum-exp = log L.
   config 3: 64 sequences, cache lengths U[256, 16384] from seed 0 (the same
             draw as bench.py --config 3), per-row RoPE positions
   config 4: 8 sequences x 131073 cached tokens (split-KV, many splits)
-  config 5: 128 sequences x 8193 tokens, e4m3 latent cache with fp32 scales
+  config 5: 128 sequences x 8193 tokens, e4m3 latent cache with fp32 scales,
+            both the plain decode launch and the fused-append one the decode
+            step runs
   config 2: the drop-in module against the reference restatement (RefMLA) at
             full size: 32 sequences prefilled to 4096 tokens, then decode
             steps; the latent cache bit-exact against torch's LayerNorm of
@@ -164,6 +166,59 @@ def test_config5_fp8_cache(gpu):
     deq = lambda r, L: lo.fp8_dequantize(ckv[r, :L], scale[r, :L])
     ref, ref_lse = ref_attention_fp32(q_abs, rotated_q_pe(q_pe, cos, sin, torch.zeros(B, dtype=torch.int32)),
                                       deq, lambda r, L: kpe[r, :L].float(), lens)
+    torch.cuda.synchronize()
+    check(out, ref)
+    check_lse(lse, ref_lse)
+    check_zero_query_rows(lse, lens, [0])
+
+
+def test_config5_fused_append_fp8(gpu):
+    """Config 5's decode step as it runs: the fused-append e4m3 instance
+    (mla_decode_attn_append) at 128 rows x 8192 cached tokens, appending
+    token 8192 and attending over all 8193.  The appended row (codes, scale,
+    k_pe) bit-exact against torch's LayerNorm + the e4m3 emulation; o_lat and
+    the log-sum-exp against the fp32 restatement over the cache as left by
+    the launch."""
+    say("config 5 fused: 128 rows x 8192 tokens + append, e4m3 cache")
+    B, S = 128, 8193
+    gd = torch.Generator(device=gpu).manual_seed(51)
+    y = torch.randn(B, S, R, generator=gd, device=gpu)
+    y[..., 0] = ramp(S, gpu)
+    y = y.view(B * S, R).to(torch.bfloat16)
+    codes, scale = lo.fp8_quantize(y)
+    del y
+    cache = LatentCache(codes.view(B, S, R), torch.randn(B, S, P, generator=gd, device=gpu).to(torch.bfloat16),
+                        scale.view(B, S).float())
+    del codes, scale
+    cos, sin = tables(S, gpu)
+    q_abs = (0.5 * torch.randn(B, H, R, generator=gd, device=gpu)).to(torch.bfloat16)
+    q_pe = (0.5 * torch.randn(B, H, P, generator=gd, device=gpu)).to(torch.bfloat16)
+    q_abs[0] = 0
+    q_pe[0] = 0
+    kv = torch.randn(B, R + P, generator=gd, device=gpu).to(torch.bfloat16)  # the step's wkv_a rows
+    ln_w = (1 + 0.1 * torch.randn(R, generator=gd, device=gpu)).to(torch.bfloat16)
+    ln_b = (0.1 * torch.randn(R, generator=gd, device=gpu)).to(torch.bfloat16)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    sp = torch.full((B,), S - 1, dtype=torch.int32, device=gpu)
+    n_splits, min_chunk = kernels.plan_splits(B, S)
+    lse = torch.full((B, H), float("nan"), device=gpu)
+    out = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE, start_pos=sp, rows_per_seq=1,
+                                   n_splits=n_splits, min_chunk=min_chunk, lse_out=lse,
+                                   append=kernels.FusedAppend(kv, ln_w, ln_b, 1e-5, err))
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    # the appended row: kv_norm (torch's CPU LayerNorm order), then e4m3 per token
+    kvc = kv.cpu()
+    yn = lo.layernorm_aten(kvc[:, :R], ln_w.cpu(), ln_b.cpu(), 1e-5)[0]
+    want_codes, want_scale = lo.fp8_quantize(yn)
+    assert torch.equal(cache.ckv[:, S - 1].cpu(), want_codes)
+    assert torch.equal(cache.scale[:, S - 1].cpu(), want_scale)
+    # a one-token call rotates k_pe at position 0 (chunk-local): unchanged bits
+    assert torch.equal(cache.kpe[:, S - 1].cpu().view(torch.int16), kvc[:, R:].view(torch.int16))
+    lens = torch.full((B,), S, dtype=torch.int32)
+    deq = lambda r, L: lo.fp8_dequantize(cache.ckv[r, :L], cache.scale[r, :L])
+    ref, ref_lse = ref_attention_fp32(q_abs, rotated_q_pe(q_pe, cos, sin, torch.zeros(B, dtype=torch.int32)),
+                                      deq, lambda r, L: cache.kpe[r, :L].float(), lens)
     torch.cuda.synchronize()
     check(out, ref)
     check_lse(lse, ref_lse)

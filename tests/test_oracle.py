@@ -303,18 +303,51 @@ def test_fp8_amax_encodes_to_e4m3_max():
 
 
 def test_ref_module_decode_equals_recompute():
-    """Cached decode == full recompute of the last position (fp32), i.e. the
-    cache path of the restatement is consistent with its no-cache path."""
+    """The restatement's cache path against its no-cache path (fp32).
+    With the rope projections zeroed (q_pe = k_pe = 0, so RoPE positions play
+    no part), a 5-token prefill followed by a cached one-token decode gives
+    the last position of one causal 6-token forward without a cache.  With
+    RoPE active, the cached c_kv rows match those of a 6-token prefill (to
+    the projections' rounding), k_pe rows 0..4 too, and row 5 is the
+    un-rotated k_pe: the decode call rotates
+    its token by position 0 (chunk-local positions, positional_encoding.py:
+    49-50)."""
     cfg = MLAConfig(n_embd=128, max_batch_size=1, max_seq_len=16)
-    m = RefMLA(cfg)
-    init_weights(m, 12)
-    m.eval()
     g = torch.Generator().manual_seed(13)
     x = torch.randn(1, 6, 128, generator=g)
-    enable_cache(m)
+
+    def module(rope_zero):
+        m = RefMLA(cfg)
+        init_weights(m, 12)
+        m.eval()
+        if rope_zero:
+            with torch.no_grad():
+                m.wq.weight.view(16, 192, 128)[:, 128:] = 0
+                m.wkv_a.weight[256:] = 0
+        return m
+
+    cached, plain = module(True), module(True)
+    enable_cache(cached)
     with torch.no_grad():
-        m(x[:, :5], 0)
-        dec = m(x[:, 5:6], 5)
-    # Recompute differs only by RoPE positions (chunk-local): decode rotates
-    # at position 0, so compare with RoPE-free positions via a 1-token batch.
-    assert dec.shape == (1, 1, 128) and torch.isfinite(dec).all()
+        cached(x[:, :5], 0)
+        dec = cached(x[:, 5:6], 5)
+        full = plain(x, 0)  # no cache: causal SDPA over the 6 tokens
+    assert dec.shape == (1, 1, 128)
+    err = (dec - full[:, 5:6]).abs().max().item()
+    assert err <= 1e-6 * max(1.0, full.abs().max().item()), err
+    # the same comparison with a one-position mismatch must fail
+    assert (dec - full[:, 4:5]).abs().max().item() > 1e-3
+
+    a, b = module(False), module(False)
+    enable_cache(a)
+    enable_cache(b)
+    with torch.no_grad():
+        a(x[:, :5], 0)
+        a(x[:, 5:6], 5)
+        b(x, 0)
+        _, _, _, k_pe_last = b.project(x[:, 5:6])
+    # (the projections over 5 + 1 rows and over 6 rows may round differently)
+    assert (a.kv_cache[:, :6] - b.kv_cache[:, :6]).abs().max().item() <= 1e-5
+    assert (a.pe_cache[:, :5] - b.pe_cache[:, :5]).abs().max().item() <= 1e-5
+    assert torch.equal(a.pe_cache[0, 5], k_pe_last.reshape(-1))
+    assert (a.pe_cache[0, 5] - b.pe_cache[0, 5]).abs().max().item() > 1e-2
