@@ -90,9 +90,20 @@ struct DecGeo {
   static constexpr int kSub = kLat + kPe + kSc;
   static constexpr int kStage = C_DT == 2 ? kSubTok * 2 * RP : 0;            // e4m3: decoded bf16 tile
   static constexpr int kVm = (kLat + kPe) / 1024 + (C_DT == 2 ? 1 : 0);      // vm operations per sub-tile
-  static constexpr int kCap = 3;                                              // sub-tiles in flight, at most
-  static constexpr int NBUF = cmin(cmin(kCap + 1, (kLdsMax / kDecWaves - kStage) / kSub), 63 / kVm + 1);
-  static constexpr int kWave = NBUF * kSub + kStage;  // LDS bytes per wave
+  // The ring: kFill sub-tiles are issued ahead of the loop; while one is
+  // processed, at most kCap more are in flight.  Fewer bytes in flight stream
+  // faster here: 2 and 2 (three buffers) against 3 and 3 (four buffers)
+  // measured 18.1 against 18.4-18.9 us per config-2 launch, and 89.9
+  // against 90.6-91.1 us at config 5 (e4m3).
+  static constexpr int kFillWant = 2, kCapWant = 2;
+  static constexpr int NBUF =
+      cmin(cmin(cmax(kCapWant + 1, kFillWant), (kLdsMax / kDecWaves - kStage) / kSub), 63 / kVm + 1);
+  static constexpr int kCap = cmin(kCapWant, NBUF - 1);
+  static constexpr int kFill = cmin(kFillWant, NBUF);
+  // The fused append's LayerNorm stages its row in a ring buffer the fill
+  // leaves free, else in an area of its own.
+  static constexpr int kLnOwn = kFill == NBUF ? ln_stage_bytes<1>() : 0;
+  static constexpr int kWave = NBUF * kSub + kStage + kLnOwn;  // LDS bytes per wave
   // epilogue: each wave stashes, in its own ring, per head a row of RP fp32
   // (+4 pad) and then its max / l / e per head
   static constexpr int kCombRow = RP + 4;
@@ -100,6 +111,7 @@ struct DecGeo {
   static constexpr int kLds = kDecWaves * kWave;
   static_assert(NBUF >= 2, "a sub-tile ring needs two buffers");
   static_assert(ln_stage_bytes<1>() <= kSub, "the fused LayerNorm stages its row in a ring buffer");
+  static_assert(kCap >= 1 && kFill >= 1 && kCap <= NBUF - 1, "ring depth");
   static_assert(kLds <= kLdsMax, "LDS budget");
   static_assert(kStash <= kWave, "a wave's epilogue stash fits its ring");
 };
@@ -335,7 +347,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
 
   // The ring fills at once: the first sub-tile right behind the query loads,
   // then (after the RoPE-row and fused-append loads) the next ones.  Every
-  // wave issues all NBUF - 1 of them, also past its own sub-tiles (they then
+  // wave issues all kFill of them, also past its own sub-tiles (they then
   // re-read the split's last row, in bounds), so one fixed wait below covers
   // the loads issued before the second.
   issue(0);
@@ -382,7 +394,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
     if (fa_wave) fin = fused_load<NB>(a.fa, r, fa_a.rope, lane);
 
 #pragma unroll
-  for (int k = 1; k < NBUF - 1; ++k) issue(k);
+  for (int k = 1; k < G::kFill; ++k) issue(k);
 
   bf16x8_t qb[2 * NB + 2];  // Q^T, set once the query has landed
   f32x4_t oacc[4 * NB];
@@ -552,7 +564,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   // Everything issued before the second sub-tile (query, first sub-tile,
   // RoPE row, fused inputs) has landed; the later sub-tiles may still be in
   // flight.
-  wait_vm<(NBUF - 2) * G::kVm>();
+  wait_vm<(G::kFill - 1) * G::kVm>();
 #pragma unroll
   for (int s = 0; s < 2 * NB; ++s) vm_release(qraw[s]);
 #pragma unroll
@@ -586,12 +598,14 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   // inputs were loaded ahead of them).
   if constexpr (FUSE)
     if (fa_wave) {
-      ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, lane, wave_lds + (NBUF - 1) * G::kSub);
+      ftok = fused_compute<C_DT, NB>(fin, a.fa.eps, a.R, lane,
+                                     wave_lds + (G::kLnOwn ? NBUF * G::kSub + G::kStage : (NBUF - 1) * G::kSub));
     }
 
   for (int k = 0; k < my_n; ++k) {  // uniform
-    if (k + NBUF - 1 < my_n) issue(k + NBUF - 1);
-    wait_subtiles<G::kVm, NBUF>(min(NBUF - 1, my_n - 1 - k));
+    if (k + G::kCap >= G::kFill && k + G::kCap < my_n) issue(k + G::kCap);
+    // sub-tiles issued so far: the fill's kFill (also past my_n), then up to k + kCap
+    wait_subtiles<G::kVm, NBUF>(max(G::kFill, min(my_n, k + G::kCap + 1)) - (k + 1));
     process(k, false);
   }
   if constexpr (FUSE)
@@ -716,10 +730,10 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_stream_probe(DecodeArgs
     lds_u8* const wave_lds = lds + w * G::kWave;
     const SubStream<C_DT, NB> ss(t0, t1, w, lane, row0, a.ckv, a.kpe, a.ckv_scale, wave_lds);
 #pragma unroll
-    for (int k = 0; k < NBUF - 1; ++k) ss.issue(k, lane);
+    for (int k = 0; k < G::kFill; ++k) ss.issue(k, lane);
     for (int k = 0; k < ss.my_n; ++k) {  // uniform
-      if (k + NBUF - 1 < ss.my_n) ss.issue(k + NBUF - 1, lane);
-      wait_subtiles<G::kVm, NBUF>(min(NBUF - 1, ss.my_n - 1 - k));
+      if (k + G::kCap >= G::kFill && k + G::kCap < ss.my_n) ss.issue(k + G::kCap, lane);
+      wait_subtiles<G::kVm, NBUF>(max(G::kFill, min(ss.my_n, k + G::kCap + 1)) - (k + 1));
       u32x4v_t v = ds_read16<0>(lds_off(wave_lds + (k % NBUF) * G::kSub) + 16 * lane);
       lds_fence();
       tie(v);

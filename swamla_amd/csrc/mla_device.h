@@ -239,14 +239,20 @@ __device__ __forceinline__ void read_stream(uint32_t addr, uint32_t (&xs)[16]) {
 // (ln_stage_bytes<IN_DT>() bytes of LDS that only this wavefront touches
 // while this runs), so the LayerNorm reads the row from memory once.  A
 // wavefront's LDS operations complete in order, so the reads see the writes.
-template <int IN_DT, int K>
+//
+// G = 16: the row is held by an aligned group of 16 lanes (bf16, R <= 256,
+// K = 16; lane = the lane in the group), and `buf` needs ln_stage_g16_bytes:
+// the 512-byte row and the tail reads past it.
+constexpr int ln_stage_g16_bytes() { return 544; }
+template <int IN_DT, int K, int G = 64>
 __device__ __forceinline__ LnRow ln_gather(const uint32_t (&xw)[IN_DT == 1 ? (K + 1) / 2 : K], int R, int lane,
                                            lds_u8* buf) {
   constexpr int V = IN_DT == 1 ? 16 : 8;
   constexpr int HV = V / 8;
   constexpr int ES = IN_DT == 1 ? 2 : 4;  // bytes per element
   constexpr int W = IN_DT == 1 ? (K + 1) / 2 : K;
-  static_assert(64 * K * ES <= ln_stage_bytes<IN_DT>(), "staging area");
+  static_assert(G == 64 ? 64 * K * ES <= ln_stage_bytes<IN_DT>() : (G == 16 && IN_DT == 1 && K == 16),
+                "staging area");
   const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(buf));
   ln_detail::write_lane<ES, K, W, 0>(base + ES * K * lane, xw);
   // the lane of stream (chunk sc, half sh, lane sk) reads elements s0 + j V,
@@ -265,16 +271,30 @@ __device__ __forceinline__ LnRow ln_gather(const uint32_t (&xw)[IN_DT == 1 ? (K 
   return x;
 }
 
-template <int IN_DT>
+// The value of v on lane idx of the caller's lane group: the whole wavefront
+// (G = 64; idx uniform) or the caller's aligned group of 16 lanes (G = 16).
+template <int G>
+__device__ __forceinline__ uint32_t grp_lane(uint32_t v, int idx, int lane) {
+  static_assert(G == 64 || G == 16, "lane groups of 64 or 16");
+  if constexpr (G == 64) return __builtin_amdgcn_readlane(v, idx);
+  else return static_cast<uint32_t>(__shfl(static_cast<int>(v), (lane & ~(G - 1)) + idx, 64));
+}
+
+// The statistics of one row held by a group of G lanes (lane = the lane in
+// the wavefront; the group's lanes play lanes 0 .. G-1 of the description
+// above).  G = 16 covers rows whose streams fit the group: one chunk, i.e.
+// R < 272 for bf16 input (the 4-tokens-per-wavefront append at R_pad = 256).
+template <int IN_DT, int G = 64>
 __device__ __forceinline__ LnStats aten_ln_stats(const LnRow& x, int R, float eps, int lane) {
 #pragma clang fp contract(off)
   constexpr int V = IN_DT == 1 ? 16 : 8;         // values per input vector
   constexpr int HV = V / 8;                       // 8-lane float vectors per input vector
-  constexpr int kMaxChunks = IN_DT == 1 ? 2 : 4;  // R <= 512
+  constexpr int kMaxChunks = G == 16 ? 16 / (8 * HV) : (IN_DT == 1 ? 2 : 4);  // R <= 512 (G = 64)
+  const int gbase = lane & ~(G - 1);
   const int n = R / V;
   const int chunks = (n + 15) >> 4;
-  // --- streams (lanes 0..31; a lane past the chunks has none)
-  const int sc = lane / (8 * HV);
+  // --- streams (lanes 0..31 of the group; a lane past the chunks has none)
+  const int sc = (lane & (G - 1)) / (8 * HV);
   int scnt = n - 16 * sc;
   scnt = scnt < 0 ? 0 : (scnt > 16 ? 16 : scnt);
   float s1 = 0.f, s2 = 0.f;
@@ -300,7 +320,7 @@ __device__ __forceinline__ LnStats aten_ln_stats(const LnRow& x, int R, float ep
 #pragma unroll
       for (int h = 0; h < HV; ++h) {
         const int src = (i * HV + h) * 8 + k;
-        ln_stack_merge(ci, __shfl(s1, src, 64), __shfl(s2, src, 64), c0, a1, a2);
+        ln_stack_merge(ci, __shfl(s1, gbase + src, 64), __shfl(s2, gbase + src, 64), c0, a1, a2);
       }
       if (depth == 2 && ((i + 1) & 1) == 0) {
         ln_stack_merge(c0, a1, a2, c1, b1, b2);
@@ -315,7 +335,7 @@ __device__ __forceinline__ LnStats aten_ln_stats(const LnRow& x, int R, float ep
   int cnt = 0;
   float m1 = 0.f, m2 = 0.f;
   for (int i = 0; i < R - n * V; ++i) {  // uniform, < V
-    const float xv = ln_val<IN_DT>(__builtin_amdgcn_readlane(x.xt, i));
+    const float xv = ln_val<IN_DT>(grp_lane<G>(x.xt, i, lane));
     const float d = xv - m1;
     ++cnt;
     m1 = m1 + __fdiv_rn(d, static_cast<float>(cnt));
@@ -324,8 +344,8 @@ __device__ __forceinline__ LnStats aten_ln_stats(const LnRow& x, int R, float ep
   const int per_lane = n * HV;
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
-    const float l1 = u2f(__builtin_amdgcn_readlane(f2u(a1), kk));
-    const float l2 = u2f(__builtin_amdgcn_readlane(f2u(a2), kk));
+    const float l1 = u2f(grp_lane<G>(f2u(a1), kk, lane));
+    const float l2 = u2f(grp_lane<G>(f2u(a2), kk, lane));
     const int tot = cnt + per_lane;
     const float c = tot == 0 ? 0.f : __fdiv_rn(static_cast<float>(per_lane), static_cast<float>(tot));
     const float d = l1 - m1;
@@ -371,8 +391,9 @@ __device__ __forceinline__ void encode_bf16_lane(const float (&y)[K], uint16_t (
 
 // e4m3 per token: y is first rounded to bf16 (the value a bf16 cache would
 // hold), amax over the token, scale = max(amax,1e-12)/448, code = RNE(y/scale).
-// Padding channels (y = 0) encode as 0.
-template <int K>
+// Padding channels (y = 0) encode as 0.  The token is held by G lanes: the
+// wavefront (64) or an aligned group of 16.
+template <int K, int G = 64>
 __device__ __forceinline__ void encode_e4m3_lane(const float (&y)[K], uint8_t (&codes)[K], float& scale) {
   float yb[K];
   float amax = 0.f;
@@ -382,7 +403,7 @@ __device__ __forceinline__ void encode_e4m3_lane(const float (&y)[K], uint8_t (&
     amax = fmaxf(amax, fabsf(yb[i]));
   }
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, m));
+  for (int m = 1; m < G; m <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, m));
   scale = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
 #pragma unroll
   for (int i = 0; i < K; ++i) codes[i] = f32_to_e4m3(__fdiv_rn(yb[i], scale));

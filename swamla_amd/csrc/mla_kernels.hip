@@ -106,6 +106,97 @@ __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Kernel 1 at prompt sizes: bf16 rows of R_pad = 256 channels, four tokens
+// per wavefront, one aligned group of 16 lanes per token (16 tokens per
+// block).  Lane l of a group owns latent channels 16 l .. 16 l + 15 (two
+// 16-byte loads and stores) and k_pe values 4 l .. 4 l + 3.  The LayerNorm
+// statistics are aten_ln_stats on the group: for a bf16 row of at most 256
+// channels ATen's vectorised pass has at most 16 Welford streams, one per
+// lane of the group, so every lane runs one and the statistics are the same
+// arithmetic, bit for bit, as the one-token-per-wavefront kernel's.
+// ---------------------------------------------------------------------------
+template <int C_DT>
+__global__ __launch_bounds__(256) void mla_append_g16_kernel(AppendArgs a) {
+  constexpr int RP = 256, K = 16;  // channels per lane
+  constexpr int kStage = ln_stage_g16_bytes();
+  __shared__ __attribute__((aligned(16))) uint8_t stage[16 * kStage];
+  const int lane = threadIdx.x & 63, l16 = lane & 15;
+  const int slot = threadIdx.x >> 4;  // the block's token
+  const int tok = blockIdx.x * 16 + slot;
+  if (tok >= a.n_tok) return;  // the whole group
+  const TokAddr ta = tok_addr(a.ad, tok);
+  const int b = ta.b, pos = ta.pos, rp = ta.rope;
+  if (b < 0 || b >= a.cache_b || pos < 0 || pos >= a.cache_s || rp < 0 || rp >= a.rope_len) {
+    if (l16 == 0 && a.err_flag) a.err_flag[0] = 1;
+    return;
+  }
+  // the row, the LayerNorm parameters and the rope pairs as packed bf16 words
+  const uint16_t* row = static_cast<const uint16_t*>(a.kv_in) + static_cast<int64_t>(tok) * a.in_rs;
+  uint32_t xw[K / 2], ww[K / 2], bw[K / 2], pe[2];
+  load_lane<K / 2>(reinterpret_cast<const uint32_t*>(row) + (K / 2) * l16, xw);
+  load_lane<2>(reinterpret_cast<const uint32_t*>(row + RP) + 2 * l16, pe);
+  const LnStats st = aten_ln_stats<1, 16>(
+      ln_gather<1, K, 16>(xw, a.R, l16, (lds_u8*)(stage) + slot * kStage), a.R, a.eps, lane);
+  // The LayerNorm parameters are loaded after the statistics (the compiler
+  // would hoist them): fewer registers live across the statistics, 71
+  // against 87 VGPRs, measured 43.8 against 47.8 us at 131,072 tokens.
+  asm volatile("" ::: "memory");
+  load_lane<K / 2>(static_cast<const uint32_t*>(a.ln_w) + (K / 2) * l16, ww);
+  load_lane<K / 2>(static_cast<const uint32_t*>(a.ln_b) + (K / 2) * l16, bw);
+  // the affine, one channel at a time (channels >= R are padding: 0)
+  auto yv = [&](int i) {
+    const int h = (i & 1) * 16;
+    const float x = u2f((xw[i >> 1] >> h) << 16), w = u2f((ww[i >> 1] >> h) << 16), bb = u2f((bw[i >> 1] >> h) << 16);
+    return K * l16 + i < a.R ? aten_ln_affine<1>(x, w, bb, st) : 0.f;
+  };
+  // bf16 of each channel (the value a bf16 cache holds; e4m3 encodes it)
+  uint32_t yw[K / 2];
+#pragma unroll
+  for (int i = 0; i < K / 2; ++i) yw[i] = f32_to_bf16(yv(2 * i)) | (static_cast<uint32_t>(f32_to_bf16(yv(2 * i + 1))) << 16);
+
+  const int64_t crow = static_cast<int64_t>(b) * a.cache_s + pos;
+  if constexpr (C_DT == 1) {
+    store_lane<K / 2>(reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.ckv) + crow * RP) + (K / 2) * l16, yw);
+  } else {
+    // e4m3 per token: amax over the group's channels, scale = max(amax,
+    // 1e-12) / 448, code = RNE(y / scale) of the bf16-rounded channel
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < K / 2; ++i) amax = fmaxf(amax, fmaxf(fabsf(u2f(yw[i] << 16)), fabsf(u2f(yw[i] & 0xFFFF0000u))));
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, shfl_xor_f32(amax, m));
+    const float scale = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
+    uint32_t cw[K / 4];
+#pragma unroll
+    for (int q = 0; q < K / 4; ++q) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 4 * q + e;
+        const float yb = u2f((yw[i >> 1] >> ((i & 1) * 16)) << 16);
+        c |= static_cast<uint32_t>(f32_to_e4m3(__fdiv_rn(yb, scale))) << (8 * e);
+      }
+      cw[q] = c;
+    }
+    store_lane<K / 4>(reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.ckv) + crow * RP) + (K / 4) * l16, cw);
+    if (l16 == 0) a.ckv_scale[crow] = scale;
+  }
+
+  // RoPE on k_pe: the lane's pairs 2 l16 and 2 l16 + 1
+  const uint32_t cw = static_cast<const uint32_t*>(a.cos_tab)[static_cast<int64_t>(rp) * (kP / 4) + l16];
+  const uint32_t sw = static_cast<const uint32_t*>(a.sin_tab)[static_cast<int64_t>(rp) * (kP / 4) + l16];
+  uint32_t ow[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float o1, o2;
+    rope_pair<1>(bf16_to_f32(pe[j] & 0xFFFF), bf16_to_f32(pe[j] >> 16), bf16_to_f32(j ? cw >> 16 : cw & 0xFFFF),
+                 bf16_to_f32(j ? sw >> 16 : sw & 0xFFFF), o1, o2);
+    ow[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+  }
+  store_lane<2>(reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.kpe) + crow * kP) + 2 * l16, ow);
+}
+
+// ---------------------------------------------------------------------------
 // Kernel 2 (fp32 models): the same maths on the VALU in fp32.  One block of
 // 256 threads per (row, split); 16-token tiles staged in LDS.
 // ---------------------------------------------------------------------------
@@ -352,6 +443,17 @@ namespace swamla {
 int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s) {
   const dim3 grid((a.n_tok + 3) / 4), block(256);
   if (a.n_tok == 0) return 0;
+  // bf16 rows of 256 padded channels whose vectors are 16-byte aligned: four
+  // tokens per wavefront
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (in_dt == 1 && (c_dt == 1 || c_dt == 2) && padded_rank(a.R) == 256 && a16(a.kv_in) && a.in_rs % 8 == 0 &&
+      a16(a.ln_w) && a16(a.ln_b) && (reinterpret_cast<uintptr_t>(a.cos_tab) & 3) == 0 &&
+      (reinterpret_cast<uintptr_t>(a.sin_tab) & 3) == 0) {
+    const dim3 g16((a.n_tok + 15) / 16);
+    if (c_dt == 1) hipLaunchKernelGGL(mla_append_g16_kernel<1>, g16, block, 0, s, a);
+    else hipLaunchKernelGGL(mla_append_g16_kernel<2>, g16, block, 0, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+  }
   const int rc = with_nb(a.R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value;
     if (in_dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_append_kernel<1, 1, NB>), grid, block, 0, s, a);
