@@ -32,11 +32,12 @@ int ok() {
 
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
-int check_geometry(int32_t H, int32_t R, int32_t P) {
-  if (H != 16 || P != 64 || R < 1 || R > 64 * swamla::kMaxNB)
+// allow32: the entry point also runs 32 heads in one launch.
+int check_geometry(int32_t H, int32_t R, int32_t P, bool allow32 = false) {
+  if ((H != 16 && !(allow32 && H == 32)) || P != 64 || R < 1 || R > 64 * swamla::kMaxNB)
     return fail(SWAMLA_ERR_UNSUPPORTED,
-                "unsupported geometry H=%d R=%d P=%d (this build: H=16, P=64, 1 <= R <= %d)", H, R, P,
-                64 * swamla::kMaxNB);
+                "unsupported geometry H=%d R=%d P=%d (this build: H=16%s, P=64, 1 <= R <= %d)", H, R, P,
+                allow32 ? " or 32" : "", 64 * swamla::kMaxNB);
   return SWAMLA_OK;
 }
 
@@ -192,8 +193,11 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
                  int32_t R, int32_t P, float sm_scale, int32_t n_splits, int32_t min_chunk, int32_t balance,
                  int32_t* plan, float* o_part, float* lse_part, void* o_lat, int64_t o_rs, int64_t o_hs,
                  float* lse_out, int32_t dtype, int32_t cache_dtype, swamla::DecodeArgs* a,
-                 int32_t max_rows = 65535) {
-  if (int e = check_geometry(H, R, P)) return e;
+                 int32_t max_rows = 65535, bool allow32 = false) {
+  if (int e = check_geometry(H, R, P, allow32)) return e;
+  if (H == 32 && (dtype != SWAMLA_DTYPE_BF16 || cache_dtype != SWAMLA_DTYPE_BF16 || swamla::padded_rank(R) > 256))
+    return fail(SWAMLA_ERR_UNSUPPORTED,
+                "%s: 32 heads in one launch are built for a bf16 model and cache with kv_lora_rank <= 256", fn);
   if (int e = check_pair(dtype, cache_dtype)) return e;
   if (n_rows < 0 || n_rows > max_rows)
     return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_rows=%d outside [0, %d]", fn, n_rows, max_rows);
@@ -251,6 +255,7 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
                           cache_batch, cache_seq, ad,      n_rows,    sm_scale * log2e, n_splits,
                           min_chunk, balance,   plan,      o_part,    lse_part,  o_lat,
                           o_rs,      o_hs,      lse_out,   swamla::AppendArgs{}};
+  a->H = H;
   return SWAMLA_OK;
 }
 
@@ -273,7 +278,7 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const
                            sin_tab, rope_len, ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, row_seq,
                            kv_len, q_rope_pos, start_pos, rows_per_seq, rope_abs, n_rows, H, R, P, sm_scale,
                            n_splits, min_chunk, balance_blocks, plan, o_part, lse_part, o_lat, o_rs, o_hs, lse_out,
-                           dtype, cache_dtype, &a))
+                           dtype, cache_dtype, &a, 65535, true))
     return e;
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_attn: no kernel for this dtype pair");
@@ -300,7 +305,7 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
                            ckv_cache, kpe_cache, ckv_scale, cache_batch, cache_seq, nullptr, nullptr, nullptr,
                            start_pos, 1, rope_abs, n_rows, H, R, P, sm_scale, n_splits, min_chunk,
                            balance_blocks, plan, o_part, lse_part, o_lat, o_rs, o_hs, lse_out, dtype, cache_dtype,
-                           &a))
+                           &a, 65535, true))
     return e;
   if (n_rows > 0 && !kv_in) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null input rows", fn);
   if (!ln_w || !ln_b) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null LayerNorm pointer", fn);
@@ -415,7 +420,7 @@ int mla_merge(const float* o_part, const float* lse_part, const int32_t* row_seq
               const int32_t* start_pos, int32_t rows_per_seq, int64_t cache_batch, int64_t cache_seq,
               int32_t n_rows, int32_t H, int32_t R, int32_t n_splits, int32_t min_chunk, const int32_t* plan,
               void* o_lat, int64_t o_rs, int64_t o_hs, float* lse_out, int32_t dtype, void* stream) {
-  if (int e = check_geometry(H, R, 64)) return e;
+  if (int e = check_geometry(H, R, 64, true)) return e;
   if (!model_elem(dtype)) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: dtype %d not built", dtype);
   if (n_rows < 0 || n_rows > 65535)
     return fail(SWAMLA_ERR_INVALID_ARG, "mla_merge: n_rows=%d outside [0, 65535]", n_rows);
@@ -437,6 +442,7 @@ int mla_merge(const float* o_part, const float* lse_part, const int32_t* row_seq
     return fail(SWAMLA_ERR_MISALIGNED, "mla_merge: misaligned partials, plan or output");
   swamla::MergeArgs a{o_part, lse_part, ad,   cache_batch, cache_seq, n_rows, n_splits,
                       min_chunk, plan, R, o_lat, o_rs, o_hs, lse_out};
+  a.H = H;
   const int rc = swamla::launch_merge(a, dtype, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge: no kernel for dtype %d", dtype);
   if (rc != 0) return hip_fail("mla_merge");
@@ -512,7 +518,7 @@ int mla_merge_project(const float* o_part, const float* lse_part, const void* o_
                       int32_t min_chunk, const int32_t* plan, const void* w, int64_t w_rs, int64_t w_hs,
                       int32_t Dv,
                       void* y, int64_t y_rs, int64_t y_hs, int32_t dtype, void* stream) {
-  if (int e = check_geometry(H, R, 64)) return e;
+  if (int e = check_geometry(H, R, 64, true)) return e;
   if (dtype != SWAMLA_DTYPE_BF16)
     return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge_project: dtype %d not built (bf16 only)", dtype);
   if (Dv != 128) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge_project: Dv=%d (this build: 128)", Dv);
@@ -540,6 +546,7 @@ int mla_merge_project(const float* o_part, const float* lse_part, const void* o_
                 "mla_merge_project: o_lat and w need 16-byte aligned bases and strides that are multiples of 8");
   swamla::MergeProjectArgs a{o_part, lse_part, o_lat, o_rs, o_hs, ad, cache_batch, cache_seq, n_rows,
                              n_splits, min_chunk, plan, R, w, w_rs, w_hs, y, y_rs, y_hs};
+  a.H = H;
   const int rc = swamla::launch_merge_project(a, static_cast<hipStream_t>(stream));
   if (rc != 0) return hip_fail("mla_merge_project");
   return ok();

@@ -76,6 +76,7 @@ struct DecodeArgs {
   // fa.ad is always this launch's `ad` (dense, T = 1): the kernel derives the
   // token's position from the row's.
   AppendArgs fa;
+  int H = 16;  // query heads: 16, or 32 (bf16 model and cache: one launch of two head groups)
 };
 
 struct MergeArgs {
@@ -89,6 +90,7 @@ struct MergeArgs {
   void* o_lat;
   int64_t o_rs, o_hs;
   float* lse_out;
+  int H = 16;  // heads of the partials ([rows, splits, H, R_pad]) and outputs
 };
 
 // Batched small-row linear layer: Y[b] = X[b] W[b]^T (+ bias[b]), bf16.
@@ -121,6 +123,7 @@ struct MergeProjectArgs {
   int64_t w_rs, w_hs;
   void* y;
   int64_t y_rs, y_hs;
+  int H = 16;  // heads of the partials ([rows, splits, H, R_pad]) and of y
 };
 
 int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s);

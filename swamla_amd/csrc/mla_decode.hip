@@ -80,8 +80,9 @@ __device__ __forceinline__ int swp(int t) { return (t >> 1) & 7; }
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
-// Geometry of one instance (cache dtype, R_pad = 64 NB).
-template <int C_DT, int NB>
+// Geometry of one instance (cache dtype, R_pad = 64 NB, HG head groups of 16
+// heads: 4 HG waves per workgroup).
+template <int C_DT, int NB, int HG = 1>
 struct DecGeo {
   static constexpr int RP = 64 * NB;
   static constexpr int kLat = C_DT == 2 ? kSubTok * RP : kSubTok * 2 * RP;  // latent bytes of a sub-tile
@@ -94,10 +95,12 @@ struct DecGeo {
   // processed, at most kCap more are in flight.  Fewer bytes in flight stream
   // faster here: 2 and 2 (three buffers) against 3 and 3 (four buffers)
   // measured 18.1 against 18.4-18.9 us per config-2 launch, and 89.9
-  // against 90.6-91.1 us at config 5 (e4m3).
-  static constexpr int kFillWant = 2, kCapWant = 2;
+  // against 90.6-91.1 us at config 5 (e4m3).  Two head groups (eight waves)
+  // keep one sub-tile in flight: two buffers per wave fill the 160 KB.
+  static constexpr int kWavesWG = kDecWaves * HG;
+  static constexpr int kFillWant = HG == 1 ? 2 : 1, kCapWant = HG == 1 ? 2 : 1;
   static constexpr int NBUF =
-      cmin(cmin(cmax(kCapWant + 1, kFillWant), (kLdsMax / kDecWaves - kStage) / kSub), 63 / kVm + 1);
+      cmin(cmin(cmax(kCapWant + 1, kFillWant), (kLdsMax / kWavesWG - kStage) / kSub), 63 / kVm + 1);
   static constexpr int kCap = cmin(kCapWant, NBUF - 1);
   static constexpr int kFill = cmin(kFillWant, NBUF);
   // The fused append's LayerNorm stages its row in a ring buffer the fill
@@ -108,7 +111,7 @@ struct DecGeo {
   // (+4 pad) and then its max / l / e per head
   static constexpr int kCombRow = RP + 4;
   static constexpr int kStash = (kH * kCombRow + 3 * kH) * 4;
-  static constexpr int kLds = kDecWaves * kWave;
+  static constexpr int kLds = kWavesWG * kWave;
   static_assert(NBUF >= 2, "a sub-tile ring needs two buffers");
   static_assert(ln_stage_bytes<1>() <= kSub, "the fused LayerNorm stages its row in a ring buffer");
   static_assert(kCap >= 1 && kFill >= 1 && kCap <= NBUF - 1, "ring depth");
@@ -198,9 +201,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 // instructions: bf16 rows with their 16-byte chunks swizzled (slot s of row
 // tt holds chunk s ^ swz(tt), rope rows ^ swp(tt)), e4m3 code rows as they
 // lie.  A sub-tile past the split's end re-reads its last row (in bounds).
-template <int C_DT, int NB>
+template <int C_DT, int NB, int HG = 1>
 struct SubStream {
-  using G = DecGeo<C_DT, NB>;
+  using G = DecGeo<C_DT, NB, HG>;
   static constexpr int kLatQ = G::kLat / 1024;
   static constexpr int kLatRow = C_DT == 2 ? G::RP : 2 * G::RP;  // bytes of a latent cache row
   int t0, t_last, rem, my_n, j_base, w;
@@ -274,14 +277,19 @@ struct SubStream {
 
 }  // namespace
 
-template <int C_DT, bool FUSE, int NB>
-__global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a) {
-  using G = DecGeo<C_DT, NB>;
+template <int C_DT, bool FUSE, int NB, int HG>
+__global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeArgs a) {
+  using G = DecGeo<C_DT, NB, HG>;
   constexpr int RP = G::RP, NBUF = G::NBUF;
+  constexpr int HT = kH * HG;  // heads of the launch
   __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[G::kLds];
   lds_u8* const lds = (lds_u8*)(lds_raw);  // the LDS address space, for the DMA and typed LDS access
 
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Waves 4 hg .. 4 hg + 3 serve heads 16 hg .. 16 hg + 15: each head group
+  // streams the split into its own rings (the second group's reads of the
+  // same lines are L2 hits) and runs its own online softmax.
+  const int wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup
+  const int hg = wg / kDecWaves, w = wg % kDecWaves;               // head group, wave in it
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   if constexpr (FUSE) {
@@ -312,11 +320,11 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   // 32 kb + 8 g); issued before anything waits.  These and the other loads
   // ahead of the first tile are vm_load()s, released after the explicit wait
   // below.
-  const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + r * a.qa_rs + n * a.qa_hs;
+  const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + r * a.qa_rs + (kH * hg + n) * a.qa_hs;
   uint32_t qraw[2 * NB][4];
 #pragma unroll
   for (int s = 0; s < 2 * NB; ++s) vm_load<4>(qa + 32 * s + 8 * g, qraw[s]);
-  const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + r * a.qp_rs + n * a.qp_hs;
+  const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + r * a.qp_rs + (kH * hg + n) * a.qp_hs;
   uint32_t praw[2][4];
 #pragma unroll
   for (int s = 0; s < 2; ++s) vm_load<4>(qp + 32 * s + 8 * g, praw[s]);
@@ -338,9 +346,9 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   const int64_t row0 = static_cast<int64_t>((b < 0 || b >= a.cache_b) ? 0 : b) * a.cache_s;
 
   // ---- this wave's sub-tiles; wave w's k-th goes to ring buffer k % NBUF
-  lds_u8* const wave_lds = lds + w * G::kWave;
+  lds_u8* const wave_lds = lds + wg * G::kWave;
   lds_u8* const stage = wave_lds + NBUF * G::kSub;  // e4m3 only
-  const SubStream<C_DT, NB> ss(t0, t1, w, lane, row0, a.ckv, a.kpe, a.ckv_scale, wave_lds);
+  const SubStream<C_DT, NB, HG> ss(t0, t1, w, lane, row0, a.ckv, a.kpe, a.ckv_scale, wave_lds);
   const int rem = ss.rem, my_n = ss.my_n;
   auto sub_of = [&](int k) { return ss.sub_of(k); };
   auto issue = [&](int k) { ss.issue(k, lane); };
@@ -388,6 +396,8 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
       }
     }
   }
+  // the wave holding the new token's sub-tile, in each head group (each
+  // computes the token's row, the same bits; head group 0 stores it)
   const bool fa_wave = FUSE && fa_own && w == fa_w;  // wave-uniform
   FusedIn<NB> fin;
   if constexpr (FUSE)
@@ -609,7 +619,8 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
     process(k, false);
   }
   if constexpr (FUSE)
-    if (fa_wave) fused_store<C_DT, NB>(a.fa, static_cast<int64_t>(fa_a.b) * a.fa.cache_s + fa_a.pos, ftok, lane);
+    if (fa_wave && hg == 0)
+      fused_store<C_DT, NB>(a.fa, static_cast<int64_t>(fa_a.b) * a.fa.cache_s + fa_a.pos, ftok, lane);
 
   // ---- combine the four waves: per head max, sum and O (fixed order)
   float l_w = l_part + shfl_xor_f32(l_part, 16);
@@ -619,7 +630,8 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   // The wave's ring is free once its own loads have landed: it stashes its
   // O^T rows and per-head max / l / e there, without waiting for the others.
   wait_vm<0>();  // (the ring's loads past the wave's own sub-tiles included)
-  auto stash_of = [&](int v) { return reinterpret_cast<float*>(lds_raw + v * G::kWave); };
+  // (stash_of(v): wave v of this head group)
+  auto stash_of = [&](int v) { return reinterpret_cast<float*>(lds_raw + (kDecWaves * hg + v) * G::kWave); };
   float* const mine = stash_of(w);
   if (g == 0) {
     mine[kH * G::kCombRow + n] = m_run;
@@ -633,10 +645,10 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
         make_float4(oacc[mb][0], oacc[mb][1], oacc[mb][2], oacc[mb][3]);
   __syncthreads();  // every wave's stash is written
 
-  // wave w finishes heads 4w .. 4w + 3: lane -> head 4w + g, channels
-  // 64 i + 4 n .. +4 for i < NB (the 16 lanes of a head read and write
-  // consecutive 16-byte pieces)
-  const int h = kDecWaves * w + g;
+  // wave w finishes heads 4w .. 4w + 3 of its group: lane -> head 4w + g,
+  // channels 64 i + 4 n .. +4 for i < NB (the 16 lanes of a head read and
+  // write consecutive 16-byte pieces); hh is the head in the launch
+  const int h = kDecWaves * w + g, hh = kH * hg + h;
   float mw[kDecWaves], lw[kDecWaves], ew[kDecWaves];
   float M = -INFINITY;
 #pragma unroll
@@ -673,7 +685,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
   }
   const float lse2 = Etot > 0.f ? M + __log2f(Etot) : -INFINITY;  // log2 domain
   if (ns <= 1) {
-    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + h * a.o_hs + c0;
+    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + hh * a.o_hs + c0;
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       uint2 pk;
@@ -681,12 +693,12 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
       pk.y = pack_bf16x2(o[4 * i + 2] * inv, o[4 * i + 3] * inv);
       *reinterpret_cast<uint2*>(op + 64 * i) = pk;
     }
-    if (a.lse_out && n == 0) a.lse_out[static_cast<int64_t>(r) * kH + h] = lse2 * kLn2;
+    if (a.lse_out && n == 0) a.lse_out[static_cast<int64_t>(r) * HT + hh] = lse2 * kLn2;
     return;
   }
   // partials: non-temporal stores (every workgroup writes at its end, and the
   // merge reads them in the next launch, from another XCD's view of memory)
-  const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * kH + h;
+  const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * HT + hh;
   float* op = a.o_part + pidx * RP + c0;
 #pragma unroll
   for (int i = 0; i < NB; ++i)
@@ -728,7 +740,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_stream_probe(DecodeArgs
     const int t1 = min(L, t0 + rsp.chunk);
     const int64_t row0 = static_cast<int64_t>(b) * a.cache_s;
     lds_u8* const wave_lds = lds + w * G::kWave;
-    const SubStream<C_DT, NB> ss(t0, t1, w, lane, row0, a.ckv, a.kpe, a.ckv_scale, wave_lds);
+    const SubStream<C_DT, NB, 1> ss(t0, t1, w, lane, row0, a.ckv, a.kpe, a.ckv_scale, wave_lds);
 #pragma unroll
     for (int k = 0; k < G::kFill; ++k) ss.issue(k, lane);
     for (int k = 0; k < ss.my_n; ++k) {  // uniform
@@ -748,12 +760,25 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_stream_probe(DecodeArgs
 // Launchers behind the C-ABI (argument validation lives in mla_abi.cpp).
 // ===========================================================================
 namespace {
+// The instance for (cache dtype, fused append, head groups): two head groups
+// (32 heads) are built for the bf16 cache at R_pad <= 256, where the rings of
+// eight waves fit the LDS.
 template <int NB>
-const void* decode_kernel(int c_dt, bool fuse) {
-  if (c_dt == 1 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<1, false, NB>);
-  if (c_dt == 2 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<2, false, NB>);
-  if (c_dt == 1) return reinterpret_cast<const void*>(&mla_decode_dma<1, true, NB>);
-  if (c_dt == 2) return reinterpret_cast<const void*>(&mla_decode_dma<2, true, NB>);
+const void* decode_kernel(int c_dt, bool fuse, int hg) {
+  if (hg == 2) {
+    if constexpr (NB <= 4) {
+      if (c_dt != 1) return nullptr;
+      return fuse ? reinterpret_cast<const void*>(&mla_decode_dma<1, true, NB, 2>)
+                  : reinterpret_cast<const void*>(&mla_decode_dma<1, false, NB, 2>);
+    } else {
+      return nullptr;
+    }
+  }
+  if (hg != 1) return nullptr;
+  if (c_dt == 1 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<1, false, NB, 1>);
+  if (c_dt == 2 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<2, false, NB, 1>);
+  if (c_dt == 1) return reinterpret_cast<const void*>(&mla_decode_dma<1, true, NB, 1>);
+  if (c_dt == 2) return reinterpret_cast<const void*>(&mla_decode_dma<2, true, NB, 1>);
   return nullptr;
 }
 }  // namespace
@@ -761,18 +786,19 @@ const void* decode_kernel(int c_dt, bool fuse) {
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
   if (dt == 0) {
-    if (c_dt != 0 || a.fa.kv_in != nullptr) return -1;
+    if (c_dt != 0 || a.fa.kv_in != nullptr || a.H != kH) return -1;
     return launch_decode_f32(a, s);
   }
-  if (dt != 1) return -1;
+  if (dt != 1 || a.H % kH != 0) return -1;
+  const int hg = a.H / kH;
   const dim3 grid = a.balance > 0 ? dim3(a.balance, 1) : dim3(a.n_splits, a.n_rows);
   const bool fuse = a.fa.kv_in != nullptr;
   const int rc = with_nb(a.R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value;
-    const void* fn = decode_kernel<NB>(c_dt, fuse);
+    const void* fn = decode_kernel<NB>(c_dt, fuse, hg);
     if (!fn) return -1;
     void* args[] = {const_cast<DecodeArgs*>(&a)};
-    return hipLaunchKernel(fn, grid, dim3(kDecWaves * 64), args, 0, s) == hipSuccess ? 0 : -2;
+    return hipLaunchKernel(fn, grid, dim3(kDecWaves * 64 * hg), args, 0, s) == hipSuccess ? 0 : -2;
   });
   if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;
@@ -800,7 +826,7 @@ int decode_blocks_per_cu(int dt, int c_dt, int R, bool fuse, int* blocks) {
   if (dt != 1) return -1;
   return with_nb(R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value;
-    const void* fn = decode_kernel<NB>(c_dt, fuse);
+    const void* fn = decode_kernel<NB>(c_dt, fuse, 1);
     if (!fn) return -1;
     int nblk = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nblk, fn, kDecWaves * 64, 0) != hipSuccess || nblk < 1)

@@ -346,11 +346,11 @@ template <int DT, bool TWO>
 __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
   const int h = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
   const int rp = 64 * ((a.R + 63) / 64);
-  const int64_t base = static_cast<int64_t>(r) * a.n_splits * kH + h;  // (row, split 0, head) slot
+  const int64_t base = static_cast<int64_t>(r) * a.n_splits * a.H + h;  // (row, split 0, head) slot
   const int plan = a.plan ? *a.plan : 0;
   const int L = clamped_row_len(a.ad, r, a.cache_b, a.cache_s);
   const int last = a.n_splits - 1;
-  const float le = a.lse_part[base + static_cast<int64_t>(min(lane, last)) * kH];
+  const float le = a.lse_part[base + static_cast<int64_t>(min(lane, last)) * a.H];
   const int c0 = 4 * lane, c1 = c0 + 256;
   const bool on0 = c0 < rp, on1 = c1 < rp;
   // channels read: a lane past the row re-reads channel 0 (its sums are not stored)
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
   auto load_group = [&](int g, int s_max) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float* p = a.o_part + (base + static_cast<int64_t>(min(g + j, s_max)) * kH) * rp;
+      const float* p = a.o_part + (base + static_cast<int64_t>(min(g + j, s_max)) * a.H) * rp;
       v[j] = *reinterpret_cast<const float4*>(p + c0r);
       u[j] = z;
       if constexpr (TWO) u[j] = *reinterpret_cast<const float4*>(p + c1r);
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
   const int ns = min(row_splits(L, a.n_splits, a.min_chunk, plan).ns, a.n_splits);
   if (ns <= 1) return;
 
-  auto lse_of = [&](int s) { return s < ns ? a.lse_part[base + static_cast<int64_t>(s) * kH] : -INFINITY; };
+  auto lse_of = [&](int s) { return s < ns ? a.lse_part[base + static_cast<int64_t>(s) * a.H] : -INFINITY; };
   const float l0 = lane < ns ? le : -INFINITY;
   float M = l0;
   for (int s = lane + 64; s < ns; s += 64) M = fmaxf(M, lse_of(s));
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
   };
   if (on0) store(c0, a0);
   if (TWO && on1) store(c1, a1);
-  if (a.lse_out && lane == 0) a.lse_out[static_cast<int64_t>(r) * kH + h] = M + __logf(tot);
+  if (a.lse_out && lane == 0) a.lse_out[static_cast<int64_t>(r) * a.H + h] = M + __logf(tot);
 }
 
 }  // namespace swamla
@@ -493,7 +493,7 @@ int decode_f32_blocks_per_cu(int R, int* blocks) {
 
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s) {
   if (a.n_rows == 0 || a.n_splits <= 1) return 0;
-  const dim3 grid(kH, a.n_rows), block(64);
+  const dim3 grid(a.H, a.n_rows), block(64);
   const bool two = a.R > 256;  // the padded row spans a second 256-channel chunk
   if (dt == 1 && two) hipLaunchKernelGGL((mla_merge_kernel<1, true>), grid, block, 0, s, a);
   else if (dt == 1) hipLaunchKernelGGL((mla_merge_kernel<1, false>), grid, block, 0, s, a);

@@ -132,7 +132,8 @@ __global__ __launch_bounds__(NW * 64) void mla_linear_kernel(LinearArgs a) {
 // ---------------------------------------------------------------------------
 template <int DV, int ROWS, int NB, int G>
 __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs a) {
-  constexpr int R = 64 * NB, H = 16;  // R: the padded latent width R_pad
+  constexpr int R = 64 * NB;  // R: the padded latent width R_pad
+  const int H = a.H;          // heads (16 or 32)
   constexpr int kMpXRow = 2 * R + 16;  // LDS bytes per merged row (padded)
   constexpr int kTilesPerWave = DV / 16 / 4;
   static_assert(ROWS == 2 || ROWS == 4 || ROWS == 8, "rows per block");
@@ -142,12 +143,12 @@ __global__ __launch_bounds__(256) void mla_merge_project_kernel(MergeProjectArgs
   __shared__ __attribute__((aligned(16))) float comb_a[G > 1 ? G * ROWS * R : 4];
   // XCD-aware block order: workgroups go to the 8 XCDs round-robin by linear
   // id, so id -> (XCD id % 8, slot id / 8) -> head-major index m gives each
-  // XCD the blocks of 2 whole heads, and each XCD's L2 fetches only those
+  // XCD the blocks of H / 8 whole heads, and each XCD's L2 fetches only those
   // heads' W_uv (instead of every head's: 8 MB of fetches at 16 heads).
-  // The grid has 16 gx blocks, a multiple of 8.
+  // The grid has H gx blocks, a multiple of 8.
   const int gx = gridDim.x;
   const int id = blockIdx.y * gx + blockIdx.x;
-  const int m = (id & 7) * (2 * gx) + (id >> 3);
+  const int m = (id & 7) * ((H >> 3) * gx) + (id >> 3);
   const int h = m / gx, r0 = (m - h * gx) * ROWS;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -598,8 +599,8 @@ int launch_merge_project(const MergeProjectArgs& a, hipStream_t s) {
   if (a.n_rows == 0) return 0;
   // rows per block: about one (rows, head) block per CU; every block reads
   // its head's whole W_uv slice, so fewer rows mean more re-reads of it
-  const int rows = a.n_rows * 16 <= 2 * 256 ? 2 : (a.n_rows * 16 <= 4 * 256 ? 4 : 8);
-  const dim3 grid((a.n_rows + rows - 1) / rows, 16), block(256);
+  const int rows = a.n_rows * a.H <= 2 * 256 ? 2 : (a.n_rows * a.H <= 4 * 256 ? 4 : 8);
+  const dim3 grid((a.n_rows + rows - 1) / rows, a.H), block(256);
   const int rc = with_nb(a.R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value;
     // more than 8 splits per row: every wave of the block takes a share of them

@@ -17,6 +17,10 @@ import torch
 from . import _abi
 
 R, P, H = 256, 64, 16  # R: the default kv_lora_rank (any 1..MAX_RANK is built)
+# Heads one decode launch takes: 16, or 32 for a bf16 model and cache with
+# R_pad <= 256 (two head groups in one workgroup, each cache tile streamed once
+# per workgroup for both).
+DECODE_HEADS = (16, 32)
 MAX_RANK = 512
 
 
@@ -284,17 +288,17 @@ class DecodeWorkspace:
     plan: torch.Tensor
 
     @staticmethod
-    def allocate(n_rows: int, n_splits: int, device, rank: int = R) -> "DecodeWorkspace":
+    def allocate(n_rows: int, n_splits: int, device, rank: int = R, heads: int = H) -> "DecodeWorkspace":
         rows = max(n_rows, 1)
         return DecodeWorkspace(
-            torch.empty(rows, n_splits, H, padded_rank(rank), dtype=torch.float32, device=device),
-            torch.empty(rows, n_splits, H, dtype=torch.float32, device=device),
+            torch.empty(rows, n_splits, heads, padded_rank(rank), dtype=torch.float32, device=device),
+            torch.empty(rows, n_splits, heads, dtype=torch.float32, device=device),
             torch.zeros(1, dtype=torch.int32, device=device),
         )
 
-    def fits(self, n_rows: int, n_splits: int, rank: int = R) -> bool:
+    def fits(self, n_rows: int, n_splits: int, rank: int = R, heads: int = H) -> bool:
         return (self.o_part.shape[0] >= n_rows and self.o_part.shape[1] == n_splits
-                and self.o_part.shape[3] == padded_rank(rank))
+                and self.o_part.shape[2] == heads and self.o_part.shape[3] == padded_rank(rank))
 
 
 @dataclass
@@ -338,7 +342,9 @@ def decode_attention(
     """Absorbed attention of query rows over the latent cache (+ merge).
 
     q_abs [rows, H, R_pad] (channels >= the cache's rank are ignored) and
-    q_pe [rows, H, P] may be strided views (unit last stride).  Addressing:
+    q_pe [rows, H, P] may be strided views (unit last stride); H is 16, or
+    32 for a bf16 model and cache at R_pad <= 256 (one launch of two head
+    groups: the cache is streamed once for both).  Addressing:
     explicit (row_seq, kv_len, q_rope_pos) or dense (start_pos [rows /
     rows_per_seq], causal).  Returns o_lat [rows, H, R_pad], whose padding
     channels are 0 (``out`` may be a strided view, e.g. a transpose of a
@@ -360,23 +366,26 @@ def decode_attention(
     dt = cache.model_dtype
     rows = q_abs.shape[0]
     rk, rp = cache.rank, cache.rank_pad
-    if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (H, rp) or q_abs.stride(2) != 1:
-        raise ValueError(f"q_abs must be [rows, {H}, {rp}] (R_pad) with unit last stride")
-    if q_pe.dim() != 3 or tuple(q_pe.shape) != (rows, H, P) or q_pe.stride(2) != 1:
-        raise ValueError(f"q_pe must be [rows, {H}, {P}] with unit last stride")
+    nh = q_abs.shape[1] if q_abs.dim() == 3 else H
+    if nh not in DECODE_HEADS:
+        raise ValueError(f"q_abs has {nh} heads; one decode launch takes {DECODE_HEADS}")
+    if q_abs.dim() != 3 or tuple(q_abs.shape[1:]) != (nh, rp) or q_abs.stride(2) != 1:
+        raise ValueError(f"q_abs must be [rows, {nh}, {rp}] (R_pad) with unit last stride")
+    if q_pe.dim() != 3 or tuple(q_pe.shape) != (rows, nh, P) or q_pe.stride(2) != 1:
+        raise ValueError(f"q_pe must be [rows, {nh}, {P}] with unit last stride")
     if q_abs.dtype != dt or q_pe.dtype != dt or cos_tab.dtype != dt:
         raise TypeError(f"query and RoPE tensors must be {dt}")
     (p_seq, p_len, p_rope), p_sp = _addressing(
         rows, (row_seq, kv_len, q_rope_pos), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
     if out is None:
-        out = torch.empty(rows, H, rp, dtype=dt, device=dev)
-    if tuple(out.shape) != (rows, H, rp) or out.stride(2) != 1 or out.dtype != dt:
+        out = torch.empty(rows, nh, rp, dtype=dt, device=dev)
+    if tuple(out.shape) != (rows, nh, rp) or out.stride(2) != 1 or out.dtype != dt:
         raise ValueError("out must be [rows, H, R_pad] in the model dtype with unit last stride")
     if n_splits > 1:
         if workspace is None:
-            workspace = DecodeWorkspace.allocate(rows, n_splits, dev, rank=rk)
-        if not workspace.fits(rows, n_splits, rk):
-            raise ValueError("workspace does not fit (rows, n_splits, rank)")
+            workspace = DecodeWorkspace.allocate(rows, n_splits, dev, rank=rk, heads=nh)
+        if not workspace.fits(rows, n_splits, rk, nh):
+            raise ValueError("workspace does not fit (rows, n_splits, heads, rank)")
     plan = workspace.plan if (balance > 0 and workspace is not None) else None
     lib = _abi.lib()
     stream = _abi.stream_handle(dev)
@@ -402,7 +411,7 @@ def decode_attention(
                 cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
                 cache.ckv.shape[0], cache.ckv.shape[1], p_sp, int(bool(rope_abs)),
-                rows, H, rk, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
+                rows, nh, rk, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
                 _abi.ptr(workspace.o_part if workspace else None),
                 _abi.ptr(workspace.lse_part if workspace else None),
                 out.data_ptr(), out.stride(0), out.stride(1), _abi.ptr(lse_out),
@@ -418,7 +427,7 @@ def decode_attention(
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
                 cache.ckv.shape[0], cache.ckv.shape[1],
                 p_seq, p_len, p_rope, p_sp, int(rows_per_seq), int(bool(rope_abs)),
-                rows, H, rk, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
+                rows, nh, rk, P, float(sm_scale), n_splits, min_chunk, int(balance), _abi.ptr(plan),
                 _abi.ptr(workspace.o_part if workspace else None),
                 _abi.ptr(workspace.lse_part if workspace else None),
                 out.data_ptr(), out.stride(0), out.stride(1), _abi.ptr(lse_out),
@@ -429,7 +438,7 @@ def decode_attention(
         _abi.check(
             lib.mla_merge(
                 workspace.o_part.data_ptr(), workspace.lse_part.data_ptr(), p_seq, p_len, p_sp,
-                int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1], rows, H, rk, n_splits, min_chunk,
+                int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1], rows, nh, rk, n_splits, min_chunk,
                 _abi.ptr(plan), out.data_ptr(), out.stride(0), out.stride(1),
                 _abi.ptr(lse_out), _abi.dtype_code(dt), stream,
             )
@@ -690,17 +699,20 @@ def merge_project(
     rows = o_lat.shape[0]
     Dv = w_uv.shape[1]
     rk, rp = cache.rank, cache.rank_pad
-    if o_lat.dim() != 3 or tuple(o_lat.shape[1:]) != (H, rp) or o_lat.stride(2) != 1:
-        raise ValueError(f"o_lat must be [rows, {H}, {rp}] (R_pad) with unit last stride")
-    if w_uv.dim() != 3 or tuple(w_uv.shape) != (H, Dv, rp) or w_uv.stride(2) != 1:
-        raise ValueError(f"w_uv must be [{H}, Dv, {rp}] (R_pad) with unit last stride")
-    if tuple(out.shape) != (rows, H, Dv) or out.stride(2) != 1:
-        raise ValueError(f"out must be [{rows}, {H}, {Dv}] with unit last stride")
+    nh = o_lat.shape[1] if o_lat.dim() == 3 else H
+    if nh not in DECODE_HEADS:
+        raise ValueError(f"o_lat has {nh} heads; merge_project takes {DECODE_HEADS}")
+    if o_lat.dim() != 3 or tuple(o_lat.shape[1:]) != (nh, rp) or o_lat.stride(2) != 1:
+        raise ValueError(f"o_lat must be [rows, {nh}, {rp}] (R_pad) with unit last stride")
+    if w_uv.dim() != 3 or tuple(w_uv.shape) != (nh, Dv, rp) or w_uv.stride(2) != 1:
+        raise ValueError(f"w_uv must be [{nh}, Dv, {rp}] (R_pad) with unit last stride")
+    if tuple(out.shape) != (rows, nh, Dv) or out.stride(2) != 1:
+        raise ValueError(f"out must be [{rows}, {nh}, {Dv}] with unit last stride")
     if not (o_lat.dtype == w_uv.dtype == out.dtype == torch.bfloat16):
         raise TypeError("merge_project: bf16 tensors only")
     (p_seq, p_len, _), p_sp = _addressing(
         rows, (row_seq, kv_len, None), start_pos, rows_per_seq, ("row_seq", "kv_len", "q_rope_pos"))
-    if (n_splits > 1 or balanced) and (workspace is None or not workspace.fits(rows, n_splits, rk)):
+    if (n_splits > 1 or balanced) and (workspace is None or not workspace.fits(rows, n_splits, rk, nh)):
         raise ValueError("merge_project needs the decode call's workspace")
     _abi.check(
         _abi.lib().mla_merge_project(
@@ -708,7 +720,7 @@ def merge_project(
             _abi.ptr(workspace.lse_part if n_splits > 1 else None),
             o_lat.data_ptr(), o_lat.stride(0), o_lat.stride(1),
             p_len, p_seq, p_sp, int(rows_per_seq), cache.ckv.shape[0], cache.ckv.shape[1],
-            rows, H, rk, n_splits, min_chunk, _abi.ptr(workspace.plan if balanced else None),
+            rows, nh, rk, n_splits, min_chunk, _abi.ptr(workspace.plan if balanced else None),
             w_uv.data_ptr(), w_uv.stride(1), w_uv.stride(0), Dv,
             out.data_ptr(), out.stride(0), out.stride(1), _abi.DTYPE_BF16, _abi.stream_handle(dev),
         )

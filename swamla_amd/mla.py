@@ -21,9 +21,11 @@ What runs where (per forward, bf16 model):
     mla_head_product   q_abs = q_nope . W_uk and o = o_lat . W_uv^T
     mla_append, then mla_prefill_attn (or mla_decode_attn + mla_merge)
   fp32 models use the ATen products and batched absorption around mla_append
-  and the fp32 decode kernel.  The attention launches take 16 heads each:
-  other head counts run as ceil(H / 16) launches over zero-padded query heads
-  (the fused decode step is built for 16 heads).
+  and the fp32 decode kernel.  The attention launches take 16 heads each,
+  and a bf16 decode launch over a bf16 cache of R_pad <= 256 also 32 (two head
+  groups in one workgroup, the cache streamed once for both): other head
+  counts run as ceil(H / 16) launches over zero-padded query heads (the fused
+  decode step is built for 16 and 32 heads).
 
 Differences from the reference, all deliberate:
   * attention is absorbed: the reference re-projects the whole cache through
@@ -433,11 +435,21 @@ class MLA(nn.Module):
         q_pe = y[:, H * R: H * (R + P)].view(n, H, P)
         return q_abs, q_pe, y[:, H * (R + P):]
 
+    def _decode_heads(self) -> int:
+        """Heads one decode launch takes for this module: all 32 of a bf16
+        module with a bf16 cache at R_pad <= 256 (two head groups streaming
+        the cache once), else 16."""
+        if (self.n_heads == 32 and not self.fp8_cache and self.rank_pad <= 256
+                and self.wkv_a.weight.dtype == torch.bfloat16):
+            return 32
+        return kernels.H
+
     def _fused_step_ok(self, x: torch.Tensor, n: int) -> bool:
-        """The decode-step kernels cover bf16 modules with 16 heads, at most
-        128 query rows, no q low-rank path and 128-aligned model widths."""
+        """The decode-step kernels cover bf16 modules with 16 heads (or 32,
+        in one launch), at most 128 query rows, no q low-rank path and
+        128-aligned model widths."""
         return (
-            self.n_heads == kernels.H
+            self.n_heads == self._decode_heads()
             and self.q_lora_rank == 0
             and x.dtype == torch.bfloat16
             and self.wq.weight.dtype == torch.bfloat16
@@ -482,12 +494,12 @@ class MLA(nn.Module):
                 return cap, min_chunk, bal
         return n_splits, min_chunk, 0
 
-    def _workspace_for(self, n_rows: int, n_splits: int, device) -> Optional[DecodeWorkspace]:
+    def _workspace_for(self, n_rows: int, n_splits: int, device, heads: int = kernels.H) -> Optional[DecodeWorkspace]:
         if n_splits <= 1:
             return None
         ws = self._workspace
-        if ws is None or not ws.fits(n_rows, n_splits, self.kv_lora_rank) or ws.o_part.device != device:
-            ws = DecodeWorkspace.allocate(n_rows, n_splits, device, rank=self.kv_lora_rank)
+        if ws is None or not ws.fits(n_rows, n_splits, self.kv_lora_rank, heads) or ws.o_part.device != device:
+            ws = DecodeWorkspace.allocate(n_rows, n_splits, device, rank=self.kv_lora_rank, heads=heads)
             self._workspace = ws
         return ws
 
@@ -665,7 +677,7 @@ class MLA(nn.Module):
             n_splits, balance = 1, 0
         if fused:
             o_lat = torch.empty(n, H, self.rank_pad, dtype=x.dtype, device=dev)
-            ws = self._workspace_for(n, n_splits, dev)
+            ws = self._workspace_for(n, n_splits, dev, heads=H)
             if prefill:
                 kernels.prefill_attention(q_abs, q_pe, cos, sin, cache, self.softmax_scale, start_pos=sp,
                                           rows_per_seq=T, rope_abs=rope_abs, out=o_lat)
@@ -693,10 +705,11 @@ class MLA(nn.Module):
             return self.resid_dropout(out)  # mla.py:490-495
 
         # Other calls: the absorbed products, then attention.  The attention
-        # kernels take 16 heads per launch, so H heads run as ceil(H / 16)
-        # launches over query rows padded with zero heads (whose outputs are
-        # dropped).
-        rp, HK = self.rank_pad, kernels.H
+        # kernels take 16 heads per launch (the decode kernel also 32), so H
+        # heads run as ceil(H / HK) launches over query rows padded with zero
+        # heads (whose outputs are dropped).
+        rp = self.rank_pad
+        HK = self._decode_heads() if (not prefill and x.dtype == torch.bfloat16) else kernels.H
         Hp = -(-H // HK) * HK
         # prompt-sized bf16 calls: per-head MFMA products that read q and o_lat
         # in place and write q_abs in the attention kernels' layout and o in
@@ -718,7 +731,7 @@ class MLA(nn.Module):
             q_nope = q[:, :, :Dn].transpose(0, 1).contiguous()  # [H, n, Dn]
             q_abs[:, :H] = torch.bmm(q_nope, w_uk).transpose(0, 1)  # [n, H, R_pad]
         o_lat = torch.empty(n, Hp, rp, dtype=x.dtype, device=dev)
-        ws = None if prefill else self._workspace_for(n, n_splits, dev)
+        ws = None if prefill else self._workspace_for(n, n_splits, dev, heads=HK)
         for h0 in range(0, Hp, HK):
             hs = slice(h0, h0 + HK)
             if prefill:

@@ -481,3 +481,15 @@ def test_probes_reject(lib):
     assert stream(sp=None) == E_ARG
     assert stream(ns=0) == E_ARG
     assert stream(ckv=FAKE + 8) == E_MIS
+
+
+def test_32_heads_only_where_built(lib):
+    """32 heads in one launch: bf16 model and cache with R_pad <= 256; any
+    other combination, and other head counts, are rejected before any HIP
+    call."""
+    E_UNS = -2
+    assert _decode(lib, H=32, dt=0, c_dt=0) == E_UNS              # fp32 model
+    assert _decode(lib, H=32, c_dt=2, scale=FAKE) == E_UNS        # e4m3 cache
+    assert _decode(lib, H=32, R=300, qa_rs=32 * 320, qa_hs=320, o_rs=32 * 320, o_hs=320) == E_UNS
+    assert _decode(lib, H=48) == E_UNS and _decode(lib, H=8) == E_UNS
+    assert "32" in lib.mla_last_error().decode()

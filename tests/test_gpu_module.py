@@ -15,7 +15,7 @@ import torch
 
 from oracle import latent_ops as lo
 from oracle.mla_ref import MLAConfig, RefMLA, enable_cache, init_weights
-from swamla_amd import MLA
+from swamla_amd import MLA, kernels
 
 pytestmark = pytest.mark.gpu
 
@@ -275,17 +275,27 @@ def test_module_any_rank_and_q_lora(gpu, dtype, rank, q_lora, dim):
 @pytest.mark.parametrize("n_head,dim,nope,rank", [(12, 1024, 128, 256), (32, 1024, 128, 256), (8, 512, 128, 173),
                                                   (32, 1024, 64, 256)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_module_other_head_counts(gpu, dtype, n_head, dim, nope, rank):
+def test_module_other_head_counts(gpu, dtype, n_head, dim, nope, rank, monkeypatch):
     """The reference presets' head counts (moe-1b: 12, xl: 32,
     swa_mla_model.py:618-640; 32 heads of 64 nope channels is the
-    cudnn-compatible layout, :697-698), run as 16-head launches over
-    zero-padded query heads: a 160-token prompt (the prompt-sized products),
-    then decode steps at batch 2, against the reference restatement with the
-    same weights; cache rows bit-exact."""
+    cudnn-compatible layout, :697-698): a 160-token prompt (the prompt-sized
+    products), then decode steps at batch 2, against the reference
+    restatement with the same weights; cache rows bit-exact.  bf16 modules
+    with 32 heads run every attention call as one 32-head launch (the cache
+    streamed once); other counts as 16-head launches over zero-padded query
+    heads."""
     say(f"n_head={n_head} dim={dim} nope={nope} rank={rank} dtype={dtype}")
     cfg = MLAConfig(n_embd=dim, n_head=n_head, max_batch_size=2, max_seq_len=192, kv_lora_rank=rank,
                     qk_nope_head_dim=nope)
     ref, ours = make_pair(cfg, 41 + n_head, dtype, gpu, ln_random=True)
+    calls = []
+    real = kernels.decode_attention
+
+    def spy(q_abs, *a, **k):
+        calls.append(q_abs.shape[1])
+        return real(q_abs, *a, **k)
+
+    monkeypatch.setattr(kernels, "decode_attention", spy)
     g = torch.Generator().manual_seed(42 + n_head)
     x = torch.randn(2, 160, dim, generator=g).to(dtype)
     xs = [x.to(gpu)]
@@ -297,6 +307,10 @@ def test_module_other_head_counts(gpu, dtype, n_head, dim, nope, rank):
             close(ours(xs[-1], 160 + step), ref(xd, 160 + step), dtype)
     torch.cuda.synchronize()
     assert_cache_bits(ours, xs, dtype)
+    if n_head == 32 and dtype == torch.bfloat16:
+        assert calls == [32] * 7, calls  # one launch per call: the prompt and each decode step
+    else:
+        assert calls == [16] * (7 * -(-n_head // 16)), calls
 
 
 def test_out_of_range_positions_raise(gpu):
