@@ -85,6 +85,8 @@ def parse():
     p.add_argument("--ctx", type=int, default=None, help="prefilled context (the maximum for the ragged config)")
     p.add_argument("--dim", type=int, default=None)
     p.add_argument("--cache", choices=["bf16", "fp8"], default=None)
+    p.add_argument("--heads", type=int, default=16, choices=[16, 32],
+                   help="query heads (32: the xl preset's count, one attention launch of two head groups)")
     p.add_argument("--kernel-reps", type=int, default=50, help="roofline launches per layer")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -137,7 +139,7 @@ def kernel_source_hash() -> str:
     return h.hexdigest()[:16]
 
 
-def measured_traffic(B: int, L: int, cache: str):
+def measured_traffic(B: int, L: int, cache: str, heads: int = H):
     """HBM bytes per decode launch from a committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (profiles/*_traffic.md) taken on this kernel source at
     this launch shape, else None (counters cannot be read from inside this
@@ -154,7 +156,8 @@ def measured_traffic(B: int, L: int, cache: str):
             key, sep, val = line.partition(": ")
             if sep and key.isidentifier():
                 fields[key] = val.strip()
-        if fields.get("kernel_source_sha256_16") == src and fields.get("launch") == f"B={B} L={L} cache={cache}":
+        launch = f"B={B} L={L} cache={cache}" + (f" heads={heads}" if heads != H else "")
+        if fields.get("kernel_source_sha256_16") == src and fields.get("launch") == launch:
             try:
                 return int(fields["traffic_bytes_per_launch"]), os.path.relpath(path, ROOT)
             except (KeyError, ValueError):
@@ -162,16 +165,16 @@ def measured_traffic(B: int, L: int, cache: str):
     return None, None
 
 
-def attention_bytes(B: int, L: int, fp8: bool) -> int:
+def attention_bytes(B: int, L: int, fp8: bool, heads: int = H) -> int:
     per_tok = R * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0)
-    return B * L * per_tok + B * H * (R + P) * 2 + B * H * R * 2
+    return B * L * per_tok + B * heads * (R + P) * 2 + B * heads * R * 2
 
 
-def attention_bytes_rows(lens, fp8: bool) -> int:
+def attention_bytes_rows(lens, fp8: bool, heads: int = H) -> int:
     """Algorithmic bytes of one decode launch over rows of lengths ``lens``."""
     per_tok = R * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0)
     B = int(lens.numel())
-    return int(lens.sum()) * per_tok + B * H * (R + P) * 2 + B * H * R * 2
+    return int(lens.sum()) * per_tok + B * heads * (R + P) * 2 + B * heads * R * 2
 
 
 def append_bytes(B: int, fp8: bool) -> int:
@@ -197,7 +200,7 @@ def build_layers(args, dev, torch):
     from swamla_amd import MLA, MLAConfig
 
     max_seq = (args.ctx + max(args.steps + args.warmup, args.canonical_steps) + 63) // 64 * 64
-    cfg = MLAConfig(n_embd=args.dim, max_batch_size=args.batch, max_seq_len=max_seq)
+    cfg = MLAConfig(n_embd=args.dim, n_head=args.heads, max_batch_size=args.batch, max_seq_len=max_seq)
     layers = []
     g = torch.Generator(device=dev).manual_seed(1234)
     for i in range(args.layers):
@@ -236,7 +239,8 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
     with torch.no_grad():
         for m, x in zip(layers, xs):
             B = x.shape[0]
-            q = m.wq(x).view(B, H, -1)
+            NH = args.heads
+            q = m.wq(x).view(B, NH, -1)
             w_uk, _ = m.absorbed_weights()
             q_abs = torch.bmm(q[:, :, :128].transpose(0, 1).contiguous(), w_uk)  # [H, B, R]
             kv = m.wkv_a(x).view(B, -1)  # the step's new tokens (wkv_a output rows)
@@ -245,9 +249,9 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
             sp = (lens - 1).to(device=dev, dtype=torch.int32)  # row b attends [0, lens[b])
             # the plan MLA.forward uses for a start_pos tensor
             n_splits, min_chunk, balance = m._decode_plan(B, L, dev, True)
-            ws = kernels.DecodeWorkspace.allocate(B, n_splits, dev)
+            ws = kernels.DecodeWorkspace.allocate(B, n_splits, dev, heads=NH)
             plan = _abi.ptr(ws.plan if balance else None)
-            o_lat = torch.empty(H, B, R, dtype=torch.bfloat16, device=dev)
+            o_lat = torch.empty(NH, B, R, dtype=torch.bfloat16, device=dev)
             cos, sin = m.rope.half_tables()
             qa, qp, ol = q_abs.transpose(0, 1), q[:, :, 128:], o_lat.transpose(0, 1)
             # the step's attention launch: one-token append folded into decode
@@ -258,12 +262,12 @@ def time_decode_kernel(layers, xs, lens, args, dev, torch):
                 cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                 cache.ckv.data_ptr(), cache.kpe.data_ptr(), _abi.ptr(cache.scale),
                 cache.ckv.shape[0], cache.ckv.shape[1], sp.data_ptr(), 0,
-                B, H, R, P, float(m.softmax_scale), n_splits, min_chunk, balance, plan,
+                B, NH, R, P, float(m.softmax_scale), n_splits, min_chunk, balance, plan,
                 ws.o_part.data_ptr(), ws.lse_part.data_ptr(),
                 ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16, cache.cache_code, h,
             )
             margs = (ws.o_part.data_ptr(), ws.lse_part.data_ptr(), None, None, sp.data_ptr(), 1,
-                     cache.ckv.shape[0], cache.ckv.shape[1], B, H, R, n_splits, min_chunk, plan,
+                     cache.ckv.shape[0], cache.ckv.shape[1], B, NH, R, n_splits, min_chunk, plan,
                      ol.data_ptr(), ol.stride(0), ol.stride(1), None, _abi.DTYPE_BF16, h)
             preps.append((dargs, (q, q_abs, kv, sp, ws, o_lat, cos, sin), L, B, n_splits, margs, balance))
 
@@ -549,9 +553,9 @@ def main() -> int:
     ceiling = read_ceiling(dev, torch)
     log(f"read ceiling {ceiling:.0f} GB/s; cache stream alone "
         + (f"{stream_us:.2f} us" if stream_us is not None else "n/a (balanced plan)"))
-    abytes = attention_bytes_rows(lens, fp8) + append_bytes(B, fp8)
+    abytes = attention_bytes_rows(lens, fp8, args.heads) + append_bytes(B, fp8)
     stream_bytes = int(lens.sum()) * (R * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0))
-    traffic, traffic_src = measured_traffic(B, L, args.cache) if not args.ragged else (None, None)
+    traffic, traffic_src = measured_traffic(B, L, args.cache, args.heads) if not args.ragged else (None, None)
     achieved = abytes / (graph_us * 1e-6) / 1e9
     warm = abytes / (warm_us * 1e-6) / 1e9
     log(f"decode kernel: {graph_us:.2f} us cold, graph-replayed ({achieved:.0f} GB/s), {cold_us:.2f} us cold on the "
@@ -559,7 +563,7 @@ def main() -> int:
     # algorithmic bytes of one full layer-step (attention + append + weights), mean context
     w_bytes = sum(p.numel() * p.element_size() for p in layers[0].parameters())
     mid = lens0 + (args.steps + 1) // 2
-    step_bytes = attention_bytes_rows(mid, fp8) + w_bytes + append_bytes(args.batch, fp8)
+    step_bytes = attention_bytes_rows(mid, fp8, args.heads) + w_bytes + append_bytes(args.batch, fp8)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -568,8 +572,10 @@ def main() -> int:
         log(f"cpu: {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
 
     line = {
-        "metric": ("MLA decode tok/s + achieved HBM GB/s (% peak), bs=32 ctx=4096 bf16" if args.config == 2
-                   else f"MLA decode tok/s + achieved HBM GB/s (% peak), config {args.config}"),
+        "metric": ("MLA decode tok/s + achieved HBM GB/s (% peak), bs=32 ctx=4096 bf16"
+                   if args.config == 2 and args.heads == H
+                   else f"MLA decode tok/s + achieved HBM GB/s (% peak), config {args.config}"
+                        + (f", {args.heads} heads" if args.heads != H else "")),
         "value": value,
         "unit": "tok/s",
         "n_gpus": 1,
@@ -587,7 +593,7 @@ def main() -> int:
         "config": {
             "workload": WORKLOADS[args.config],
             "batch": args.batch, "ctx": args.ctx, "decode_steps": args.steps, "n_embd": args.dim,
-            "heads": H, "kv_lora_rank": R, "rope_dim": P, "cache": args.cache,
+            "heads": args.heads, "kv_lora_rank": R, "rope_dim": P, "cache": args.cache,
             "layers_rotated": len(layers),
             "value_counts": "tokens x layers per second (each token counted once per MLA layer)",
             "step_unit": (f"one step = one graph replay of the {len(layers)}-layer stack (ms_per_step x steps = "

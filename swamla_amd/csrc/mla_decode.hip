@@ -136,13 +136,17 @@ __device__ __forceinline__ void wait_subtiles(int ahead) {
   wait_vm<0>();
 }
 
-// 16 bytes per lane from global memory into LDS at dst + 16 * lane
-// (non-temporal: the cache is streamed once).
+// 16 (4) bytes per lane from global memory into LDS at dst + 16 (4) * lane.
+// AUX 2 marks the load non-temporal (one head group: the cache is streamed
+// once); two head groups load the same lines twice and keep them cacheable
+// (AUX 0), so the second group's requests hit the L2.
+template <int AUX = 2>
 __device__ __forceinline__ void dma16(const void* src, lds_u8* dst) {
-  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 16, 0, 2);
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 16, 0, AUX);
 }
+template <int AUX = 2>
 __device__ __forceinline__ void dma4(const void* src, lds_u8* dst) {
-  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 4, 0, 2);
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 4, 0, AUX);
 }
 
 template <typename T>
@@ -206,6 +210,7 @@ struct SubStream {
   using G = DecGeo<C_DT, NB, HG>;
   static constexpr int kLatQ = G::kLat / 1024;
   static constexpr int kLatRow = C_DT == 2 ? G::RP : 2 * G::RP;  // bytes of a latent cache row
+  static constexpr int kAux = HG == 1 ? 2 : 0;                      // see dma16
   int t0, t_last, rem, my_n, j_base, w;
   int64_t row0;
   const uint8_t* ckv;
@@ -249,10 +254,10 @@ struct SubStream {
       const uint8_t* lb = ckv + (row0 + tb) * kLatRow;
       const uint8_t* pb = kpe + (row0 + tb) * (2 * kP);
 #pragma unroll
-      for (int q = 0; q < kLatQ; ++q) dma16(lb + lat_off[q], dst + 1024 * q);
+      for (int q = 0; q < kLatQ; ++q) dma16<kAux>(lb + lat_off[q], dst + 1024 * q);
 #pragma unroll
-      for (int q = 0; q < 2; ++q) dma16(pb + pe_off[q], dst + G::kLat + 1024 * q);
-      if constexpr (C_DT == 2) dma4(scale + row0 + tb + (lane & 15), dst + G::kLat + G::kPe);
+      for (int q = 0; q < 2; ++q) dma16<kAux>(pb + pe_off[q], dst + G::kLat + 1024 * q);
+      if constexpr (C_DT == 2) dma4<kAux>(scale + row0 + tb + (lane & 15), dst + G::kLat + G::kPe);
       return;
     }
     // the split's last, partial sub-tile: rows past its end re-read its last row
@@ -260,17 +265,17 @@ struct SubStream {
     for (int q = 0; q < kLatQ; ++q) {
       const int tt = (1024 * q + 16 * lane) / kLatRow;
       const int tok = min(tb + tt, t_last);
-      dma16(ckv + (row0 + tok) * kLatRow + (lat_off[q] - tt * kLatRow), dst + 1024 * q);
+      dma16<kAux>(ckv + (row0 + tok) * kLatRow + (lat_off[q] - tt * kLatRow), dst + 1024 * q);
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int tt = 8 * q + (lane >> 3);
       const int tok = min(tb + tt, t_last);
-      dma16(kpe + (row0 + tok) * (2 * kP) + (pe_off[q] - tt * (2 * kP)), dst + G::kLat + 1024 * q);
+      dma16<kAux>(kpe + (row0 + tok) * (2 * kP) + (pe_off[q] - tt * (2 * kP)), dst + G::kLat + 1024 * q);
     }
     if constexpr (C_DT == 2) {
       const int tok = min(tb + (lane & 15), t_last);
-      dma4(scale + row0 + tok, dst + G::kLat + G::kPe);
+      dma4<kAux>(scale + row0 + tok, dst + G::kLat + G::kPe);
     }
   }
 };
