@@ -29,7 +29,7 @@ B*(R+P)*2 read and B*(R+P)*2 written (+ LayerNorm parameters).
 Ceiling legs beside it (measurement kernels, not the product path):
 roofline.ceiling_gbs is the plain HBM read rate of the GPU
 (mla_probe_read over 1 GiB per launch, regions alternated so the Infinity
-Cache serves nothing), and roofline.stream_only_us the same decode launches'
+Cache serves nothing, best of four grid sizes), and roofline.stream_only_us the same decode launches'
 cache stream with the arithmetic left out (mla_probe_cache_stream), timed the
 same way as avg_launch_us.
 
@@ -340,40 +340,49 @@ def median(xs):
     return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
 
 
+CEILING_GRIDS = (256, 512, 1024, 2048)
+
+
 def read_ceiling(dev, torch, gib: int = 1):
     """HBM read ceiling of this GPU: mla_probe_read streaming ``gib`` GiB per
     launch with 16-byte non-temporal loads, alternating between two disjoint
     regions (each far above the 256 MB Infinity Cache), replayed from a HIP
-    graph; median GB/s over TIMING_REPS repetitions."""
+    graph, at each grid size of CEILING_GRIDS (256-thread workgroups).  How
+    many bytes are in flight changes the rate on this GPU, so the ceiling is
+    the best grid's median GB/s over TIMING_REPS repetitions; returns
+    (ceiling, {grid: median GB/s})."""
     from swamla_amd import _abi
 
     lib = _abi.lib()
     nbytes = gib << 30
     buf = torch.empty(2 * nbytes, dtype=torch.uint8, device=dev)
     buf.view(torch.int32).random_(0, 1 << 30)
-    grid = 256 * 8
-    sink = torch.empty(grid * 256, dtype=torch.int32, device=dev)
+    sink = torch.empty(max(CEILING_GRIDS) * 256, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        hc = torch.cuda.current_stream(dev).cuda_stream
-        for i in range(2):
-            _abi.check(lib.mla_probe_read(buf.data_ptr() + i * nbytes, nbytes, sink.data_ptr(), grid, hc))
-    graph.replay()
-    torch.cuda.synchronize()
-    rates = []
-    reps = 5
-    for _ in range(TIMING_REPS):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        e1.record(stream)
+    by_grid = {}
+    for grid in CEILING_GRIDS:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            hc = torch.cuda.current_stream(dev).cuda_stream
+            for i in range(2):
+                _abi.check(lib.mla_probe_read(buf.data_ptr() + i * nbytes, nbytes, sink.data_ptr(), grid, hc))
+        graph.replay()
         torch.cuda.synchronize()
-        rates.append(2 * reps * nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+        rates = []
+        reps = 2
+        for _ in range(TIMING_REPS):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            rates.append(2 * reps * nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+        by_grid[grid] = median(rates)
+        del graph
     del buf
-    return median(rates)
+    return max(by_grid.values()), by_grid
 
 
 def cpu_baseline(args, torch):
@@ -550,7 +559,7 @@ def main() -> int:
     lens = lens0 + args.canonical_steps  # the configuration's end lengths (config 2: 4224)
     cold_us, graph_us, warm_us, merge_us, L, B, n_splits, balance, stream_us = time_decode_kernel(
         layers, xs, lens, args, dev, torch)
-    ceiling = read_ceiling(dev, torch)
+    ceiling, ceiling_by_grid = read_ceiling(dev, torch)
     log(f"read ceiling {ceiling:.0f} GB/s; cache stream alone "
         + (f"{stream_us:.2f} us" if stream_us is not None else "n/a (balanced plan)"))
     abytes = attention_bytes_rows(lens, fp8, args.heads) + append_bytes(B, fp8)
@@ -628,8 +637,9 @@ def main() -> int:
                             + f", caches rotated over {len(layers)} layers"),
             "ceiling_gbs": ceiling,
             "ceiling_source": ("mla_probe_read: 1 GiB per launch with 16-byte non-temporal loads, alternating "
-                               "over two disjoint 1 GiB regions, graph-replayed (the plain HBM read rate of "
-                               "this GPU)"),
+                               "over two disjoint 1 GiB regions, graph-replayed, best of the grid sizes in "
+                               "ceiling_by_grid (the plain HBM read rate of this GPU)"),
+            "ceiling_by_grid": {str(g): r for g, r in ceiling_by_grid.items()},
             "frac_of_ceiling": achieved / ceiling,
             "stream_only_us": stream_us,
             "stream_only_gbs": (stream_bytes / (stream_us * 1e-6) / 1e9) if stream_us else None,
