@@ -65,7 +65,9 @@ def compile_commands(output: str = OUTPUT) -> tuple[list[list[str]], list[str]]:
         obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
         cmds.append([hipcc(), *base_flags(), *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj])
         objs.append(obj)
-    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", output]
+    # -z defs: an unresolved symbol (for example a kernel stub the host pass
+    # did not emit) fails the link instead of the first load
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *objs, "-o", output]
     return cmds, link
 
 

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "mla_args.h"
 #include "mla_device.h"
 #include "mla_plan.h"
@@ -358,6 +360,462 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
 }
 
 
+// ---------------------------------------------------------------------------
+// Prefill attention on 32x32x16 MFMAs (bf16 cache, R_pad a multiple of 128).
+// A workgroup of four waves (one per SIMD) takes eight consecutive query
+// tokens of one sequence, two per wave: the wave's 32 MFMA columns are
+// (query, head) = (n >> 4, n & 15).  Per 64-token cache tile, staged in LDS
+// once for the workgroup (each wave loads 16 of the rows as whole lines):
+//   S^T[32 tok x 32 col] = K . Q^T   two 32-token halves, A = K rows from
+//                                    LDS, B = Q^T in registers for the whole
+//                                    walk (R_pad / 16 + 4 k-steps);
+//   online softmax per column        the lane holds 16 tokens of its column
+//                                    per half-tile, the other lane half the
+//                                    other 16 (one permlane32 swap);
+//   O^T[32 ch x 32 col] += V^T . P^T per 32-channel block, A = C^T read
+//                                    transposed from LDS (ds_read_b64_tr_b16),
+//                                    B = the bf16 weights straight from the
+//                                    score registers.
+// The score accumulator's lane layout (row 8(r/4) + 4(l/32) + r%4, column
+// l%32) is the PV product's B operand once the k slots of the 16-token step
+// are taken as tokens {4h .. 4h+3, 8+4h .. 8+4h+3} for lane half h, which is
+// also the order in which the two transposed reads of C^T deliver them.  Each
+// K or C^T byte read from LDS feeds 32 columns instead of 16, so the tile's
+// LDS traffic per query is half that of mla_prefill_mfma.
+// LDS: latent rows at a 2 R_pad pitch with 16-byte chunk c of row t at
+// (c & ~15) | ((c ^ p2_swz(t)) & 15): the K read (one chunk of 16 rows per
+// 16 lanes) and the transposed read (4 rows x 64 bytes per 32 lanes) both
+// hit 64 distinct banks (measured: no bank conflicts); rope rows (128 bytes)
+// at chunk c ^ ((t >> 1) & 7).  The rows arrive by LDS DMA
+// (global_load_lds_dwordx4, 1 KB per instruction, the swizzle applied to the
+// global addresses), so no register or LDS-store instruction stages them.
+// Three tile buffers: iteration j waits for its own DMAs of tile j + 1,
+// passes one barrier, starts tile j + 2's DMAs into the buffer tile j - 1
+// left, then runs tile j + 1's QK and tile j's PV back to back.  The operand
+// reads run a fixed number of MFMAs ahead with explicit waits, and the
+// softmax step of tile j + 1 is placed between PV MFMAs, where its VALU work
+// overlaps the matrix pipe.  Each wave is alone on its SIMD (about 230
+// VGPRs and 240 AGPRs: O^T, the scores and Q^T live in AGPRs, from which the
+// MFMAs read directly).
+// ---------------------------------------------------------------------------
+namespace {
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+constexpr int kP2Waves = 4;  // waves per workgroup, one per SIMD
+constexpr int kP2Qpw = 2;    // query tokens per wave (x 16 heads = 32 MFMA columns)
+constexpr int kP2Tok = 64;   // cache tokens per LDS tile
+constexpr int kP2Bufs = 3;
+
+__device__ __forceinline__ int p2_swz(int t) { return ((t & 3) << 2) | ((t >> 2) & 3); }
+typedef unsigned int p2_u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+// LDS operand reads issued as inline assembly, so that their order and the
+// waits for them are the source's: the compiler would otherwise keep one
+// read in flight per MFMA.  Results are taken only after p2_wait_lgkm<N>()
+// (LDS operations complete in order) and p2_tie(), which redefines the value
+// so that no use moves above the wait.
+template <int OFF>
+__device__ __forceinline__ p2_u32x4_t p2_read16(uint32_t addr) {
+  p2_u32x4_t v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+template <int OFF>
+__device__ __forceinline__ s16x4_t p2_read_tr(uint32_t addr) {
+  s16x4_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void p2_wait_lgkm() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+template <typename T>
+__device__ __forceinline__ void p2_tie(T& v) { asm volatile("" : "+v"(v)); }
+// 16 bytes per lane from global memory into LDS at dst + 16 lane (cacheable:
+// the workgroups of one sequence read the same rows)
+__device__ __forceinline__ void p2_dma16(const void* src, lds_u8* dst) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 16, 0, 0);
+}
+template <int I, int N, typename F>
+__device__ __forceinline__ void p2_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    p2_for<I + 1, N>(f);
+  }
+}
+template <int A, int B>
+constexpr int p2_min() { return A < B ? A : B; }
+__device__ __forceinline__ int p2_pos(int c, int t) { return (c & ~15) | ((c ^ p2_swz(t)) & 15); }
+}  // namespace
+
+template <int NB>
+__global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a) {
+  static_assert(NB % 2 == 0, "latent rows of a multiple of 256 bytes");
+  constexpr int RP = 64 * NB;
+  constexpr int kRow = 2 * RP;                  // bytes per latent row
+  constexpr int kLat = kP2Tok * kRow;           // latent bytes per tile
+  constexpr int kPeR = 2 * kP;                  // bytes per rope row
+  constexpr int kBuf = kLat + kP2Tok * kPeR;    // bytes per tile buffer
+  constexpr int KS = RP / 16;                   // latent k-steps of the QK product
+  constexpr int CB = RP / 32;                   // 32-channel blocks of the PV product
+  constexpr int LQ = 16 * kRow / 1024;          // latent DMAs per wave per tile (16 rows)
+  constexpr int kRowsPerDma = 1024 / kRow;
+  constexpr int QG = kP2Waves * kP2Qpw;         // query tokens per workgroup
+  // Three buffers as three arrays: every access names its array at compile
+  // time (the loop is unrolled by three), so the compiler's wait counting can
+  // tell a read of one buffer from the DMA still filling another.
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[kBuf];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[kBuf];
+  __shared__ __attribute__((aligned(16))) uint8_t lds2[kBuf];
+  auto buf = [&](auto bi) __attribute__((always_inline)) -> lds_u8* {
+    if constexpr (decltype(bi)::value == 0) return (lds_u8*)lds0;
+    else if constexpr (decltype(bi)::value == 1) return (lds_u8*)lds1;
+    else return (lds_u8*)lds2;
+  };
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31, hf = lane >> 5;  // column, lane half
+  const int head = n & 15;
+  const int T = a.ad.T;
+  const int b = blockIdx.y;
+  // Later query groups attend to more of the cache: the grid runs them first.
+  const int t_first = QG * (gridDim.x - 1 - blockIdx.x);
+  const int t_last_q = min(t_first + QG - 1, T - 1);
+  const int sp = a.ad.start_pos[b];
+  const bool b_ok = b < a.cache_b;
+  const int tt = t_first + kP2Qpw * w + (n >> 4);  // this column's query (surplus ones repeat the last)
+  const bool valid = tt < T;
+  const int tq = min(tt, t_last_q);
+  const int64_t rq = static_cast<int64_t>(b) * T + tq;
+  int Lq = b_ok ? sp + tq + 1 : 0;
+  Lq = min(max(Lq, 0), static_cast<int>(a.cache_s));
+  int Lb = b_ok ? sp + t_last_q + 1 : 0;  // the block's range: its last query's
+  Lb = min(max(Lb, 0), static_cast<int>(a.cache_s));
+  const int n_tiles = (Lb + kP2Tok - 1) / kP2Tok;  // block-uniform
+  const int64_t cache_row0 = static_cast<int64_t>(b_ok ? b : 0) * a.cache_s;
+  const int t_last = Lb > 0 ? Lb - 1 : 0;
+  // this sequence's cache rows (32-bit lane offsets from a uniform base)
+  const uint8_t* const ckv = static_cast<const uint8_t*>(a.ckv) + cache_row0 * kRow;
+  const uint8_t* const kpe = static_cast<const uint8_t*>(a.kpe) + cache_row0 * kPeR;
+
+  // ---- DMA of this wave's 16 rows of tile j (rows 16w .. 16w + 15) straight
+  // into LDS, 1 KB per instruction: LDS chunk p of row t holds cache chunk
+  // p ^ swizzle(t) (the XOR is its own inverse).
+  uint32_t lat_src[LQ], pe_src[2];  // lane offsets within a tile's rows, row index excluded
+  int lat_row[LQ], pe_row[2];
+#pragma unroll
+  for (int q = 0; q < LQ; ++q) {
+    const int t = 16 * w + kRowsPerDma * q + (16 * lane) / kRow, pch = ((16 * lane) % kRow) / 16;
+    lat_row[q] = t;
+    lat_src[q] = 16 * p2_pos(pch, t);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int t = 16 * w + 8 * q + (lane >> 3);
+    pe_row[q] = t;
+    pe_src[q] = 16 * ((lane & 7) ^ ((t >> 1) & 7));
+  }
+  auto dma_tile = [&](int j, lds_u8* dst) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < LQ; ++q) {
+      const uint32_t row = min(j * kP2Tok + lat_row[q], t_last);
+      p2_dma16(ckv + (row * kRow + lat_src[q]), dst + (16 * w + kRowsPerDma * q) * kRow);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t row = min(j * kP2Tok + pe_row[q], t_last);
+      p2_dma16(kpe + (row * kPeR + pe_src[q]), dst + kLat + (16 * w + 8 * q) * kPeR);
+    }
+  };
+
+  // ---- Q^T operands: column n, channels 16 ks + 8 hf .. + 7 (k-steps KS.. are the rope part)
+  bf16x8_t qb[KS + 4];
+  {
+    const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + rq * a.qa_rs + head * a.qa_hs;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)  // channels >= R zeroed
+      qb[ks] = as_bf16x8(mask_bf16x8(*reinterpret_cast<const uint4*>(qa + 16 * ks + 8 * hf), a.R - (16 * ks + 8 * hf)));
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + rq * a.qp_rs + head * a.qp_hs;
+    int rp = a.ad.rope_abs ? sp + tq : tq;
+    rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
+    const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
+    const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c0 = 16 * s + 8 * hf;
+      const uint4 raw = *reinterpret_cast<const uint4*>(qp + c0);
+      const uint2 cr = *reinterpret_cast<const uint2*>(ct + c0 / 2);
+      const uint2 sr = *reinterpret_cast<const uint2*>(st + c0 / 2);
+      const uint32_t wv_in[4] = {raw.x, raw.y, raw.z, raw.w};
+      const uint32_t cw2[2] = {cr.x, cr.y}, sw2[2] = {sr.x, sr.y};
+      uint32_t wv[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const uint32_t cj = (jj & 1) ? (cw2[jj >> 1] >> 16) : (cw2[jj >> 1] & 0xFFFF);
+        const uint32_t sj = (jj & 1) ? (sw2[jj >> 1] >> 16) : (sw2[jj >> 1] & 0xFFFF);
+        float o1, o2;
+        rope_pair<1>(bf16_to_f32(wv_in[jj] & 0xFFFF), bf16_to_f32(wv_in[jj] >> 16), bf16_to_f32(cj), bf16_to_f32(sj), o1,
+                     o2);
+        wv[jj] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+      }
+      qb[KS + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS + 4; ++ks) asm volatile("" : "+a"(qb[ks]));  // kept in AGPRs: MFMA reads B from there
+  }
+
+  f32x16_t oacc[CB];
+#pragma unroll
+  for (int i = 0; i < CB; ++i) oacc[i] = f32x16_t{};
+  float m_run = -INFINITY, l_part = 0.f;
+
+  // ---- per-lane operand offsets (bytes within a tile buffer).  The swizzle
+  // XORs only the low four bits of a chunk index, so each read is a per-lane
+  // table entry plus a compile-time offset (the ds_read immediate):
+  //   K latent, k-step ks, half h2: ko[ks % 8] + 256 (ks / 8) + 32 h2 kRow
+  //   K rope, k-step s, half h2:    po[s] + 32 h2 kPeR
+  //   C^T, k-step s, block cb, read e: to[e][cb % 4] + 16 s kRow + 256 (cb / 4)
+  const int fl = p2_swz(n & 15);  // rows 32 h2 + n of a tile
+  const int pe_sw = (n >> 1) & 7;
+  const int G = lane >> 4, jj = lane & 15, g2 = G & 1;  // transposed reads: 16-lane group, lane in group
+  uint32_t ko[8], po[4], to[2][4];
+#pragma unroll
+  for (int k8 = 0; k8 < 8; ++k8) ko[k8] = n * kRow + 16 * ((2 * k8 + hf) ^ fl);
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) po[s4] = kLat + n * kPeR + 16 * ((2 * s4 + hf) ^ pe_sw);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int r = 8 * e + 4 * hf + (jj >> 2);  // row within a 16-token k-step
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4)
+      to[e][c4] = r * kRow + 16 * ((4 * c4 + 2 * g2 + ((jj & 3) >> 1)) ^ p2_swz(r)) + 8 * (jj & 1);
+  }
+  static_assert(KS <= 16 && kRow % 256 == 0, "the latent read table covers 16 k-steps of 256-byte row halves");
+
+  // qk(j, base): scores of tile j, scaled to the log2 domain and masked.
+  // The 2 (KS + 4) K reads run kQkAhead ahead of their MFMAs.
+  constexpr int kQkReads = 2 * (KS + 4), kQkAhead = 6;
+  f32x16_t sc[2];
+  int sc_tile = 0;  // the tile sc holds (scaled and masked in the softmax step)
+  auto qk = [&](int j, const lds_u8* base_p) __attribute__((always_inline)) {
+    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(base_p));
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) sc[h2] = f32x16_t{};
+    p2_u32x4_t kr[kQkReads];
+    auto rd = [&](auto I) __attribute__((always_inline)) {
+      constexpr int i = decltype(I)::value, ks = i / 2, h2 = i % 2;
+      if constexpr (ks < KS) kr[i] = p2_read16<256 * (ks / 8) + 32 * h2 * kRow>(base + ko[ks % 8]);
+      else kr[i] = p2_read16<32 * h2 * kPeR>(base + po[ks - KS]);
+    };
+    p2_for<0, kQkAhead>(rd);
+    p2_for<0, kQkReads>([&](auto I) __attribute__((always_inline)) {
+      constexpr int i = decltype(I)::value, ks = i / 2, h2 = i % 2;
+      if constexpr (i + kQkAhead < kQkReads) {
+        rd(std::integral_constant<int, i + kQkAhead>{});
+        p2_wait_lgkm<kQkAhead>();
+      } else {
+        p2_wait_lgkm<kQkReads - 1 - i>();
+      }
+      p2_tie(kr[i]);
+      sc[h2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[ks], sc[h2], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    sc_tile = j;
+  };
+  // smax(): the online-softmax step of the scores sc, without touching O:
+  // the new reference m_new (moved lazily, when a column's maximum grows by
+  // more than 2^kLazy), the rescale factor alpha of what was accumulated so
+  // far, and the bf16 weights pbn in the PV operand order (k-step s = 2 h2 +
+  // sb: registers 8 sb .. 8 sb + 7 of half h2) with their sum.  The caller
+  // rescales O after the PV product of the previous tile, which used the old
+  // reference.  Branch-free, so it shares one scheduling region with that
+  // product.
+  bf16x8_t pb[4], pbn[4];
+  float alpha = 1.f, lsum = 0.f, m_new = -INFINITY;
+  bool moved = false;
+  // part 0: the tile maximum and the new reference; parts 1, 2: the weights
+  // of half-tile 0, 1
+  float mref = 0.f;
+  auto smax_part = [&](auto P) __attribute__((always_inline)) {
+    constexpr int part = decltype(P)::value;
+    if constexpr (part == 0) {
+      // Tokens at or past a column's causal end score -inf; only the tiles
+      // that reach the end of one of the wave's queries need the compares.
+      if (!__all(sc_tile * kP2Tok + kP2Tok <= Lq)) {
+        const int tok0 = sc_tile * kP2Tok + 4 * hf;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int tok = tok0 + 32 * h2 + 8 * (r >> 2) + (r & 3);
+            if (tok >= Lq) sc[h2][r] = -INFINITY;
+          }
+      }
+      float mt = -INFINITY;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[h2][r]);
+      const uint32_t u = f2u(mt);
+      const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      // the column's tile maximum (both lane halves), in the log2 domain (the scale is positive)
+      mt = fmaxf(u2f(r32[0]), u2f(r32[1])) * a.scale_log2;
+      moved = __any(mt > m_run + kLazy);
+      m_new = moved ? fmaxf(m_run, mt) : m_run;
+      // a column still without a valid token (both -inf) keeps alpha = 1, not
+      // NaN: the wave's other query can move its own maximum
+      alpha = m_new == m_run ? 1.f : exp2f(m_run - m_new);
+      // A column with no valid token yet (reference still -inf) takes weight 0, not NaN.
+      mref = m_new == -INFINITY ? 0.f : -m_new;  // (negated: the weights are exp2(s scale - m))
+      lsum = 0.f;
+      p2_tie(mref);  // keeps this part where it is placed (the compiler would sink it to its uses)
+      p2_tie(alpha);
+    } else {
+      constexpr int h2 = part - 1;
+      // weights exp2(s scale - m) with one rounding before the exponential
+      // (v_exp_f32: the arguments are at most kLazy, so no range reduction),
+      // rounded to bf16; their sum with one dot2 per pair
+      const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        uint32_t pw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h2][8 * sb + 2 * e], a.scale_log2, mref));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h2][8 * sb + 2 * e + 1], a.scale_log2, mref));
+          pw[e] = pack_bf16x2(p0, p1);
+          lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw[e]), ones, lsum, false);
+        }
+        pbn[2 * h2 + sb] = as_bf16x8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
+        p2_tie(pbn[2 * h2 + sb]);
+      }
+      p2_tie(lsum);
+    }
+  };
+  auto smax = [&]() __attribute__((always_inline)) {
+    smax_part(std::integral_constant<int, 0>{});
+    smax_part(std::integral_constant<int, 1>{});
+    smax_part(std::integral_constant<int, 2>{});
+  };
+  // the softmax parts placed after PV MFMAs M/8, 3M/8 and 5M/8 (M = 4 CB)
+  auto smax_mid = [&](auto I) __attribute__((always_inline)) {
+    constexpr int m = decltype(I)::value, M = 4 * CB;
+    if constexpr (m == M / 8) smax_part(std::integral_constant<int, 0>{});
+    else if constexpr (m == 3 * M / 8) smax_part(std::integral_constant<int, 1>{});
+    else if constexpr (m == 5 * M / 8) smax_part(std::integral_constant<int, 2>{});
+  };
+  // commit(): the reference and weight sum move to the new tile; O is
+  // rescaled if any column's reference moved (rare after the first tiles).
+  auto commit = [&]() __attribute__((always_inline)) {
+    l_part = l_part * alpha + lsum;
+    m_run = m_new;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) pb[s4] = pbn[s4];
+    if (moved) {
+#pragma unroll
+      for (int i = 0; i < CB; ++i) {  // one block at a time: few registers live
+        oacc[i] = oacc[i] * alpha;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  // pv(base, mid): O^T[32 cb + ., col] += C^T . P^T over a tile's four
+  // 16-token k-steps, the two transposed reads of each MFMA kPvAhead MFMAs
+  // ahead; mid(I) runs after MFMA I (the next tile's softmax work, which
+  // then overlaps the MFMAs in flight).
+  constexpr int kPvMfma = 4 * CB, kPvAhead = 6;
+  auto pv = [&](const lds_u8* base_p, auto&& mid) __attribute__((always_inline)) {
+    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(base_p));
+    s16x4_t cr[kPvMfma][2];
+    auto rd = [&](auto I) __attribute__((always_inline)) {
+      constexpr int m = decltype(I)::value, s4 = m / CB, cb = m % CB;
+      constexpr int imm = 16 * s4 * kRow + 256 * (cb / 4);
+      cr[m][0] = p2_read_tr<imm>(base + to[0][cb % 4]);
+      cr[m][1] = p2_read_tr<imm>(base + to[1][cb % 4]);
+    };
+    p2_for<0, kPvAhead>(rd);
+    p2_for<0, kPvMfma>([&](auto I) __attribute__((always_inline)) {
+      constexpr int m = decltype(I)::value, s4 = m / CB, cb = m % CB;
+      if constexpr (m + kPvAhead < kPvMfma) {
+        rd(std::integral_constant<int, m + kPvAhead>{});
+        p2_wait_lgkm<2 * kPvAhead>();
+      } else {
+        p2_wait_lgkm<2 * (kPvMfma - 1 - m)>();
+      }
+      p2_tie(cr[m][0]);
+      p2_tie(cr[m][1]);
+      oacc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat_bf16x8(cr[m][0], cr[m][1]), pb[s4], oacc[cb], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      mid(I);
+    });
+  };
+  auto no_mid = [](auto) {};
+
+  // Iteration j < n_tiles - 1 (tile j in buffer j % 3, tile j + 1 in
+  // (j + 1) % 3): wait for this wave's DMAs of tile j + 1 and meet at the
+  // barrier (tile j + 1 complete, every wave done with iteration j - 1 and so
+  // with buffer (j + 2) % 3), start tile j + 2's DMAs into that buffer (past
+  // the last tile they re-read its rows: in bounds, never read), then tile
+  // j + 1's QK and softmax step with tile j's PV in one region, then the
+  // commit.
+  auto iter = [&](int j, auto bc) __attribute__((always_inline)) {
+    constexpr int C = decltype(bc)::value;
+    using N1 = std::integral_constant<int, (C + 1) % 3>;
+    using N2 = std::integral_constant<int, (C + 2) % 3>;
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): this wave's DMAs of tile j + 1 landed
+    lds_barrier();
+    dma_tile(j + 2, buf(N2{}));
+    qk(j + 1, buf(N1{}));
+    pv(buf(bc), smax_mid);
+    commit();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  if (n_tiles > 0) {
+    dma_tile(0, buf(I0{}));
+    dma_tile(1, buf(I1{}));  // past the last tile: re-reads its rows
+    __builtin_amdgcn_s_waitcnt((LQ + 2) | (7 << 4) | (15 << 8));  // vmcnt(LQ + 2): tile 0's DMAs landed
+    lds_barrier();
+    qk(0, buf(I0{}));
+    smax();
+    commit();
+    int j = 0;
+    for (; j + 3 < n_tiles; j += 3) {  // block-uniform; unrolled by three for the static buffers
+      iter(j, I0{});
+      iter(j + 1, I1{});
+      iter(j + 2, I2{});
+    }
+    // the remaining one to three tiles: j .. n_tiles - 1 (tile j in buffer 0)
+    if (j + 1 < n_tiles) iter(j, I0{});
+    if (j + 2 < n_tiles) iter(j + 1, I1{});
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+    lds_barrier();
+    const int last = n_tiles - 1 - j;  // 0, 1 or 2
+    if (last == 0) pv(buf(I0{}), no_mid);
+    else if (last == 1) pv(buf(I1{}), no_mid);
+    else pv(buf(I2{}), no_mid);
+  }
+
+  float l_w = l_part + shfl_xor_f32(l_part, 32);
+  const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
+  if (valid) {
+    // lane (n, hf): channels 32 cb + 8 r4 + 4 hf + {0..3}
+    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + rq * a.o_rs + head * a.o_hs + 4 * hf;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        uint2 pk;
+        pk.x = pack_bf16x2(oacc[cb][4 * r4] * inv, oacc[cb][4 * r4 + 1] * inv);
+        pk.y = pack_bf16x2(oacc[cb][4 * r4 + 2] * inv, oacc[cb][4 * r4 + 3] * inv);
+        *reinterpret_cast<uint2*>(op + 32 * cb + 8 * r4) = pk;
+      }
+  }
+}
+
 int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
   const int T = a.ad.T;
@@ -366,6 +824,14 @@ int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   // Each wave accumulates all R_pad output channels of its query: built for
   // R_pad <= 256 (larger ranks take the per-row decode path).
   if (a.R > 256) return -1;
+  if (dt == 1 && c_dt == 1 && padded_rank(a.R) % 128 == 0) {
+    // bf16 cache, latent rows of a multiple of 256 bytes: the 32x32x16 kernel
+    // (the same eight query tokens per workgroup, so the same grid)
+    static_assert(kP2Waves * kP2Qpw == kNw * kQpw, "query tokens per workgroup");
+    if (padded_rank(a.R) == 256) hipLaunchKernelGGL(mla_prefill_m32<4>, grid, dim3(kP2Waves * 64), 0, s, a);
+    else hipLaunchKernelGGL(mla_prefill_m32<2>, grid, dim3(kP2Waves * 64), 0, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+  }
   const int rc = with_nb(a.R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value < 4 ? decltype(nb)::value : 4;
     if (dt == 1 && c_dt == 1)
