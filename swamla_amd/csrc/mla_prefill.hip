@@ -446,6 +446,10 @@ __device__ __forceinline__ void p2_for(F&& f) {
 }
 template <int A, int B>
 constexpr int p2_min() { return A < B ? A : B; }
+// LDS reads issued for stream slots 0 .. i when the first QK slots take one
+// read each and the rest two
+template <int QK>
+constexpr int p2_nreads(int i) { return i < QK ? i + 1 : QK + 2 * (i - QK + 1); }
 __device__ __forceinline__ int p2_pos(int c, int t) { return (c & ~15) | ((c ^ p2_swz(t)) & 15); }
 }  // namespace
 
@@ -753,6 +757,58 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
   };
   auto no_mid = [](auto) {};
 
+  // qkpv(jn, bq, bp, at, mid): tile jn's QK (slots 0 .. kQkReads - 1, one K
+  // read each) and the previous tile's PV (the following slots, two C^T
+  // reads each) as one stream of MFMAs, with kInFlight LDS reads kept in
+  // flight across the boundary between the two products: at about 300 cycles
+  // of LDS latency under load, the reads in flight, not the LDS bandwidth,
+  // set the rate.  at() runs after the first MFMA (the next tile's DMAs),
+  // mid(m) after PV MFMA m (the softmax step).
+  constexpr int kSlots = kQkReads + kPvMfma, kReads = kQkReads + 2 * kPvMfma, kInFlight = 12;
+  static_assert(kInFlight < 16, "lgkmcnt range");
+  auto qkpv = [&](int jn, const lds_u8* bq_p, const lds_u8* bp_p, auto&& at, auto&& mid) __attribute__((always_inline)) {
+    const uint32_t bq = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(bq_p));
+    const uint32_t bp = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(bp_p));
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) sc[h2] = f32x16_t{};
+    sc_tile = jn;  // before the softmax step placed in the PV slots reads it
+    p2_u32x4_t kr[kQkReads];
+    s16x4_t cr[kPvMfma][2];
+    auto rd = [&](auto R) __attribute__((always_inline)) {  // read R of the stream
+      constexpr int r = decltype(R)::value;
+      if constexpr (r < kQkReads) {
+        constexpr int ks = r / 2, h2 = r % 2;
+        if constexpr (ks < KS) kr[r] = p2_read16<256 * (ks / 8) + 32 * h2 * kRow>(bq + ko[ks % 8]);
+        else kr[r] = p2_read16<32 * h2 * kPeR>(bq + po[ks - KS]);
+      } else {
+        constexpr int m = (r - kQkReads) / 2, e = (r - kQkReads) % 2, s4 = m / CB, cb = m % CB;
+        cr[m][e] = p2_read_tr<16 * s4 * kRow + 256 * (cb / 4)>(bp + to[e][cb % 4]);
+      }
+    };
+    p2_for<0, p2_min<kInFlight, kReads>()>(rd);
+    p2_for<0, kSlots>([&](auto I) __attribute__((always_inline)) {
+      constexpr int i = decltype(I)::value;
+      constexpr int done = p2_nreads<kQkReads>(i);  // reads this slot needs complete
+      constexpr int before = p2_min<(i == 0 ? 0 : p2_nreads<kQkReads>(i - 1)) + kInFlight, kReads>();
+      constexpr int upto = p2_min<done + kInFlight, kReads>();  // reads issued after this slot's issue step
+      p2_for<before, upto>(rd);
+      p2_wait_lgkm<upto - done>();
+      if constexpr (i < kQkReads) {
+        constexpr int ks = i / 2, h2 = i % 2;
+        p2_tie(kr[i]);
+        sc[h2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[ks], sc[h2], 0, 0, 0);
+      } else {
+        constexpr int m = i - kQkReads, s4 = m / CB, cb = m % CB;
+        p2_tie(cr[m][0]);
+        p2_tie(cr[m][1]);
+        oacc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat_bf16x8(cr[m][0], cr[m][1]), pb[s4], oacc[cb], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (i == 0) at();
+      if constexpr (i >= kQkReads) mid(std::integral_constant<int, i - kQkReads>{});
+    });
+  };
+
   // Iteration j < n_tiles - 1 (tile j in buffer j % 3, tile j + 1 in
   // (j + 1) % 3): wait for this wave's DMAs of tile j + 1 and meet at the
   // barrier (tile j + 1 complete, every wave done with iteration j - 1 and so
@@ -766,9 +822,7 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
     using N2 = std::integral_constant<int, (C + 2) % 3>;
     __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): this wave's DMAs of tile j + 1 landed
     lds_barrier();
-    dma_tile(j + 2, buf(N2{}));
-    qk(j + 1, buf(N1{}));
-    pv(buf(bc), smax_mid);
+    qkpv(j + 1, buf(N1{}), buf(bc), [&]() __attribute__((always_inline)) { dma_tile(j + 2, buf(N2{})); }, smax_mid);
     commit();
   };
   using I0 = std::integral_constant<int, 0>;
