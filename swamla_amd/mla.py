@@ -296,6 +296,10 @@ class MLA(nn.Module):
         to R_pad; ``src`` itself is used when kv_lora_rank needs no padding."""
         if self.rank_pad == self.kv_lora_rank:
             return src.detach()
+        return self._derived(name, src, build)
+
+    def _derived(self, name: str, src: torch.Tensor, build) -> torch.Tensor:
+        """``build()``, cached under ``name`` until ``src`` changes."""
         key = (src.data_ptr(), src._version, src.dtype, src.device)
         hit = self._padded_w.get(name)
         if hit is None or hit[0] != key:
@@ -339,6 +343,16 @@ class MLA(nn.Module):
             return view()
         return self._padded("w_uv", self.wkv_b.weight, lambda: kernels.pad_rank(view(), R))
 
+    def _w_uv_fused(self) -> torch.Tensor:
+        """_w_uv() over the fused step's heads (zero for the padding heads)."""
+        H = self.n_heads
+        Hp = self._fused_heads() or H
+        if Hp == H:
+            return self._w_uv()
+        w_uv = self._w_uv()
+        return self._derived("w_uv.fused", self.wkv_b.weight,
+                             lambda: torch.cat([w_uv, w_uv.new_zeros((Hp - H,) + tuple(w_uv.shape[1:]))], 0))
+
     def _w_uk_t(self) -> torch.Tensor:
         """W_uk^T [H, R_pad, nope] for mla_head_product (its rows are the
         latent channels; zero beyond kv_lora_rank)."""
@@ -379,34 +393,54 @@ class MLA(nn.Module):
         key = tuple(None if t is None else (t.data_ptr(), t._version, t.dtype, t.device) for t in ws)
         if self._decode_w is None or self._decode_w[0] != key:
             H, Dn, R, rp = self.n_heads, self.qk_nope_head_dim, self.kv_lora_rank, self.rank_pad
+            Hp = self._fused_heads() or H  # heads past H: zero rows (padding to a launch's 16 heads)
             wq = self.wq.weight.detach().view(H, self.qk_head_dim, self.dim)
             w_uk = kernels.pad_rank(self.wkv_b.weight.detach().view(H, -1, R)[:, :Dn].float(), R)  # [H, Dn, R_pad]
             w_abs = torch.bmm(w_uk.transpose(1, 2).contiguous(), wq[:, :Dn].float().contiguous())
+            w_pe = wq[:, Dn:].float()
+            if Hp > H:
+                w_abs = torch.cat([w_abs, w_abs.new_zeros((Hp - H,) + tuple(w_abs.shape[1:]))], 0)
+                w_pe = torch.cat([w_pe, w_pe.new_zeros((Hp - H,) + tuple(w_pe.shape[1:]))], 0)
             wkv_a, bkv_a = self._wkv_a_padded()
             w_in = torch.cat(
-                [w_abs.reshape(H * rp, self.dim), wq[:, Dn:].float().reshape(-1, self.dim), wkv_a.float()], 0,
+                [w_abs.reshape(Hp * rp, self.dim), w_pe.reshape(-1, self.dim), wkv_a.float()], 0,
             ).to(self.wq.weight.dtype).contiguous()
             b_in = None
             if self.wq.bias is not None and self.wkv_a.bias is not None:
                 bq = self.wq.bias.detach().view(H, self.qk_head_dim)
                 b_abs = torch.bmm(bq[:, None, :Dn].float(), w_uk).reshape(H * rp)
-                b_in = torch.cat([b_abs, bq[:, Dn:].float().reshape(-1), bkv_a.float()]
-                                 ).to(self.wq.bias.dtype).contiguous()
+                b_pe = bq[:, Dn:].float().reshape(-1)
+                if Hp > H:
+                    b_abs = torch.cat([b_abs, b_abs.new_zeros((Hp - H) * rp)])
+                    b_pe = torch.cat([b_pe, b_pe.new_zeros((Hp - H) * (self.qk_head_dim - Dn))])
+                b_in = torch.cat([b_abs, b_pe, bkv_a.float()]).to(self.wq.bias.dtype).contiguous()
             wp = None
             if w_in.is_cuda and kernels.packed_ok(1, w_in.shape[0], w_in.shape[1]):
                 wp = kernels.pack_weight(w_in)
             self._decode_w = (key, w_in, b_in, wp)
         return self._decode_w[1], self._decode_w[2]
 
+    def _wo_fused(self) -> torch.Tensor:
+        """wo.weight over the fused step's heads: its own columns, followed by
+        zero columns for the padding heads (whose read-out is zero)."""
+        H, Dv = self.n_heads, self.v_head_dim
+        Hp = self._fused_heads() or H
+        if Hp == H:
+            return self.wo.weight.detach()
+        w = self.wo.weight.detach()
+        return self._derived("wo.weight.fused", self.wo.weight,
+                             lambda: torch.cat([w, w.new_zeros(w.shape[0], (Hp - H) * Dv)], 1))
+
     def _packed_wo(self) -> Optional["kernels.PackedWeight"]:
-        """wo.weight in mla_linear_packed's layout (None when its shape is not
-        covered); rebuilt when the weight changes."""
+        """_wo_fused() in mla_linear_packed's layout (None when its shape is
+        not covered); rebuilt when the weight changes."""
         w = self.wo.weight
-        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        key = (w.data_ptr(), w._version, w.dtype, w.device, self._fused_heads())
         if self._wo_packed is None or self._wo_packed[0] != key:
             wp = None
-            if w.is_cuda and w.dtype == torch.bfloat16 and kernels.packed_ok(1, w.shape[0], w.shape[1]):
-                wp = kernels.pack_weight(w.detach())
+            wf = self._wo_fused()
+            if wf.is_cuda and wf.dtype == torch.bfloat16 and kernels.packed_ok(1, wf.shape[0], wf.shape[1]):
+                wp = kernels.pack_weight(wf)
             self._wo_packed = (key, wp)
         return self._wo_packed[1]
 
@@ -418,7 +452,7 @@ class MLA(nn.Module):
         128 rows: 340 workgroups) the library GEMM (hipBLASLt through
         torch.nn.functional.linear) is faster, 9.4 against 15.1 us at 128 x 5440 x 1024; else
         mla_linear."""
-        n, H, R, P = x.shape[0] * x.shape[1], self.n_heads, self.rank_pad, self.qk_rope_head_dim
+        n, H, R, P = x.shape[0] * x.shape[1], self._fused_heads() or self.n_heads, self.rank_pad, self.qk_rope_head_dim
         w_in, b_in = self.decode_weights()
         wp = self._decode_w[3]
         xf = x.reshape(n, self.dim)
@@ -444,12 +478,23 @@ class MLA(nn.Module):
             return 32
         return kernels.H
 
+    def _fused_heads(self) -> Optional[int]:
+        """Heads of the fused step's launches: the module's own 16 or 32 (as
+        one decode launch takes them), 16 for fewer heads (zero-padded: the
+        padding heads' query rows, read-out and wo columns are zero), else
+        None."""
+        if self.n_heads == self._decode_heads():
+            return self.n_heads
+        if self.n_heads < kernels.H:
+            return kernels.H
+        return None
+
     def _fused_step_ok(self, x: torch.Tensor, n: int) -> bool:
-        """The decode-step kernels cover bf16 modules with 16 heads (or 32,
-        in one launch), at most 128 query rows, no q low-rank path and
+        """The decode-step kernels cover bf16 modules with up to 16 heads (or
+        32, in one launch), at most 128 query rows, no q low-rank path and
         128-aligned model widths."""
         return (
-            self.n_heads == self._decode_heads()
+            self._fused_heads() is not None
             and self.q_lora_rank == 0
             and x.dtype == torch.bfloat16
             and self.wq.weight.dtype == torch.bfloat16
@@ -676,8 +721,9 @@ class MLA(nn.Module):
         if prefill:
             n_splits, balance = 1, 0
         if fused:
-            o_lat = torch.empty(n, H, self.rank_pad, dtype=x.dtype, device=dev)
-            ws = self._workspace_for(n, n_splits, dev, heads=H)
+            Hp = self._fused_heads()  # the launches' heads: H, or 16 with zero padding heads
+            o_lat = torch.empty(n, Hp, self.rank_pad, dtype=x.dtype, device=dev)
+            ws = self._workspace_for(n, n_splits, dev, heads=Hp)
             if prefill:
                 kernels.prefill_attention(q_abs, q_pe, cos, sin, cache, self.softmax_scale, start_pos=sp,
                                           rows_per_seq=T, rope_abs=rope_abs, out=o_lat)
@@ -692,16 +738,16 @@ class MLA(nn.Module):
                 )
             # o[r, h*Dv + d] = W_uv[h][d] . merged o_lat[r, h]: split merge and
             # read-out in one launch, written straight in wo's input layout
-            w_uv = self._w_uv()
-            o = torch.empty(n, H * Dv, dtype=x.dtype, device=dev)
-            kernels.merge_project(o_lat, w_uv, o.view(n, H, Dv), cache, n_splits=n_splits, min_chunk=min_chunk,
+            w_uv = self._w_uv_fused()
+            o = torch.empty(n, Hp * Dv, dtype=x.dtype, device=dev)
+            kernels.merge_project(o_lat, w_uv, o.view(n, Hp, Dv), cache, n_splits=n_splits, min_chunk=min_chunk,
                                   workspace=ws, start_pos=sp, rows_per_seq=T, balanced=balance > 0)
             wo_b = None if self.wo.bias is None else self.wo.bias.detach()
             wo_p = self._packed_wo()
             if wo_p is not None and kernels.packed_ok(n, wo_p.N, wo_p.K):
                 out = kernels.linear_packed(o, wo_p, bias=wo_b).view(B, T, self.dim)
             else:
-                out = kernels.linear(o, self.wo.weight.detach(), bias=wo_b).view(B, T, self.dim)
+                out = kernels.linear(o, self._wo_fused(), bias=wo_b).view(B, T, self.dim)
             return self.resid_dropout(out)  # mla.py:490-495
 
         # Other calls: the absorbed products, then attention.  The attention

@@ -283,7 +283,8 @@ def test_module_other_head_counts(gpu, dtype, n_head, dim, nope, rank, monkeypat
     restatement with the same weights; cache rows bit-exact.  bf16 modules
     with 32 heads run every attention call as one 32-head launch (the cache
     streamed once); other counts as 16-head launches over zero-padded query
-    heads."""
+    heads.  bf16 decode steps take the fused step, with fewer than 16 heads
+    padded to 16 (zero query rows, read-out and wo columns)."""
     say(f"n_head={n_head} dim={dim} nope={nope} rank={rank} dtype={dtype}")
     cfg = MLAConfig(n_embd=dim, n_head=n_head, max_batch_size=2, max_seq_len=192, kv_lora_rank=rank,
                     qk_nope_head_dim=nope)
@@ -296,6 +297,14 @@ def test_module_other_head_counts(gpu, dtype, n_head, dim, nope, rank, monkeypat
         return real(q_abs, *a, **k)
 
     monkeypatch.setattr(kernels, "decode_attention", spy)
+    fused = []
+    real_mp = kernels.merge_project
+
+    def spy_mp(o_lat, *a, **k):
+        fused.append(o_lat.shape[1])
+        return real_mp(o_lat, *a, **k)
+
+    monkeypatch.setattr(kernels, "merge_project", spy_mp)
     g = torch.Generator().manual_seed(42 + n_head)
     x = torch.randn(2, 160, dim, generator=g).to(dtype)
     xs = [x.to(gpu)]
@@ -311,6 +320,12 @@ def test_module_other_head_counts(gpu, dtype, n_head, dim, nope, rank, monkeypat
         assert calls == [32] * 7, calls  # one launch per call: the prompt and each decode step
     else:
         assert calls == [16] * (7 * -(-n_head // 16)), calls
+    # bf16 decode steps run the fused four-launch step (its merge + read-out
+    # launch), fewer than 16 heads padded to 16 with zero heads
+    if dtype == torch.bfloat16:
+        assert fused == [max(n_head, 16)] * 6, fused
+    else:
+        assert fused == [], fused
 
 
 def test_out_of_range_positions_raise(gpu):
