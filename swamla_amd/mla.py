@@ -453,21 +453,76 @@ class MLA(nn.Module):
         torch.nn.functional.linear) is faster, 9.4 against 15.1 us at 128 x 5440 x 1024; else
         mla_linear."""
         n, H, R, P = x.shape[0] * x.shape[1], self._fused_heads() or self.n_heads, self.rank_pad, self.qk_rope_head_dim
-        w_in, b_in = self.decode_weights()
-        wp = self._decode_w[3]
         xf = x.reshape(n, self.dim)
+        if self.q_lora_rank > 0:
+            # wq_a with wkv_a in one product, q_norm, then wq_b with W_uk absorbed
+            (w1, b1, w1p), (w2, b2, w2p) = self._decode_weights_lora()
+            y1 = self._product(xf, w1, b1, w1p)
+            ql = self.q_lora_rank
+            qn = torch.nn.functional.layer_norm(y1[:, :ql], (ql,), self.q_norm.weight, self.q_norm.bias,
+                                                self.q_norm.eps)  # mla.py:102, :286
+            y = self._product(qn, w2, b2, w2p)
+            return y[:, : H * R].view(n, H, R), y[:, H * R:].view(n, H, P), y1[:, ql:]
+        w_in, b_in = self.decode_weights()
+        y = self._product(xf, w_in, b_in, self._decode_w[3])
+        q_abs = y[:, : H * R].view(n, H, R)
+        q_pe = y[:, H * R: H * (R + P)].view(n, H, P)
+        return q_abs, q_pe, y[:, H * (R + P):]
+
+    def _product(self, x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor],
+                 wp: Optional["kernels.PackedWeight"]) -> torch.Tensor:
+        """x . w^T (+ b) for the decode step: mla_linear_packed with the packed
+        copy while its grid fits the CUs in one round; past that, or for a K
+        the kernels do not take, the library GEMM; else mla_linear."""
+        n, K = x.shape
         if wp is not None and kernels.packed_ok(n, wp.N, wp.K):
             if self._num_cus is None:
                 self._num_cus = torch.cuda.get_device_properties(x.device).multi_processor_count
             if kernels.packed_blocks(n, wp.N, wp.K) <= self._num_cus:
-                y = kernels.linear_packed(xf, wp, bias=b_in)
-            else:
-                y = torch.nn.functional.linear(xf, w_in, b_in)
-        else:
-            y = kernels.linear(xf, w_in, bias=b_in)
-        q_abs = y[:, : H * R].view(n, H, R)
-        q_pe = y[:, H * R: H * (R + P)].view(n, H, P)
-        return q_abs, q_pe, y[:, H * (R + P):]
+                return kernels.linear_packed(x, wp, bias=b)
+            return torch.nn.functional.linear(x, w, b)
+        if K % 128 == 0 and x.stride(1) == 1:
+            return kernels.linear(x, w, bias=b)
+        return torch.nn.functional.linear(x, w, b)
+
+    def _decode_weights_lora(self):
+        """The q low-rank module's two stacked decode-step weights, each as
+        (weight, bias or None, packed copy or None): [wq_a | wkv_a (R_pad +
+        P rows)] over the model width, and [W_uk[h]^T . wq_b_nope[h] per head
+        (padded to the fused step's heads) | wq_b_pe] over q_lora_rank (the
+        absorbed block formed in fp32, rounded once)."""
+        ws = (self.wq_a.weight, self.wq_b.weight, self.wkv_a.weight, self.wkv_b.weight, self.wq_a.bias,
+              self.wq_b.bias, self.wkv_a.bias)
+        key = tuple(None if t is None else (t.data_ptr(), t._version, t.dtype, t.device) for t in ws)
+        if self._decode_w is None or self._decode_w[0] != key:
+            H, Dn, R, rp, ql = self.n_heads, self.qk_nope_head_dim, self.kv_lora_rank, self.rank_pad, self.q_lora_rank
+            Hp = self._fused_heads() or H
+            dt = self.wq_a.weight.dtype
+            wkv_a, bkv_a = self._wkv_a_padded()
+            w1 = torch.cat([self.wq_a.weight.detach(), wkv_a], 0).to(dt).contiguous()
+            b1 = None
+            if self.wq_a.bias is not None:
+                b1 = torch.cat([self.wq_a.bias.detach(), bkv_a]).to(dt).contiguous()
+            wqb = self.wq_b.weight.detach().view(H, self.qk_head_dim, ql)
+            w_uk = kernels.pad_rank(self.wkv_b.weight.detach().view(H, -1, R)[:, :Dn].float(), R)  # [H, Dn, R_pad]
+            w_abs = torch.bmm(w_uk.transpose(1, 2).contiguous(), wqb[:, :Dn].float().contiguous())  # [H, R_pad, ql]
+            w_pe = wqb[:, Dn:].float()
+            if Hp > H:
+                w_abs = torch.cat([w_abs, w_abs.new_zeros((Hp - H,) + tuple(w_abs.shape[1:]))], 0)
+                w_pe = torch.cat([w_pe, w_pe.new_zeros((Hp - H,) + tuple(w_pe.shape[1:]))], 0)
+            w2 = torch.cat([w_abs.reshape(Hp * rp, ql), w_pe.reshape(-1, ql)], 0).to(dt).contiguous()
+            b2 = None
+            if self.wq_b.bias is not None:
+                bq = self.wq_b.bias.detach().view(H, self.qk_head_dim)
+                b_abs = torch.bmm(bq[:, None, :Dn].float(), w_uk).reshape(H * rp)
+                b_pe = bq[:, Dn:].float().reshape(-1)
+                if Hp > H:
+                    b_abs = torch.cat([b_abs, b_abs.new_zeros((Hp - H) * rp)])
+                    b_pe = torch.cat([b_pe, b_pe.new_zeros((Hp - H) * (self.qk_head_dim - Dn))])
+                b2 = torch.cat([b_abs, b_pe]).to(dt).contiguous()
+            pk = lambda w: kernels.pack_weight(w) if (w.is_cuda and kernels.packed_ok(1, w.shape[0], w.shape[1])) else None
+            self._decode_w = (key, (w1, b1, pk(w1)), (w2, b2, pk(w2)))
+        return self._decode_w[1], self._decode_w[2]
 
     def _decode_heads(self) -> int:
         """Heads one decode launch takes for this module: all 32 of a bf16
@@ -491,17 +546,20 @@ class MLA(nn.Module):
 
     def _fused_step_ok(self, x: torch.Tensor, n: int) -> bool:
         """The decode-step kernels cover bf16 modules with up to 16 heads (or
-        32, in one launch), at most 128 query rows, no q low-rank path and
-        128-aligned model widths."""
+        32, in one launch), at most 128 query rows and 128-aligned model
+        widths; a q low-rank module runs its query through two products with
+        q_norm between them."""
+        wq = self.wq if self.q_lora_rank == 0 else self.wq_a
+        q_bias = (wq.bias is not None) if self.q_lora_rank == 0 else (
+            (self.wq_a.bias is not None) and (self.wq_b.bias is not None))
         return (
             self._fused_heads() is not None
-            and self.q_lora_rank == 0
             and x.dtype == torch.bfloat16
-            and self.wq.weight.dtype == torch.bfloat16
+            and wq.weight.dtype == torch.bfloat16
             and 0 < n <= kernels.LINEAR_MAX_ROWS
             and self.dim % 128 == 0
             and (self.n_heads * self.v_head_dim) % 128 == 0
-            and (self.wq.bias is None) == (self.wkv_a.bias is None)
+            and q_bias == (self.wkv_a.bias is not None)
             and self.v_head_dim == 128
         )
 

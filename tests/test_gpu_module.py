@@ -249,14 +249,19 @@ def test_no_cache_forward_matches_reference(gpu):
     (256, 96, 256), (200, 160, 1024), (300, 0, 1024),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_module_any_rank_and_q_lora(gpu, dtype, rank, q_lora, dim):
+def test_module_any_rank_and_q_lora(gpu, dtype, rank, q_lora, dim, monkeypatch):
     """kv_lora_rank other than 256 (the real model scales it per layer:
     swa_mla_model.py:216-247) and the low-rank query path (mla.py:98-103):
     a prefill chunk, then decode steps at batch 2, against the reference
-    restatement with the same weights; cache rows bit-exact."""
+    restatement with the same weights; cache rows bit-exact.  bf16 decode
+    steps take the fused step (a q low-rank module through its two products
+    with q_norm between them)."""
     say(f"rank={rank} q_lora={q_lora} dim={dim} dtype={dtype}")
     cfg = MLAConfig(n_embd=dim, max_batch_size=2, max_seq_len=192, kv_lora_rank=rank, q_lora_rank=q_lora)
     ref, ours = make_pair(cfg, 31 + rank, dtype, gpu, ln_random=True)
+    fused = []
+    real_mp = kernels.merge_project
+    monkeypatch.setattr(kernels, "merge_project", lambda *a, **k: (fused.append(1), real_mp(*a, **k))[1])
     assert ours.kv_cache.shape[-1] == 64 * -(-rank // 64)
     g = torch.Generator().manual_seed(32 + rank)
     x = torch.randn(2, 40, dim, generator=g).to(dtype)
@@ -270,6 +275,7 @@ def test_module_any_rank_and_q_lora(gpu, dtype, rank, q_lora, dim):
     torch.cuda.synchronize()
     assert_cache_bits(ours, xs, dtype)
     assert bool((ours.kv_cache[:2, :46, rank:].float() == 0).all())
+    assert len(fused) == (7 if dtype == torch.bfloat16 else 0), fused  # the 80-row prompt and six steps
 
 
 @pytest.mark.parametrize("n_head,dim,nope,rank", [(12, 1024, 128, 256), (32, 1024, 128, 256), (8, 512, 128, 173),
