@@ -22,9 +22,9 @@
  * Geometry of this build: heads H = 16, qk_rope_head_dim P = 64 and any
  * kv_lora_rank 1 <= R <= 512 (the real model scales the rank per layer).
  * mla_decode_attn, mla_decode_attn_append, mla_merge and mla_merge_project
- * also take H = 32 in one launch for a bf16 model and cache with R_pad <= 256
- * (the reference's xl preset, models/swa_mla_model.py:618-640: the decode
- * workgroup runs two 16-head groups over the same cache tiles).
+ * also take H = 32 in one launch for a bf16 model with R_pad <= 256 (the
+ * reference's xl preset, models/swa_mla_model.py:618-640: each decode wave
+ * serves two 16-head groups from the same cache tiles, streamed once).
  * Other values return SWAMLA_ERR_UNSUPPORTED.  Latent rows are laid out with
  * R_pad = 64 * ceil(R / 64) channels (R_pad = R for the BASELINE rank 256):
  * caches, queries, outputs, partials and the latent half of input rows hold

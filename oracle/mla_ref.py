@@ -6,6 +6,9 @@ line, including their quirks:
     (positional_encoding.py:30-34, :49-50; mla.py:299-303, :318-323);
   * interleaved pairs, cos/sin buffers converted with the module dtype and
     every op rounded in that dtype (positional_encoding.py:21-28, :57-60);
+  * a call longer than the table rebuilds it in fp32 on the buffers' device
+    (positional_encoding.py:44-46, :64-86), so a bf16 module's rotation turns
+    fp32 and its SDPA then receives fp32 queries/keys with bf16 values;
   * caches are ``torch.zeros`` buffers created by ``set_inference_mode``
     (mla.py:207-215), so they must be enabled before ``.to(dtype)``;
   * attention re-projects the whole cache through wkv_b and runs SDPA with
@@ -65,11 +68,24 @@ class RefRoPE(nn.Module):
         xr = x.view(B, Hh, T, D // 2, 2)
         x1, x2 = xr[..., 0].contiguous(), xr[..., 1].contiguous()
         if T > self.max_seq_len:
-            raise ValueError("oracle RoPE: T beyond the table")
+            self._extend_cos_sin_cache(T)
         cos = self.cos_cached[:, :, :T, : (D // 2)].expand(B, Hh, T, -1).contiguous()
         sin = self.sin_cached[:, :, :T, : (D // 2)].expand(B, Hh, T, -1).contiguous()
         rotated = torch.stack([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)
         return rotated.view(B, Hh, T, D).contiguous()
+
+    def _extend_cos_sin_cache(self, new_max_len: int) -> None:  # :64-86
+        """Rebuilds the table in fp32 on the buffers' device for new_max_len
+        positions and replaces the buffers (their dtype becomes fp32)."""
+        if new_max_len <= self.max_seq_len:
+            return
+        self.max_seq_len = new_max_len
+        dev = self.cos_cached.device
+        inv_freq = (1.0 / (self.base ** (torch.arange(0, self.dim, 2).float() / self.dim))).to(dev)
+        t = torch.arange(new_max_len, device=dev).type_as(inv_freq)
+        emb = torch.cat((torch.einsum("i,j->ij", t, inv_freq),) * 2, dim=-1)
+        self.register_buffer("cos_cached", emb.cos().view(1, 1, new_max_len, self.dim), persistent=False)
+        self.register_buffer("sin_cached", emb.sin().view(1, 1, new_max_len, self.dim), persistent=False)
 
     def forward(self, x: torch.Tensor, seq_len=None) -> torch.Tensor:  # :88-91
         if seq_len is None:

@@ -195,9 +195,9 @@ int check_decode(const char* fn, const void* q_abs, int64_t q_abs_rs, int64_t q_
                  float* lse_out, int32_t dtype, int32_t cache_dtype, swamla::DecodeArgs* a,
                  int32_t max_rows = 65535, bool allow32 = false) {
   if (int e = check_geometry(H, R, P, allow32)) return e;
-  if (H == 32 && (dtype != SWAMLA_DTYPE_BF16 || cache_dtype != SWAMLA_DTYPE_BF16 || swamla::padded_rank(R) > 256))
+  if (H == 32 && (dtype != SWAMLA_DTYPE_BF16 || swamla::padded_rank(R) > 256))
     return fail(SWAMLA_ERR_UNSUPPORTED,
-                "%s: 32 heads in one launch are built for a bf16 model and cache with kv_lora_rank <= 256", fn);
+                "%s: 32 heads in one launch are built for a bf16 model with kv_lora_rank <= 256", fn);
   if (int e = check_pair(dtype, cache_dtype)) return e;
   if (n_rows < 0 || n_rows > max_rows)
     return fail(SWAMLA_ERR_INVALID_ARG, "%s: n_rows=%d outside [0, %d]", fn, n_rows, max_rows);

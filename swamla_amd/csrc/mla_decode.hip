@@ -81,7 +81,7 @@ constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 // Geometry of one instance (cache dtype, R_pad = 64 NB, HG head groups of 16
-// heads: 4 HG waves per workgroup).
+// heads, all served by each of the workgroup's four waves).
 template <int C_DT, int NB, int HG = 1>
 struct DecGeo {
   static constexpr int RP = 64 * NB;
@@ -95,10 +95,9 @@ struct DecGeo {
   // processed, at most kCap more are in flight.  Fewer bytes in flight stream
   // faster here: 2 and 2 (three buffers) against 3 and 3 (four buffers)
   // measured 18.1 against 18.4-18.9 us per config-2 launch, and 89.9
-  // against 90.6-91.1 us at config 5 (e4m3).  Two head groups (eight waves)
-  // keep one sub-tile in flight: two buffers per wave fill the 160 KB.
-  static constexpr int kWavesWG = kDecWaves * HG;
-  static constexpr int kFillWant = HG == 1 ? 2 : 1, kCapWant = HG == 1 ? 2 : 1;
+  // against 90.6-91.1 us at config 5 (e4m3).
+  static constexpr int kWavesWG = kDecWaves;
+  static constexpr int kFillWant = 2, kCapWant = 2;
   static constexpr int NBUF =
       cmin(cmin(cmax(kCapWant + 1, kFillWant), (kLdsMax / kWavesWG - kStage) / kSub), 63 / kVm + 1);
   static constexpr int kCap = cmin(kCapWant, NBUF - 1);
@@ -106,17 +105,18 @@ struct DecGeo {
   // The fused append's LayerNorm stages its row in a ring buffer the fill
   // leaves free, else in an area of its own.
   static constexpr int kLnOwn = kFill == NBUF ? ln_stage_bytes<1>() : 0;
-  static constexpr int kWave = NBUF * kSub + kStage + kLnOwn;  // LDS bytes per wave
-  // epilogue: each wave stashes, in its own ring, per head a row of RP fp32
-  // (+4 pad) and then its max / l / e per head
+  // epilogue: each wave stashes, in its own LDS area, per head group and head
+  // a row of RP fp32 (+4 pad), then its max / l / e per head
   static constexpr int kCombRow = RP + 4;
-  static constexpr int kStash = (kH * kCombRow + 3 * kH) * 4;
+  static constexpr int kStashG = kH * kCombRow + 3 * kH;  // floats per head group
+  static constexpr int kStash = HG * kStashG * 4;
+  static constexpr int kRing = NBUF * kSub + kStage + kLnOwn;
+  static constexpr int kWave = cmax(kRing, kStash);  // LDS bytes per wave
   static constexpr int kLds = kWavesWG * kWave;
   static_assert(NBUF >= 2, "a sub-tile ring needs two buffers");
   static_assert(ln_stage_bytes<1>() <= kSub, "the fused LayerNorm stages its row in a ring buffer");
   static_assert(kCap >= 1 && kFill >= 1 && kCap <= NBUF - 1, "ring depth");
   static_assert(kLds <= kLdsMax, "LDS budget");
-  static_assert(kStash <= kWave, "a wave's epilogue stash fits its ring");
 };
 
 // s_waitcnt vmcnt(N) (gfx9 encoding; expcnt / lgkmcnt not waited for).
@@ -136,17 +136,13 @@ __device__ __forceinline__ void wait_subtiles(int ahead) {
   wait_vm<0>();
 }
 
-// 16 (4) bytes per lane from global memory into LDS at dst + 16 (4) * lane.
-// AUX 2 marks the load non-temporal (one head group: the cache is streamed
-// once); two head groups load the same lines twice and keep them cacheable
-// (AUX 0), so the second group's requests hit the L2.
-template <int AUX = 2>
+// 16 (4) bytes per lane from global memory into LDS at dst + 16 (4) * lane,
+// non-temporal (aux 2): the cache is streamed once.
 __device__ __forceinline__ void dma16(const void* src, lds_u8* dst) {
-  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 16, 0, AUX);
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 16, 0, 2);
 }
-template <int AUX = 2>
 __device__ __forceinline__ void dma4(const void* src, lds_u8* dst) {
-  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 4, 0, AUX);
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void*>(dst), 4, 0, 2);
 }
 
 template <typename T>
@@ -210,7 +206,6 @@ struct SubStream {
   using G = DecGeo<C_DT, NB, HG>;
   static constexpr int kLatQ = G::kLat / 1024;
   static constexpr int kLatRow = C_DT == 2 ? G::RP : 2 * G::RP;  // bytes of a latent cache row
-  static constexpr int kAux = HG == 1 ? 2 : 0;                      // see dma16
   int t0, t_last, rem, my_n, j_base, w;
   int64_t row0;
   const uint8_t* ckv;
@@ -254,10 +249,10 @@ struct SubStream {
       const uint8_t* lb = ckv + (row0 + tb) * kLatRow;
       const uint8_t* pb = kpe + (row0 + tb) * (2 * kP);
 #pragma unroll
-      for (int q = 0; q < kLatQ; ++q) dma16<kAux>(lb + lat_off[q], dst + 1024 * q);
+      for (int q = 0; q < kLatQ; ++q) dma16(lb + lat_off[q], dst + 1024 * q);
 #pragma unroll
-      for (int q = 0; q < 2; ++q) dma16<kAux>(pb + pe_off[q], dst + G::kLat + 1024 * q);
-      if constexpr (C_DT == 2) dma4<kAux>(scale + row0 + tb + (lane & 15), dst + G::kLat + G::kPe);
+      for (int q = 0; q < 2; ++q) dma16(pb + pe_off[q], dst + G::kLat + 1024 * q);
+      if constexpr (C_DT == 2) dma4(scale + row0 + tb + (lane & 15), dst + G::kLat + G::kPe);
       return;
     }
     // the split's last, partial sub-tile: rows past its end re-read its last row
@@ -265,17 +260,17 @@ struct SubStream {
     for (int q = 0; q < kLatQ; ++q) {
       const int tt = (1024 * q + 16 * lane) / kLatRow;
       const int tok = min(tb + tt, t_last);
-      dma16<kAux>(ckv + (row0 + tok) * kLatRow + (lat_off[q] - tt * kLatRow), dst + 1024 * q);
+      dma16(ckv + (row0 + tok) * kLatRow + (lat_off[q] - tt * kLatRow), dst + 1024 * q);
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int tt = 8 * q + (lane >> 3);
       const int tok = min(tb + tt, t_last);
-      dma16<kAux>(kpe + (row0 + tok) * (2 * kP) + (pe_off[q] - tt * (2 * kP)), dst + G::kLat + 1024 * q);
+      dma16(kpe + (row0 + tok) * (2 * kP) + (pe_off[q] - tt * (2 * kP)), dst + G::kLat + 1024 * q);
     }
     if constexpr (C_DT == 2) {
       const int tok = min(tb + (lane & 15), t_last);
-      dma4<kAux>(scale + row0 + tok, dst + G::kLat + G::kPe);
+      dma4(scale + row0 + tok, dst + G::kLat + G::kPe);
     }
   }
 };
@@ -283,18 +278,17 @@ struct SubStream {
 }  // namespace
 
 template <int C_DT, bool FUSE, int NB, int HG>
-__global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeArgs a) {
+__global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a) {
   using G = DecGeo<C_DT, NB, HG>;
   constexpr int RP = G::RP, NBUF = G::NBUF;
   constexpr int HT = kH * HG;  // heads of the launch
   __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[G::kLds];
   lds_u8* const lds = (lds_u8*)(lds_raw);  // the LDS address space, for the DMA and typed LDS access
 
-  // Waves 4 hg .. 4 hg + 3 serve heads 16 hg .. 16 hg + 15: each head group
-  // streams the split into its own rings (the second group's reads of the
-  // same lines are L2 hits) and runs its own online softmax.
-  const int wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup
-  const int hg = wg / kDecWaves, w = wg % kDecWaves;               // head group, wave in it
+  // Each wave serves all HG head groups (heads 16 hg .. 16 hg + 15) from one
+  // stream of its sub-tiles: every operand read from LDS feeds one MFMA per
+  // head group, and each head group runs its own online softmax.
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   if constexpr (FUSE) {
@@ -325,14 +319,19 @@ __global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeA
   // 32 kb + 8 g); issued before anything waits.  These and the other loads
   // ahead of the first tile are vm_load()s, released after the explicit wait
   // below.
-  const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + r * a.qa_rs + (kH * hg + n) * a.qa_hs;
-  uint32_t qraw[2 * NB][4];
+  uint32_t qraw[HG][2 * NB][4], praw[HG][2][4];
 #pragma unroll
-  for (int s = 0; s < 2 * NB; ++s) vm_load<4>(qa + 32 * s + 8 * g, qraw[s]);
-  const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + r * a.qp_rs + (kH * hg + n) * a.qp_hs;
-  uint32_t praw[2][4];
+  for (int hg = 0; hg < HG; ++hg) {
+    const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + r * a.qa_rs + (kH * hg + n) * a.qa_hs;
 #pragma unroll
-  for (int s = 0; s < 2; ++s) vm_load<4>(qp + 32 * s + 8 * g, praw[s]);
+    for (int s = 0; s < 2 * NB; ++s) vm_load<4>(qa + 32 * s + 8 * g, qraw[hg][s]);
+  }
+#pragma unroll
+  for (int hg = 0; hg < HG; ++hg) {
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + r * a.qp_rs + (kH * hg + n) * a.qp_hs;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) vm_load<4>(qp + 32 * s + 8 * g, praw[hg][s]);
+  }
 
   const int b = ra.b;
   int L = ra.pos;
@@ -351,7 +350,7 @@ __global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeA
   const int64_t row0 = static_cast<int64_t>((b < 0 || b >= a.cache_b) ? 0 : b) * a.cache_s;
 
   // ---- this wave's sub-tiles; wave w's k-th goes to ring buffer k % NBUF
-  lds_u8* const wave_lds = lds + wg * G::kWave;
+  lds_u8* const wave_lds = lds + w * G::kWave;
   lds_u8* const stage = wave_lds + NBUF * G::kSub;  // e4m3 only
   const SubStream<C_DT, NB, HG> ss(t0, t1, w, lane, row0, a.ckv, a.kpe, a.ckv_scale, wave_lds);
   const int rem = ss.rem, my_n = ss.my_n;
@@ -401,8 +400,7 @@ __global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeA
       }
     }
   }
-  // the wave holding the new token's sub-tile, in each head group (each
-  // computes the token's row, the same bits; head group 0 stores it)
+  // the wave holding the new token's sub-tile
   const bool fa_wave = FUSE && fa_own && w == fa_w;  // wave-uniform
   FusedIn<NB> fin;
   if constexpr (FUSE)
@@ -411,11 +409,17 @@ __global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeA
 #pragma unroll
   for (int k = 1; k < G::kFill; ++k) issue(k);
 
-  bf16x8_t qb[2 * NB + 2];  // Q^T, set once the query has landed
-  f32x4_t oacc[4 * NB];
+  bf16x8_t qb[HG][2 * NB + 2];  // Q^T, set once the query has landed
+  f32x4_t oacc[HG][4 * NB];
+  float m_run[HG], l_part[HG], e_part[HG];
 #pragma unroll
-  for (int i = 0; i < 4 * NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_part = 0.f, e_part = 0.f;
+  for (int hg = 0; hg < HG; ++hg) {
+#pragma unroll
+    for (int i = 0; i < 4 * NB; ++i) oacc[hg][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[hg] = -INFINITY;
+    l_part[hg] = 0.f;
+    e_part[hg] = 0.f;
+  }
   FusedTok<C_DT, NB> ftok;
 
   // Operand addresses within a sub-tile (bytes), K = kSwG chunks per swizzle
@@ -508,58 +512,70 @@ __global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeA
       ctr[MB] = ds_read_tr16<16 * kGrp * (MB / kPvM)>(lat + pv_m[MB % kPvM]);
     });
 
-    // S^T = K . Q^T
-    f32x4_t s_c = {0.f, 0.f, 0.f, 0.f}, s_p = {0.f, 0.f, 0.f, 0.f};
+    // S^T = K . Q^T, per head group from the same K registers
+    f32x4_t s_c[HG], s_p[HG];
 #pragma unroll
-    for (int i = 0; i < 2 * NB; ++i)
-      s_c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[i], s_c, 0, 0, 0);
+    for (int hg = 0; hg < HG; ++hg) {
+      s_c[hg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      s_p[hg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const bf16x8_t kp = __builtin_bit_cast(bf16x8_t, kr[2 * NB + i]);
-      if constexpr (C_DT == 2) s_p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp, qb[2 * NB + i], s_p, 0, 0, 0);
-      else s_c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp, qb[2 * NB + i], s_c, 0, 0, 0);
+      for (int i = 0; i < 2 * NB; ++i)
+        s_c[hg] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[hg][i], s_c[hg], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const bf16x8_t kp = __builtin_bit_cast(bf16x8_t, kr[2 * NB + i]);
+        if constexpr (C_DT == 2) s_p[hg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp, qb[hg][2 * NB + i], s_p[hg], 0, 0, 0);
+        else s_c[hg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp, qb[hg][2 * NB + i], s_c[hg], 0, 0, 0);
+      }
     }
 
     const float sc4[4] = {scv.x, scv.y, scv.z, scv.w};
-    float x[4];
+    s16x4_t pb[HG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float sv = (C_DT == 2) ? (sc4[i] * s_c[i] + s_p[i]) : s_c[i];
-      x[i] = tb + 4 * g + i < t1 ? sv * a.scale_log2 : -INFINITY;
-    }
-    float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    mt = wave_max_rows(mt);  // head n's maximum over the sub-tile (finite: token tb is valid)
-    if (__any(mt > m_run + kLazy)) {
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = exp2f(m_run - m_new);
-      m_run = m_new;
-      l_part *= alpha;
-      e_part *= alpha;
+    for (int hg = 0; hg < HG; ++hg) {
+      float x[4];
 #pragma unroll
-      for (int i = 0; i < 4 * NB; ++i) oacc[i] = oacc[i] * alpha;
-    }
-    float p[4];
+      for (int i = 0; i < 4; ++i) {
+        const float sv = (C_DT == 2) ? (sc4[i] * s_c[hg][i] + s_p[hg][i]) : s_c[hg][i];
+        x[i] = tb + 4 * g + i < t1 ? sv * a.scale_log2 : -INFINITY;
+      }
+      float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      mt = wave_max_rows(mt);  // head n's maximum over the sub-tile (finite: token tb is valid)
+      if (__any(mt > m_run[hg] + kLazy)) {
+        const float m_new = fmaxf(m_run[hg], mt);
+        const float alpha = exp2f(m_run[hg] - m_new);
+        m_run[hg] = m_new;
+        l_part[hg] *= alpha;
+        e_part[hg] *= alpha;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = exp2f(x[i] - m_run);
-    // bf16 weights (hardware RNE); l sums exactly those values, so a constant
-    // latent row is reproduced exactly; e sums the fp32 weights for the
-    // log-sum-exp (the bf16 roundings would move it by up to 2^-9 relative)
-    const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
-    l_part += (u2f(w01 << 16) + u2f(w01 & 0xFFFF0000u)) + (u2f(w23 << 16) + u2f(w23 & 0xFFFF0000u));
-    e_part += (p[0] + p[1]) + (p[2] + p[3]);
-    uint2 pw = make_uint2(w01, w23);
-    if constexpr (C_DT == 2) {
-      pw.x = pack_bf16x2(u2f(w01 << 16) * sc4[0], u2f(w01 & 0xFFFF0000u) * sc4[1]);
-      pw.y = pack_bf16x2(u2f(w23 << 16) * sc4[2], u2f(w23 & 0xFFFF0000u) * sc4[3]);
+        for (int i = 0; i < 4 * NB; ++i) oacc[hg][i] = oacc[hg][i] * alpha;
+      }
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = exp2f(x[i] - m_run[hg]);
+      // bf16 weights (hardware RNE); l sums exactly those values, so a constant
+      // latent row is reproduced exactly; e sums the fp32 weights for the
+      // log-sum-exp (the bf16 roundings would move it by up to 2^-9 relative)
+      const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
+      l_part[hg] += (u2f(w01 << 16) + u2f(w01 & 0xFFFF0000u)) + (u2f(w23 << 16) + u2f(w23 & 0xFFFF0000u));
+      e_part[hg] += (p[0] + p[1]) + (p[2] + p[3]);
+      uint2 pw = make_uint2(w01, w23);
+      if constexpr (C_DT == 2) {
+        pw.x = pack_bf16x2(u2f(w01 << 16) * sc4[0], u2f(w01 & 0xFFFF0000u) * sc4[1]);
+        pw.y = pack_bf16x2(u2f(w23 << 16) * sc4[2], u2f(w23 & 0xFFFF0000u) * sc4[3]);
+      }
+      pb[hg] = __builtin_bit_cast(s16x4_t, pw);
     }
-    const s16x4_t pb = __builtin_bit_cast(s16x4_t, pw);
 
-    // O^T[16 mb + ., head] += C^T . P^T
+    // O^T[16 mb + ., head] += C^T . P^T, per head group from the same C^T registers
     lds_fence();
 #pragma unroll
     for (int mb = 0; mb < 4 * NB; ++mb) {
       tie(ctr[mb]);
-      oacc[mb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ctr[mb], pb, oacc[mb], 0, 0, 0);
+#pragma unroll
+      for (int hg = 0; hg < HG; ++hg)
+        oacc[hg][mb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ctr[mb], pb[hg], oacc[hg][mb], 0, 0, 0);
     }
   };
 
@@ -568,23 +584,32 @@ __global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeA
   // discarded.  It brings the body into the instruction cache (a cold first
   // pass costs over a microsecond) while the loads are in flight.
 #pragma unroll
-  for (int i = 0; i < 2 * NB + 2; ++i) qb[i] = as_bf16x8(make_uint4(0u, 0u, 0u, 0u));
+  for (int hg = 0; hg < HG; ++hg)
+#pragma unroll
+    for (int i = 0; i < 2 * NB + 2; ++i) qb[hg][i] = as_bf16x8(make_uint4(0u, 0u, 0u, 0u));
   process(0, true);
 #pragma unroll
-  for (int i = 0; i < 4 * NB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  m_run = -INFINITY;
-  l_part = 0.f;
-  e_part = 0.f;
+  for (int hg = 0; hg < HG; ++hg) {
+#pragma unroll
+    for (int i = 0; i < 4 * NB; ++i) oacc[hg][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[hg] = -INFINITY;
+    l_part[hg] = 0.f;
+    e_part[hg] = 0.f;
+  }
 
   // Everything issued before the second sub-tile (query, first sub-tile,
   // RoPE row, fused inputs) has landed; the later sub-tiles may still be in
   // flight.
   wait_vm<(G::kFill - 1) * G::kVm>();
 #pragma unroll
-  for (int s = 0; s < 2 * NB; ++s) vm_release(qraw[s]);
+  for (int hg = 0; hg < HG; ++hg) {
+#pragma unroll
+    for (int s = 0; s < 2 * NB; ++s) vm_release(qraw[hg][s]);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) vm_release(praw[hg][s]);
+  }
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    vm_release(praw[s]);
     vm_release(cr[s]);
     vm_release(sr[s]);
   }
@@ -592,21 +617,25 @@ __global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeA
 
   // ---- Q^T registers: latent channels >= R zeroed, q_pe rotated (per-op rounded)
 #pragma unroll
-  for (int s = 0; s < 2 * NB; ++s)
-    qb[s] = as_bf16x8(mask_bf16x8(make_uint4(qraw[s][0], qraw[s][1], qraw[s][2], qraw[s][3]), a.R - (32 * s + 8 * g)));
+  for (int hg = 0; hg < HG; ++hg) {
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    uint32_t wv[4];
+    for (int s = 0; s < 2 * NB; ++s)
+      qb[hg][s] = as_bf16x8(mask_bf16x8(make_uint4(qraw[hg][s][0], qraw[hg][s][1], qraw[hg][s][2], qraw[hg][s][3]),
+                                        a.R - (32 * s + 8 * g)));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t cj = (j & 1) ? (cr[s][j >> 1] >> 16) : (cr[s][j >> 1] & 0xFFFF);
-      const uint32_t sj = (j & 1) ? (sr[s][j >> 1] >> 16) : (sr[s][j >> 1] & 0xFFFF);
-      float o1, o2;
-      rope_pair<1>(bf16_to_f32(praw[s][j] & 0xFFFF), bf16_to_f32(praw[s][j] >> 16), bf16_to_f32(cj), bf16_to_f32(sj),
-                   o1, o2);
-      wv[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+    for (int s = 0; s < 2; ++s) {
+      uint32_t wv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t cj = (j & 1) ? (cr[s][j >> 1] >> 16) : (cr[s][j >> 1] & 0xFFFF);
+        const uint32_t sj = (j & 1) ? (sr[s][j >> 1] >> 16) : (sr[s][j >> 1] & 0xFFFF);
+        float o1, o2;
+        rope_pair<1>(bf16_to_f32(praw[hg][s][j] & 0xFFFF), bf16_to_f32(praw[hg][s][j] >> 16), bf16_to_f32(cj),
+                     bf16_to_f32(sj), o1, o2);
+        wv[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+      }
+      qb[hg][2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
     }
-    qb[2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
   }
 
   // The new token's cache row, computed while the first tiles stream in (its
@@ -624,92 +653,100 @@ __global__ __launch_bounds__(kDecWaves * 64 * HG, 1) void mla_decode_dma(DecodeA
     process(k, false);
   }
   if constexpr (FUSE)
-    if (fa_wave && hg == 0)
+    if (fa_wave)
       fused_store<C_DT, NB>(a.fa, static_cast<int64_t>(fa_a.b) * a.fa.cache_s + fa_a.pos, ftok, lane);
 
   // ---- combine the four waves: per head max, sum and O (fixed order)
-  float l_w = l_part + shfl_xor_f32(l_part, 16);
-  l_w += shfl_xor_f32(l_w, 32);
-  float e_w = e_part + shfl_xor_f32(e_part, 16);
-  e_w += shfl_xor_f32(e_w, 32);
-  // The wave's ring is free once its own loads have landed: it stashes its
-  // O^T rows and per-head max / l / e there, without waiting for the others.
+  // The wave's LDS area is free once its own loads have landed: it stashes
+  // its O^T rows and per-head max / l / e there, without waiting for the others.
   wait_vm<0>();  // (the ring's loads past the wave's own sub-tiles included)
-  // (stash_of(v): wave v of this head group)
-  auto stash_of = [&](int v) { return reinterpret_cast<float*>(lds_raw + (kDecWaves * hg + v) * G::kWave); };
-  float* const mine = stash_of(w);
-  if (g == 0) {
-    mine[kH * G::kCombRow + n] = m_run;
-    mine[kH * G::kCombRow + kH + n] = l_w;
-    mine[kH * G::kCombRow + 2 * kH + n] = e_w;
-  }
-  // lane (n, g) holds O^T[16 mb + 4 g + i][head n]
+  // (stash_of(v, hg): wave v's stash of head group hg)
+  auto stash_of = [&](int v, int hg) {
+    return reinterpret_cast<float*>(lds_raw + v * G::kWave) + hg * G::kStashG;
+  };
 #pragma unroll
-  for (int mb = 0; mb < 4 * NB; ++mb)
-    *reinterpret_cast<float4*>(mine + n * G::kCombRow + 16 * mb + 4 * g) =
-        make_float4(oacc[mb][0], oacc[mb][1], oacc[mb][2], oacc[mb][3]);
+  for (int hg = 0; hg < HG; ++hg) {
+    float l_w = l_part[hg] + shfl_xor_f32(l_part[hg], 16);
+    l_w += shfl_xor_f32(l_w, 32);
+    float e_w = e_part[hg] + shfl_xor_f32(e_part[hg], 16);
+    e_w += shfl_xor_f32(e_w, 32);
+    float* const mine = stash_of(w, hg);
+    if (g == 0) {
+      mine[kH * G::kCombRow + n] = m_run[hg];
+      mine[kH * G::kCombRow + kH + n] = l_w;
+      mine[kH * G::kCombRow + 2 * kH + n] = e_w;
+    }
+    // lane (n, g) holds O^T[16 mb + 4 g + i][head n]
+#pragma unroll
+    for (int mb = 0; mb < 4 * NB; ++mb)
+      *reinterpret_cast<float4*>(mine + n * G::kCombRow + 16 * mb + 4 * g) =
+          make_float4(oacc[hg][mb][0], oacc[hg][mb][1], oacc[hg][mb][2], oacc[hg][mb][3]);
+  }
   __syncthreads();  // every wave's stash is written
 
-  // wave w finishes heads 4w .. 4w + 3 of its group: lane -> head 4w + g,
-  // channels 64 i + 4 n .. +4 for i < NB (the 16 lanes of a head read and
-  // write consecutive 16-byte pieces); hh is the head in the launch
-  const int h = kDecWaves * w + g, hh = kH * hg + h;
-  float mw[kDecWaves], lw[kDecWaves], ew[kDecWaves];
-  float M = -INFINITY;
+  // wave w finishes heads 4w .. 4w + 3 of each head group: lane -> head
+  // 4w + g, channels 64 i + 4 n .. +4 for i < NB (the 16 lanes of a head
+  // read and write consecutive 16-byte pieces); hh is the head in the launch
+  const int h = kDecWaves * w + g, c0 = 4 * n;
+#pragma unroll 1
+  for (int hg = 0; hg < HG; ++hg) {
+    const int hh = kH * hg + h;
+    float mw[kDecWaves], lw[kDecWaves], ew[kDecWaves];
+    float M = -INFINITY;
 #pragma unroll
-  for (int v = 0; v < kDecWaves; ++v) {
-    const float* ml = stash_of(v) + kH * G::kCombRow;
-    mw[v] = ml[h];
-    lw[v] = ml[kH + h];
-    ew[v] = ml[2 * kH + h];
-    M = fmaxf(M, mw[v]);
-  }
-  float sc[kDecWaves], Ltot = 0.f, Etot = 0.f;
-#pragma unroll
-  for (int v = 0; v < kDecWaves; ++v) {
-    sc[v] = mw[v] == -INFINITY ? 0.f : exp2f(mw[v] - M);
-    Ltot += sc[v] * lw[v];
-    Etot += sc[v] * ew[v];
-  }
-  const float inv = Ltot > 0.f ? 1.f / Ltot : 0.f;
-  const int c0 = 4 * n;
-  float o[4 * NB];
-#pragma unroll
-  for (int i = 0; i < 4 * NB; ++i) o[i] = 0.f;
-#pragma unroll
-  for (int v = 0; v < kDecWaves; ++v) {
-    const float* src = stash_of(v) + h * G::kCombRow + c0;
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const float4 t = *reinterpret_cast<const float4*>(src + 64 * i);
-      o[4 * i + 0] += sc[v] * t.x;
-      o[4 * i + 1] += sc[v] * t.y;
-      o[4 * i + 2] += sc[v] * t.z;
-      o[4 * i + 3] += sc[v] * t.w;
+    for (int v = 0; v < kDecWaves; ++v) {
+      const float* ml = stash_of(v, hg) + kH * G::kCombRow;
+      mw[v] = ml[h];
+      lw[v] = ml[kH + h];
+      ew[v] = ml[2 * kH + h];
+      M = fmaxf(M, mw[v]);
     }
-  }
-  const float lse2 = Etot > 0.f ? M + __log2f(Etot) : -INFINITY;  // log2 domain
-  if (ns <= 1) {
-    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + hh * a.o_hs + c0;
+    float sc[kDecWaves], Ltot = 0.f, Etot = 0.f;
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      uint2 pk;
-      pk.x = pack_bf16x2(o[4 * i] * inv, o[4 * i + 1] * inv);
-      pk.y = pack_bf16x2(o[4 * i + 2] * inv, o[4 * i + 3] * inv);
-      *reinterpret_cast<uint2*>(op + 64 * i) = pk;
+    for (int v = 0; v < kDecWaves; ++v) {
+      sc[v] = mw[v] == -INFINITY ? 0.f : exp2f(mw[v] - M);
+      Ltot += sc[v] * lw[v];
+      Etot += sc[v] * ew[v];
     }
-    if (a.lse_out && n == 0) a.lse_out[static_cast<int64_t>(r) * HT + hh] = lse2 * kLn2;
-    return;
-  }
-  // partials: non-temporal stores (every workgroup writes at its end, and the
-  // merge reads them in the next launch, from another XCD's view of memory)
-  const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * HT + hh;
-  float* op = a.o_part + pidx * RP + c0;
+    const float inv = Ltot > 0.f ? 1.f / Ltot : 0.f;
+    float o[4 * NB];
 #pragma unroll
-  for (int i = 0; i < NB; ++i)
-    __builtin_nontemporal_store(f32x4_t{o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv},
-                                reinterpret_cast<f32x4_t*>(op + 64 * i));
-  if (n == 0) __builtin_nontemporal_store(lse2 * kLn2, a.lse_part + pidx);
+    for (int i = 0; i < 4 * NB; ++i) o[i] = 0.f;
+#pragma unroll
+    for (int v = 0; v < kDecWaves; ++v) {
+      const float* src = stash_of(v, hg) + h * G::kCombRow + c0;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const float4 t = *reinterpret_cast<const float4*>(src + 64 * i);
+        o[4 * i + 0] += sc[v] * t.x;
+        o[4 * i + 1] += sc[v] * t.y;
+        o[4 * i + 2] += sc[v] * t.z;
+        o[4 * i + 3] += sc[v] * t.w;
+      }
+    }
+    const float lse2 = Etot > 0.f ? M + __log2f(Etot) : -INFINITY;  // log2 domain
+    if (ns <= 1) {
+      uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + hh * a.o_hs + c0;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        uint2 pk;
+        pk.x = pack_bf16x2(o[4 * i] * inv, o[4 * i + 1] * inv);
+        pk.y = pack_bf16x2(o[4 * i + 2] * inv, o[4 * i + 3] * inv);
+        *reinterpret_cast<uint2*>(op + 64 * i) = pk;
+      }
+      if (a.lse_out && n == 0) a.lse_out[static_cast<int64_t>(r) * HT + hh] = lse2 * kLn2;
+      continue;
+    }
+    // partials: non-temporal stores (every workgroup writes at its end, and the
+    // merge reads them in the next launch, from another XCD's view of memory)
+    const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * HT + hh;
+    float* op = a.o_part + pidx * RP + c0;
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      __builtin_nontemporal_store(f32x4_t{o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv},
+                                  reinterpret_cast<f32x4_t*>(op + 64 * i));
+    if (n == 0) __builtin_nontemporal_store(lse2 * kLn2, a.lse_part + pidx);
+  }
 }
 
 // ===========================================================================
@@ -766,18 +803,18 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_stream_probe(DecodeArgs
 // ===========================================================================
 namespace {
 // The instance for (cache dtype, fused append, head groups): two head groups
-// (32 heads) are built for the bf16 cache at R_pad <= 256, where the rings of
-// eight waves fit the LDS.
+// (32 heads) are built for R_pad <= 256, where both groups' queries and
+// accumulators fit one wave's registers.
 template <int NB>
 const void* decode_kernel(int c_dt, bool fuse, int hg) {
   if (hg == 2) {
     if constexpr (NB <= 4) {
-      if (c_dt != 1) return nullptr;
-      return fuse ? reinterpret_cast<const void*>(&mla_decode_dma<1, true, NB, 2>)
-                  : reinterpret_cast<const void*>(&mla_decode_dma<1, false, NB, 2>);
-    } else {
-      return nullptr;
+      if (c_dt == 1 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<1, false, NB, 2>);
+      if (c_dt == 2 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<2, false, NB, 2>);
+      if (c_dt == 1) return reinterpret_cast<const void*>(&mla_decode_dma<1, true, NB, 2>);
+      if (c_dt == 2) return reinterpret_cast<const void*>(&mla_decode_dma<2, true, NB, 2>);
     }
+    return nullptr;
   }
   if (hg != 1) return nullptr;
   if (c_dt == 1 && !fuse) return reinterpret_cast<const void*>(&mla_decode_dma<1, false, NB, 1>);
@@ -803,7 +840,7 @@ int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
     const void* fn = decode_kernel<NB>(c_dt, fuse, hg);
     if (!fn) return -1;
     void* args[] = {const_cast<DecodeArgs*>(&a)};
-    return hipLaunchKernel(fn, grid, dim3(kDecWaves * 64 * hg), args, 0, s) == hipSuccess ? 0 : -2;
+    return hipLaunchKernel(fn, grid, dim3(kDecWaves * 64), args, 0, s) == hipSuccess ? 0 : -2;
   });
   if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;

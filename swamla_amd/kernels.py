@@ -17,9 +17,8 @@ import torch
 from . import _abi
 
 R, P, H = 256, 64, 16  # R: the default kv_lora_rank (any 1..MAX_RANK is built)
-# Heads one decode launch takes: 16, or 32 for a bf16 model and cache with
-# R_pad <= 256 (two head groups in one workgroup, each cache tile streamed once
-# per workgroup for both).
+# Heads one decode launch takes: 16, or 32 for a bf16 model with R_pad <= 256
+# (each wave serves two head groups from one stream of the cache).
 DECODE_HEADS = (16, 32)
 MAX_RANK = 512
 
@@ -343,8 +342,8 @@ def decode_attention(
 
     q_abs [rows, H, R_pad] (channels >= the cache's rank are ignored) and
     q_pe [rows, H, P] may be strided views (unit last stride); H is 16, or
-    32 for a bf16 model and cache at R_pad <= 256 (one launch of two head
-    groups: the cache is streamed once for both).  Addressing:
+    32 for a bf16 model at R_pad <= 256 (one launch of two head groups:
+    the cache is streamed once for both).  Addressing:
     explicit (row_seq, kv_len, q_rope_pos) or dense (start_pos [rows /
     rows_per_seq], causal).  Returns o_lat [rows, H, R_pad], whose padding
     channels are 0 (``out`` may be a strided view, e.g. a transpose of a

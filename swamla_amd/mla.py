@@ -526,9 +526,9 @@ class MLA(nn.Module):
 
     def _decode_heads(self) -> int:
         """Heads one decode launch takes for this module: all 32 of a bf16
-        module with a bf16 cache at R_pad <= 256 (two head groups streaming
-        the cache once), else 16."""
-        if (self.n_heads == 32 and not self.fp8_cache and self.rank_pad <= 256
+        module at R_pad <= 256 (each wave serves both head groups from one
+        stream of the cache), else 16."""
+        if (self.n_heads == 32 and self.rank_pad <= 256
                 and self.wkv_a.weight.dtype == torch.bfloat16):
             return 32
         return kernels.H
@@ -747,10 +747,16 @@ class MLA(nn.Module):
         else:
             # No cache (mla.py:419-423): attend over this call's tokens only.
             if T > self.rope.cos_cached.shape[2]:
-                # the reference grows its table in fp32 here (positional_encoding.py:44-46, :64-86), which
-                # also turns its rotation into fp32 arithmetic; this path does not reproduce that
-                raise ValueError(f"seqlen {T} exceeds the RoPE table ({self.rope.cos_cached.shape[2]} positions, "
-                                 f"max_seq_len)")
+                # The table grows to T positions in fp32 (positional_encoding.py:44-46, :64-86). For an
+                # fp32 module nothing else changes. For bf16 the reference's rotation then yields fp32
+                # q_pe / k_pe, and its SDPA receives fp32 queries and keys with bf16 values and raises
+                # (mla.py:555-601); this path raises before changing the table.
+                if x.dtype != torch.float32 or self.rope.cos_cached.dtype != torch.float32:
+                    raise ValueError(
+                        f"seqlen {T} exceeds the RoPE table ({self.rope.cos_cached.shape[2]} positions): the "
+                        f"table grows in fp32, which only an fp32 module can use (the reference's attention "
+                        f"rejects the mixed dtypes that growth makes in a {x.dtype} module)")
+                self.rope.extend(T)
             cache = LatentCache.allocate(B, T, x.dtype, dev, fp8=self.fp8_cache, rank=R)
             sp = torch.zeros(B, dtype=torch.int32, device=dev)
             max_len = T

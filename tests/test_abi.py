@@ -358,6 +358,26 @@ def test_rope_table_bitwise_equal_to_reference():
     assert cos.shape == (300, 32) and torch.equal(cos, ref.rope.cos_cached[0, 0, :, :32])
 
 
+def test_rope_extend_matches_reference_growth():
+    """MLA.rope.extend grows the table like positional_encoding.py:64-86: the
+    same fp32 table as the restatement's growth, bit for bit, in fp32 even in a
+    bf16 module, with max_seq_len moved to the new length."""
+    ref = RefMLA(small_cfg(max_seq_len=16)).to(torch.bfloat16)
+    ours = MLA(small_cfg(max_seq_len=16)).to(torch.bfloat16)
+    ours.rope.half_tables()
+    ref.rope(torch.zeros(1, 1, 50, 64, dtype=torch.bfloat16))
+    ours.rope.extend(50)
+    assert ours.rope.max_seq_len == ref.rope.max_seq_len == 50
+    assert ours.rope.cos_cached.dtype == torch.float32
+    assert torch.equal(ours.rope.cos_cached, ref.rope.cos_cached)
+    assert torch.equal(ours.rope.sin_cached, ref.rope.sin_cached)
+    cos, _ = ours.rope.half_tables()
+    assert cos.shape == (50, 32) and cos.dtype == torch.float32
+    assert len(ours.rope._retired) == 1  # the old half tables stay alive
+    ours.rope.extend(20)  # never shrinks
+    assert ours.rope.max_seq_len == 50
+
+
 def test_inference_mode_allocation_and_clear():
     m = MLA(small_cfg()).to(torch.bfloat16)
     m.set_inference_mode(True)  # works directly (the reference's raises KeyError)
@@ -484,12 +504,11 @@ def test_probes_reject(lib):
 
 
 def test_32_heads_only_where_built(lib):
-    """32 heads in one launch: bf16 model and cache with R_pad <= 256; any
-    other combination, and other head counts, are rejected before any HIP
-    call."""
+    """32 heads in one launch: bf16 model (bf16 or e4m3 cache) with R_pad <=
+    256; any other combination, and other head counts, are rejected before
+    any HIP call."""
     E_UNS = -2
     assert _decode(lib, H=32, dt=0, c_dt=0) == E_UNS              # fp32 model
-    assert _decode(lib, H=32, c_dt=2, scale=FAKE) == E_UNS        # e4m3 cache
     assert _decode(lib, H=32, R=300, qa_rs=32 * 320, qa_hs=320, o_rs=32 * 320, o_hs=320) == E_UNS
     assert _decode(lib, H=48) == E_UNS and _decode(lib, H=8) == E_UNS
     assert "32" in lib.mla_last_error().decode()

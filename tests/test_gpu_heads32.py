@@ -1,14 +1,14 @@
-"""GPU parity of the 32-head decode launch (two head groups of 16 in one
-workgroup, each streaming the same cache tiles; the xl preset's n_head = 32
-and the cudnn-compatible 32-head layout, models/swa_mla_model.py:618-640,
-:696-699; attention as models/mla.py:417-487).
+"""GPU parity of the 32-head decode launch (each wave serves two head groups
+of 16 from one stream of the cache; the xl preset's n_head = 32 and the
+cudnn-compatible 32-head layout, models/swa_mla_model.py:618-640, :696-699;
+attention as models/mla.py:417-487), bf16 and e4m3 caches.
 
-Bar: identical bits to two 16-head launches on the same inputs.  Each head
-group deals the split's sub-tiles to its waves exactly as a 16-head launch
-does and combines its waves in the same fixed order, so outputs, split
-partials, log-sum-exps and (with the fused append) cache rows must match bit
-for bit; plus the fp64 oracle at the north-star tolerance and the LSE to
-1e-4."""
+Bar: identical bits to two 16-head launches on the same inputs.  The split's
+sub-tiles are dealt to the waves exactly as in a 16-head launch, each head
+group runs its own online softmax on the same operands and the waves are
+combined in the same fixed order, so outputs, split partials, log-sum-exps
+and (with the fused append) cache rows must match bit for bit; plus the fp64
+oracle at the north-star tolerance and the LSE to 1e-4."""
 import pytest
 import torch
 
@@ -34,13 +34,18 @@ def tables(S, device):
             sin.to(torch.bfloat16)[0, 0, :, :32].contiguous().to(device))
 
 
-def make(gpu, B, S, seed, rank=R):
+def make(gpu, B, S, seed, rank=R, fp8=False):
     g = torch.Generator(device=gpu).manual_seed(seed)
     rp = kernels.padded_rank(rank)
-    cache = LatentCache.allocate(B, S, torch.bfloat16, gpu, rank=rank)
+    cache = LatentCache.allocate(B, S, torch.bfloat16, gpu, rank=rank, fp8=fp8)
     ckv = torch.randn(B, S, rp, generator=g, device=gpu)
     ckv[..., rank:] = 0
-    cache.ckv.copy_(ckv.to(torch.bfloat16))
+    if fp8:
+        codes, scale = lo.fp8_quantize(ckv.to(torch.bfloat16).view(B * S, rp).cpu())
+        cache.ckv.copy_(codes.view(B, S, rp))
+        cache.scale.copy_(scale.view(B, S))
+    else:
+        cache.ckv.copy_(ckv.to(torch.bfloat16))
     cache.kpe.copy_(torch.randn(B, S, P, generator=g, device=gpu).to(torch.bfloat16))
     q_abs = (0.4 * torch.randn(B, 32, rp, generator=g, device=gpu)).to(torch.bfloat16)
     q_pe = (0.4 * torch.randn(B, 32, P, generator=g, device=gpu)).to(torch.bfloat16)
@@ -48,7 +53,7 @@ def make(gpu, B, S, seed, rank=R):
 
 
 def clone(c):
-    return LatentCache(c.ckv.clone(), c.kpe.clone())
+    return LatentCache(c.ckv.clone(), c.kpe.clone(), None if c.scale is None else c.scale.clone(), c.rank)
 
 
 STARTS = [0, 15, 16, 300, 1023, 2047, 3000, 4094]
@@ -57,10 +62,11 @@ STARTS = [0, 15, 16, 300, 1023, 2047, 3000, 4094]
 @pytest.mark.parametrize("n_splits,min_chunk", [(1, 256), (8, 256), (40, 64)])
 @pytest.mark.parametrize("fused", [False, True], ids=["plain", "fused"])
 @pytest.mark.parametrize("merge", [True, False], ids=["merge", "partials"])
-def test_32_heads_equal_two_16_head_launches(gpu, n_splits, min_chunk, fused, merge):
-    say(f"32 heads: n_splits={n_splits} min_chunk={min_chunk} fused={fused} merge={merge}")
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "e4m3"])
+def test_32_heads_equal_two_16_head_launches(gpu, n_splits, min_chunk, fused, merge, fp8):
+    say(f"32 heads: n_splits={n_splits} min_chunk={min_chunk} fused={fused} merge={merge} fp8={fp8}")
     B, S = len(STARTS), 4096
-    cache0, q_abs, q_pe = make(gpu, B, S, 7 + n_splits)
+    cache0, q_abs, q_pe = make(gpu, B, S, 7 + n_splits, fp8=fp8)
     cos, sin = tables(S, gpu)
     sp = torch.tensor(STARTS, dtype=torch.int32, device=gpu)
     g = torch.Generator(device=gpu).manual_seed(3)
@@ -94,6 +100,8 @@ def test_32_heads_equal_two_16_head_launches(gpu, n_splits, min_chunk, fused, me
     c32, o32, l32, p32 = run(32)
     c16, o16, l16, p16 = run(16)
     assert torch.equal(c32.ckv, c16.ckv) and torch.equal(c32.kpe, c16.kpe)
+    if fp8:
+        assert torch.equal(c32.scale, c16.scale)
     assert torch.equal(torch.isnan(o32), torch.isnan(o16))
     assert torch.equal(torch.nan_to_num(o32).view(torch.int16), torch.nan_to_num(o16).view(torch.int16))
     if merge:
@@ -106,10 +114,11 @@ def test_32_heads_equal_two_16_head_launches(gpu, n_splits, min_chunk, fused, me
         assert torch.equal(torch.nan_to_num(b32), torch.nan_to_num(b16))
 
 
-def test_32_heads_against_fp64_oracle(gpu):
-    say("32 heads vs fp64 oracle")
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "e4m3"])
+def test_32_heads_against_fp64_oracle(gpu, fp8):
+    say(f"32 heads vs fp64 oracle, fp8={fp8}")
     B, S, rank = 3, 1500, 200
-    cache, q_abs, q_pe = make(gpu, B, S, 11, rank=rank)
+    cache, q_abs, q_pe = make(gpu, B, S, 11, rank=rank, fp8=fp8)
     cos, sin = tables(S, gpu)
     lens = [1500, 977, 64]
     sp = torch.tensor([L - 1 for L in lens], dtype=torch.int32, device=gpu)
@@ -119,7 +128,8 @@ def test_32_heads_against_fp64_oracle(gpu):
     torch.cuda.synchronize()
     # chunk-local RoPE: a one-token row is rotated at position 0 (identity)
     o64, l64 = lo.absorbed_attention_f64(q_abs.cpu()[..., :rank], q_pe.cpu(), cache.ckv.cpu()[..., :rank],
-                                         cache.kpe.cpu(), lens, [0, 1, 2], SCALE)
+                                         cache.kpe.cpu(), lens, [0, 1, 2], SCALE,
+                                         ckv_scale=cache.scale.cpu() if fp8 else None)
     check(out.cpu()[..., :rank], o64)
     assert bool((out[..., rank:] == 0).all())
     check_lse(lse, l64)

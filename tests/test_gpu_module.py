@@ -244,6 +244,29 @@ def test_no_cache_forward_matches_reference(gpu):
         close(ours(x.to(gpu), 0), ref(x, 0), dtype)
 
 
+def test_no_cache_forward_grows_rope_table_fp32(gpu):
+    """An fp32 no-cache call longer than max_seq_len grows the RoPE table to
+    the call's length on the module's device (positional_encoding.py:44-46,
+    :64-86) and matches the restatement, which grows its table on the CPU."""
+    say("no-cache forward, RoPE growth")
+    cfg = MLAConfig(n_embd=256, max_batch_size=2, max_seq_len=32)
+    ref = RefMLA(cfg)
+    init_weights(ref, 29)
+    ref.eval()
+    ours = MLA(cfg)
+    ours.load_state_dict(ref.state_dict())
+    ours.eval().to(gpu)
+    g = torch.Generator().manual_seed(30)
+    x = torch.randn(2, 75, 256, generator=g)
+    with torch.no_grad():
+        close(ours(x.to(gpu), 0), ref(x, 0), torch.float32)
+    assert ours.rope.max_seq_len == ref.rope.max_seq_len == 75
+    assert ours.rope.cos_cached.device.type == "cuda"
+    x2 = torch.randn(2, 40, 256, generator=g)  # within the grown table
+    with torch.no_grad():
+        close(ours(x2.to(gpu), 0), ref(x2, 0), torch.float32)
+
+
 @pytest.mark.parametrize("rank,q_lora,dim", [
     (128, 0, 256), (173, 0, 256), (320, 0, 256), (449, 0, 256), (512, 0, 256),
     (256, 96, 256), (200, 160, 1024), (300, 0, 1024),
@@ -339,7 +362,8 @@ def test_out_of_range_positions_raise(gpu):
     does: at once when they are known on the host (int or CPU tensor); for a
     device tensor the kernels skip the token and flag it, check_cache_errors()
     raises, and so does the next eager call once the flag has been read back.
-    A no-cache call longer than the RoPE table raises."""
+    A no-cache call of a bf16 module longer than the RoPE table raises (the
+    reference's grown fp32 table makes its attention see mixed dtypes)."""
     say("out-of-range positions")
     dtype = torch.bfloat16
     cfg = MLAConfig(n_embd=256, max_batch_size=2, max_seq_len=64)

@@ -189,6 +189,48 @@ def test_rope_preserves_pair_norms_fp64():
     assert torch.allclose(nx, ny, rtol=5e-7, atol=0)
 
 
+def test_rope_growth_equals_a_longer_table():
+    """Growth (positional_encoding.py:44-46, :64-86) on the CPU rebuilds the
+    table with the same ops, so a grown table equals one built at the longer
+    length bit for bit, its entries are cos / sin of t * base^(-2i/dim)
+    (fp64 closed form, to fp32 accuracy), and it stays fp32 whatever the
+    module dtype was."""
+    rope = RefRoPE(64, 16).to(torch.bfloat16)
+    x = torch.randn(1, 2, 40, 64).to(torch.bfloat16)
+    y = rope(x)
+    assert rope.max_seq_len == 40 and rope.cos_cached.dtype == torch.float32
+    fresh = RefRoPE(64, 40)
+    assert torch.equal(rope.cos_cached, fresh.cos_cached) and torch.equal(rope.sin_cached, fresh.sin_cached)
+    t = torch.arange(40, dtype=torch.float64)[:, None]
+    ang = t * 10000.0 ** (-torch.arange(0, 64, 2, dtype=torch.float64) / 64)
+    assert torch.allclose(rope.cos_cached[0, 0, :, :32].double(), ang.cos(), atol=4e-6, rtol=0)
+    assert torch.allclose(rope.sin_cached[0, 0, :, :32].double(), ang.sin(), atol=4e-6, rtol=0)
+    # the rotation after growth is bf16 x fp32, so its result is fp32
+    assert y.dtype == torch.float32
+
+
+def test_ref_module_growth_fp32_and_bf16():
+    """No-cache calls longer than max_seq_len: an fp32 module's output equals
+    that of a module built with a longer table (growth changes nothing else);
+    a bf16 module's grown fp32 rotation meets bf16 values in SDPA, which
+    raises (mla.py:555-601)."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(1, 40, 128, generator=g)
+    outs = []
+    for L in (16, 64):
+        m = RefMLA(MLAConfig(n_embd=128, max_batch_size=1, max_seq_len=L))
+        init_weights(m, 22)
+        m.eval()
+        with torch.no_grad():
+            outs.append(m(x, 0))
+    assert torch.equal(outs[0], outs[1])
+    m = RefMLA(MLAConfig(n_embd=128, max_batch_size=1, max_seq_len=16))
+    init_weights(m, 22)
+    m.eval().to(torch.bfloat16)
+    with torch.no_grad(), pytest.raises(RuntimeError):
+        m(x.to(torch.bfloat16), 0)
+
+
 # ---------------------------------------------------------------- attention
 def _unabsorbed_f64(q_nope, q_pe, c, kpe, w_uk, w_uv, scale):
     """mla.py:427-437 + SDPA in fp64 for one row: q [H, .], c [L, R]."""
