@@ -115,9 +115,12 @@ __global__ __launch_bounds__(256) void mla_append_kernel(AppendArgs a) {
 // lane of the group, so every lane runs one and the statistics are the same
 // arithmetic, bit for bit, as the one-token-per-wavefront kernel's.
 // ---------------------------------------------------------------------------
-template <int C_DT>
+// RC > 0: the kernel for kv_lora_rank RC exactly (the statistics' counts,
+// divisions and padding masks fold at compile time); RC = 0: any R.
+template <int C_DT, int RC>
 __global__ __launch_bounds__(256) void mla_append_g16_kernel(AppendArgs a) {
   constexpr int RP = 256, K = 16;  // channels per lane
+  const int R = RC > 0 ? RC : a.R;
   constexpr int kStage = ln_stage_g16_bytes();
   __shared__ __attribute__((aligned(16))) uint8_t stage[16 * kStage];
   const int lane = threadIdx.x & 63, l16 = lane & 15;
@@ -136,7 +139,7 @@ __global__ __launch_bounds__(256) void mla_append_g16_kernel(AppendArgs a) {
   load_lane<K / 2>(reinterpret_cast<const uint32_t*>(row) + (K / 2) * l16, xw);
   load_lane<2>(reinterpret_cast<const uint32_t*>(row + RP) + 2 * l16, pe);
   const LnStats st = aten_ln_stats<1, 16>(
-      ln_gather<1, K, 16>(xw, a.R, l16, (lds_u8*)(stage) + slot * kStage), a.R, a.eps, lane);
+      ln_gather<1, K, 16>(xw, R, l16, (lds_u8*)(stage) + slot * kStage), R, a.eps, lane);
   // The LayerNorm parameters are loaded after the statistics (the compiler
   // would hoist them): fewer registers live across the statistics, 71
   // against 87 VGPRs, measured 43.8 against 47.8 us at 131,072 tokens.
@@ -147,12 +150,15 @@ __global__ __launch_bounds__(256) void mla_append_g16_kernel(AppendArgs a) {
   auto yv = [&](int i) {
     const int h = (i & 1) * 16;
     const float x = u2f((xw[i >> 1] >> h) << 16), w = u2f((ww[i >> 1] >> h) << 16), bb = u2f((bw[i >> 1] >> h) << 16);
-    return K * l16 + i < a.R ? aten_ln_affine<1>(x, w, bb, st) : 0.f;
+    return (RC >= RP || K * l16 + i < R) ? aten_ln_affine<1>(x, w, bb, st) : 0.f;
   };
-  // bf16 of each channel (the value a bf16 cache holds; e4m3 encodes it)
+  // bf16 of each channel (the value a bf16 cache holds; e4m3 encodes it):
+  // the hardware's round-to-nearest-even conversion, two channels per
+  // instruction (finite values and infinities as f32_to_bf16; a NaN stays a
+  // NaN, its payload bits are not kept equal to any other path's)
   uint32_t yw[K / 2];
 #pragma unroll
-  for (int i = 0; i < K / 2; ++i) yw[i] = f32_to_bf16(yv(2 * i)) | (static_cast<uint32_t>(f32_to_bf16(yv(2 * i + 1))) << 16);
+  for (int i = 0; i < K / 2; ++i) yw[i] = pack_bf16x2(yv(2 * i), yv(2 * i + 1));
 
   const int64_t crow = static_cast<int64_t>(b) * a.cache_s + pos;
   if constexpr (C_DT == 1) {
@@ -191,7 +197,7 @@ __global__ __launch_bounds__(256) void mla_append_g16_kernel(AppendArgs a) {
     float o1, o2;
     rope_pair<1>(bf16_to_f32(pe[j] & 0xFFFF), bf16_to_f32(pe[j] >> 16), bf16_to_f32(j ? cw >> 16 : cw & 0xFFFF),
                  bf16_to_f32(j ? sw >> 16 : sw & 0xFFFF), o1, o2);
-    ow[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+    ow[j] = pack_bf16x2(o1, o2);
   }
   store_lane<2>(reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.kpe) + crow * kP) + 2 * l16, ow);
 }
@@ -450,8 +456,13 @@ int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s) {
       a16(a.ln_w) && a16(a.ln_b) && (reinterpret_cast<uintptr_t>(a.cos_tab) & 3) == 0 &&
       (reinterpret_cast<uintptr_t>(a.sin_tab) & 3) == 0) {
     const dim3 g16((a.n_tok + 15) / 16);
-    if (c_dt == 1) hipLaunchKernelGGL(mla_append_g16_kernel<1>, g16, block, 0, s, a);
-    else hipLaunchKernelGGL(mla_append_g16_kernel<2>, g16, block, 0, s, a);
+    if (a.R == 256) {
+      if (c_dt == 1) hipLaunchKernelGGL((mla_append_g16_kernel<1, 256>), g16, block, 0, s, a);
+      else hipLaunchKernelGGL((mla_append_g16_kernel<2, 256>), g16, block, 0, s, a);
+    } else {
+      if (c_dt == 1) hipLaunchKernelGGL((mla_append_g16_kernel<1, 0>), g16, block, 0, s, a);
+      else hipLaunchKernelGGL((mla_append_g16_kernel<2, 0>), g16, block, 0, s, a);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -2;
   }
   const int rc = with_nb(a.R, [&](auto nb) {

@@ -40,8 +40,8 @@ def close(out, ref, rtol, atol):
 
 
 # ------------------------------------------------------------------ append
-def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0, rank=R):
-    say(f"append case dtype={dtype} fp8={fp8} n_tok={n_tok} rank={rank}")
+def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0, rank=R, special=False):
+    say(f"append case dtype={dtype} fp8={fp8} n_tok={n_tok} rank={rank} special={special}")
     rp = kernels.padded_rank(rank)
     g = torch.Generator().manual_seed(seed)
     # rows [R_pad latent | P rope] with 16 spare columns; the latent padding
@@ -50,6 +50,18 @@ def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0, rank=R):
     kv = kv.to(dtype)
     w = (1 + 0.1 * torch.randn(rank, generator=g)).to(dtype)
     b = (0.1 * torch.randn(rank, generator=g)).to(dtype)
+    nan_rows = []
+    if special:
+        # non-finite rows (NaN outputs; the payload bits of a NaN are not
+        # compared), a NaN in a rope pair, and channels with w = 0 whose
+        # outputs are b: subnormal bf16 values, which must survive the
+        # rounding unchanged
+        kv[0, 3] = float("nan")
+        kv[1, 10] = float("inf")
+        kv[2, rp + 5] = float("nan")
+        w[20:24] = 0
+        b[20:24] = torch.tensor([2.0 ** -130, -2.0 ** -128, 2.0 ** -133, 3 * 2.0 ** -133]).to(dtype)
+        nan_rows = [0, 1]
     seq = torch.randint(0, B, (n_tok,), generator=g, dtype=torch.int32)
     # distinct destination per token: a random permutation of the (b, pos) grid
     flat = torch.randperm(B * S, generator=g)[:n_tok]
@@ -75,7 +87,9 @@ def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0, rank=R):
     # padding
     y = lo.layernorm_aten(kv[:, :rank], w, b, 1e-5)[0]
     ref_ln = torch.nn.functional.layer_norm(kv[:, :rank], (rank,), w, b, 1e-5)
-    assert torch.equal(y.view(torch.uint8), ref_ln.view(torch.uint8)), "oracle LayerNorm differs from torch's"
+    fin = [i for i in range(n_tok) if i not in nan_rows]
+    assert torch.equal(y[fin].view(torch.uint8), ref_ln[fin].view(torch.uint8)), "oracle LayerNorm differs from torch's"
+    assert bool(torch.isnan(y[nan_rows]).all()) and bool(torch.isnan(ref_ln[nan_rows]).all())
     y = torch.cat([y, torch.zeros(n_tok, rp - rank, dtype=y.dtype)], 1)
     cos_c, sin_c = cos.cpu(), sin.cpu()
     kpe = lo.rope_interleaved(kv[:, rp:rp + P], cos_c[rpos.long()], sin_c[rpos.long()])
@@ -91,6 +105,12 @@ def _append_case(gpu, dtype, fp8, n_tok=37, B=4, S=64, seed=0, rank=R):
         exp_c[seq.long(), dst.long()] = y
     exp_p[seq.long(), dst.long()] = kpe
     got_c, got_p = cache.ckv.cpu(), cache.kpe.cpu()
+    if special:
+        # NaN cells: NaN on both sides, then compared as one canonical pattern
+        for t in (got_c, exp_c, got_p, exp_p):
+            t[torch.isnan(t)] = float("nan")
+        assert bool((cache.ckv[seq[:2].long(), dst[:2].long(), :rank].isnan()).all().item())
+        assert bool(got_c[seq[2].long(), dst[2].long(), 20:24].view(torch.int16).eq(b[20:24].view(torch.int16)).all())
     if dtype == torch.float32 or fp8:
         assert torch.equal(got_c, exp_c), "latent rows differ"
     else:
@@ -110,6 +130,15 @@ def test_append_bit_exact_any_rank(gpu, dtype, fp8, rank):
     """kv_lora_rank other than 256 (the real model scales it per layer): rows
     padded to a multiple of 64 channels, the padding written as zeros."""
     _append_case(gpu, dtype, fp8, rank=rank, seed=rank)
+
+
+@pytest.mark.parametrize("n_tok", [37, 200])
+def test_append_special_values(gpu, n_tok):
+    """Non-finite rows give NaN rows, as torch's LayerNorm does; subnormal bf16
+    outputs (w = 0, b subnormal) are kept bit for bit.  200 tokens take the
+    grouped prompt-size kernel, 37 as well (any count uses it for aligned
+    rank-256 bf16 rows)."""
+    _append_case(gpu, torch.bfloat16, False, n_tok=n_tok, B=4, S=64, seed=9, special=True)
 
 
 def test_append_many_tokens_bit_exact(gpu):
