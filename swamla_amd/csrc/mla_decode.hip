@@ -629,10 +629,8 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
       for (int j = 0; j < 4; ++j) {
         const uint32_t cj = (j & 1) ? (cr[s][j >> 1] >> 16) : (cr[s][j >> 1] & 0xFFFF);
         const uint32_t sj = (j & 1) ? (sr[s][j >> 1] >> 16) : (sr[s][j >> 1] & 0xFFFF);
-        float o1, o2;
-        rope_pair<1>(bf16_to_f32(praw[hg][s][j] & 0xFFFF), bf16_to_f32(praw[hg][s][j] >> 16), bf16_to_f32(cj),
-                     bf16_to_f32(sj), o1, o2);
-        wv[j] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+        wv[j] = rope_bf16_packed(bf16_to_f32(praw[hg][s][j] & 0xFFFF), bf16_to_f32(praw[hg][s][j] >> 16),
+                                 bf16_to_f32(cj), bf16_to_f32(sj));
       }
       qb[hg][2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
     }

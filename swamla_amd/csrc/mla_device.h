@@ -512,6 +512,16 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
+// rope_pair<1> (every product and sum rounded to bf16) with the roundings
+// done by the hardware conversion, two values per instruction; returns the
+// rotated pair packed as bf16 (o1 in the low half).  Finite values and
+// infinities round exactly as f32_to_bf16 does (a NaN stays a NaN).
+__device__ __forceinline__ uint32_t rope_bf16_packed(float x1, float x2, float c, float s) {
+#pragma clang fp contract(off)
+  const uint32_t p = pack_bf16x2(x1 * c, x2 * s);
+  const uint32_t q = pack_bf16x2(x2 * c, x1 * s);
+  return pack_bf16x2(u2f(p << 16) - u2f(p & 0xFFFF0000u), u2f(q << 16) + u2f(q & 0xFFFF0000u));
+}
 
 // Max over lanes l, l^16, l^32, l^48 (the four lane groups sharing a head)
 // with the gfx950 row-swap permutes: after permlane16_swap(v, v) the pair of

@@ -112,9 +112,7 @@ __device__ __forceinline__ FusedTok<C_DT, NB> fused_compute(const FusedIn<NB>& f
 #pragma unroll
     for (int i = 0; i < NB; ++i) t.row[i] = e4m3_to_bf16_bits(t.codes[i]);
   }
-  float o1, o2;
-  rope_pair<1>(u2f(f.pe << 16), u2f(f.pe & 0xFFFF0000u), u2f(f.c << 16), u2f(f.s << 16), o1, o2);
-  t.pe = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+  t.pe = rope_bf16_packed(u2f(f.pe << 16), u2f(f.pe & 0xFFFF0000u), u2f(f.c << 16), u2f(f.s << 16));
   return t;
 }
 

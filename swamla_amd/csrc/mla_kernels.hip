@@ -194,10 +194,8 @@ __global__ __launch_bounds__(256) void mla_append_g16_kernel(AppendArgs a) {
   uint32_t ow[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    float o1, o2;
-    rope_pair<1>(bf16_to_f32(pe[j] & 0xFFFF), bf16_to_f32(pe[j] >> 16), bf16_to_f32(j ? cw >> 16 : cw & 0xFFFF),
-                 bf16_to_f32(j ? sw >> 16 : sw & 0xFFFF), o1, o2);
-    ow[j] = pack_bf16x2(o1, o2);
+    ow[j] = rope_bf16_packed(bf16_to_f32(pe[j] & 0xFFFF), bf16_to_f32(pe[j] >> 16),
+                             bf16_to_f32(j ? cw >> 16 : cw & 0xFFFF), bf16_to_f32(j ? sw >> 16 : sw & 0xFFFF));
   }
   store_lane<2>(reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.kpe) + crow * kP) + 2 * l16, ow);
 }

@@ -149,10 +149,8 @@ __global__ __launch_bounds__(NW * 64, kPrefillOcc) void mla_prefill_mfma(DecodeA
       for (int jj = 0; jj < 4; ++jj) {
         const uint32_t cj = (jj & 1) ? (cw2[jj >> 1] >> 16) : (cw2[jj >> 1] & 0xFFFF);
         const uint32_t sj = (jj & 1) ? (sw2[jj >> 1] >> 16) : (sw2[jj >> 1] & 0xFFFF);
-        float o1, o2;
-        rope_pair<1>(bf16_to_f32(wv_in[jj] & 0xFFFF), bf16_to_f32(wv_in[jj] >> 16), bf16_to_f32(cj),
-                     bf16_to_f32(sj), o1, o2);
-        wv[jj] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+        wv[jj] = rope_bf16_packed(bf16_to_f32(wv_in[jj] & 0xFFFF), bf16_to_f32(wv_in[jj] >> 16), bf16_to_f32(cj),
+                                  bf16_to_f32(sj));
       }
       qb[qi][2 * NB + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
     }
@@ -432,6 +430,20 @@ __device__ __forceinline__ void p2_wait_lgkm() {
 }
 template <typename T>
 __device__ __forceinline__ void p2_tie(T& v) { asm volatile("" : "+v"(v)); }
+// s_waitcnt vmcnt(N) alone (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void p2_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// 8-byte store as inline assembly (one vector-memory instruction whatever
+// the compiler would make of it: the prologue's vmcnt waits count them)
+template <int OFF>
+__device__ __forceinline__ void p2_store8(void* p, uint32_t lo, uint32_t hi) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  const u32x2_t v = {lo, hi};
+  asm volatile("global_store_dwordx2 %0, %1, off offset:%2" ::"v"(p), "v"(v), "i"(OFF) : "memory");
+}
 // 16 bytes per lane from global memory into LDS at dst + 16 lane (cacheable:
 // the workgroups of one sequence read the same rows)
 __device__ __forceinline__ void p2_dma16(const void* src, lds_u8* dst) {
@@ -472,25 +484,59 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
   __shared__ __attribute__((aligned(16))) uint8_t lds0[kBuf];
   __shared__ __attribute__((aligned(16))) uint8_t lds1[kBuf];
   __shared__ __attribute__((aligned(16))) uint8_t lds2[kBuf];
+  // the query rows' staging area of waves 2 and 3 (waves 0 and 1 stage theirs
+  // in lds2, whose first tile arrives after the loop's first barrier)
+  __shared__ __attribute__((aligned(16))) uint8_t lds3[kBuf];
   auto buf = [&](auto bi) __attribute__((always_inline)) -> lds_u8* {
     if constexpr (decltype(bi)::value == 0) return (lds_u8*)lds0;
     else if constexpr (decltype(bi)::value == 1) return (lds_u8*)lds1;
     else return (lds_u8*)lds2;
   };
 
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int T = a.ad.T;
+  // Persistent workgroups: item k is query group G - 1 - k / B of row k % B
+  // (the later query groups, which attend to more of the cache, come
+  // first), and workgroup x takes items r X + x in even rounds r and
+  // r X + X - 1 - x in odd ones (X workgroups), so each pair of rounds deals
+  // every workgroup about the same number of tiles.
+  const int n_groups = (T + QG - 1) / QG;
+  const int B = a.n_rows / T;
+  const int n_items = n_groups * B;
+  // An item's output stores are issued at the next item's start, after its
+  // loads (the vmcnt waits for those loads then do not wait for the stores).
+  constexpr int kStores = CB * 4;  // 8-byte stores per lane and item
+  bool pending = false;            // uniform
+  uint32_t pend[CB][4][2];
+  uint16_t* pend_op = nullptr;
+  auto flush = [&]() __attribute__((always_inline)) {
+    p2_for<0, CB>([&](auto cbI) {
+      constexpr int cb = decltype(cbI)::value;
+      p2_for<0, 4>([&](auto r4I) {
+        constexpr int r4 = decltype(r4I)::value;
+        p2_store8<2 * (32 * cb + 8 * r4)>(pend_op, pend[cb][r4][0], pend[cb][r4][1]);
+      });
+    });
+  };
+  for (int round = 0;; ++round) {
+  const int item = round * static_cast<int>(gridDim.x) +
+                   ((round & 1) ? static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)
+                                : static_cast<int>(blockIdx.x));
+  if (item >= n_items) break;  // uniform
+  // The lane's indices are re-derived per item from an opaque copy of the
+  // thread id: nothing computed from them is hoisted out of the item loop
+  // and kept live across it (the body uses every register).
+  int tid = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(tid));
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int n = lane & 31, hf = lane >> 5;  // column, lane half
   const int head = n & 15;
-  const int T = a.ad.T;
-  const int b = blockIdx.y;
-  // Later query groups attend to more of the cache: the grid runs them first.
-  const int t_first = QG * (gridDim.x - 1 - blockIdx.x);
+  const int b = item % B;
+  const int t_first = QG * (n_groups - 1 - item / B);
   const int t_last_q = min(t_first + QG - 1, T - 1);
   const int sp = a.ad.start_pos[b];
   const bool b_ok = b < a.cache_b;
   const int tt = t_first + kP2Qpw * w + (n >> 4);  // this column's query (surplus ones repeat the last)
-  const bool valid = tt < T;
   const int tq = min(tt, t_last_q);
   const int64_t rq = static_cast<int64_t>(b) * T + tq;
   int Lq = b_ok ? sp + tq + 1 : 0;
@@ -534,41 +580,104 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
     }
   };
 
-  // ---- Q^T operands: column n, channels 16 ks + 8 hf .. + 7 (k-steps KS.. are the rope part)
-  bf16x8_t qb[KS + 4];
+  // ---- Q^T operands: column n (query n >> 4 of the wave, head n & 15),
+  // channels 16 ks + 8 hf .. + 7 (k-steps KS.. are the rope part).  The
+  // wave's 32 query rows are copied into its staging area by LDS DMA in whole
+  // lines (1 KB per instruction): column n's latent chunk c at slot (c & 16) |
+  // ((c ^ n) & 15), its rope chunk c at (c ^ (n >> 1)) & 7, so that the
+  // operand reads (chunk 2 ks + hf of 16 columns per read cycle) hit distinct
+  // banks.  Loaded per lane instead, 16 bytes of 32 rows per instruction, the
+  // rows took several microseconds per item.
+  constexpr int kQLat = 32 * kRow;                // latent bytes of the wave's 32 columns
+  constexpr int kQBytes = kQLat + 32 * kPeR;
+  constexpr int kQDma = kQBytes / 1024;           // DMA instructions for the wave's rows
+  static_assert(kQLat % 1024 == 0 && 2 * kQBytes <= kBuf, "two waves' rows fit a staging buffer");
+  lds_u8* const qs = ((w >> 1) == 0 ? (lds_u8*)lds2 : (lds_u8*)lds3) + (w & 1) * kQBytes;
+  const int tq_w = min(t_first + kP2Qpw * w, t_last_q);  // the wave's first query (surplus ones repeat the last)
+  const int64_t rq_w = static_cast<int64_t>(b) * T + tq_w;
+  const int rq_step = min(t_first + kP2Qpw * w + 1, t_last_q) - tq_w;  // 0 or 1
+  p2_for<0, kQDma>([&](auto iI) {
+    constexpr int i = decltype(iI)::value;
+    const int o = 1024 * i + 16 * lane;
+    if constexpr (1024 * i < kQLat) {
+      const int col = o / kRow, sl = (o % kRow) / 16, ch = (sl & 16) | ((sl ^ col) & 15);
+      const uint16_t* src = static_cast<const uint16_t*>(a.q_abs) + (rq_w + (col >> 4) * rq_step) * a.qa_rs +
+                            (col & 15) * a.qa_hs + 8 * ch;
+      p2_dma16(src, qs + 1024 * i);
+    } else {
+      const int o2 = o - kQLat, col = o2 / kPeR, ch = ((o2 % kPeR) / 16 ^ (col >> 1)) & 7;
+      const uint16_t* src = static_cast<const uint16_t*>(a.q_pe) + (rq_w + (col >> 4) * rq_step) * a.qp_rs +
+                            (col & 15) * a.qp_hs + 8 * ch;
+      p2_dma16(src, qs + 1024 * i);
+    }
+  });
+  // the RoPE row of the column's query (cos / sin as 4 x 2 words each)
+  uint32_t cr[4][2], sr[4][2];
   {
-    const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + rq * a.qa_rs + head * a.qa_hs;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)  // channels >= R zeroed
-      qb[ks] = as_bf16x8(mask_bf16x8(*reinterpret_cast<const uint4*>(qa + 16 * ks + 8 * hf), a.R - (16 * ks + 8 * hf)));
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q_pe) + rq * a.qp_rs + head * a.qp_hs;
     int rp = a.ad.rope_abs ? sp + tq : tq;
     rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
     const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
     const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int c0 = 16 * s + 8 * hf;
-      const uint4 raw = *reinterpret_cast<const uint4*>(qp + c0);
-      const uint2 cr = *reinterpret_cast<const uint2*>(ct + c0 / 2);
-      const uint2 sr = *reinterpret_cast<const uint2*>(st + c0 / 2);
-      const uint32_t wv_in[4] = {raw.x, raw.y, raw.z, raw.w};
-      const uint32_t cw2[2] = {cr.x, cr.y}, sw2[2] = {sr.x, sr.y};
+    for (int s4 = 0; s4 < 4; ++s4) {
+      vm_load<2>(ct + (16 * s4 + 8 * hf) / 2, cr[s4]);
+      vm_load<2>(st + (16 * s4 + 8 * hf) / 2, sr[s4]);
+    }
+  }
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  // tiles 0 and 1 (a tile past the last, or with no tile at all, re-reads an
+  // in-bounds row), then the previous item's output
+  dma_tile(0, buf(I0{}));
+  dma_tile(1, buf(I1{}));
+  // in flight, in issue order: query rows (kQDma), cos / sin (8), tile 0 and
+  // tile 1 (LQ + 2 each); then the previous item's stores (kStores), issued
+  // once the query rows are in (queued ahead of them, the stores held back
+  // their arrival)
+  constexpr int kTileVm = LQ + 2;
+  p2_wait_vm<8 + 2 * kTileVm>();
+  const bool flushed = pending;  // uniform
+  if (flushed) flush();
+  bf16x8_t qb[KS + 4];
+  {
+    const uint32_t q0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(qs)) + n * kRow;
+    const int nx = (n ^ hf) & 15;  // (2 ks + hf) ^ n = 2 ks ^ (n ^ hf) on the low four bits
+    p2_u32x4_t qr[KS + 4];
+    p2_for<0, KS>([&](auto ksI) {
+      constexpr int ks = decltype(ksI)::value;
+      qr[ks] = p2_read16<16 * ((2 * ks) & 16)>(q0 + 16 * (((2 * ks) & 15) ^ nx));
+    });
+    const uint32_t p0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(qs)) + kQLat + n * kPeR;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) qr[KS + s4] = p2_read16<0>(p0 + 16 * (((2 * s4 + hf) ^ (n >> 1)) & 7));
+    p2_wait_lgkm<0>();
+#pragma unroll
+    for (int ks = 0; ks < KS + 4; ++ks) p2_tie(qr[ks]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)  // channels >= R zeroed
+      qb[ks] = as_bf16x8(mask_bf16x8(make_uint4(qr[ks].x, qr[ks].y, qr[ks].z, qr[ks].w), a.R - (16 * ks + 8 * hf)));
+    if (flushed) p2_wait_vm<2 * kTileVm + kStores>();
+    else p2_wait_vm<2 * kTileVm>();
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      vm_release(cr[s4]);
+      vm_release(sr[s4]);
+      const uint32_t wv_in[4] = {qr[KS + s4].x, qr[KS + s4].y, qr[KS + s4].z, qr[KS + s4].w};
       uint32_t wv[4];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const uint32_t cj = (jj & 1) ? (cw2[jj >> 1] >> 16) : (cw2[jj >> 1] & 0xFFFF);
-        const uint32_t sj = (jj & 1) ? (sw2[jj >> 1] >> 16) : (sw2[jj >> 1] & 0xFFFF);
-        float o1, o2;
-        rope_pair<1>(bf16_to_f32(wv_in[jj] & 0xFFFF), bf16_to_f32(wv_in[jj] >> 16), bf16_to_f32(cj), bf16_to_f32(sj), o1,
-                     o2);
-        wv[jj] = f32_to_bf16(o1) | (static_cast<uint32_t>(f32_to_bf16(o2)) << 16);
+      for (int j2 = 0; j2 < 4; ++j2) {
+        const uint32_t cj = (j2 & 1) ? (cr[s4][j2 >> 1] >> 16) : (cr[s4][j2 >> 1] & 0xFFFF);
+        const uint32_t sj = (j2 & 1) ? (sr[s4][j2 >> 1] >> 16) : (sr[s4][j2 >> 1] & 0xFFFF);
+        wv[j2] = rope_bf16_packed(bf16_to_f32(wv_in[j2] & 0xFFFF), bf16_to_f32(wv_in[j2] >> 16), bf16_to_f32(cj),
+                                  bf16_to_f32(sj));
       }
-      qb[KS + s] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
+      qb[KS + s4] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
     }
 #pragma unroll
     for (int ks = 0; ks < KS + 4; ++ks) asm volatile("" : "+a"(qb[ks]));  // kept in AGPRs: MFMA reads B from there
   }
+  pending = false;
 
   f32x16_t oacc[CB];
 #pragma unroll
@@ -825,13 +934,9 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
     qkpv(j + 1, buf(N1{}), buf(bc), [&]() __attribute__((always_inline)) { dma_tile(j + 2, buf(N2{})); }, smax_mid);
     commit();
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
   if (n_tiles > 0) {
-    dma_tile(0, buf(I0{}));
-    dma_tile(1, buf(I1{}));  // past the last tile: re-reads its rows
-    __builtin_amdgcn_s_waitcnt((LQ + 2) | (7 << 4) | (15 << 8));  // vmcnt(LQ + 2): tile 0's DMAs landed
+    if (flushed) p2_wait_vm<kTileVm + kStores>();  // tile 0's DMAs landed
+    else p2_wait_vm<kTileVm>();
     lds_barrier();
     qk(0, buf(I0{}));
     smax();
@@ -853,21 +958,26 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
     else pv(buf(I2{}), no_mid);
   }
 
-  float l_w = l_part + shfl_xor_f32(l_part, 32);
+  if (n_tiles == 0) p2_wait_vm<0>();  // the unused tile copies land before the buffers are reused
+  // The output, stored at the next item's start (or after the last item):
+  // lane (n, hf) holds channels 32 cb + 8 r4 + 4 hf + {0..3} of its column.
+  // A surplus column repeats the block's last query, so its values equal
+  // that query's, and it stores them to that query's row.
+  const float l_w = l_part + shfl_xor_f32(l_part, 32);
   const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
-  if (valid) {
-    // lane (n, hf): channels 32 cb + 8 r4 + 4 hf + {0..3}
-    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + rq * a.o_rs + head * a.o_hs + 4 * hf;
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
+  for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        uint2 pk;
-        pk.x = pack_bf16x2(oacc[cb][4 * r4] * inv, oacc[cb][4 * r4 + 1] * inv);
-        pk.y = pack_bf16x2(oacc[cb][4 * r4 + 2] * inv, oacc[cb][4 * r4 + 3] * inv);
-        *reinterpret_cast<uint2*>(op + 32 * cb + 8 * r4) = pk;
-      }
+    for (int r4 = 0; r4 < 4; ++r4) {
+      pend[cb][r4][0] = pack_bf16x2(oacc[cb][4 * r4] * inv, oacc[cb][4 * r4 + 1] * inv);
+      pend[cb][r4][1] = pack_bf16x2(oacc[cb][4 * r4 + 2] * inv, oacc[cb][4 * r4 + 3] * inv);
+    }
+  pend_op = static_cast<uint16_t*>(a.o_lat) + rq * a.o_rs + head * a.o_hs + 4 * hf;
+  pending = true;
+  // every wave is done with the LDS buffers before the next item's DMAs
+  __syncthreads();
   }
+  if (pending) flush();
 }
 
 int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
@@ -882,8 +992,15 @@ int launch_prefill(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
     // bf16 cache, latent rows of a multiple of 256 bytes: the 32x32x16 kernel
     // (the same eight query tokens per workgroup, so the same grid)
     static_assert(kP2Waves * kP2Qpw == kNw * kQpw, "query tokens per workgroup");
-    if (padded_rank(a.R) == 256) hipLaunchKernelGGL(mla_prefill_m32<4>, grid, dim3(kP2Waves * 64), 0, s, a);
-    else hipLaunchKernelGGL(mla_prefill_m32<2>, grid, dim3(kP2Waves * 64), 0, s, a);
+    // one persistent workgroup per CU (the kernel's LDS takes the CU)
+    int dev = 0, n_cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cus < 1)
+      return -2;
+    const int items = static_cast<int>(grid.x * grid.y);
+    const dim3 pgrid(std::min(items, n_cus));
+    if (padded_rank(a.R) == 256) hipLaunchKernelGGL(mla_prefill_m32<4>, pgrid, dim3(kP2Waves * 64), 0, s, a);
+    else hipLaunchKernelGGL(mla_prefill_m32<2>, pgrid, dim3(kP2Waves * 64), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -2;
   }
   const int rc = with_nb(a.R, [&](auto nb) {
