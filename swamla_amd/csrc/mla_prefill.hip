@@ -518,464 +518,466 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
     });
   };
   for (int round = 0;; ++round) {
-  const int item = round * static_cast<int>(gridDim.x) +
-                   ((round & 1) ? static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)
-                                : static_cast<int>(blockIdx.x));
-  if (item >= n_items) break;  // uniform
-  // The lane's indices are re-derived per item from an opaque copy of the
-  // thread id: nothing computed from them is hoisted out of the item loop
-  // and kept live across it (the body uses every register).
-  int tid = static_cast<int>(threadIdx.x);
-  asm volatile("" : "+v"(tid));
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int n = lane & 31, hf = lane >> 5;  // column, lane half
-  const int head = n & 15;
-  const int b = item % B;
-  const int t_first = QG * (n_groups - 1 - item / B);
-  const int t_last_q = min(t_first + QG - 1, T - 1);
-  const int sp = a.ad.start_pos[b];
-  const bool b_ok = b < a.cache_b;
-  const int tt = t_first + kP2Qpw * w + (n >> 4);  // this column's query (surplus ones repeat the last)
-  const int tq = min(tt, t_last_q);
-  const int64_t rq = static_cast<int64_t>(b) * T + tq;
-  int Lq = b_ok ? sp + tq + 1 : 0;
-  Lq = min(max(Lq, 0), static_cast<int>(a.cache_s));
-  int Lb = b_ok ? sp + t_last_q + 1 : 0;  // the block's range: its last query's
-  Lb = min(max(Lb, 0), static_cast<int>(a.cache_s));
-  const int n_tiles = (Lb + kP2Tok - 1) / kP2Tok;  // block-uniform
-  const int64_t cache_row0 = static_cast<int64_t>(b_ok ? b : 0) * a.cache_s;
-  const int t_last = Lb > 0 ? Lb - 1 : 0;
-  // this sequence's cache rows (32-bit lane offsets from a uniform base)
-  const uint8_t* const ckv = static_cast<const uint8_t*>(a.ckv) + cache_row0 * kRow;
-  const uint8_t* const kpe = static_cast<const uint8_t*>(a.kpe) + cache_row0 * kPeR;
+    const int item = round * static_cast<int>(gridDim.x) +
+                     ((round & 1) ? static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)
+                                  : static_cast<int>(blockIdx.x));
+    if (item >= n_items) break;  // uniform
+    // The lane's indices are re-derived per item from an opaque copy of the
+    // thread id: nothing computed from them is hoisted out of the item loop
+    // and kept live across it (the body uses every register).
+    int tid = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tid));
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int n = lane & 31, hf = lane >> 5;  // column, lane half
+    const int head = n & 15;
+    const int b = item % B;
+    const int t_first = QG * (n_groups - 1 - item / B);
+    const int t_last_q = min(t_first + QG - 1, T - 1);
+    const int sp = a.ad.start_pos[b];
+    const bool b_ok = b < a.cache_b;
+    const int tt = t_first + kP2Qpw * w + (n >> 4);  // this column's query (surplus ones repeat the last)
+    const int tq = min(tt, t_last_q);
+    const int64_t rq = static_cast<int64_t>(b) * T + tq;
+    int Lq = b_ok ? sp + tq + 1 : 0;
+    Lq = min(max(Lq, 0), static_cast<int>(a.cache_s));
+    int Lb = b_ok ? sp + t_last_q + 1 : 0;  // the block's range: its last query's
+    Lb = min(max(Lb, 0), static_cast<int>(a.cache_s));
+    const int n_tiles = (Lb + kP2Tok - 1) / kP2Tok;  // block-uniform
+    const int64_t cache_row0 = static_cast<int64_t>(b_ok ? b : 0) * a.cache_s;
+    const int t_last = Lb > 0 ? Lb - 1 : 0;
+    // this sequence's cache rows (32-bit lane offsets from a uniform base)
+    const uint8_t* const ckv = static_cast<const uint8_t*>(a.ckv) + cache_row0 * kRow;
+    const uint8_t* const kpe = static_cast<const uint8_t*>(a.kpe) + cache_row0 * kPeR;
 
-  // ---- DMA of this wave's 16 rows of tile j (rows 16w .. 16w + 15) straight
-  // into LDS, 1 KB per instruction: LDS chunk p of row t holds cache chunk
-  // p ^ swizzle(t) (the XOR is its own inverse).
-  uint32_t lat_src[LQ], pe_src[2];  // lane offsets within a tile's rows, row index excluded
-  int lat_row[LQ], pe_row[2];
-#pragma unroll
-  for (int q = 0; q < LQ; ++q) {
-    const int t = 16 * w + kRowsPerDma * q + (16 * lane) / kRow, pch = ((16 * lane) % kRow) / 16;
-    lat_row[q] = t;
-    lat_src[q] = 16 * p2_pos(pch, t);
-  }
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int t = 16 * w + 8 * q + (lane >> 3);
-    pe_row[q] = t;
-    pe_src[q] = 16 * ((lane & 7) ^ ((t >> 1) & 7));
-  }
-  auto dma_tile = [&](int j, lds_u8* dst) __attribute__((always_inline)) {
+    // ---- DMA of this wave's 16 rows of tile j (rows 16w .. 16w + 15) straight
+    // into LDS, 1 KB per instruction: LDS chunk p of row t holds cache chunk
+    // p ^ swizzle(t) (the XOR is its own inverse).
+    uint32_t lat_src[LQ], pe_src[2];  // lane offsets within a tile's rows, row index excluded
+    int lat_row[LQ], pe_row[2];
 #pragma unroll
     for (int q = 0; q < LQ; ++q) {
-      const uint32_t row = min(j * kP2Tok + lat_row[q], t_last);
-      p2_dma16(ckv + (row * kRow + lat_src[q]), dst + (16 * w + kRowsPerDma * q) * kRow);
+      const int t = 16 * w + kRowsPerDma * q + (16 * lane) / kRow, pch = ((16 * lane) % kRow) / 16;
+      lat_row[q] = t;
+      lat_src[q] = 16 * p2_pos(pch, t);
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const uint32_t row = min(j * kP2Tok + pe_row[q], t_last);
-      p2_dma16(kpe + (row * kPeR + pe_src[q]), dst + kLat + (16 * w + 8 * q) * kPeR);
+      const int t = 16 * w + 8 * q + (lane >> 3);
+      pe_row[q] = t;
+      pe_src[q] = 16 * ((lane & 7) ^ ((t >> 1) & 7));
     }
-  };
-
-  // ---- Q^T operands: column n (query n >> 4 of the wave, head n & 15),
-  // channels 16 ks + 8 hf .. + 7 (k-steps KS.. are the rope part).  The
-  // wave's 32 query rows are copied into its staging area by LDS DMA in whole
-  // lines (1 KB per instruction): column n's latent chunk c at slot (c & 16) |
-  // ((c ^ n) & 15), its rope chunk c at (c ^ (n >> 1)) & 7, so that the
-  // operand reads (chunk 2 ks + hf of 16 columns per read cycle) hit distinct
-  // banks.  Loaded per lane instead, 16 bytes of 32 rows per instruction, the
-  // rows took several microseconds per item.
-  constexpr int kQLat = 32 * kRow;                // latent bytes of the wave's 32 columns
-  constexpr int kQBytes = kQLat + 32 * kPeR;
-  constexpr int kQDma = kQBytes / 1024;           // DMA instructions for the wave's rows
-  static_assert(kQLat % 1024 == 0 && 2 * kQBytes <= kBuf, "two waves' rows fit a staging buffer");
-  lds_u8* const qs = ((w >> 1) == 0 ? (lds_u8*)lds2 : (lds_u8*)lds3) + (w & 1) * kQBytes;
-  const int tq_w = min(t_first + kP2Qpw * w, t_last_q);  // the wave's first query (surplus ones repeat the last)
-  const int64_t rq_w = static_cast<int64_t>(b) * T + tq_w;
-  const int rq_step = min(t_first + kP2Qpw * w + 1, t_last_q) - tq_w;  // 0 or 1
-  p2_for<0, kQDma>([&](auto iI) {
-    constexpr int i = decltype(iI)::value;
-    const int o = 1024 * i + 16 * lane;
-    if constexpr (1024 * i < kQLat) {
-      const int col = o / kRow, sl = (o % kRow) / 16, ch = (sl & 16) | ((sl ^ col) & 15);
-      const uint16_t* src = static_cast<const uint16_t*>(a.q_abs) + (rq_w + (col >> 4) * rq_step) * a.qa_rs +
-                            (col & 15) * a.qa_hs + 8 * ch;
-      p2_dma16(src, qs + 1024 * i);
-    } else {
-      const int o2 = o - kQLat, col = o2 / kPeR, ch = ((o2 % kPeR) / 16 ^ (col >> 1)) & 7;
-      const uint16_t* src = static_cast<const uint16_t*>(a.q_pe) + (rq_w + (col >> 4) * rq_step) * a.qp_rs +
-                            (col & 15) * a.qp_hs + 8 * ch;
-      p2_dma16(src, qs + 1024 * i);
-    }
-  });
-  // the RoPE row of the column's query (cos / sin as 4 x 2 words each)
-  uint32_t cr[4][2], sr[4][2];
-  {
-    int rp = a.ad.rope_abs ? sp + tq : tq;
-    rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
-    const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
-    const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
+    auto dma_tile = [&](int j, lds_u8* dst) __attribute__((always_inline)) {
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      vm_load<2>(ct + (16 * s4 + 8 * hf) / 2, cr[s4]);
-      vm_load<2>(st + (16 * s4 + 8 * hf) / 2, sr[s4]);
-    }
-  }
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  // tiles 0 and 1 (a tile past the last, or with no tile at all, re-reads an
-  // in-bounds row), then the previous item's output
-  dma_tile(0, buf(I0{}));
-  dma_tile(1, buf(I1{}));
-  // in flight, in issue order: query rows (kQDma), cos / sin (8), tile 0 and
-  // tile 1 (LQ + 2 each); then the previous item's stores (kStores), issued
-  // once the query rows are in (queued ahead of them, the stores held back
-  // their arrival)
-  constexpr int kTileVm = LQ + 2;
-  p2_wait_vm<8 + 2 * kTileVm>();
-  const bool flushed = pending;  // uniform
-  if (flushed) flush();
-  bf16x8_t qb[KS + 4];
-  {
-    const uint32_t q0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(qs)) + n * kRow;
-    const int nx = (n ^ hf) & 15;  // (2 ks + hf) ^ n = 2 ks ^ (n ^ hf) on the low four bits
-    p2_u32x4_t qr[KS + 4];
-    p2_for<0, KS>([&](auto ksI) {
-      constexpr int ks = decltype(ksI)::value;
-      qr[ks] = p2_read16<16 * ((2 * ks) & 16)>(q0 + 16 * (((2 * ks) & 15) ^ nx));
-    });
-    const uint32_t p0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(qs)) + kQLat + n * kPeR;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) qr[KS + s4] = p2_read16<0>(p0 + 16 * (((2 * s4 + hf) ^ (n >> 1)) & 7));
-    p2_wait_lgkm<0>();
-#pragma unroll
-    for (int ks = 0; ks < KS + 4; ++ks) p2_tie(qr[ks]);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)  // channels >= R zeroed
-      qb[ks] = as_bf16x8(mask_bf16x8(make_uint4(qr[ks].x, qr[ks].y, qr[ks].z, qr[ks].w), a.R - (16 * ks + 8 * hf)));
-    if (flushed) p2_wait_vm<2 * kTileVm + kStores>();
-    else p2_wait_vm<2 * kTileVm>();
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      vm_release(cr[s4]);
-      vm_release(sr[s4]);
-      const uint32_t wv_in[4] = {qr[KS + s4].x, qr[KS + s4].y, qr[KS + s4].z, qr[KS + s4].w};
-      uint32_t wv[4];
-#pragma unroll
-      for (int j2 = 0; j2 < 4; ++j2) {
-        const uint32_t cj = (j2 & 1) ? (cr[s4][j2 >> 1] >> 16) : (cr[s4][j2 >> 1] & 0xFFFF);
-        const uint32_t sj = (j2 & 1) ? (sr[s4][j2 >> 1] >> 16) : (sr[s4][j2 >> 1] & 0xFFFF);
-        wv[j2] = rope_bf16_packed(bf16_to_f32(wv_in[j2] & 0xFFFF), bf16_to_f32(wv_in[j2] >> 16), bf16_to_f32(cj),
-                                  bf16_to_f32(sj));
+      for (int q = 0; q < LQ; ++q) {
+        const uint32_t row = min(j * kP2Tok + lat_row[q], t_last);
+        p2_dma16(ckv + (row * kRow + lat_src[q]), dst + (16 * w + kRowsPerDma * q) * kRow);
       }
-      qb[KS + s4] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
-    }
 #pragma unroll
-    for (int ks = 0; ks < KS + 4; ++ks) asm volatile("" : "+a"(qb[ks]));  // kept in AGPRs: MFMA reads B from there
-  }
-  pending = false;
-
-  f32x16_t oacc[CB];
-#pragma unroll
-  for (int i = 0; i < CB; ++i) oacc[i] = f32x16_t{};
-  float m_run = -INFINITY, l_part = 0.f;
-
-  // ---- per-lane operand offsets (bytes within a tile buffer).  The swizzle
-  // XORs only the low four bits of a chunk index, so each read is a per-lane
-  // table entry plus a compile-time offset (the ds_read immediate):
-  //   K latent, k-step ks, half h2: ko[ks % 8] + 256 (ks / 8) + 32 h2 kRow
-  //   K rope, k-step s, half h2:    po[s] + 32 h2 kPeR
-  //   C^T, k-step s, block cb, read e: to[e][cb % 4] + 16 s kRow + 256 (cb / 4)
-  const int fl = p2_swz(n & 15);  // rows 32 h2 + n of a tile
-  const int pe_sw = (n >> 1) & 7;
-  const int G = lane >> 4, jj = lane & 15, g2 = G & 1;  // transposed reads: 16-lane group, lane in group
-  uint32_t ko[8], po[4], to[2][4];
-#pragma unroll
-  for (int k8 = 0; k8 < 8; ++k8) ko[k8] = n * kRow + 16 * ((2 * k8 + hf) ^ fl);
-#pragma unroll
-  for (int s4 = 0; s4 < 4; ++s4) po[s4] = kLat + n * kPeR + 16 * ((2 * s4 + hf) ^ pe_sw);
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int r = 8 * e + 4 * hf + (jj >> 2);  // row within a 16-token k-step
-#pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4)
-      to[e][c4] = r * kRow + 16 * ((4 * c4 + 2 * g2 + ((jj & 3) >> 1)) ^ p2_swz(r)) + 8 * (jj & 1);
-  }
-  static_assert(KS <= 16 && kRow % 256 == 0, "the latent read table covers 16 k-steps of 256-byte row halves");
-
-  // qk(j, base): scores of tile j, scaled to the log2 domain and masked.
-  // The 2 (KS + 4) K reads run kQkAhead ahead of their MFMAs.
-  constexpr int kQkReads = 2 * (KS + 4), kQkAhead = 6;
-  f32x16_t sc[2];
-  int sc_tile = 0;  // the tile sc holds (scaled and masked in the softmax step)
-  auto qk = [&](int j, const lds_u8* base_p) __attribute__((always_inline)) {
-    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(base_p));
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) sc[h2] = f32x16_t{};
-    p2_u32x4_t kr[kQkReads];
-    auto rd = [&](auto I) __attribute__((always_inline)) {
-      constexpr int i = decltype(I)::value, ks = i / 2, h2 = i % 2;
-      if constexpr (ks < KS) kr[i] = p2_read16<256 * (ks / 8) + 32 * h2 * kRow>(base + ko[ks % 8]);
-      else kr[i] = p2_read16<32 * h2 * kPeR>(base + po[ks - KS]);
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t row = min(j * kP2Tok + pe_row[q], t_last);
+        p2_dma16(kpe + (row * kPeR + pe_src[q]), dst + kLat + (16 * w + 8 * q) * kPeR);
+      }
     };
-    p2_for<0, kQkAhead>(rd);
-    p2_for<0, kQkReads>([&](auto I) __attribute__((always_inline)) {
-      constexpr int i = decltype(I)::value, ks = i / 2, h2 = i % 2;
-      if constexpr (i + kQkAhead < kQkReads) {
-        rd(std::integral_constant<int, i + kQkAhead>{});
-        p2_wait_lgkm<kQkAhead>();
+
+    // ---- Q^T operands: column n (query n >> 4 of the wave, head n & 15),
+    // channels 16 ks + 8 hf .. + 7 (k-steps KS.. are the rope part).  The
+    // wave's 32 query rows are copied into its staging area by LDS DMA in whole
+    // lines (1 KB per instruction): column n's latent chunk c at slot (c & 16) |
+    // ((c ^ n) & 15), its rope chunk c at (c ^ (n >> 1)) & 7, so that the
+    // operand reads (chunk 2 ks + hf of 16 columns per read cycle) hit distinct
+    // banks.  Loaded per lane instead, 16 bytes of 32 rows per instruction, the
+    // rows took several microseconds per item.
+    constexpr int kQLat = 32 * kRow;                // latent bytes of the wave's 32 columns
+    constexpr int kQBytes = kQLat + 32 * kPeR;
+    constexpr int kQDma = kQBytes / 1024;           // DMA instructions for the wave's rows
+    static_assert(kQLat % 1024 == 0 && 2 * kQBytes <= kBuf, "two waves' rows fit a staging buffer");
+    lds_u8* const qs = ((w >> 1) == 0 ? (lds_u8*)lds2 : (lds_u8*)lds3) + (w & 1) * kQBytes;
+    const int tq_w = min(t_first + kP2Qpw * w, t_last_q);  // the wave's first query (surplus ones repeat the last)
+    const int64_t rq_w = static_cast<int64_t>(b) * T + tq_w;
+    const int rq_step = min(t_first + kP2Qpw * w + 1, t_last_q) - tq_w;  // 0 or 1
+    p2_for<0, kQDma>([&](auto iI) {
+      constexpr int i = decltype(iI)::value;
+      const int o = 1024 * i + 16 * lane;
+      if constexpr (1024 * i < kQLat) {
+        const int col = o / kRow, sl = (o % kRow) / 16, ch = (sl & 16) | ((sl ^ col) & 15);
+        const uint16_t* src = static_cast<const uint16_t*>(a.q_abs) + (rq_w + (col >> 4) * rq_step) * a.qa_rs +
+                              (col & 15) * a.qa_hs + 8 * ch;
+        p2_dma16(src, qs + 1024 * i);
       } else {
-        p2_wait_lgkm<kQkReads - 1 - i>();
+        const int o2 = o - kQLat, col = o2 / kPeR, ch = ((o2 % kPeR) / 16 ^ (col >> 1)) & 7;
+        const uint16_t* src = static_cast<const uint16_t*>(a.q_pe) + (rq_w + (col >> 4) * rq_step) * a.qp_rs +
+                              (col & 15) * a.qp_hs + 8 * ch;
+        p2_dma16(src, qs + 1024 * i);
       }
-      p2_tie(kr[i]);
-      sc[h2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[ks], sc[h2], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
     });
-    sc_tile = j;
-  };
-  // smax(): the online-softmax step of the scores sc, without touching O:
-  // the new reference m_new (moved lazily, when a column's maximum grows by
-  // more than 2^kLazy), the rescale factor alpha of what was accumulated so
-  // far, and the bf16 weights pbn in the PV operand order (k-step s = 2 h2 +
-  // sb: registers 8 sb .. 8 sb + 7 of half h2) with their sum.  The caller
-  // rescales O after the PV product of the previous tile, which used the old
-  // reference.  Branch-free, so it shares one scheduling region with that
-  // product.
-  bf16x8_t pb[4], pbn[4];
-  float alpha = 1.f, lsum = 0.f, m_new = -INFINITY;
-  bool moved = false;
-  // part 0: the tile maximum and the new reference; parts 1, 2: the weights
-  // of half-tile 0, 1
-  float mref = 0.f;
-  auto smax_part = [&](auto P) __attribute__((always_inline)) {
-    constexpr int part = decltype(P)::value;
-    if constexpr (part == 0) {
-      // Tokens at or past a column's causal end score -inf; only the tiles
-      // that reach the end of one of the wave's queries need the compares.
-      if (!__all(sc_tile * kP2Tok + kP2Tok <= Lq)) {
-        const int tok0 = sc_tile * kP2Tok + 4 * hf;
+    // the RoPE row of the column's query (cos / sin as 4 x 2 words each)
+    uint32_t cr[4][2], sr[4][2];
+    {
+      int rp = a.ad.rope_abs ? sp + tq : tq;
+      rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
+      const uint16_t* ct = static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
+      const uint16_t* st = static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        vm_load<2>(ct + (16 * s4 + 8 * hf) / 2, cr[s4]);
+        vm_load<2>(st + (16 * s4 + 8 * hf) / 2, sr[s4]);
+      }
+    }
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    // tiles 0 and 1 (a tile past the last, or with no tile at all, re-reads an
+    // in-bounds row), then the previous item's output
+    dma_tile(0, buf(I0{}));
+    dma_tile(1, buf(I1{}));
+    // in flight, in issue order: query rows (kQDma), cos / sin (8), tile 0 and
+    // tile 1 (LQ + 2 each); then the previous item's stores (kStores), issued
+    // once the query rows are in (queued ahead of them, the stores held back
+    // their arrival)
+    constexpr int kTileVm = LQ + 2;
+    p2_wait_vm<8 + 2 * kTileVm>();
+    const bool flushed = pending;  // uniform
+    if (flushed) flush();
+    bf16x8_t qb[KS + 4];
+    {
+      const uint32_t q0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(qs)) + n * kRow;
+      const int nx = (n ^ hf) & 15;  // (2 ks + hf) ^ n = 2 ks ^ (n ^ hf) on the low four bits
+      p2_u32x4_t qr[KS + 4];
+      p2_for<0, KS>([&](auto ksI) {
+        constexpr int ks = decltype(ksI)::value;
+        qr[ks] = p2_read16<16 * ((2 * ks) & 16)>(q0 + 16 * (((2 * ks) & 15) ^ nx));
+      });
+      const uint32_t p0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(qs)) + kQLat + n * kPeR;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) qr[KS + s4] = p2_read16<0>(p0 + 16 * (((2 * s4 + hf) ^ (n >> 1)) & 7));
+      p2_wait_lgkm<0>();
+#pragma unroll
+      for (int ks = 0; ks < KS + 4; ++ks) p2_tie(qr[ks]);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)  // channels >= R zeroed
+        qb[ks] = as_bf16x8(mask_bf16x8(make_uint4(qr[ks].x, qr[ks].y, qr[ks].z, qr[ks].w), a.R - (16 * ks + 8 * hf)));
+      if (flushed) p2_wait_vm<2 * kTileVm + kStores>();
+      else p2_wait_vm<2 * kTileVm>();
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        vm_release(cr[s4]);
+        vm_release(sr[s4]);
+        const uint32_t wv_in[4] = {qr[KS + s4].x, qr[KS + s4].y, qr[KS + s4].z, qr[KS + s4].w};
+        uint32_t wv[4];
+#pragma unroll
+        for (int j2 = 0; j2 < 4; ++j2) {
+          const uint32_t cj = (j2 & 1) ? (cr[s4][j2 >> 1] >> 16) : (cr[s4][j2 >> 1] & 0xFFFF);
+          const uint32_t sj = (j2 & 1) ? (sr[s4][j2 >> 1] >> 16) : (sr[s4][j2 >> 1] & 0xFFFF);
+          wv[j2] = rope_bf16_packed(bf16_to_f32(wv_in[j2] & 0xFFFF), bf16_to_f32(wv_in[j2] >> 16), bf16_to_f32(cj),
+                                    bf16_to_f32(sj));
+        }
+        qb[KS + s4] = as_bf16x8(make_uint4(wv[0], wv[1], wv[2], wv[3]));
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS + 4; ++ks) asm volatile("" : "+a"(qb[ks]));  // kept in AGPRs: MFMA reads B from there
+    }
+    pending = false;
+
+    f32x16_t oacc[CB];
+#pragma unroll
+    for (int i = 0; i < CB; ++i) oacc[i] = f32x16_t{};
+    float m_run = -INFINITY, l_part = 0.f;
+
+    // ---- per-lane operand offsets (bytes within a tile buffer).  The swizzle
+    // XORs only the low four bits of a chunk index, so each read is a per-lane
+    // table entry plus a compile-time offset (the ds_read immediate):
+    //   K latent, k-step ks, half h2: ko[ks % 8] + 256 (ks / 8) + 32 h2 kRow
+    //   K rope, k-step s, half h2:    po[s] + 32 h2 kPeR
+    //   C^T, k-step s, block cb, read e: to[e][cb % 4] + 16 s kRow + 256 (cb / 4)
+    const int fl = p2_swz(n & 15);  // rows 32 h2 + n of a tile
+    const int pe_sw = (n >> 1) & 7;
+    const int G = lane >> 4, jj = lane & 15, g2 = G & 1;  // transposed reads: 16-lane group, lane in group
+    uint32_t ko[8], po[4], to[2][4];
+#pragma unroll
+    for (int k8 = 0; k8 < 8; ++k8) ko[k8] = n * kRow + 16 * ((2 * k8 + hf) ^ fl);
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) po[s4] = kLat + n * kPeR + 16 * ((2 * s4 + hf) ^ pe_sw);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = 8 * e + 4 * hf + (jj >> 2);  // row within a 16-token k-step
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4)
+        to[e][c4] = r * kRow + 16 * ((4 * c4 + 2 * g2 + ((jj & 3) >> 1)) ^ p2_swz(r)) + 8 * (jj & 1);
+    }
+    static_assert(KS <= 16 && kRow % 256 == 0, "the latent read table covers 16 k-steps of 256-byte row halves");
+
+    // qk(j, base): scores of tile j, scaled to the log2 domain and masked.
+    // The 2 (KS + 4) K reads run kQkAhead ahead of their MFMAs.
+    constexpr int kQkReads = 2 * (KS + 4), kQkAhead = 6;
+    f32x16_t sc[2];
+    int sc_tile = 0;  // the tile sc holds (scaled and masked in the softmax step)
+    auto qk = [&](int j, const lds_u8* base_p) __attribute__((always_inline)) {
+      const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(base_p));
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) sc[h2] = f32x16_t{};
+      p2_u32x4_t kr[kQkReads];
+      auto rd = [&](auto I) __attribute__((always_inline)) {
+        constexpr int i = decltype(I)::value, ks = i / 2, h2 = i % 2;
+        if constexpr (ks < KS) kr[i] = p2_read16<256 * (ks / 8) + 32 * h2 * kRow>(base + ko[ks % 8]);
+        else kr[i] = p2_read16<32 * h2 * kPeR>(base + po[ks - KS]);
+      };
+      p2_for<0, kQkAhead>(rd);
+      p2_for<0, kQkReads>([&](auto I) __attribute__((always_inline)) {
+        constexpr int i = decltype(I)::value, ks = i / 2, h2 = i % 2;
+        if constexpr (i + kQkAhead < kQkReads) {
+          rd(std::integral_constant<int, i + kQkAhead>{});
+          p2_wait_lgkm<kQkAhead>();
+        } else {
+          p2_wait_lgkm<kQkReads - 1 - i>();
+        }
+        p2_tie(kr[i]);
+        sc[h2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[ks], sc[h2], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      sc_tile = j;
+    };
+    // smax(): the online-softmax step of the scores sc, without touching O:
+    // the new reference m_new (moved lazily, when a column's maximum grows by
+    // more than 2^kLazy), the rescale factor alpha of what was accumulated so
+    // far, and the bf16 weights pbn in the PV operand order (k-step s = 2 h2 +
+    // sb: registers 8 sb .. 8 sb + 7 of half h2) with their sum.  The caller
+    // rescales O after the PV product of the previous tile, which used the old
+    // reference.  Branch-free, so it shares one scheduling region with that
+    // product.
+    bf16x8_t pb[4], pbn[4];
+    float alpha = 1.f, lsum = 0.f, m_new = -INFINITY;
+    bool moved = false;
+    // part 0: the tile maximum and the new reference; parts 1, 2: the weights
+    // of half-tile 0, 1
+    float mref = 0.f;
+    auto smax_part = [&](auto P) __attribute__((always_inline)) {
+      constexpr int part = decltype(P)::value;
+      if constexpr (part == 0) {
+        // Tokens at or past a column's causal end score -inf; only the tiles
+        // that reach the end of one of the wave's queries need the compares.
+        if (!__all(sc_tile * kP2Tok + kP2Tok <= Lq)) {
+          const int tok0 = sc_tile * kP2Tok + 4 * hf;
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int tok = tok0 + 32 * h2 + 8 * (r >> 2) + (r & 3);
+              if (tok >= Lq) sc[h2][r] = -INFINITY;
+            }
+        }
+        float mt = -INFINITY;
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int tok = tok0 + 32 * h2 + 8 * (r >> 2) + (r & 3);
-            if (tok >= Lq) sc[h2][r] = -INFINITY;
+          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[h2][r]);
+        const uint32_t u = f2u(mt);
+        const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        // the column's tile maximum (both lane halves), in the log2 domain (the scale is positive)
+        mt = fmaxf(u2f(r32[0]), u2f(r32[1])) * a.scale_log2;
+        moved = __any(mt > m_run + kLazy);
+        m_new = moved ? fmaxf(m_run, mt) : m_run;
+        // a column still without a valid token (both -inf) keeps alpha = 1, not
+        // NaN: the wave's other query can move its own maximum
+        alpha = m_new == m_run ? 1.f : exp2f(m_run - m_new);
+        // A column with no valid token yet (reference still -inf) takes weight 0, not NaN.
+        mref = m_new == -INFINITY ? 0.f : -m_new;  // (negated: the weights are exp2(s scale - m))
+        lsum = 0.f;
+        p2_tie(mref);  // keeps this part where it is placed (the compiler would sink it to its uses)
+        p2_tie(alpha);
+      } else {
+        constexpr int h2 = part - 1;
+        // weights exp2(s scale - m) with one rounding before the exponential
+        // (v_exp_f32: the arguments are at most kLazy, so no range reduction),
+        // rounded to bf16; their sum with one dot2 per pair
+        const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          uint32_t pw[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h2][8 * sb + 2 * e], a.scale_log2, mref));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h2][8 * sb + 2 * e + 1], a.scale_log2, mref));
+            pw[e] = pack_bf16x2(p0, p1);
+            lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw[e]), ones, lsum, false);
           }
-      }
-      float mt = -INFINITY;
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[h2][r]);
-      const uint32_t u = f2u(mt);
-      const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-      // the column's tile maximum (both lane halves), in the log2 domain (the scale is positive)
-      mt = fmaxf(u2f(r32[0]), u2f(r32[1])) * a.scale_log2;
-      moved = __any(mt > m_run + kLazy);
-      m_new = moved ? fmaxf(m_run, mt) : m_run;
-      // a column still without a valid token (both -inf) keeps alpha = 1, not
-      // NaN: the wave's other query can move its own maximum
-      alpha = m_new == m_run ? 1.f : exp2f(m_run - m_new);
-      // A column with no valid token yet (reference still -inf) takes weight 0, not NaN.
-      mref = m_new == -INFINITY ? 0.f : -m_new;  // (negated: the weights are exp2(s scale - m))
-      lsum = 0.f;
-      p2_tie(mref);  // keeps this part where it is placed (the compiler would sink it to its uses)
-      p2_tie(alpha);
-    } else {
-      constexpr int h2 = part - 1;
-      // weights exp2(s scale - m) with one rounding before the exponential
-      // (v_exp_f32: the arguments are at most kLazy, so no range reduction),
-      // rounded to bf16; their sum with one dot2 per pair
-      const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        uint32_t pw[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h2][8 * sb + 2 * e], a.scale_log2, mref));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h2][8 * sb + 2 * e + 1], a.scale_log2, mref));
-          pw[e] = pack_bf16x2(p0, p1);
-          lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw[e]), ones, lsum, false);
+          pbn[2 * h2 + sb] = as_bf16x8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
+          p2_tie(pbn[2 * h2 + sb]);
         }
-        pbn[2 * h2 + sb] = as_bf16x8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        p2_tie(pbn[2 * h2 + sb]);
-      }
-      p2_tie(lsum);
-    }
-  };
-  auto smax = [&]() __attribute__((always_inline)) {
-    smax_part(std::integral_constant<int, 0>{});
-    smax_part(std::integral_constant<int, 1>{});
-    smax_part(std::integral_constant<int, 2>{});
-  };
-  // the softmax parts placed after PV MFMAs M/8, 3M/8 and 5M/8 (M = 4 CB)
-  auto smax_mid = [&](auto I) __attribute__((always_inline)) {
-    constexpr int m = decltype(I)::value, M = 4 * CB;
-    if constexpr (m == M / 8) smax_part(std::integral_constant<int, 0>{});
-    else if constexpr (m == 3 * M / 8) smax_part(std::integral_constant<int, 1>{});
-    else if constexpr (m == 5 * M / 8) smax_part(std::integral_constant<int, 2>{});
-  };
-  // commit(): the reference and weight sum move to the new tile; O is
-  // rescaled if any column's reference moved (rare after the first tiles).
-  auto commit = [&]() __attribute__((always_inline)) {
-    l_part = l_part * alpha + lsum;
-    m_run = m_new;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) pb[s4] = pbn[s4];
-    if (moved) {
-#pragma unroll
-      for (int i = 0; i < CB; ++i) {  // one block at a time: few registers live
-        oacc[i] = oacc[i] * alpha;
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  };
-  // pv(base, mid): O^T[32 cb + ., col] += C^T . P^T over a tile's four
-  // 16-token k-steps, the two transposed reads of each MFMA kPvAhead MFMAs
-  // ahead; mid(I) runs after MFMA I (the next tile's softmax work, which
-  // then overlaps the MFMAs in flight).
-  constexpr int kPvMfma = 4 * CB, kPvAhead = 6;
-  auto pv = [&](const lds_u8* base_p, auto&& mid) __attribute__((always_inline)) {
-    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(base_p));
-    s16x4_t cr[kPvMfma][2];
-    auto rd = [&](auto I) __attribute__((always_inline)) {
-      constexpr int m = decltype(I)::value, s4 = m / CB, cb = m % CB;
-      constexpr int imm = 16 * s4 * kRow + 256 * (cb / 4);
-      cr[m][0] = p2_read_tr<imm>(base + to[0][cb % 4]);
-      cr[m][1] = p2_read_tr<imm>(base + to[1][cb % 4]);
-    };
-    p2_for<0, kPvAhead>(rd);
-    p2_for<0, kPvMfma>([&](auto I) __attribute__((always_inline)) {
-      constexpr int m = decltype(I)::value, s4 = m / CB, cb = m % CB;
-      if constexpr (m + kPvAhead < kPvMfma) {
-        rd(std::integral_constant<int, m + kPvAhead>{});
-        p2_wait_lgkm<2 * kPvAhead>();
-      } else {
-        p2_wait_lgkm<2 * (kPvMfma - 1 - m)>();
-      }
-      p2_tie(cr[m][0]);
-      p2_tie(cr[m][1]);
-      oacc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat_bf16x8(cr[m][0], cr[m][1]), pb[s4], oacc[cb], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      mid(I);
-    });
-  };
-  auto no_mid = [](auto) {};
-
-  // qkpv(jn, bq, bp, at, mid): tile jn's QK (slots 0 .. kQkReads - 1, one K
-  // read each) and the previous tile's PV (the following slots, two C^T
-  // reads each) as one stream of MFMAs, with kInFlight LDS reads kept in
-  // flight across the boundary between the two products: at about 300 cycles
-  // of LDS latency under load, the reads in flight, not the LDS bandwidth,
-  // set the rate.  at() runs after the first MFMA (the next tile's DMAs),
-  // mid(m) after PV MFMA m (the softmax step).
-  constexpr int kSlots = kQkReads + kPvMfma, kReads = kQkReads + 2 * kPvMfma, kInFlight = 12;
-  static_assert(kInFlight < 16, "lgkmcnt range");
-  auto qkpv = [&](int jn, const lds_u8* bq_p, const lds_u8* bp_p, auto&& at, auto&& mid) __attribute__((always_inline)) {
-    const uint32_t bq = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(bq_p));
-    const uint32_t bp = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(bp_p));
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) sc[h2] = f32x16_t{};
-    sc_tile = jn;  // before the softmax step placed in the PV slots reads it
-    p2_u32x4_t kr[kQkReads];
-    s16x4_t cr[kPvMfma][2];
-    auto rd = [&](auto R) __attribute__((always_inline)) {  // read R of the stream
-      constexpr int r = decltype(R)::value;
-      if constexpr (r < kQkReads) {
-        constexpr int ks = r / 2, h2 = r % 2;
-        if constexpr (ks < KS) kr[r] = p2_read16<256 * (ks / 8) + 32 * h2 * kRow>(bq + ko[ks % 8]);
-        else kr[r] = p2_read16<32 * h2 * kPeR>(bq + po[ks - KS]);
-      } else {
-        constexpr int m = (r - kQkReads) / 2, e = (r - kQkReads) % 2, s4 = m / CB, cb = m % CB;
-        cr[m][e] = p2_read_tr<16 * s4 * kRow + 256 * (cb / 4)>(bp + to[e][cb % 4]);
+        p2_tie(lsum);
       }
     };
-    p2_for<0, p2_min<kInFlight, kReads>()>(rd);
-    p2_for<0, kSlots>([&](auto I) __attribute__((always_inline)) {
-      constexpr int i = decltype(I)::value;
-      constexpr int done = p2_nreads<kQkReads>(i);  // reads this slot needs complete
-      constexpr int before = p2_min<(i == 0 ? 0 : p2_nreads<kQkReads>(i - 1)) + kInFlight, kReads>();
-      constexpr int upto = p2_min<done + kInFlight, kReads>();  // reads issued after this slot's issue step
-      p2_for<before, upto>(rd);
-      p2_wait_lgkm<upto - done>();
-      if constexpr (i < kQkReads) {
-        constexpr int ks = i / 2, h2 = i % 2;
-        p2_tie(kr[i]);
-        sc[h2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[ks], sc[h2], 0, 0, 0);
-      } else {
-        constexpr int m = i - kQkReads, s4 = m / CB, cb = m % CB;
+    auto smax = [&]() __attribute__((always_inline)) {
+      smax_part(std::integral_constant<int, 0>{});
+      smax_part(std::integral_constant<int, 1>{});
+      smax_part(std::integral_constant<int, 2>{});
+    };
+    // the softmax parts placed after PV MFMAs M/8, 3M/8 and 5M/8 (M = 4 CB)
+    auto smax_mid = [&](auto I) __attribute__((always_inline)) {
+      constexpr int m = decltype(I)::value, M = 4 * CB;
+      if constexpr (m == M / 8) smax_part(std::integral_constant<int, 0>{});
+      else if constexpr (m == 3 * M / 8) smax_part(std::integral_constant<int, 1>{});
+      else if constexpr (m == 5 * M / 8) smax_part(std::integral_constant<int, 2>{});
+    };
+    // commit(): the reference and weight sum move to the new tile; O is
+    // rescaled if any column's reference moved (rare after the first tiles).
+    auto commit = [&]() __attribute__((always_inline)) {
+      l_part = l_part * alpha + lsum;
+      m_run = m_new;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) pb[s4] = pbn[s4];
+      if (moved) {
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {  // one block at a time: few registers live
+          oacc[i] = oacc[i] * alpha;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    // pv(base, mid): O^T[32 cb + ., col] += C^T . P^T over a tile's four
+    // 16-token k-steps, the two transposed reads of each MFMA kPvAhead MFMAs
+    // ahead; mid(I) runs after MFMA I (the next tile's softmax work, which
+    // then overlaps the MFMAs in flight).
+    constexpr int kPvMfma = 4 * CB, kPvAhead = 6;
+    auto pv = [&](const lds_u8* base_p, auto&& mid) __attribute__((always_inline)) {
+      const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(base_p));
+      s16x4_t cr[kPvMfma][2];
+      auto rd = [&](auto I) __attribute__((always_inline)) {
+        constexpr int m = decltype(I)::value, s4 = m / CB, cb = m % CB;
+        constexpr int imm = 16 * s4 * kRow + 256 * (cb / 4);
+        cr[m][0] = p2_read_tr<imm>(base + to[0][cb % 4]);
+        cr[m][1] = p2_read_tr<imm>(base + to[1][cb % 4]);
+      };
+      p2_for<0, kPvAhead>(rd);
+      p2_for<0, kPvMfma>([&](auto I) __attribute__((always_inline)) {
+        constexpr int m = decltype(I)::value, s4 = m / CB, cb = m % CB;
+        if constexpr (m + kPvAhead < kPvMfma) {
+          rd(std::integral_constant<int, m + kPvAhead>{});
+          p2_wait_lgkm<2 * kPvAhead>();
+        } else {
+          p2_wait_lgkm<2 * (kPvMfma - 1 - m)>();
+        }
         p2_tie(cr[m][0]);
         p2_tie(cr[m][1]);
         oacc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat_bf16x8(cr[m][0], cr[m][1]), pb[s4], oacc[cb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mid(I);
+      });
+    };
+    auto no_mid = [](auto) {};
+
+    // qkpv(jn, bq, bp, at, mid): tile jn's QK (slots 0 .. kQkReads - 1, one K
+    // read each) and the previous tile's PV (the following slots, two C^T
+    // reads each) as one stream of MFMAs, with kInFlight LDS reads kept in
+    // flight across the boundary between the two products: at about 300 cycles
+    // of LDS latency under load, the reads in flight, not the LDS bandwidth,
+    // set the rate.  at() runs after the first MFMA (the next tile's DMAs),
+    // mid(m) after PV MFMA m (the softmax step).
+    constexpr int kSlots = kQkReads + kPvMfma, kReads = kQkReads + 2 * kPvMfma, kInFlight = 12;
+    static_assert(kInFlight < 16, "lgkmcnt range");
+    auto qkpv = [&](int jn, const lds_u8* bq_p, const lds_u8* bp_p, auto&& at,
+                    auto&& mid) __attribute__((always_inline)) {
+      const uint32_t bq = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(bq_p));
+      const uint32_t bp = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(bp_p));
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) sc[h2] = f32x16_t{};
+      sc_tile = jn;  // before the softmax step placed in the PV slots reads it
+      p2_u32x4_t kr[kQkReads];
+      s16x4_t cr[kPvMfma][2];
+      auto rd = [&](auto R) __attribute__((always_inline)) {  // read R of the stream
+        constexpr int r = decltype(R)::value;
+        if constexpr (r < kQkReads) {
+          constexpr int ks = r / 2, h2 = r % 2;
+          if constexpr (ks < KS) kr[r] = p2_read16<256 * (ks / 8) + 32 * h2 * kRow>(bq + ko[ks % 8]);
+          else kr[r] = p2_read16<32 * h2 * kPeR>(bq + po[ks - KS]);
+        } else {
+          constexpr int m = (r - kQkReads) / 2, e = (r - kQkReads) % 2, s4 = m / CB, cb = m % CB;
+          cr[m][e] = p2_read_tr<16 * s4 * kRow + 256 * (cb / 4)>(bp + to[e][cb % 4]);
+        }
+      };
+      p2_for<0, p2_min<kInFlight, kReads>()>(rd);
+      p2_for<0, kSlots>([&](auto I) __attribute__((always_inline)) {
+        constexpr int i = decltype(I)::value;
+        constexpr int done = p2_nreads<kQkReads>(i);  // reads this slot needs complete
+        constexpr int before = p2_min<(i == 0 ? 0 : p2_nreads<kQkReads>(i - 1)) + kInFlight, kReads>();
+        constexpr int upto = p2_min<done + kInFlight, kReads>();  // reads issued after this slot's issue step
+        p2_for<before, upto>(rd);
+        p2_wait_lgkm<upto - done>();
+        if constexpr (i < kQkReads) {
+          constexpr int ks = i / 2, h2 = i % 2;
+          p2_tie(kr[i]);
+          sc[h2] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kr[i]), qb[ks], sc[h2], 0, 0, 0);
+        } else {
+          constexpr int m = i - kQkReads, s4 = m / CB, cb = m % CB;
+          p2_tie(cr[m][0]);
+          p2_tie(cr[m][1]);
+          oacc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cat_bf16x8(cr[m][0], cr[m][1]), pb[s4], oacc[cb], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (i == 0) at();
+        if constexpr (i >= kQkReads) mid(std::integral_constant<int, i - kQkReads>{});
+      });
+    };
+
+    // Iteration j < n_tiles - 1 (tile j in buffer j % 3, tile j + 1 in
+    // (j + 1) % 3): wait for this wave's DMAs of tile j + 1 and meet at the
+    // barrier (tile j + 1 complete, every wave done with iteration j - 1 and so
+    // with buffer (j + 2) % 3), start tile j + 2's DMAs into that buffer (past
+    // the last tile they re-read its rows: in bounds, never read), then tile
+    // j + 1's QK and softmax step with tile j's PV in one region, then the
+    // commit.
+    auto iter = [&](int j, auto bc) __attribute__((always_inline)) {
+      constexpr int C = decltype(bc)::value;
+      using N1 = std::integral_constant<int, (C + 1) % 3>;
+      using N2 = std::integral_constant<int, (C + 2) % 3>;
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): this wave's DMAs of tile j + 1 landed
+      lds_barrier();
+      qkpv(j + 1, buf(N1{}), buf(bc), [&]() __attribute__((always_inline)) { dma_tile(j + 2, buf(N2{})); }, smax_mid);
+      commit();
+    };
+    if (n_tiles > 0) {
+      if (flushed) p2_wait_vm<kTileVm + kStores>();  // tile 0's DMAs landed
+      else p2_wait_vm<kTileVm>();
+      lds_barrier();
+      qk(0, buf(I0{}));
+      smax();
+      commit();
+      int j = 0;
+      for (; j + 3 < n_tiles; j += 3) {  // block-uniform; unrolled by three for the static buffers
+        iter(j, I0{});
+        iter(j + 1, I1{});
+        iter(j + 2, I2{});
       }
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (i == 0) at();
-      if constexpr (i >= kQkReads) mid(std::integral_constant<int, i - kQkReads>{});
-    });
-  };
-
-  // Iteration j < n_tiles - 1 (tile j in buffer j % 3, tile j + 1 in
-  // (j + 1) % 3): wait for this wave's DMAs of tile j + 1 and meet at the
-  // barrier (tile j + 1 complete, every wave done with iteration j - 1 and so
-  // with buffer (j + 2) % 3), start tile j + 2's DMAs into that buffer (past
-  // the last tile they re-read its rows: in bounds, never read), then tile
-  // j + 1's QK and softmax step with tile j's PV in one region, then the
-  // commit.
-  auto iter = [&](int j, auto bc) __attribute__((always_inline)) {
-    constexpr int C = decltype(bc)::value;
-    using N1 = std::integral_constant<int, (C + 1) % 3>;
-    using N2 = std::integral_constant<int, (C + 2) % 3>;
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): this wave's DMAs of tile j + 1 landed
-    lds_barrier();
-    qkpv(j + 1, buf(N1{}), buf(bc), [&]() __attribute__((always_inline)) { dma_tile(j + 2, buf(N2{})); }, smax_mid);
-    commit();
-  };
-  if (n_tiles > 0) {
-    if (flushed) p2_wait_vm<kTileVm + kStores>();  // tile 0's DMAs landed
-    else p2_wait_vm<kTileVm>();
-    lds_barrier();
-    qk(0, buf(I0{}));
-    smax();
-    commit();
-    int j = 0;
-    for (; j + 3 < n_tiles; j += 3) {  // block-uniform; unrolled by three for the static buffers
-      iter(j, I0{});
-      iter(j + 1, I1{});
-      iter(j + 2, I2{});
+      // the remaining one to three tiles: j .. n_tiles - 1 (tile j in buffer 0)
+      if (j + 1 < n_tiles) iter(j, I0{});
+      if (j + 2 < n_tiles) iter(j + 1, I1{});
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+      lds_barrier();
+      const int last = n_tiles - 1 - j;  // 0, 1 or 2
+      if (last == 0) pv(buf(I0{}), no_mid);
+      else if (last == 1) pv(buf(I1{}), no_mid);
+      else pv(buf(I2{}), no_mid);
     }
-    // the remaining one to three tiles: j .. n_tiles - 1 (tile j in buffer 0)
-    if (j + 1 < n_tiles) iter(j, I0{});
-    if (j + 2 < n_tiles) iter(j + 1, I1{});
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
-    lds_barrier();
-    const int last = n_tiles - 1 - j;  // 0, 1 or 2
-    if (last == 0) pv(buf(I0{}), no_mid);
-    else if (last == 1) pv(buf(I1{}), no_mid);
-    else pv(buf(I2{}), no_mid);
-  }
 
-  if (n_tiles == 0) p2_wait_vm<0>();  // the unused tile copies land before the buffers are reused
-  // The output, stored at the next item's start (or after the last item):
-  // lane (n, hf) holds channels 32 cb + 8 r4 + 4 hf + {0..3} of its column.
-  // A surplus column repeats the block's last query, so its values equal
-  // that query's, and it stores them to that query's row.
-  const float l_w = l_part + shfl_xor_f32(l_part, 32);
-  const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
+    if (n_tiles == 0) p2_wait_vm<0>();  // the unused tile copies land before the buffers are reused
+    // The output, stored at the next item's start (or after the last item):
+    // lane (n, hf) holds channels 32 cb + 8 r4 + 4 hf + {0..3} of its column.
+    // A surplus column repeats the block's last query, so its values equal
+    // that query's, and it stores them to that query's row.
+    const float l_w = l_part + shfl_xor_f32(l_part, 32);
+    const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb)
+    for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      pend[cb][r4][0] = pack_bf16x2(oacc[cb][4 * r4] * inv, oacc[cb][4 * r4 + 1] * inv);
-      pend[cb][r4][1] = pack_bf16x2(oacc[cb][4 * r4 + 2] * inv, oacc[cb][4 * r4 + 3] * inv);
-    }
-  pend_op = static_cast<uint16_t*>(a.o_lat) + rq * a.o_rs + head * a.o_hs + 4 * hf;
-  pending = true;
-  // every wave is done with the LDS buffers before the next item's DMAs
-  __syncthreads();
+      for (int r4 = 0; r4 < 4; ++r4) {
+        pend[cb][r4][0] = pack_bf16x2(oacc[cb][4 * r4] * inv, oacc[cb][4 * r4 + 1] * inv);
+        pend[cb][r4][1] = pack_bf16x2(oacc[cb][4 * r4 + 2] * inv, oacc[cb][4 * r4 + 3] * inv);
+      }
+    pend_op = static_cast<uint16_t*>(a.o_lat) + rq * a.o_rs + head * a.o_hs + 4 * hf;
+    pending = true;
+    // every wave is done with the LDS buffers before the next item's DMAs
+    __syncthreads();
   }
   if (pending) flush();
 }
