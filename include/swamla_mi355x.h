@@ -20,7 +20,12 @@
  *                      (latent c_kv only; k_pe stays in the model dtype)
  *
  * Geometry of this build: heads H = 16, qk_rope_head_dim P = 64 and any
- * kv_lora_rank 1 <= R <= 512 (the real model scales the rank per layer).
+ * kv_lora_rank 1 <= R <= 1024 (the real model scales the rank per layer,
+ * models/swa_mla_model.py:216-247, up to twice its base).  mla_append,
+ * mla_merge, mla_decode_attn and mla_decode_attn_noalloc take every such
+ * rank (decode attention above 512 runs a VALU kernel);
+ * mla_decode_attn_append, mla_merge_project and the measurement probes take
+ * R <= 512, mla_prefill_attn R <= 256.
  * mla_decode_attn, mla_decode_attn_append, mla_merge and mla_merge_project
  * also take H = 32 in one launch for a bf16 model with R_pad <= 256 (the
  * reference's xl preset, models/swa_mla_model.py:618-640: each decode wave

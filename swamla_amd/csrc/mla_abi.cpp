@@ -32,12 +32,14 @@ int ok() {
 
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
-// allow32: the entry point also runs 32 heads in one launch.
+// allow32: the entry point also runs 32 heads in one launch.  Ranks above
+// 64 kMaxNB are built for the append, the merge and the decode attention
+// (VALU kernel); the other entry points return UNSUPPORTED for them.
 int check_geometry(int32_t H, int32_t R, int32_t P, bool allow32 = false) {
-  if ((H != 16 && !(allow32 && H == 32)) || P != 64 || R < 1 || R > 64 * swamla::kMaxNB)
+  if ((H != 16 && !(allow32 && H == 32)) || P != 64 || R < 1 || R > 64 * swamla::kMaxNBWide)
     return fail(SWAMLA_ERR_UNSUPPORTED,
                 "unsupported geometry H=%d R=%d P=%d (this build: H=16%s, P=64, 1 <= R <= %d)", H, R, P,
-                allow32 ? " or 32" : "", 64 * swamla::kMaxNB);
+                allow32 ? " or 32" : "", 64 * swamla::kMaxNBWide);
   return SWAMLA_OK;
 }
 
@@ -175,7 +177,7 @@ int mla_append(const void* kv_in, int64_t in_row_stride, int32_t n_tok, const in
                        cos_tab,  sin_tab,       rope_len,  ckv_cache,   kpe_cache, ckv_scale,
                        cache_batch, cache_seq,  err_flag};
   const int rc = swamla::launch_append(a, in_dtype, cache_dtype, static_cast<hipStream_t>(stream));
-  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_append: no kernel for this dtype pair");
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_append: no kernel for this dtype pair and rank");
   if (rc != 0) return hip_fail("mla_append");
   return ok();
 }
@@ -281,7 +283,7 @@ int mla_decode_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, const
                            dtype, cache_dtype, &a, 65535, true))
     return e;
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
-  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_attn: no kernel for this dtype pair");
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_decode_attn: no kernel for this dtype pair, head count and rank");
   if (rc != 0) return hip_fail("mla_decode_attn");
   return ok();
 }
@@ -326,7 +328,7 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride, const void*
                             cos_tab, sin_tab,       rope_len,    ckv_cache, kpe_cache, ckv_scale,
                             cache_batch, cache_seq, err_flag};
   const int rc = swamla::launch_decode(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
-  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair", fn);
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair, head count and rank", fn);
   if (rc != 0) return hip_fail(fn);
   return ok();
 }
@@ -376,7 +378,7 @@ int mla_decode_attn_noalloc(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_h
   a.plan = plan;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   int rc = swamla::launch_decode(a, dtype, cache_dtype, st);
-  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair", fn);
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair, head count and rank", fn);
   if (rc != 0) return hip_fail(fn);
   if (n_splits == 1 || n_rows == 0) return ok();
   // every partial the merge reads was written by the launch above
@@ -411,7 +413,7 @@ int mla_prefill_attn(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_hs, cons
   if (n_rows / tokens_per_seq > 65535)
     return fail(SWAMLA_ERR_INVALID_ARG, "%s: %d sequences exceed 65535", fn, n_rows / tokens_per_seq);
   const int rc = swamla::launch_prefill(a, dtype, cache_dtype, static_cast<hipStream_t>(stream));
-  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair", fn);
+  if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair, head count and rank", fn);
   if (rc != 0) return hip_fail(fn);
   return ok();
 }
@@ -519,6 +521,8 @@ int mla_merge_project(const float* o_part, const float* lse_part, const void* o_
                       int32_t Dv,
                       void* y, int64_t y_rs, int64_t y_hs, int32_t dtype, void* stream) {
   if (int e = check_geometry(H, R, 64, true)) return e;
+  if (swamla::padded_rank(R) > 64 * swamla::kMaxNB)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge_project: kv_lora_rank %d (built up to %d)", R, 64 * swamla::kMaxNB);
   if (dtype != SWAMLA_DTYPE_BF16)
     return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge_project: dtype %d not built (bf16 only)", dtype);
   if (Dv != 128) return fail(SWAMLA_ERR_UNSUPPORTED, "mla_merge_project: Dv=%d (this build: 128)", Dv);
@@ -618,6 +622,8 @@ int mla_probe_cache_stream(const void* ckv_cache, const void* kpe_cache, const f
                            void* stream) {
   const char* fn = "mla_probe_cache_stream";
   if (int e = check_geometry(16, R, 64)) return e;
+  if (swamla::padded_rank(R) > 64 * swamla::kMaxNB)
+    return fail(SWAMLA_ERR_UNSUPPORTED, "%s: kv_lora_rank %d (built up to %d)", fn, R, 64 * swamla::kMaxNB);
   if (cache_dtype != SWAMLA_DTYPE_BF16 && cache_dtype != SWAMLA_DTYPE_FP8)
     return fail(SWAMLA_ERR_UNSUPPORTED, "%s: cache dtype %d (bf16 or fp8 caches of a bf16 model)", fn, cache_dtype);
   if (!ckv_cache || !kpe_cache || !start_pos || !sink || (cache_dtype == SWAMLA_DTYPE_FP8 && !ckv_scale))

@@ -7,7 +7,10 @@
 
 namespace swamla {
 
-constexpr int kMaxNB = 8;  // latent rows of at most 64 kMaxNB = 512 channels (kv_lora_rank)
+constexpr int kMaxNB = 8;  // latent rows of at most 64 kMaxNB = 512 channels for the MFMA kernels
+// Ranks up to 64 kMaxNBWide = 1024 channels: the append, the merge and the
+// wide-rank decode kernel (mla_decode_vec).
+constexpr int kMaxNBWide = 16;
 
 // Padded latent width of a rank: R_pad = 64 ceil(R / 64).
 inline constexpr int padded_rank(int R) { return 64 * ((R + 63) / 64); }

@@ -43,8 +43,8 @@
 
 namespace swamla {
 
-int launch_decode_f32(const DecodeArgs& a, hipStream_t s);
-int decode_f32_blocks_per_cu(int R, int* blocks);
+int launch_decode_vec(const DecodeArgs& a, int dt, int c_dt, hipStream_t s);
+int decode_vec_blocks_per_cu(int dt, int c_dt, int R, int* blocks);
 
 namespace {
 
@@ -825,9 +825,10 @@ const void* decode_kernel(int c_dt, bool fuse, int hg) {
 
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
-  if (dt == 0) {
-    if (c_dt != 0 || a.fa.kv_in != nullptr || a.H != kH) return -1;
-    return launch_decode_f32(a, s);
+  if (dt == 0 || padded_rank(a.R) > 64 * kMaxNB) {
+    // the VALU kernel: fp32 models, and ranks above the MFMA kernel's
+    if (a.fa.kv_in != nullptr || a.H != kH) return -1;
+    return launch_decode_vec(a, dt, c_dt, s);
   }
   if (dt != 1 || a.H % kH != 0) return -1;
   const int hg = a.H / kH;
@@ -862,7 +863,7 @@ int launch_stream_probe(const DecodeArgs& a, int c_dt, uint32_t* sink, hipStream
 // Workgroups of a decode launch one CU holds at once: the MFMA kernel takes a
 // whole CU (its LDS ring), the fp32 kernel's own count.
 int decode_blocks_per_cu(int dt, int c_dt, int R, bool fuse, int* blocks) {
-  if (dt == 0) return (c_dt == 0 && !fuse) ? decode_f32_blocks_per_cu(R, blocks) : -1;
+  if (dt == 0 || padded_rank(R) > 64 * kMaxNB) return fuse ? -1 : decode_vec_blocks_per_cu(dt, c_dt, R, blocks);
   if (dt != 1) return -1;
   return with_nb(R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value;

@@ -289,7 +289,7 @@ __device__ __forceinline__ LnStats aten_ln_stats(const LnRow& x, int R, float ep
 #pragma clang fp contract(off)
   constexpr int V = IN_DT == 1 ? 16 : 8;         // values per input vector
   constexpr int HV = V / 8;                       // 8-lane float vectors per input vector
-  constexpr int kMaxChunks = G == 16 ? 16 / (8 * HV) : (IN_DT == 1 ? 2 : 4);  // R <= 512 (G = 64)
+  constexpr int kMaxChunks = G == 16 ? 16 / (8 * HV) : (IN_DT == 1 ? 4 : 8);  // R <= 1024 (G = 64)
   const int gbase = lane & ~(G - 1);
   const int n = R / V;
   const int chunks = (n + 15) >> 4;
@@ -308,11 +308,19 @@ __device__ __forceinline__ LnStats aten_ln_stats(const LnRow& x, int R, float ep
       s2 = __builtin_fmaf(d, xv - s1, s2);
     }
   }
-  // --- stack merges (lane k = lane % 8 keeps lane k's accumulators)
+  // --- stack merges (lane k = lane % 8 keeps lane k's accumulators): a
+  // binary counter over the chunks, depth ceil(log2(chunks)) (at least 1)
   const int k = lane & 7;
-  const int depth = chunks <= 2 ? 1 : 2;
-  int c0 = 0, c1 = 0;
-  float a1 = 0.f, a2 = 0.f, b1 = 0.f, b2 = 0.f;
+  constexpr int kMaxDepth = kMaxChunks <= 2 ? 1 : (kMaxChunks <= 4 ? 2 : 3);
+  const int depth = chunks <= 2 ? 1 : (chunks <= 4 ? 2 : 3);
+  int sc_[kMaxDepth];
+  float s1_[kMaxDepth], s2_[kMaxDepth];
+#pragma unroll
+  for (int j = 0; j < kMaxDepth; ++j) {
+    sc_[j] = 0;
+    s1_[j] = 0.f;
+    s2_[j] = 0.f;
+  }
 #pragma unroll
   for (int i = 0; i < kMaxChunks; ++i) {
     if (i < chunks) {  // uniform
@@ -320,17 +328,28 @@ __device__ __forceinline__ LnStats aten_ln_stats(const LnRow& x, int R, float ep
 #pragma unroll
       for (int h = 0; h < HV; ++h) {
         const int src = (i * HV + h) * 8 + k;
-        ln_stack_merge(ci, __shfl(s1, gbase + src, 64), __shfl(s2, gbase + src, 64), c0, a1, a2);
+        ln_stack_merge(ci, __shfl(s1, gbase + src, 64), __shfl(s2, gbase + src, 64), sc_[0], s1_[0], s2_[0]);
       }
-      if (depth == 2 && ((i + 1) & 1) == 0) {
-        ln_stack_merge(c0, a1, a2, c1, b1, b2);
-        c0 = 0;
-        a1 = 0.f;
-        a2 = 0.f;
+      // carry: level j - 1 moves into level j while the counter's low bits are zero
+      int carry = i + 1;
+      bool go = true;
+#pragma unroll
+      for (int j = 1; j < kMaxDepth; ++j) {
+        go = go && j < depth && (carry & 1) == 0;
+        if (go) {
+          ln_stack_merge(sc_[j - 1], s1_[j - 1], s2_[j - 1], sc_[j], s1_[j], s2_[j]);
+          sc_[j - 1] = 0;
+          s1_[j - 1] = 0.f;
+          s2_[j - 1] = 0.f;
+        }
+        carry >>= 1;
       }
     }
   }
-  if (depth == 2) ln_stack_merge(c1, b1, b2, c0, a1, a2);
+#pragma unroll
+  for (int j = 1; j < kMaxDepth; ++j)
+    if (j < depth) ln_stack_merge(sc_[j], s1_[j], s2_[j], sc_[0], s1_[0], s2_[0]);
+  const float a1 = s1_[0], a2 = s2_[0];
   // --- scalar tail, then the 8 lanes (values uniform across the wave)
   int cnt = 0;
   float m1 = 0.f, m2 = 0.f;

@@ -201,11 +201,16 @@ __global__ __launch_bounds__(256) void mla_append_g16_kernel(AppendArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2 (fp32 models): the same maths on the VALU in fp32.  One block of
-// 256 threads per (row, split); 16-token tiles staged in LDS.
+// Kernel 2 on the VALU in fp32: fp32 models (any rank), and bf16 models at
+// ranks above the MFMA kernel's 512 (up to 1024).  One block of 256 threads
+// per (row, split); 16-token tiles staged in LDS as fp32 (bf16 values
+// widened, e4m3 codes times the token's scale).  DT: model dtype (queries,
+// RoPE tables, k_pe cache, output: 0 fp32 / 1 bf16, whose q_pe rotation
+// rounds every product and sum to bf16 as the MFMA kernels' does); C_DT:
+// latent cache (0 fp32 / 1 bf16 / 2 e4m3).
 // ---------------------------------------------------------------------------
-template <int NB>
-__global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
+template <int DT, int C_DT, int NB>
+__global__ __launch_bounds__(256) void mla_decode_vec(DecodeArgs a) {
   constexpr int TT = 16;
   constexpr int RP = 64 * NB, KC = RP + kP;  // channels scored per cached token
   constexpr int CPV = RP / 16;               // output channels per thread
@@ -243,18 +248,21 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
 
   int rp = ra.rope;
   rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
-  const float* qa = static_cast<const float*>(a.q_abs) + r * a.qa_rs;
-  const float* qp = static_cast<const float*>(a.q_pe) + r * a.qp_rs;
-  const float* ct = static_cast<const float*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
-  const float* st = static_cast<const float*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
+  using E = Elem<DT>;
+  using T = typename E::T;
+  const T* qa = static_cast<const T*>(a.q_abs) + r * a.qa_rs;
+  const T* qp = static_cast<const T*>(a.q_pe) + r * a.qp_rs;
+  const T* ct = static_cast<const T*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2);
+  const T* st = static_cast<const T*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2);
   for (int i = t; i < kH * RP; i += 256) {
     const int h = i / RP, c = i % RP;
-    q_s[h][c] = c < a.R ? qa[h * a.qa_hs + c] : 0.f;  // the padding channels are zero
+    q_s[h][c] = c < a.R ? E::ld(qa, h * a.qa_hs + c) : 0.f;  // the padding channels are zero
   }
   for (int i = t; i < kH * kP / 2; i += 256) {
     const int h = i / (kP / 2), pi = i % (kP / 2);
     float o1, o2;
-    rope_pair<0>(qp[h * a.qp_hs + 2 * pi], qp[h * a.qp_hs + 2 * pi + 1], ct[pi], st[pi], o1, o2);
+    rope_pair<DT>(E::ld(qp, h * a.qp_hs + 2 * pi), E::ld(qp, h * a.qp_hs + 2 * pi + 1), E::ld(ct, pi), E::ld(st, pi),
+                  o1, o2);
     q_s[h][RP + 2 * pi] = o1;
     q_s[h][RP + 2 * pi + 1] = o2;
   }
@@ -267,15 +275,19 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
 #pragma unroll
   for (int j = 0; j < CPV; ++j) o[j] = 0.f;
 
-  const float* ckv = static_cast<const float*>(a.ckv);
-  const float* kpe = static_cast<const float*>(a.kpe);
+  const T* kpe = static_cast<const T*>(a.kpe);
+  auto latent = [&](int64_t row, int c) -> float {
+    if constexpr (C_DT == 0) return static_cast<const float*>(a.ckv)[row * RP + c];
+    else if constexpr (C_DT == 1) return bf16_to_f32(static_cast<const uint16_t*>(a.ckv)[row * RP + c]);
+    else return e4m3_to_f32(static_cast<const uint8_t*>(a.ckv)[row * RP + c]) * a.ckv_scale[row];
+  };
   for (int base = t0; base < t1; base += TT) {
     __syncthreads();
     for (int i = t; i < TT * KC; i += 256) {
       const int j = i / KC, c = i % KC;
       const int tok = base + j;
       float v = 0.f;
-      if (tok < t1) v = c < RP ? ckv[(row0 + tok) * RP + c] : kpe[(row0 + tok) * kP + (c - RP)];
+      if (tok < t1) v = c < RP ? latent(row0 + tok, c) : E::ld(kpe, (row0 + tok) * kP + (c - RP));
       k_s[j][c] = v;
     }
     __syncthreads();
@@ -315,9 +327,9 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
   const float Lh = l_s[h_pv];
   const float inv = Lh > 0.f ? 1.f / Lh : 0.f;
   if (ns <= 1) {
-    float* op = static_cast<float*>(a.o_lat) + r * a.o_rs + h_pv * a.o_hs + c_pv;
+    T* op = static_cast<T*>(a.o_lat) + r * a.o_rs + h_pv * a.o_hs + c_pv;
 #pragma unroll
-    for (int jj = 0; jj < CPV; ++jj) op[jj] = o[jj] * inv;
+    for (int jj = 0; jj < CPV; ++jj) op[jj] = E::from_f32(o[jj] * inv);
     if (a.lse_out && (t & 15) == 0)
       a.lse_out[static_cast<int64_t>(r) * kH + h_pv] = (Lh > 0.f) ? (m_s[h_pv] + __log2f(Lh)) * kLn2 : -INFINITY;
     return;
@@ -346,8 +358,10 @@ __global__ __launch_bounds__(256) void mla_decode_f32(DecodeArgs a) {
 // (lse -inf) has weight 0; rows of at most one split were written by the
 // decode kernel itself.
 // ---------------------------------------------------------------------------
-template <int DT, bool TWO>
+template <int DT, int CH>
 __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
+  // CH chunks of 256 channels (R_pad <= 256 CH): lane l reads channels 4 l ..
+  // 4 l + 3 of each
   const int h = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
   const int rp = 64 * ((a.R + 63) / 64);
   const int64_t base = static_cast<int64_t>(r) * a.n_splits * a.H + h;  // (row, split 0, head) slot
@@ -355,19 +369,22 @@ __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
   const int L = clamped_row_len(a.ad, r, a.cache_b, a.cache_s);
   const int last = a.n_splits - 1;
   const float le = a.lse_part[base + static_cast<int64_t>(min(lane, last)) * a.H];
-  const int c0 = 4 * lane, c1 = c0 + 256;
-  const bool on0 = c0 < rp, on1 = c1 < rp;
   // channels read: a lane past the row re-reads channel 0 (its sums are not stored)
-  const int c0r = on0 ? c0 : 0, c1r = on1 ? c1 : 0;
+  int cr_[CH];
+  bool on_[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    on_[k] = 4 * lane + 256 * k < rp;
+    cr_[k] = on_[k] ? 4 * lane + 256 * k : 0;
+  }
   const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 v[8], u[8];
+  float4 v[CH][8];
   auto load_group = [&](int g, int s_max) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float* p = a.o_part + (base + static_cast<int64_t>(min(g + j, s_max)) * a.H) * rp;
-      v[j] = *reinterpret_cast<const float4*>(p + c0r);
-      u[j] = z;
-      if constexpr (TWO) u[j] = *reinterpret_cast<const float4*>(p + c1r);
+#pragma unroll
+      for (int k = 0; k < CH; ++k) v[k][j] = *reinterpret_cast<const float4*>(p + cr_[k]);
     }
   };
   load_group(0, last);
@@ -391,7 +408,9 @@ __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
   tot = lane_group_sum<64>(tot);
   const float inv = tot > 0.f ? 1.f / tot : 0.f;
 
-  float4 a0 = z, a1 = z;
+  float4 acc[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) acc[k] = z;
   float wl = w0;  // weight of split (g & ~63) + lane
   for (int g = 0; g < ns; g += 8) {
     if (g > 0) {
@@ -406,33 +425,31 @@ __global__ __launch_bounds__(64) void mla_merge_kernel(MergeArgs a) {
       const bool in = g + j < ns;  // uniform
       const float wj = u2f(__builtin_amdgcn_readlane(f2u(wl), (g & 63) + j));
       if (in) {
-        a0.x += wj * v[j].x;
-        a0.y += wj * v[j].y;
-        a0.z += wj * v[j].z;
-        a0.w += wj * v[j].w;
-        if constexpr (TWO) {
-          a1.x += wj * u[j].x;
-          a1.y += wj * u[j].y;
-          a1.z += wj * u[j].z;
-          a1.w += wj * u[j].w;
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          acc[k].x += wj * v[k][j].x;
+          acc[k].y += wj * v[k][j].y;
+          acc[k].z += wj * v[k][j].z;
+          acc[k].w += wj * v[k][j].w;
         }
       }
     }
   }
-  auto store = [&](int c, const float4& acc) {
+  auto store = [&](int c, const float4& ac) {
     if constexpr (DT == 0) {
       float* op = static_cast<float*>(a.o_lat) + r * a.o_rs + h * a.o_hs;
-      *reinterpret_cast<float4*>(op + c) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+      *reinterpret_cast<float4*>(op + c) = make_float4(ac.x * inv, ac.y * inv, ac.z * inv, ac.w * inv);
     } else {
       uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + h * a.o_hs;
       uint2 pk;
-      pk.x = f32_to_bf16(acc.x * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.y * inv)) << 16);
-      pk.y = f32_to_bf16(acc.z * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.w * inv)) << 16);
+      pk.x = f32_to_bf16(ac.x * inv) | (static_cast<uint32_t>(f32_to_bf16(ac.y * inv)) << 16);
+      pk.y = f32_to_bf16(ac.z * inv) | (static_cast<uint32_t>(f32_to_bf16(ac.w * inv)) << 16);
       *reinterpret_cast<uint2*>(op + c) = pk;
     }
   };
-  if (on0) store(c0, a0);
-  if (TWO && on1) store(c1, a1);
+#pragma unroll
+  for (int k = 0; k < CH; ++k)
+    if (on_[k]) store(4 * lane + 256 * k, acc[k]);
   if (a.lse_out && lane == 0) a.lse_out[static_cast<int64_t>(r) * a.H + h] = M + __logf(tot);
 }
 
@@ -463,7 +480,7 @@ int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s) {
     }
     return hipGetLastError() == hipSuccess ? 0 : -2;
   }
-  const int rc = with_nb(a.R, [&](auto nb) {
+  const int rc = with_nb_wide(a.R, [&](auto nb) {
     constexpr int NB = decltype(nb)::value;
     if (in_dt == 1 && c_dt == 1) hipLaunchKernelGGL((mla_append_kernel<1, 1, NB>), grid, block, 0, s, a);
     else if (in_dt == 1 && c_dt == 2) hipLaunchKernelGGL((mla_append_kernel<1, 2, NB>), grid, block, 0, s, a);
@@ -477,25 +494,40 @@ int launch_append(const AppendArgs& a, int in_dt, int c_dt, hipStream_t s) {
 
 // The fp32 decode kernel (fp32 models); the MFMA kernel's launcher in
 // mla_decode.hip dispatches here for them.
-int launch_decode_f32(const DecodeArgs& a, hipStream_t s) {
+namespace {
+// The VALU decode instance: fp32 models with an fp32 cache at any rank; bf16
+// models with a bf16 or e4m3 cache at ranks above kMaxNB (the MFMA kernel
+// takes the others).
+template <int NB>
+const void* decode_vec_kernel(int dt, int c_dt) {
+  if (dt == 0 && c_dt == 0) return reinterpret_cast<const void*>(&mla_decode_vec<0, 0, NB>);
+  if constexpr (NB > kMaxNB) {
+    if (dt == 1 && c_dt == 1) return reinterpret_cast<const void*>(&mla_decode_vec<1, 1, NB>);
+    if (dt == 1 && c_dt == 2) return reinterpret_cast<const void*>(&mla_decode_vec<1, 2, NB>);
+  }
+  return nullptr;
+}
+}  // namespace
+
+int launch_decode_vec(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   const dim3 grid = a.balance > 0 ? dim3(a.balance, 1) : dim3(a.n_splits, a.n_rows);
-  const int rc = with_nb(a.R, [&](auto nb) {
-    constexpr int NB = decltype(nb)::value;
-    hipLaunchKernelGGL((mla_decode_f32<NB>), grid, dim3(256), 0, s, a);
-    return 0;
+  const int rc = with_nb_wide(a.R, [&](auto nb) {
+    const void* fn = decode_vec_kernel<decltype(nb)::value>(dt, c_dt);
+    if (!fn) return -1;
+    void* args[] = {const_cast<DecodeArgs*>(&a)};
+    return hipLaunchKernel(fn, grid, dim3(256), args, 0, s) == hipSuccess ? 0 : -2;
   });
   if (rc != 0) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-int decode_f32_blocks_per_cu(int R, int* blocks) {
-  return with_nb(R, [&](auto nb) {
-    constexpr int NB = decltype(nb)::value;
+int decode_vec_blocks_per_cu(int dt, int c_dt, int R, int* blocks) {
+  return with_nb_wide(R, [&](auto nb) {
+    const void* fn = decode_vec_kernel<decltype(nb)::value>(dt, c_dt);
+    if (!fn) return -1;
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&mla_decode_f32<NB>), 256,
-                                                     0) != hipSuccess || n < 1)
-      return -2;
-    *blocks = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, 0) != hipSuccess || n < 1) return -2;
+    *blocks = 1;  // the split plan deals one block per CU
     return 0;
   });
 }
@@ -503,12 +535,20 @@ int decode_f32_blocks_per_cu(int R, int* blocks) {
 int launch_merge(const MergeArgs& a, int dt, hipStream_t s) {
   if (a.n_rows == 0 || a.n_splits <= 1) return 0;
   const dim3 grid(a.H, a.n_rows), block(64);
-  const bool two = a.R > 256;  // the padded row spans a second 256-channel chunk
-  if (dt == 1 && two) hipLaunchKernelGGL((mla_merge_kernel<1, true>), grid, block, 0, s, a);
-  else if (dt == 1) hipLaunchKernelGGL((mla_merge_kernel<1, false>), grid, block, 0, s, a);
-  else if (dt == 0 && two) hipLaunchKernelGGL((mla_merge_kernel<0, true>), grid, block, 0, s, a);
-  else if (dt == 0) hipLaunchKernelGGL((mla_merge_kernel<0, false>), grid, block, 0, s, a);
-  else return -1;
+  const int ch = (padded_rank(a.R) + 255) / 256;  // 256-channel chunks of the padded row
+  if (dt != 0 && dt != 1) return -1;
+  if (ch == 1) {
+    if (dt == 1) hipLaunchKernelGGL((mla_merge_kernel<1, 1>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((mla_merge_kernel<0, 1>), grid, block, 0, s, a);
+  } else if (ch == 2) {
+    if (dt == 1) hipLaunchKernelGGL((mla_merge_kernel<1, 2>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((mla_merge_kernel<0, 2>), grid, block, 0, s, a);
+  } else if (ch <= 4) {
+    if (dt == 1) hipLaunchKernelGGL((mla_merge_kernel<1, 4>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((mla_merge_kernel<0, 4>), grid, block, 0, s, a);
+  } else {
+    return -1;
+  }
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

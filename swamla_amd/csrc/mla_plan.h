@@ -296,4 +296,23 @@ int with_nb(int R, F&& f) {
   }
 }
 
+// with_nb over NB = 1..kMaxNBWide (ranks up to 1024), for the kernels built
+// that wide.
+template <typename F>
+int with_nb_wide(int R, F&& f) {
+  const int nb = (R + 63) / 64;
+  if (nb <= kMaxNB) return with_nb(R, f);
+  switch (nb) {
+    case 9: return f(std::integral_constant<int, 9>{});
+    case 10: return f(std::integral_constant<int, 10>{});
+    case 11: return f(std::integral_constant<int, 11>{});
+    case 12: return f(std::integral_constant<int, 12>{});
+    case 13: return f(std::integral_constant<int, 13>{});
+    case 14: return f(std::integral_constant<int, 14>{});
+    case 15: return f(std::integral_constant<int, 15>{});
+    case 16: return f(std::integral_constant<int, 16>{});
+    default: return -1;
+  }
+}
+
 }  // namespace swamla

@@ -20,7 +20,8 @@ R, P, H = 256, 64, 16  # R: the default kv_lora_rank (any 1..MAX_RANK is built)
 # Heads one decode launch takes: 16, or 32 for a bf16 model with R_pad <= 256
 # (each wave serves two head groups from one stream of the cache).
 DECODE_HEADS = (16, 32)
-MAX_RANK = 512
+MAX_RANK = 1024  # the append, the merge and decode attention (the VALU kernel above MFMA_MAX_RANK)
+MFMA_MAX_RANK = 512  # the MFMA decode kernel, the fused decode step, merge_project and the stream probe
 
 
 def padded_rank(rank: int) -> int:

@@ -546,14 +546,15 @@ class MLA(nn.Module):
 
     def _fused_step_ok(self, x: torch.Tensor, n: int) -> bool:
         """The decode-step kernels cover bf16 modules with up to 16 heads (or
-        32, in one launch), at most 128 query rows and 128-aligned model
-        widths; a q low-rank module runs its query through two products with
-        q_norm between them."""
+        32, in one launch), kv_lora_rank up to 512, at most 128 query rows and
+        128-aligned model widths; a q low-rank module runs its query through
+        two products with q_norm between them."""
         wq = self.wq if self.q_lora_rank == 0 else self.wq_a
         q_bias = (wq.bias is not None) if self.q_lora_rank == 0 else (
             (self.wq_a.bias is not None) and (self.wq_b.bias is not None))
         return (
             self._fused_heads() is not None
+            and self.rank_pad <= kernels.MFMA_MAX_RANK
             and x.dtype == torch.bfloat16
             and wq.weight.dtype == torch.bfloat16
             and 0 < n <= kernels.LINEAR_MAX_ROWS
@@ -589,7 +590,8 @@ class MLA(nn.Module):
         if self.split_plan not in ("auto", "static", "balanced"):
             raise ValueError(f"split_plan must be 'auto', 'static' or 'balanced', got {self.split_plan!r}")
         dt = dtype if dtype is not None else self.wkv_a.weight.dtype
-        bpc = kernels.decode_blocks_per_cu(dt, self.fp8_cache, self.kv_lora_rank, dt == torch.bfloat16, device)
+        fused = dt == torch.bfloat16 and self.rank_pad <= kernels.MFMA_MAX_RANK
+        bpc = kernels.decode_blocks_per_cu(dt, self.fp8_cache, self.kv_lora_rank, fused, device)
         n_splits, min_chunk = self._split_plan(n_rows, max_len, device, bpc)
         if self.split_plan == "balanced" or (self.split_plan == "auto" and per_row_positions):
             bal, cap = kernels.balanced_splits(n_rows, self._num_cus, bpc)

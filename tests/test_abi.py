@@ -59,7 +59,7 @@ def _decode(lib, **kw):
 @pytest.mark.parametrize(
     "kw,code",
     [
-        (dict(R=513), -2),  # kv_lora_rank 1..512
+        (dict(R=1025), -2),  # kv_lora_rank 1..1024
         (dict(R=0), -2),
         (dict(P=32), -2),
         (dict(in_dt=0, c_dt=1), -2),
@@ -94,7 +94,7 @@ def test_append_zero_tokens_is_a_noop(lib):
     "kw,code",
     [
         (dict(H=8), -2),
-        (dict(R=520), -2),
+        (dict(R=1040), -2),
         (dict(dt=1, c_dt=0), -2),
         (dict(n_rows=70000), -1),
         (dict(ns=0), -1),
@@ -211,7 +211,7 @@ def _merge(lib, **kw):
 
 def test_merge_rejects_and_noop(lib):
     assert _merge(lib, ns=1) == 0
-    assert _merge(lib, R=1024) == -2
+    assert _merge(lib, R=1025) == -2
     assert _merge(lib, o_part=None) == -1
     assert _merge(lib, dt=2) == -2
     assert _merge(lib, o_part=FAKE + 4) == -3
@@ -324,8 +324,8 @@ def test_merge_project_single_split_needs_no_partials(lib):
 
 
 def test_python_check_raises_with_message(lib):
-    rc = _append(lib, R=640)
-    with pytest.raises(_abi.SwamlaError, match="UNSUPPORTED.*R=640"):
+    rc = _append(lib, R=1088)
+    with pytest.raises(_abi.SwamlaError, match="UNSUPPORTED.*R=1088"):
         _abi.check(rc)
     with pytest.raises(RuntimeError):
         _abi.check(rc)
@@ -455,7 +455,7 @@ def test_decode_blocks_per_cu_rejects(lib):
     """Argument checks come before any HIP call."""
     bf, f32, fp8 = _abi.DTYPE_BF16, _abi.DTYPE_F32, _abi.DTYPE_FP8
     assert lib.mla_decode_blocks_per_cu(bf, bf, 0, 0) == -2
-    assert lib.mla_decode_blocks_per_cu(bf, bf, 513, 0) == -2
+    assert lib.mla_decode_blocks_per_cu(bf, bf, 1025, 0) == -2
     assert lib.mla_decode_blocks_per_cu(f32, fp8, 256, 0) == -2
     assert lib.mla_decode_blocks_per_cu(fp8, fp8, 256, 0) == -2
     assert lib.mla_decode_blocks_per_cu(bf, bf, 256, 2) == -1

@@ -124,11 +124,12 @@ def test_append_bit_exact(gpu, dtype, fp8):
     _append_case(gpu, dtype, fp8)
 
 
-@pytest.mark.parametrize("rank", [1, 64, 100, 128, 173, 200, 320, 384, 449, 512])
+@pytest.mark.parametrize("rank", [1, 64, 100, 128, 173, 200, 320, 384, 449, 512, 600, 777, 1000, 1024])
 @pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.float32, False), (torch.bfloat16, True)])
 def test_append_bit_exact_any_rank(gpu, dtype, fp8, rank):
-    """kv_lora_rank other than 256 (the real model scales it per layer): rows
-    padded to a multiple of 64 channels, the padding written as zeros."""
+    """kv_lora_rank other than 256 (the real model scales it per layer, up to
+    1024 from SWAMLAConfig's base of 512): rows padded to a multiple of 64
+    channels, the padding written as zeros."""
     _append_case(gpu, dtype, fp8, rank=rank, seed=rank)
 
 
@@ -217,11 +218,12 @@ def test_decode_short_rows(gpu, dtype, fp8):
     _decode_case(gpu, dtype, fp8, [130, 1, 63, 65], 4, 64, seed=2, **tol)
 
 
-@pytest.mark.parametrize("rank", [1, 64, 100, 128, 173, 200, 320, 384, 449, 512])
+@pytest.mark.parametrize("rank", [1, 64, 100, 128, 173, 200, 320, 384, 449, 512, 600, 777, 1024])
 @pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.bfloat16, True), (torch.float32, False)])
 def test_decode_any_rank(gpu, dtype, fp8, rank):
     """kv_lora_rank other than 256: one split, split-KV with the merge, and
-    the balanced plan; the query padding is ignored and the output padding 0."""
+    the balanced plan; the query padding is ignored and the output padding 0.
+    Ranks above 512 run the VALU decode kernel and the four-chunk merge."""
     tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else {}
     _decode_case(gpu, dtype, fp8, [1, 70, 300], 1, 256, seed=rank, rank=rank, **tol)
     _decode_case(gpu, dtype, fp8, [1000, 1, 513, 2100], 8, 64, seed=rank + 1, rank=rank, **tol)

@@ -74,7 +74,7 @@ def test_e4m3_decoders_match_torch(lib):
 
 
 # ---------------------------------------------------------------- LayerNorm
-LN_RANKS = [1, 5, 16, 64, 100, 128, 173, 192, 200, 256, 300, 320, 384, 449, 512]
+LN_RANKS = [1, 5, 16, 64, 100, 128, 173, 192, 200, 256, 300, 320, 384, 449, 512, 600, 777, 896, 1000, 1024]
 
 
 def _ln_rows(kind: str, M: int, N: int, g: torch.Generator) -> torch.Tensor:
@@ -122,6 +122,8 @@ def test_aten_layernorm_bit_exact_vs_torch(dtype, rank):
     (1, torch.bfloat16, 256),   # Welford m1 update without its fused multiply-add
     (2, torch.bfloat16, 512),   # stack merge m1 update fused (two chunks)
     (2, torch.float32, 384),    # ... and for fp32 rows (three chunks at rank 384)
+    (2, torch.float32, 840),    # ... seven chunks (the last short): a three-level stack
+    (2, torch.bfloat16, 800),   # ... four chunks of bf16 vectors (the last short)
     (4, torch.bfloat16, 256),   # lane merge m2 associated the other way
     (8, torch.bfloat16, 256),   # affine without fused multiply-adds
     (8, torch.float32, 256),
