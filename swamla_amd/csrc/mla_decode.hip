@@ -172,6 +172,12 @@ __device__ __forceinline__ u32x4v_t ds_read16(uint32_t addr) {
   return v;
 }
 template <int OFF>
+__device__ __forceinline__ s16x4_t ds_read8(uint32_t addr) {
+  s16x4_t v;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+template <int OFF>
 __device__ __forceinline__ s16x4_t ds_read_tr16(uint32_t addr) {
   s16x4_t v;
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
@@ -474,21 +480,24 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
     uint32_t lat = lds_off(sb);
     if constexpr (C_DT == 2) {
       // scales, and the codes decoded into the bf16 staging tile (swizzled as a bf16 tile)
+      // Each lane decodes 8 codes (one 16-byte chunk of bf16) per read: the
+      // 16 lanes of a store pass then write 16 consecutive chunks of one row,
+      // which the swizzle puts on 16 distinct 4-bank groups (with 16 codes
+      // per lane, a pass wrote every other chunk of a row: two-way conflicts).
       u32x4v_t sc = ds_read16<0>(lds_off(sb + G::kLat + G::kPe) + 16 * g);
-      u32x4v_t cv[NB];
-      static_for<0, NB>([&](auto q) { cv[q] = ds_read16<1024 * decltype(q)::value>(lds_off(sb) + 16 * lane); });
+      s16x4_t cv[2 * NB];
+      static_for<0, 2 * NB>([&](auto q) { cv[q] = ds_read8<512 * decltype(q)::value>(lds_off(sb) + 8 * lane); });
       lds_fence();
       tie(sc);
       scv = make_float4(u2f(sc.x), u2f(sc.y), u2f(sc.z), u2f(sc.w));
 #pragma unroll
-      for (int q = 0; q < NB; ++q) {
+      for (int q = 0; q < 2 * NB; ++q) {
         tie(cv[q]);
-        const int o = 1024 * q + 16 * lane;
+        const uint2 raw = __builtin_bit_cast(uint2, cv[q]);
+        const int o = 512 * q + 8 * lane;
         const int tt = o / RP, c0 = (o % RP) >> 3;  // chunk of the bf16 row
-        const uint2 d0 = e4m3x4_to_bf16x4_hw(cv[q].x), d1 = e4m3x4_to_bf16x4_hw(cv[q].y);
-        const uint2 d2 = e4m3x4_to_bf16x4_hw(cv[q].z), d3 = e4m3x4_to_bf16x4_hw(cv[q].w);
+        const uint2 d0 = e4m3x4_to_bf16x4_hw(raw.x), d1 = e4m3x4_to_bf16x4_hw(raw.y);
         lds_st16(stage + tt * (2 * RP) + 16 * (c0 ^ swz<NB>(tt)), make_uint4(d0.x, d0.y, d1.x, d1.y));
-        lds_st16(stage + tt * (2 * RP) + 16 * ((c0 + 1) ^ swz<NB>(tt)), make_uint4(d2.x, d2.y, d3.x, d3.y));
       }
       lat = lds_off(stage);
     }
