@@ -775,10 +775,15 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
         const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
         // the column's tile maximum (both lane halves), in the log2 domain (the scale is positive)
         mt = fmaxf(u2f(r32[0]), u2f(r32[1])) * a.scale_log2;
-        moved = __any(mt > m_run + kLazy);
-        m_new = moved ? fmaxf(m_run, mt) : m_run;
-        // a column still without a valid token (both -inf) keeps alpha = 1, not
-        // NaN: the wave's other query can move its own maximum
+        // Each column moves its own reference, only when its maximum grew by
+        // more than kLazy: its arithmetic then depends on its own scores
+        // alone, so a surplus column (repeating the block's last query, in
+        // this wave or another) computes that query's output bit for bit.
+        const bool mine = mt > m_run + kLazy;
+        moved = __any(mine);
+        m_new = mine ? fmaxf(m_run, mt) : m_run;
+        // a column that keeps its reference (or is still without a valid
+        // token: both -inf) keeps alpha = 1, not NaN
         alpha = m_new == m_run ? 1.f : exp2f(m_run - m_new);
         // A column with no valid token yet (reference still -inf) takes weight 0, not NaN.
         mref = m_new == -INFINITY ? 0.f : -m_new;  // (negated: the weights are exp2(s scale - m))
@@ -820,7 +825,8 @@ __global__ __launch_bounds__(kP2Waves * 64, 1) void mla_prefill_m32(DecodeArgs a
       else if constexpr (m == 5 * M / 8) smax_part(std::integral_constant<int, 2>{});
     };
     // commit(): the reference and weight sum move to the new tile; O is
-    // rescaled if any column's reference moved (rare after the first tiles).
+    // rescaled if any column's reference moved (rare after the first tiles;
+    // the other columns' alpha is 1).
     auto commit = [&]() __attribute__((always_inline)) {
       l_part = l_part * alpha + lsum;
       m_run = m_new;

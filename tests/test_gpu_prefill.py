@@ -123,6 +123,34 @@ def _prefill_case(gpu, fp8, B, T, starts, rope_abs, rank):
     check(dec, ref)
 
 
+@pytest.mark.parametrize("T", [13, 14, 16])
+def test_prefill_persistent_items_deterministic(gpu, T):
+    """More query groups than CUs (each persistent workgroup takes several, in
+    snake order), partial last groups (T not a multiple of 8: surplus columns
+    repeat the last query and store its row again): three launches give the
+    same bits, and the rows match the per-row decode kernel."""
+    say(f"prefill persistent items T={T}")
+    gen = torch.Generator(device=gpu).manual_seed(500 + T)
+    B, S = 300, 640
+    cache = make_cache(B, S, False, gen, gpu)
+    cos, sin = tables(S, gpu)
+    rows = B * T
+    q_abs = (0.3 * torch.randn(rows, H, R, generator=gen, device=gpu)).to(torch.bfloat16)
+    q_pe = (0.3 * torch.randn(rows, H, P, generator=gen, device=gpu)).to(torch.bfloat16)
+    sp = torch.randint(0, S - T, (B,), generator=gen, device=gpu, dtype=torch.int32)
+    outs = []
+    for _ in range(3):
+        out = torch.full((rows, H, R), float("nan"), dtype=torch.bfloat16, device=gpu)
+        kernels.prefill_attention(q_abs, q_pe, cos, sin, cache, SCALE, start_pos=sp, rows_per_seq=T, out=out)
+        outs.append(out)
+    dec = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE, start_pos=sp, rows_per_seq=T, n_splits=1,
+                                   min_chunk=64)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    check(outs[0], dec)
+
+
 def test_prefill_edges_clamp_negative_and_past_batch(gpu):
     """Rows past the cache end are clamped to it, a negative start gives
     empty rows (zeros), sequences past the cache's batch give zeros; all as
