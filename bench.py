@@ -552,16 +552,17 @@ def main() -> int:
     g = torch.Generator(device=dev).manual_seed(99)
     xs = [torch.randn(args.batch, 1, args.dim, generator=g, device=dev, dtype=torch.bfloat16) for _ in layers]
     # one start-position tensor for the whole stack, advanced once per step
-    # (every layer of a decoder sees the same positions)
+    # (every layer of a decoder sees the same positions): the last layer adds
+    # 1 after its kernels have read them, inside its last launch
     lens0 = start_lengths(args, torch)
     sp0 = lens0.to(dev)
     sp = sp0.clone()
     outs = [None] * len(layers)
+    layers[-1].advance_positions = True
 
     def stack_step():
         for i, m in enumerate(layers):
             outs[i] = m(xs[i], sp)
-        sp.add_(1)
 
     # eager warm-up (allocates workspaces), then capture one stack step
     with torch.no_grad():

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define SWAMLA_ABI_VERSION 5
+#define SWAMLA_ABI_VERSION 6
 
 enum {
   SWAMLA_OK = 0,
@@ -330,10 +330,18 @@ int mla_pack_weight(const void* w, int64_t w_rs, int32_t N, int32_t K,
  * wo (:490-495).
  * Limits: 0 <= M <= 128, N a multiple of 8, K in {512, 1024, 1536, 2048};
  * x and w_packed 16-byte aligned, x_rs a multiple of 8; y_rs >= N.
+ * advance (optional, may be null): the launch also adds 1 to advance[0 ..
+ * n_advance) (1 <= n_advance <= 512, 4-byte aligned, non-empty product).
+ * No reference counterpart: the reference's MLA takes start_pos as a host
+ * int (models/mla.py:232-236); a replayed HIP graph keeps the positions on
+ * the device, and this lets a decode step's last product advance them
+ * instead of a launch of its own.  The array must not overlap x, w_packed,
+ * bias or y.
  */
 int mla_linear_packed(const void* x, int64_t x_rs, const void* w_packed,
                       const void* bias, void* y, int64_t y_rs, int32_t M,
-                      int32_t N, int32_t K, int32_t dtype, void* stream);
+                      int32_t N, int32_t K, int32_t* advance,
+                      int32_t n_advance, int32_t dtype, void* stream);
 
 /*
  * mla_merge_project — split-KV merge fused with the W_uv read-out:

@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libswamla_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 DTYPE_F32, DTYPE_BF16, DTYPE_FP8 = 0, 1, 2
 ERR_NAMES = {
     -1: "INVALID_ARG",
@@ -116,7 +116,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mla_pack_weight.restype = ctypes.c_int
     lib.mla_pack_weight.argtypes = [_P, _I64, _I32, _I32, _P, _I32, _P]
     lib.mla_linear_packed.restype = ctypes.c_int
-    lib.mla_linear_packed.argtypes = [_P, _I64, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]
+    lib.mla_linear_packed.argtypes = [_P, _I64, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _I32, _I32, _P]
     lib.mla_linear.restype = ctypes.c_int
     lib.mla_linear.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I32, _I32, _I32, _I32, _I32, _P,

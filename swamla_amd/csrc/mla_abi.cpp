@@ -493,20 +493,25 @@ int mla_pack_weight(const void* w, int64_t w_rs, int32_t N, int32_t K, void* w_p
 }
 
 int mla_linear_packed(const void* x, int64_t x_rs, const void* w_packed, const void* bias, void* y, int64_t y_rs,
-                      int32_t M, int32_t N, int32_t K, int32_t dtype, void* stream) {
+                      int32_t M, int32_t N, int32_t K, int32_t* advance, int32_t n_advance, int32_t dtype,
+                      void* stream) {
   const char* fn = "mla_linear_packed";
   if (dtype != SWAMLA_DTYPE_BF16) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: dtype %d not built (bf16 only)", fn, dtype);
   if (M < 0 || M > 128) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: M=%d outside [0, 128]", fn, M);
   if (N < 0 || N % 8 != 0) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: N=%d is not a multiple of 8", fn, N);
   if (K != 512 && K != 1024 && K != 1536 && K != 2048)
     return fail(SWAMLA_ERR_UNSUPPORTED, "%s: K=%d (built: 512, 1024, 1536, 2048)", fn, K);
+  if (advance && (n_advance < 1 || n_advance > 512 || M == 0 || N == 0))
+    return fail(SWAMLA_ERR_INVALID_ARG, "%s: advance needs 1 <= n_advance <= 512 (got %d) and a non-empty product "
+                "(M=%d, N=%d)", fn, n_advance, M, N);
   if (M == 0 || N == 0) return ok();
   if (!x || !w_packed || !y) return fail(SWAMLA_ERR_INVALID_ARG, "%s: null x / w_packed / y", fn);
   if (x_rs < K || y_rs < N) return fail(SWAMLA_ERR_INVALID_ARG, "%s: row strides must cover K (x) and N (y)", fn);
+  if (advance && !aligned(advance, 4)) return fail(SWAMLA_ERR_MISALIGNED, "%s: advance must be 4-byte aligned", fn);
   if (!aligned(x, 16) || !aligned(w_packed, 16) || x_rs % 8 != 0 || !aligned(y, 2) || (bias && !aligned(bias, 2)))
     return fail(SWAMLA_ERR_MISALIGNED, "%s: x and w_packed need 16-byte aligned bases and x a row stride that is "
                 "a multiple of 8", fn);
-  swamla::PackedLinearArgs a{x, x_rs, w_packed, bias, y, y_rs, M, N, K};
+  swamla::PackedLinearArgs a{x, x_rs, w_packed, bias, y, y_rs, M, N, K, advance, advance ? n_advance : 0};
   const int rc = swamla::launch_linear_packed(a, static_cast<hipStream_t>(stream));
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for M=%d K=%d", fn, M, K);
   if (rc != 0) return hip_fail(fn);

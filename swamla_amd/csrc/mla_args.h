@@ -146,6 +146,11 @@ struct PackedLinearArgs {
   void* y;
   int64_t y_rs;
   int M, N, K;
+  // Optional: adv[0 .. n_adv) += 1 (a decode loop's device positions, advanced
+  // by the step's last launch instead of a kernel of its own; nothing in the
+  // product reads them).  n_adv <= the workgroup's 512 threads.
+  int32_t* adv;
+  int n_adv;
 };
 
 struct PackWeightArgs {

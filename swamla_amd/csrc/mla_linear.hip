@@ -416,6 +416,12 @@ __global__ __launch_bounds__(kPkWaves * 64) void mla_linear_packed_kernel(Packed
   const int slab = blockIdx.y;
   const int o0 = static_cast<int>(static_cast<int64_t>(blockIdx.x) * n_oct / gx);
   const int o1 = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * n_oct / gx);
+  // Position advance (one workgroup, one relaxed vector atomic per entry, no
+  // return value: nothing waits for it inside the launch; the launch's end
+  // makes it visible to the next).  Issued ahead of every load, so that no
+  // load result is live across its branch.
+  if (a.adv != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && static_cast<int>(threadIdx.x) < a.n_adv)
+    __hip_atomic_fetch_add(a.adv + threadIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // X rows of the slab, 16 bytes per thread and load (rows past M repeat the
   // last row; their results are dropped).

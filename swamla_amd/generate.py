@@ -29,7 +29,8 @@ a ``with IncrementalDecoder(model) as dec:`` block): they are switched to
 absolute RoPE positions — a new token at position p must be rotated by p,
 which is what the reference's full-context recompute does (its chunk-local
 convention rotates a one-token call by 0) — and, for graph replays, to the
-per-row split plan.  Their caches stay allocated (``MLA.clear_cache`` frees
+per-row split plan; while the graph is captured the last one advances the
+device positions (``MLA.advance_positions``).  Their caches stay allocated (``MLA.clear_cache`` frees
 them).
 
 Positions are checked on the host against the smaller of ``block_size`` and
@@ -68,14 +69,15 @@ class IncrementalDecoder:
         self.limit = self.block_size  # positions available: block_size and every cache length
         self.pos = 0
         # the attributes prefill() / the graph capture change, restored by close()
-        self._saved = [(m, m.rope_positions, m.split_plan) for m in self.mlas]
+        self._saved = [(m, m.rope_positions, m.split_plan, m.advance_positions) for m in self.mlas]
 
     def close(self) -> None:
         """Restore each MLA's RoPE convention and split plan as they were
         before this decoder touched them, and drop the captured graph."""
-        for m, rope_positions, split_plan in self._saved:
+        for m, rope_positions, split_plan, advance in self._saved:
             m.rope_positions = rope_positions
             m.split_plan = split_plan
+            m.advance_positions = advance
         self._g = None
 
     def __enter__(self) -> "IncrementalDecoder":
@@ -147,17 +149,20 @@ class IncrementalDecoder:
         sp = torch.full((idx_next.shape[0],), self.pos, dtype=torch.int32, device=dev)
         for m in self.mlas:
             m.split_plan = "static"  # a uniform batch: each row cut by its own length
+            m.advance_positions = False
+        # the last MLA of the step advances the positions (inside its last
+        # launch on the fused one-token path)
+        self.mlas[-1].advance_positions = True
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
             logits = self._run(tok, sp)
-            sp.add_(1)
         torch.cuda.current_stream(dev).wait_stream(side)
         self.pos += 1
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             out = self._run(tok, sp)
-            sp.add_(1)
+        self.mlas[-1].advance_positions = False
         self._g = (graph, tok, sp, out)
         return logits
 

@@ -647,11 +647,14 @@ def linear_packed(
     wp: PackedWeight,
     out: Optional[torch.Tensor] = None,
     bias: Optional[torch.Tensor] = None,
+    advance: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """out[m, n] = x[m, :] . w[n, :] (+ bias[n]) with w packed by pack_weight
     (mla_linear_packed): the decode step's stacked input product and wo
-    (models/mla.py:281-288, :307, :490-495)."""
-    dev = _need_gpu(x, wp.data, out, bias)
+    (models/mla.py:281-288, :307, :490-495).  ``advance`` (a contiguous int32
+    device tensor of 1 to 512 entries, not overlapping the operands): the same
+    launch adds 1 to each entry (a decode loop's device positions)."""
+    dev = _need_gpu(x, wp.data, out, bias, advance)
     if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1 or x.shape[1] != wp.K:
         raise ValueError(f"x must be [M, {wp.K}] bf16 with a unit last stride")
     M = x.shape[0]
@@ -662,10 +665,15 @@ def linear_packed(
     if bias is not None and (bias.dim() != 1 or bias.numel() != wp.N or bias.stride(0) != 1
                              or bias.dtype != x.dtype):
         raise ValueError(f"bias must be a contiguous [{wp.N}] bf16 vector")
+    n_adv = 0
+    if advance is not None:
+        if advance.dtype != torch.int32 or not advance.is_contiguous() or not 1 <= advance.numel() <= 512:
+            raise ValueError("advance must be a contiguous int32 tensor of 1 to 512 entries")
+        n_adv = advance.numel()
     _abi.check(
         _abi.lib().mla_linear_packed(
             x.data_ptr(), x.stride(0), wp.data.data_ptr(), _abi.ptr(bias), out.data_ptr(), out.stride(0),
-            M, wp.N, wp.K, _abi.DTYPE_BF16, _abi.stream_handle(dev),
+            M, wp.N, wp.K, _abi.ptr(advance), n_adv, _abi.DTYPE_BF16, _abi.stream_handle(dev),
         )
     )
     return out

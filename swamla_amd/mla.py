@@ -146,6 +146,14 @@ class MLA(nn.Module):
         # batches), "static" always cuts each row by its own length (the plan
         # an int start_pos gets: all rows alike), "balanced" always balances.
         self.split_plan = "auto"
+        # A decode loop replayed from a HIP graph keeps its positions in a
+        # device tensor and advances it after every step.  With this set, the
+        # call itself adds T (its tokens per sequence) to a start_pos tensor
+        # after its kernels have read it: a one-token step on the fused path
+        # does it inside its last launch (wo's product), other calls with an
+        # in-place add.  Meant for the last MLA a step runs.
+        self.advance_positions = False
+        self._advance_folded = False
 
     # ------------------------------------------------------------------ cache
     @property
@@ -635,12 +643,28 @@ class MLA(nn.Module):
             raise NotImplementedError("the training / autograd path is not part of this build")
         if x.device.type != "cuda":
             raise RuntimeError("swamla_amd.MLA runs on the GPU only (no CPU fallback)")
+        if self.advance_positions and not isinstance(start_pos, torch.Tensor):
+            raise ValueError("advance_positions needs start_pos as a tensor (an int cannot be advanced in place)")
         self._check_geometry()
         self._poll_cache_errors()
+        self._advance_folded = False
         with torch.no_grad():
             out = self._forward_kernels(x, start_pos)
+            if self.advance_positions and not self._advance_folded:
+                start_pos.add_(x.size(1))
         self._read_back_cache_errors()
         return out
+
+    def _advance_target(self, start_pos, sp: torch.Tensor, T: int) -> Optional[torch.Tensor]:
+        """The positions tensor a one-token step's last launch may advance
+        itself: start_pos's own storage as the kernels read it (int32,
+        contiguous, at most 512 entries), else None (forward adds in place)."""
+        if not (self.advance_positions and T == 1 and isinstance(start_pos, torch.Tensor)):
+            return None
+        if (start_pos.dtype != torch.int32 or not start_pos.is_contiguous() or sp.data_ptr() != start_pos.data_ptr()
+                or not 1 <= sp.numel() <= 512):
+            return None
+        return sp
 
     def _is_causal_prompt_mask(self, mask: torch.Tensor, T: int, start_pos) -> bool:
         """True for the mask SWAMLAModel passes with a prompt
@@ -811,7 +835,9 @@ class MLA(nn.Module):
             wo_b = None if self.wo.bias is None else self.wo.bias.detach()
             wo_p = self._packed_wo()
             if wo_p is not None and kernels.packed_ok(n, wo_p.N, wo_p.K):
-                out = kernels.linear_packed(o, wo_p, bias=wo_b).view(B, T, self.dim)
+                adv = self._advance_target(start_pos, sp, T)
+                out = kernels.linear_packed(o, wo_p, bias=wo_b, advance=adv).view(B, T, self.dim)
+                self._advance_folded = adv is not None
             else:
                 out = kernels.linear(o, self._wo_fused(), bias=wo_b).view(B, T, self.dim)
             return self.resid_dropout(out)  # mla.py:490-495

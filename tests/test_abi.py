@@ -36,7 +36,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mla_abi_version() == _abi.ABI_VERSION == 5
+    assert lib.mla_abi_version() == _abi.ABI_VERSION == 6
 
 
 def _append(lib, **kw):
@@ -260,7 +260,8 @@ def test_pack_weight_and_packed_linear_reject(lib):
     assert lib.mla_pack_weight(FAKE + 8, 1024, 48, 1024, FAKE, 1, None) == -3
     assert lib.mla_pack_weight(FAKE, 1028, 48, 1024, FAKE, 1, None) == -3
     assert lib.mla_pack_weight(FAKE, 1024, 0, 1024, None, 1, None) == 0  # empty
-    args = dict(x=FAKE, x_rs=1024, wp=FAKE, bias=None, y=FAKE, y_rs=64, M=32, N=64, K=1024, dt=1, stream=None)
+    args = dict(x=FAKE, x_rs=1024, wp=FAKE, bias=None, y=FAKE, y_rs=64, M=32, N=64, K=1024, adv=None, n_adv=0, dt=1,
+                stream=None)
 
     def lp(**kw):
         a = dict(args)
@@ -279,6 +280,12 @@ def test_pack_weight_and_packed_linear_reject(lib):
     assert lp(x_rs=1028) == -3
     assert lp(bias=FAKE + 1) == -3
     assert lp(M=0, x=None, wp=None, y=None) == 0
+    # the position advance: 1 to 512 entries, 4-byte aligned, a non-empty product
+    assert lp(adv=FAKE, n_adv=0) == -1
+    assert lp(adv=FAKE, n_adv=513) == -1
+    assert lp(adv=FAKE, n_adv=4, M=0, x=None, wp=None, y=None) == -1
+    assert "advance" in lib.mla_last_error().decode()
+    assert lp(adv=FAKE + 2, n_adv=4) == -3
     assert "mla_linear_packed" in lib.mla_last_error().decode() or lp(M=129) == -2
 
 

@@ -7,7 +7,10 @@ inside swamla_amd/libswamla_mi355x.so, disassembled with ROCm's own tools):
     attention kernels;
   * no writes through the scalar data cache (scalar memory stores and
     atomics, its write-back and discard): every store is a vector store;
-  * the MFMA kernels are there (the disassembly is of the real code).
+  * the MFMA kernels are there (the disassembly is of the real code);
+  * the decode step's kernels keep everything in registers (no scratch
+    loads or stores: a spill inside the products' load phase doubled their
+    time), and the prompt-pass attention at most its few per-item spills.
 
 CPU only; skipped when the library or the ROCm tools are absent.
 """
@@ -57,3 +60,32 @@ def test_device_code_has_no_packed_fp32_or_scalar_stores(tmp_path):
         r"\b(?:s_store_\w+|s_buffer_store_\w+|s_scratch_store_\w+|s_atomic_\w+|s_buffer_atomic_\w+|s_dcache_wb\w*"
         r"|s_dcache_discard\w*)\b", dis)
     assert not scalar_writes, f"scalar-cache writes in the device code: {sorted(set(scalar_writes))}"
+
+
+# kernel name fragment -> scratch instructions allowed in each instance
+SCRATCH_BUDGET = {
+    "mla_linear_packed_kernel": 0,
+    "mla_decode_dma": 0,
+    "mla_merge_project_kernel": 0,
+    "mla_merge_kernel": 0,
+    "mla_append_g16_kernel": 0,
+    "mla_prefill_m32": 8,  # the persistent item loop re-loads a few values once per query group
+}
+
+
+def test_hot_kernels_do_not_spill(tmp_path):
+    dis = _disassembly(tmp_path)
+    seen = {k: 0 for k in SCRATCH_BUDGET}
+    over = []
+    for body in re.split(r"\n(?=[0-9a-f]+ <[^>]+>:)", dis):
+        m = re.match(r"[0-9a-f]+ <([^>]+)>:", body)
+        if not m:
+            continue
+        for frag, budget in SCRATCH_BUDGET.items():
+            if frag in m.group(1):
+                seen[frag] += 1
+                n = len(re.findall(r"\bscratch_(?:load|store)_\w+", body))
+                if n > budget:
+                    over.append((m.group(1), n))
+    assert all(seen.values()), f"kernels missing from the disassembly: {[k for k, v in seen.items() if not v]}"
+    assert not over, f"scratch spills above budget: {over}"

@@ -213,3 +213,40 @@ def test_linear_packed_equals_in_graph_replays(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
         _ = (x.float() * 2).sum()  # unrelated eager work between replays
+
+
+@pytest.mark.parametrize("M,n_adv", [(32, 32), (128, 128), (1, 1), (100, 512)])
+def test_linear_packed_advances_positions(gpu, M, n_adv):
+    """The optional position advance: each entry gains exactly 1 per launch,
+    eager and in graph replays, and the product's bits do not change."""
+    say(f"linear_packed advance M={M} n={n_adv}")
+    g = torch.Generator().manual_seed(40 + M)
+    x = torch.randn(M, 2048, generator=g).to(torch.bfloat16).to(gpu)
+    wp = kernels.pack_weight((torch.randn(1024, 2048, generator=g) * 0.05).to(torch.bfloat16).to(gpu))
+    plain = kernels.linear_packed(x, wp)
+    pos0 = torch.randint(0, 1 << 20, (n_adv,), generator=g, dtype=torch.int32)
+    buf = torch.full((n_adv + 8,), -7, dtype=torch.int32, device=gpu)  # guard entries past the tensor
+    pos = buf[:n_adv]
+    pos.copy_(pos0.to(gpu))
+    out = kernels.linear_packed(x, wp, advance=pos)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    assert torch.equal(pos.cpu(), pos0 + 1)
+    assert bool((buf[n_adv:] == -7).all())
+    s = torch.cuda.Stream(gpu)
+    s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s):
+        kernels.linear_packed(x, wp, out=out, advance=pos)
+    torch.cuda.current_stream(gpu).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels.linear_packed(x, wp, out=out, advance=pos)
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, plain)
+        assert torch.equal(pos.cpu(), pos0 + 3 + i)
+        _ = (x.float() * 2).sum()  # unrelated eager work between replays
+    with pytest.raises(ValueError):
+        kernels.linear_packed(x, wp, advance=pos.to(torch.int64))

@@ -177,6 +177,50 @@ def test_per_sequence_start_pos(gpu, split_plan):
     close(out, torch.cat(refs), dtype)
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_advance_positions(gpu, fused):
+    """MLA.advance_positions: the call adds T to a start_pos tensor after its
+    kernels have read it: inside wo's launch on the fused one-token path (an
+    int32 device tensor), else by an in-place add.  Outputs and cache bits
+    equal those of a module that does not advance (the caller adding 1), for
+    several steps in a row; an int start_pos raises."""
+    say(f"advance_positions fused={fused}")
+    dtype = torch.bfloat16
+    cfg = MLAConfig(n_embd=1024, max_batch_size=4, max_seq_len=256)
+    _, a = make_pair(cfg, 31, dtype, gpu)
+    _, b = make_pair(cfg, 31, dtype, gpu)
+    a.advance_positions = True
+    g = torch.Generator().manual_seed(32)
+    prompt = torch.randn(4, 40, 1024, generator=g).to(dtype).to(gpu)
+    with torch.no_grad():
+        a.prefill_cache(prompt, 0)
+        b.prefill_cache(prompt, 0)
+        lens = [40, 33, 17, 40]
+        pa = torch.tensor(lens, dtype=torch.int32, device=gpu)
+        if not fused:
+            pa = pa.to(torch.int64)  # not the kernels' own storage: forward adds in place
+        pb = torch.tensor(lens, dtype=torch.int32, device=gpu)
+        for i in range(5):
+            x = torch.randn(4, 1, 1024, generator=g).to(dtype).to(gpu)
+            ya = a(x, pa)
+            assert a._advance_folded == fused
+            yb = b(x, pb)
+            pb.add_(1)
+            torch.cuda.synchronize()
+            assert torch.equal(ya, yb)
+            assert torch.equal(pa.cpu().to(torch.int32), pb.cpu())
+        assert torch.equal(pa.cpu().to(torch.int32), torch.tensor(lens, dtype=torch.int32) + 5)
+        assert torch.equal(a.kv_cache.view(torch.uint8), b.kv_cache.view(torch.uint8))
+        assert torch.equal(a.pe_cache.view(torch.uint8), b.pe_cache.view(torch.uint8))
+        # a prompt-sized chunk advances by its length
+        xs = torch.randn(4, 3, 1024, generator=g).to(dtype).to(gpu)
+        a(xs, pa)
+        assert not a._advance_folded
+        assert torch.equal(pa.cpu().to(torch.int32), torch.tensor(lens, dtype=torch.int32) + 8)
+        with pytest.raises(ValueError):
+            a(x, 50)
+
+
 def test_fp8_cache_against_emulation(gpu):
     """e4m3 latent cache vs the reference with the quantisation emulated in
     PyTorch (oracle RefMLA(fp8_cache=True))."""
