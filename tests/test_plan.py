@@ -66,3 +66,14 @@ def test_packed_blocks_mirrors_the_launcher():
     assert kernels.packed_blocks(128, 5440, 1024) == 340
     assert kernels.packed_blocks(128, 1024, 2048) == 256
     assert kernels.packed_blocks(1, 8, 512) == 1
+
+
+def test_committed_traffic_matches_the_current_kernel_source():
+    """bench.py copies an HBM traffic figure into its JSON line only from a
+    committed profile keyed to the decode kernel's current source; config 2's
+    16- and 32-head launches must have one (re-measure after a source change)."""
+    import bench
+
+    for heads in (16, 32):
+        got = bench.measured_traffic(32, 4224, "bf16", heads=heads)
+        assert got is not None and got[0] > 87_000_000, (heads, got)
