@@ -223,10 +223,14 @@ int mla_decode_attn_append(const void* kv_in, int64_t in_row_stride,
  * o_lat and lse_out receive every row's merged result.  Limit: n_rows x
  * n_splits x H x R_pad x 4 bytes of partials at most 16 MiB (n_splits == 1
  * needs none); larger calls return SWAMLA_ERR_UNSUPPORTED.  There is one
- * scratch area per GPU, shared by every call on it: calls that overlap on
- * one GPU (other streams, other threads) race and must be serialised by the
- * caller.  Nothing in the area needs clearing between calls (each launch
- * writes every partial it reads back).
+ * scratch area per GPU (16.25 MiB of device memory on every GPU the library
+ * loads on, held to the end of the process), shared by every call on it.
+ * Calls on one stream are ordered by the stream; a call on another stream
+ * is ordered after the device's last call (its stream waits for a completion
+ * event the library records after each call; host threads take turns).
+ * Calls under graph capture neither wait nor record: replays of graphs that
+ * use the area on different streams race and must be ordered by the caller.  Nothing in the area needs clearing between calls
+ * (each launch writes every partial it reads back).
  */
 int mla_decode_attn_noalloc(const void* q_abs, int64_t q_abs_rs,
                             int64_t q_abs_hs, const void* q_pe,

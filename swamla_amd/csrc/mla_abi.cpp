@@ -364,12 +364,11 @@ int mla_decode_attn_noalloc(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_h
                            balance_blocks, nullptr, stand_in, stand_in, o_lat, o_rs, o_hs, lse_out, dtype,
                            cache_dtype, &a))
     return e;
-  void* area = nullptr;
-  if (const int rc = swamla::scratch_area(&area)) {
-    if (rc == -2) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: device ordinal beyond the scratch table", fn);
-    return fail(SWAMLA_ERR_HIP, "%s: scratch address lookup failed: %s", fn, hipGetErrorString(hipGetLastError()));
-  }
-  uint8_t* const base = static_cast<uint8_t*>(area);
+  swamla::ScratchUse use(stream);
+  if (use.status == -2) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: device ordinal beyond the scratch table", fn);
+  if (use.status != 0)
+    return fail(SWAMLA_ERR_HIP, "%s: scratch set-up failed: %s", fn, hipGetErrorString(hipGetLastError()));
+  uint8_t* const base = static_cast<uint8_t*>(use.area);
   float* const o_part = reinterpret_cast<float*>(base);
   float* const lse_part = reinterpret_cast<float*>(base + swamla::kScratchPartBytes);
   int32_t* const plan = balance_blocks > 0 ? reinterpret_cast<int32_t*>(base + swamla::kScratchPlanOffset) : nullptr;
@@ -380,13 +379,17 @@ int mla_decode_attn_noalloc(const void* q_abs, int64_t q_abs_rs, int64_t q_abs_h
   int rc = swamla::launch_decode(a, dtype, cache_dtype, st);
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no kernel for this dtype pair, head count and rank", fn);
   if (rc != 0) return hip_fail(fn);
-  if (n_splits == 1 || n_rows == 0) return ok();
+  if (n_splits == 1 || n_rows == 0) {
+    use.launched();
+    return ok();
+  }
   // every partial the merge reads was written by the launch above
   swamla::MergeArgs m{o_part, lse_part, a.ad, cache_batch, cache_seq, n_rows, n_splits,
                       min_chunk, plan, R, o_lat, o_rs, o_hs, lse_out};
   rc = swamla::launch_merge(m, dtype, st);
   if (rc == -1) return fail(SWAMLA_ERR_UNSUPPORTED, "%s: no merge kernel for dtype %d", fn, dtype);
   if (rc != 0) return hip_fail(fn);
+  use.launched();
   return ok();
 }
 

@@ -15,9 +15,31 @@ constexpr size_t kScratchLseBytes = kScratchPartBytes / 64;
 constexpr size_t kScratchPlanOffset = kScratchPartBytes + kScratchLseBytes;
 constexpr size_t kScratchBytes = kScratchPlanOffset + 256;
 
-// The calling thread's current device's scratch area (its device address,
-// looked up on the device's first call).  0 on success; -1 if the HIP
-// runtime failed; -2 for a device ordinal past the ones tracked.
-int scratch_area(void** ptr);
+// One call's use of the calling thread's current device's scratch area, for
+// the length of the call (constructor to destructor; host threads take turns
+// on a device).  status: 0, and `area` holds the device address (looked up
+// on the device's first call); -1 if the HIP runtime failed; -2 for a device
+// ordinal past the ones tracked.  When the device's last call went to another
+// stream, the constructor makes this call's stream wait for that call's
+// completion event, so the two never share the area at once; after its
+// launches succeed the call marks launched(), which records its own event.
+// Calls made while their stream is being captured into a graph neither wait
+// nor record: their launches run at replay, and ordering replays that use the
+// area on different streams is the caller's.
+class ScratchUse {
+ public:
+  explicit ScratchUse(void* stream);
+  ~ScratchUse();
+  ScratchUse(const ScratchUse&) = delete;
+  ScratchUse& operator=(const ScratchUse&) = delete;
+  void launched();
+  int status = -1;
+  void* area = nullptr;
+
+ private:
+  int dev_ = -1;
+  void* stream_ = nullptr;
+  bool capturing_ = false;
+};
 
 }  // namespace swamla

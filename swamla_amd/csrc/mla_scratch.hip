@@ -1,7 +1,8 @@
 // mla_scratch.hip — the library's one piece of device state: a fixed scratch
 // area for the entry point that allocates nothing (mla_decode_attn_noalloc),
 // holding the split-KV partials and the balanced plan between the decode and
-// merge launches it makes.
+// merge launches it makes, and the bookkeeping that orders calls from
+// different streams so that they never share the area at once.
 //
 // `scratch` is a file-scope __device__ array: each GPU the library runs on
 // gets its own copy when the code object loads there, and keeps it until the
@@ -22,23 +23,50 @@ namespace {
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
-std::mutex g_mu;
+// per device: the area's address, a completion event of the last call and the
+// stream it went to (set up on the device's first call, kept to the end)
+std::mutex g_mu[kMaxDevices];
 void* g_ptr[kMaxDevices] = {};
+hipEvent_t g_done[kMaxDevices] = {};
+hipStream_t g_last[kMaxDevices] = {};
+bool g_recorded[kMaxDevices] = {};
 
 }  // namespace
 
-int scratch_area(void** ptr) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess) return -1;
-  if (dev < 0 || dev >= kMaxDevices) return -2;
-  std::lock_guard<std::mutex> lock(g_mu);
-  if (!g_ptr[dev]) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return -1;
-    g_ptr[dev] = p;
+ScratchUse::ScratchUse(void* stream) : stream_(stream) {
+  if (hipGetDevice(&dev_) != hipSuccess) return;
+  if (dev_ < 0 || dev_ >= kMaxDevices) {
+    status = -2;
+    dev_ = -1;
+    return;
   }
-  *ptr = g_ptr[dev];
-  return 0;
+  g_mu[dev_].lock();
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!g_ptr[dev_]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return;
+    if (hipEventCreateWithFlags(&g_done[dev_], hipEventDisableTiming) != hipSuccess) return;
+    g_ptr[dev_] = p;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) return;
+  capturing_ = cs != hipStreamCaptureStatusNone;
+  if (!capturing_ && g_recorded[dev_] && g_last[dev_] != st && hipStreamWaitEvent(st, g_done[dev_], 0) != hipSuccess)
+    return;
+  area = g_ptr[dev_];
+  status = 0;
+}
+
+void ScratchUse::launched() {
+  if (status != 0 || capturing_) return;
+  const hipStream_t st = static_cast<hipStream_t>(stream_);
+  if (hipEventRecord(g_done[dev_], st) != hipSuccess) return;
+  g_last[dev_] = st;
+  g_recorded[dev_] = true;
+}
+
+ScratchUse::~ScratchUse() {
+  if (dev_ >= 0) g_mu[dev_].unlock();
 }
 
 }  // namespace swamla

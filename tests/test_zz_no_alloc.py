@@ -95,3 +95,35 @@ def test_noalloc_rejects_oversize(gpu):
         out.stride(0), out.stride(1), None, _abi.DTYPE_BF16, _abi.DTYPE_BF16, _abi.stream_handle(gpu))
     assert rc == -2
     assert b"scratch" in _abi.lib().mla_last_error()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(gpu):
+    """The shared scratch on two streams: a call on stream 2, made while the
+    device's last call (on stream 1, queued behind a bounded spin) has not
+    run, waits for it instead of sharing the area at the same time; both
+    results equal the workspace path bit for bit."""
+    import time
+
+    lens, (B, S), ns, mc = [1000, 700, 64, 999], (4, 1024), 4, 64
+    say(f"noalloc two streams: rows={len(lens)} n_splits={ns}")
+    args = _inputs(gpu, False, lens, B, S, seed=77)
+    cache, q_abs, q_pe, row_seq, kv_len, rope, cos, sin = args
+    lse_ref = torch.full((len(lens), H), float("nan"), dtype=torch.float32, device=gpu)
+    ref = kernels.decode_attention(q_abs, q_pe, cos, sin, cache, SCALE, row_seq=row_seq, kv_len=kv_len,
+                                   q_rope_pos=rope, n_splits=ns, min_chunk=mc, lse_out=lse_ref)
+    s1, s2 = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        torch.cuda._sleep(20_000_000)  # a bounded spin ahead of stream 1's call (milliseconds)
+        o1, l1 = _noalloc(*args, ns, mc, 0)
+    with torch.cuda.stream(s2):
+        o2, l2 = _noalloc(*args, ns, mc, 0)
+        done2 = torch.cuda.Event()
+        done2.record(s2)
+    time.sleep(0.002)  # far longer than the call itself takes
+    # stream 2's call is still queued behind stream 1's spin and call
+    assert not done2.query()
+    torch.cuda.synchronize()
+    for o, lse in ((o1, l1), (o2, l2)):
+        assert torch.equal(o.view(torch.int16), ref.view(torch.int16))
+        assert torch.equal(lse.view(torch.int32), lse_ref.view(torch.int32))
