@@ -31,7 +31,9 @@ roofline.ceiling_gbs is the plain HBM read rate of the GPU
 (mla_probe_read over 1 GiB per launch, regions alternated so the Infinity
 Cache serves nothing, best of four grid sizes), and roofline.stream_only_us the same decode launches'
 cache stream with the arithmetic left out (mla_probe_cache_stream), timed the
-same way as avg_launch_us.
+same way as avg_launch_us.  step_account.empty_launch_us is the cost of one
+kernel node that does nothing, graph-replayed back to back: the floor each of
+the decode step's four launches pays before its work.
 
 Every figure is the median of 5 timed repetitions.  ms_per_step is per
 graph replay of the whole stack (ms_per_step x steps = the timed region);
@@ -343,6 +345,38 @@ def median(xs):
 CEILING_GRIDS = (256, 512, 1024, 2048)
 
 
+def launch_floor(dev, torch, n: int = 64) -> float:
+    """Cost of one kernel node with no work in a replayed HIP graph: n
+    back-to-back mla_probe_read launches of 256 workgroups that read nothing
+    (each thread stores one word), replayed from a graph and timed with HIP
+    events; returns the median us per launch over TIMING_REPS repetitions.
+    Every launch of the decode step pays at least this."""
+    from swamla_amd import _abi
+
+    lib = _abi.lib()
+    sink = torch.empty(256 * 256, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        hc = torch.cuda.current_stream(dev).cuda_stream
+        for _ in range(n):
+            _abi.check(lib.mla_probe_read(sink.data_ptr(), 0, sink.data_ptr(), 256, hc))
+    graph.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(TIMING_REPS):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(4):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3 / (4 * n))
+    del graph
+    return median(per)
+
+
 def read_ceiling(dev, torch, gib: int = 1):
     """HBM read ceiling of this GPU: mla_probe_read streaming ``gib`` GiB per
     launch with 16-byte non-temporal loads, alternating between two disjoint
@@ -605,6 +639,8 @@ def main() -> int:
     cold_us, graph_us, warm_us, merge_us, L, B, n_splits, balance, stream_us = time_decode_kernel(
         layers, xs, lens, args, dev, torch)
     ceiling, ceiling_by_grid = read_ceiling(dev, torch)
+    floor_us = launch_floor(dev, torch)
+    log(f"empty graph-node launch {floor_us:.2f} us")
     log(f"read ceiling {ceiling:.0f} GB/s; cache stream alone "
         + (f"{stream_us:.2f} us" if stream_us is not None else "n/a (balanced plan)"))
     abytes = attention_bytes_rows(lens, fp8, args.heads) + append_bytes(B, fp8)
@@ -696,6 +732,15 @@ def main() -> int:
             "warm_mall_avg_launch_us": warm_us,
             "merge_avg_launch_us": merge_us,
             "attention_achieved_with_merge": abytes / ((graph_us + merge_us) * 1e-6) / 1e9,
+        },
+        "step_account": {
+            "launches_per_layer_step": 4,
+            "empty_launch_us": floor_us,
+            "launch_floor_us": 4 * floor_us,
+            "source": ("launch_floor: 64 back-to-back kernel nodes of 256 workgroups that read nothing "
+                       "(mla_probe_read, 0 bytes), graph-replayed, HIP events; the decode step's four launches "
+                       "(input product, append + attention, merge + W_uv, wo) each pay at least empty_launch_us "
+                       "before any of their work"),
         },
         "cpu_baseline": cpu,
         "host": platform.node(),
