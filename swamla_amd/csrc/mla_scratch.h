@@ -19,9 +19,9 @@ constexpr size_t kScratchBytes = kScratchPlanOffset + 256;
 // the length of the call (constructor to destructor; host threads take turns
 // on a device).  status: 0, and `area` holds the device address (looked up
 // on the device's first call); -1 if the HIP runtime failed; -2 for a device
-// ordinal past the ones tracked.  When the device's last call went to another
-// stream, the constructor makes this call's stream wait for that call's
-// completion event, so the two never share the area at once; after its
+// ordinal past the ones tracked.  The constructor makes this call's stream
+// wait for the completion event of the device's last call (on whichever
+// stream it went to), so two calls never share the area at once; after its
 // launches succeed the call marks launched(), which records its own event.
 // Calls made while their stream is being captured into a graph neither wait
 // nor record: their launches run at replay, and ordering replays that use the

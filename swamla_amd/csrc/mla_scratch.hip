@@ -23,12 +23,11 @@ namespace {
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
-// per device: the area's address, a completion event of the last call and the
-// stream it went to (set up on the device's first call, kept to the end)
+// per device: the area's address and a completion event of the last call
+// (set up on the device's first call, kept to the end)
 std::mutex g_mu[kMaxDevices];
 void* g_ptr[kMaxDevices] = {};
 hipEvent_t g_done[kMaxDevices] = {};
-hipStream_t g_last[kMaxDevices] = {};
 bool g_recorded[kMaxDevices] = {};
 
 }  // namespace
@@ -51,8 +50,9 @@ ScratchUse::ScratchUse(void* stream) : stream_(stream) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess) return;
   capturing_ = cs != hipStreamCaptureStatusNone;
-  if (!capturing_ && g_recorded[dev_] && g_last[dev_] != st && hipStreamWaitEvent(st, g_done[dev_], 0) != hipSuccess)
-    return;
+  // (also on the last call's own stream: a handle can be reused by a new
+  // stream after the old one is destroyed)
+  if (!capturing_ && g_recorded[dev_] && hipStreamWaitEvent(st, g_done[dev_], 0) != hipSuccess) return;
   area = g_ptr[dev_];
   status = 0;
 }
@@ -61,7 +61,6 @@ void ScratchUse::launched() {
   if (status != 0 || capturing_) return;
   const hipStream_t st = static_cast<hipStream_t>(stream_);
   if (hipEventRecord(g_done[dev_], st) != hipSuccess) return;
-  g_last[dev_] = st;
   g_recorded[dev_] = true;
 }
 
