@@ -65,6 +65,8 @@ class IncrementalDecoder:
                 raise NotImplementedError(f"block {i} has an Engram module, whose n-gram lookup needs the token "
                                           "history; not part of this path")
             self.mlas.append(attn)
+        if not self.mlas:
+            raise ValueError("the model has no blocks: nothing to decode incrementally")
         self.block_size = int(model.config.block_size)
         self.limit = self.block_size  # positions available: block_size and every cache length
         self.pos = 0
@@ -72,7 +74,7 @@ class IncrementalDecoder:
         self._saved = [(m, m.rope_positions, m.split_plan, m.advance_positions) for m in self.mlas]
 
     def close(self) -> None:
-        """Restore each MLA's RoPE convention and split plan as they were
+        """Restore each MLA's RoPE convention, split plan and position advance as they were
         before this decoder touched them, and drop the captured graph."""
         for m, rope_positions, split_plan, advance in self._saved:
             m.rope_positions = rope_positions
