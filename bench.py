@@ -693,7 +693,8 @@ def main() -> int:
                     "(wq with W_uk absorbed, wkv_a), append + decode attention, split merge + W_uv, wo "
                     "(four launches)",
         },
-        "hbm_gbs_step": step_bytes / (ms_per_step * 1e-3) / 1e9,
+        # one layer's algorithmic bytes over one layer-step's time
+        "hbm_gbs_step": step_bytes / (us_per_layer_step * 1e-6) / 1e9,
         "roofline": {
             "kernel": "mla_decode_dma, fused-append instance (mla_decode_attn_append: one-token append + "
                       "split-KV decode attention)",
