@@ -757,6 +757,328 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
 }
 
 // ===========================================================================
+// Ranks above 512 (R_pad = 64 NB, NB = 9 .. 16), bf16 model and cache.
+// ===========================================================================
+// The per-wave design above keeps a wave's O^T for all R_pad channels (4 NB
+// accumulators) and Q^T for R_pad + 64 in registers; past NB = 8 that no
+// longer fits.  Here the four waves of a workgroup share every sub-tile of
+// the split and divide the channels instead: wave w owns the 64-channel
+// blocks c = w, w + 4, w + 8, w + 12 (those below NB) and rope dimensions
+// 16 w .. 16 w + 15.  Per 16-token sub-tile a wave
+//   * streams its own channel blocks of the 16 latent rows (2 KB each, laid
+//     out as a one-block sub-tile of the kernel above, with the same 8-chunk
+//     swizzle) and its 32-byte slice of the 16 rope rows into its own LDS
+//     ring with global_load_lds_dwordx4; a wave with fewer blocks than the
+//     most loaded one re-reads its last block into the spare slot, so every
+//     wave issues kVm instructions per sub-tile and the waits stay fixed;
+//   * forms its partial S^T[16 tok x 16 heads] over its channels
+//     (mfma_f32_16x16x32_bf16) and rope slice (mfma_f32_16x16x16_bf16);
+//   * writes the partial to a double-buffered LDS exchange area, passes one
+//     barrier, and reads the four partials back, added in wave order, so
+//     every wave holds the same scores and runs the same online softmax;
+//   * accumulates O^T for its own channels (C^T read transposed from LDS).
+// Each wave then writes its own channels of o_lat or of the split's partial;
+// wave 0 writes the log-sum-exp.  Numerics are the kernel's above: bf16
+// weights in the product, o normalised by their sum, the LSE from the fp32
+// weights, per-op rounded q_pe RoPE, query channels >= R zeroed.
+namespace {
+template <int NB>
+struct WideGeo {
+  static constexpr int RP = 64 * NB;
+  static constexpr int NBW = (NB + kDecWaves - 1) / kDecWaves;  // channel blocks of the most loaded wave
+  static constexpr int kBlk = kSubTok * 128;                    // one 64-channel block of 16 rows
+  static constexpr int kPe = 1024;                              // 16 rope slices of 32 B (+ 512 B re-read)
+  static constexpr int kSub = NBW * kBlk + kPe;                 // a wave's bytes of one sub-tile
+  static constexpr int kVm = 2 * NBW + 1;                       // DMA instructions per sub-tile
+  static constexpr int NBUF = 3, kFill = 2, kCap = 2;
+  static constexpr int kXch = 2 * kDecWaves * 1024;             // two exchange buffers of 4 waves x 64 lanes x 16 B
+  static constexpr int kWave = NBUF * kSub;
+  static constexpr int kLds = kDecWaves * kWave + kXch;
+  static_assert(kLds <= kLdsMax, "LDS budget");
+  static_assert((kFill + 1) * kVm < 64, "vmcnt range");
+};
+
+__device__ __forceinline__ void ds_write16(uint32_t addr, f32x4_t v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+}  // namespace
+
+template <int NB>
+__global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_wide(DecodeArgs a) {
+  using G = WideGeo<NB>;
+  constexpr int RP = G::RP, NBW = G::NBW, NBUF = G::NBUF;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[G::kLds];
+  lds_u8* const lds = (lds_u8*)(lds_raw);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+
+  // ---- workgroup -> (row, split), as in mla_decode_dma
+  int r = blockIdx.y, split = blockIdx.x, bal_chunk = 0;
+  TokAddr ra;
+  if (a.balance > 0) {
+    const BalancedSlot bs =
+        balanced_slot(a.ad, a.n_rows, a.cache_b, a.cache_s, a.n_splits, a.min_chunk, a.balance, blockIdx.x);
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.plan) *a.plan = bs.chunk;
+    if (!bs.ok) return;
+    r = __builtin_amdgcn_readfirstlane(bs.r);
+    split = __builtin_amdgcn_readfirstlane(bs.split);
+    bal_chunk = bs.chunk;
+    ra = bs.addr;
+  } else {
+    ra = row_addr(a.ad, r);
+  }
+
+  // ---- this wave's query: latent blocks c = w + 4 i (lane: head n, channels
+  // 64 c + 32 s + 8 g .. + 8), rope dims 16 w + 4 g .. + 4
+  uint32_t qraw[NBW][2][4], praw[2];
+  const uint16_t* qa = static_cast<const uint16_t*>(a.q_abs) + r * a.qa_rs + n * a.qa_hs;
+#pragma unroll
+  for (int i = 0; i < NBW; ++i) {
+    const int c = min(w + kDecWaves * i, NB - 1);  // a spare block re-reads a valid one (never used)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) vm_load<4>(qa + 64 * c + 32 * s + 8 * g, qraw[i][s]);
+  }
+  vm_load<2>(static_cast<const uint16_t*>(a.q_pe) + r * a.qp_rs + n * a.qp_hs + 16 * w + 4 * g, praw);
+  int rp = ra.rope;
+  rp = rp < 0 ? 0 : (rp >= a.rope_len ? static_cast<int>(a.rope_len) - 1 : rp);
+  uint32_t crw[1], srw[1];
+  vm_load<1>(static_cast<const uint16_t*>(a.cos_tab) + static_cast<int64_t>(rp) * (kP / 2) + 8 * w + 2 * g, crw);
+  vm_load<1>(static_cast<const uint16_t*>(a.sin_tab) + static_cast<int64_t>(rp) * (kP / 2) + 8 * w + 2 * g, srw);
+
+  const int b = ra.b;
+  int L = ra.pos;
+  if (L > a.cache_s) L = static_cast<int>(a.cache_s);
+  if (b < 0 || b >= a.cache_b) L = 0;
+  const RowSplits rsp = row_splits(L, a.n_splits, a.min_chunk, bal_chunk);
+  const int ns = rsp.ns;
+  if (split >= ns && !(ns == 0 && split == 0)) {
+    wait_vm<0>();
+    return;
+  }
+  if (a.balance <= 0 && ns > 0) split = ns - 1 - split;
+  const int t0 = split * rsp.chunk;  // a multiple of 16
+  const int t1 = min(L, t0 + rsp.chunk);
+  const int t_last = t1 > 0 ? t1 - 1 : 0;
+  const int n_sub = t1 > t0 ? (t1 - t0 + kSubTok - 1) / kSubTok : 0;
+  const int64_t row0 = static_cast<int64_t>((b < 0 || b >= a.cache_b) ? 0 : b) * a.cache_s;
+
+  // ---- the wave's ring: per sub-tile NBW latent blocks, then the rope slices
+  lds_u8* const wave_lds = lds + w * G::kWave;
+  lds_u8* const xch = lds + kDecWaves * G::kWave;
+  const uint8_t* const ckv = static_cast<const uint8_t*>(a.ckv);
+  const uint8_t* const kpe = static_cast<const uint8_t*>(a.kpe);
+  // DMA lane offsets: latent instruction q of a block covers rows 8 q + lane / 8,
+  // slot lane % 8 holding chunk (lane % 8) ^ swz<1>(row); rope: row (lane / 2) % 16,
+  // half lane % 2 of the wave's 32 bytes (lanes 32 .. 63 re-read lanes 0 .. 31's)
+  int lat_row[2];
+  uint32_t lat_col[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    lat_row[q] = 8 * q + (lane >> 3);
+    lat_col[q] = 16 * ((lane & 7) ^ swz<1>(lat_row[q]));
+  }
+  const int pe_row = (lane >> 1) & 15;
+  const uint32_t pe_col = 32 * w + 16 * (lane & 1);
+  auto issue = [&](int k) {
+    const int tb = t0 + kSubTok * k;
+    lds_u8* const dst = wave_lds + (k % NBUF) * G::kSub;
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int c = min(w + kDecWaves * i, NB - 1);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int tok = min(tb + lat_row[q], t_last);
+        dma16(ckv + (row0 + tok) * (2 * RP) + 128 * c + lat_col[q], dst + i * G::kBlk + 1024 * q);
+      }
+    }
+    const int tok = min(tb + pe_row, t_last);
+    dma16(kpe + (row0 + tok) * (2 * kP) + pe_col, dst + NBW * G::kBlk);
+  };
+  issue(0);
+#pragma unroll
+  for (int k = 1; k < G::kFill; ++k) issue(k);  // past n_sub: re-reads the split's last row
+
+  // operand addresses within one block (the one-block layout of mla_decode_dma)
+  const int sw_n = swz<1>(n);
+  uint32_t qk_b[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) qk_b[s] = n * 128 + 16 * ((4 * s + g) ^ sw_n);
+  const int pv_row = 4 * g + (n >> 2);
+  const int pv_sw = swz<1>(pv_row);
+  uint32_t pv_m[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) pv_m[m] = pv_row * 128 + 16 * ((2 * m + ((n & 3) >> 1)) ^ pv_sw) + 8 * (n & 1);
+  const uint32_t pe_rd = NBW * G::kBlk + n * 32 + 8 * g;
+  const uint32_t xw = lds_off(xch) + 1024 * w + 16 * lane;  // this wave's exchange slot (buffer 0)
+  const uint32_t xr = lds_off(xch) + 16 * lane;             // wave v's slot: + 1024 v
+
+  f32x4_t oacc[4 * NBW];
+#pragma unroll
+  for (int i = 0; i < 4 * NBW; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_part = 0.f, e_part = 0.f;
+
+  // queries (and everything else issued before the DMAs) have landed
+  wait_vm<G::kFill * G::kVm>();
+#pragma unroll
+  for (int i = 0; i < NBW; ++i)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) vm_release(qraw[i][s]);
+  vm_release(praw);
+  vm_release(crw);
+  vm_release(srw);
+  bf16x8_t qb[NBW][2];
+#pragma unroll
+  for (int i = 0; i < NBW; ++i)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int c = w + kDecWaves * i;
+      qb[i][s] = as_bf16x8(mask_bf16x8(make_uint4(qraw[i][s][0], qraw[i][s][1], qraw[i][s][2], qraw[i][s][3]),
+                                       a.R - (64 * c + 32 * s + 8 * g)));
+    }
+  uint32_t qp[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t cj = j ? (crw[0] >> 16) : (crw[0] & 0xFFFF);
+    const uint32_t sj = j ? (srw[0] >> 16) : (srw[0] & 0xFFFF);
+    qp[j] = rope_bf16_packed(bf16_to_f32(praw[j] & 0xFFFF), bf16_to_f32(praw[j] >> 16), bf16_to_f32(cj),
+                             bf16_to_f32(sj));
+  }
+  const s16x4_t qpe = __builtin_bit_cast(s16x4_t, make_uint2(qp[0], qp[1]));
+
+  for (int k = 0; k < n_sub; ++k) {  // uniform
+    if (k + G::kCap >= G::kFill && k + G::kCap < n_sub) issue(k + G::kCap);
+    wait_subtiles<G::kVm, NBUF>(max(G::kFill, min(n_sub, k + G::kCap + 1)) - (k + 1));
+    const int tb = t0 + kSubTok * k;
+    const uint32_t sb = lds_off(wave_lds + (k % NBUF) * G::kSub);
+    u32x4v_t kr[NBW][2];
+    static_for<0, NBW>([&](auto iI) {
+      constexpr int I = decltype(iI)::value;
+      kr[I][0] = ds_read16<I * G::kBlk>(sb + qk_b[0]);
+      kr[I][1] = ds_read16<I * G::kBlk>(sb + qk_b[1]);
+    });
+    s16x4_t kp = ds_read8<0>(sb + pe_rd);
+    lds_fence();
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      tie(kr[i][0]);
+      tie(kr[i][1]);
+    }
+    tie(kp);
+    s16x4_t ctr[NBW][4];
+    static_for<0, NBW>([&](auto iI) {
+      constexpr int I = decltype(iI)::value;
+      static_for<0, 4>([&](auto mI) {
+        constexpr int M = decltype(mI)::value;
+        ctr[I][M] = ds_read_tr16<I * G::kBlk>(sb + pv_m[M]);
+      });
+    });
+
+    // this wave's partial scores, then the exchange
+    f32x4_t sp = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+      if (w + kDecWaves * i < NB) {  // uniform
+        sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[i][0]), qb[i][0], sp, 0, 0, 0);
+        sp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[i][1]), qb[i][1], sp, 0, 0, 0);
+      }
+    // The rope term has an accumulator of its own, added on the VALU: an
+    // mfma_f32_16x16x16 taking the 16x16x32 chain's result as its C operand
+    // got too few wait states on gfx950 and read the accumulator before the
+    // chain's last product had landed (the last channel block's scores were
+    // lost); the VALU adds also keep the inline-asm store below off a
+    // matrix-core result.
+    const f32x4_t spe = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kp, qpe, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    const f32x4_t stot = f32x4_t{sp[0] + spe[0], sp[1] + spe[1], sp[2] + spe[2], sp[3] + spe[3]};
+    const uint32_t xo = 4096 * (k & 1);
+    ds_write16(xw + xo, stot);
+    lds_fence();  // the partial (and the C^T reads) are in LDS
+    __builtin_amdgcn_s_barrier();
+    u32x4v_t xv[kDecWaves];
+    static_for<0, kDecWaves>([&](auto vI) {
+      constexpr int V = decltype(vI)::value;
+      xv[V] = ds_read16<1024 * V>(xr + xo);
+    });
+    lds_fence();
+#pragma unroll
+    for (int v = 0; v < kDecWaves; ++v) tie(xv[v]);
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float sv = ((u2f(xv[0][i]) + u2f(xv[1][i])) + u2f(xv[2][i])) + u2f(xv[3][i]);
+      x[i] = tb + 4 * g + i < t1 ? sv * a.scale_log2 : -INFINITY;
+    }
+    float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    mt = wave_max_rows(mt);  // head n's maximum over the sub-tile (finite: token tb is valid)
+    if (__any(mt > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = exp2f(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+      e_part *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4 * NBW; ++i) oacc[i] = oacc[i] * alpha;
+    }
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = exp2f(x[i] - m_run);
+    const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
+    l_part += (u2f(w01 << 16) + u2f(w01 & 0xFFFF0000u)) + (u2f(w23 << 16) + u2f(w23 & 0xFFFF0000u));
+    e_part += (p[0] + p[1]) + (p[2] + p[3]);
+    const s16x4_t pb = __builtin_bit_cast(s16x4_t, make_uint2(w01, w23));
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) tie(ctr[i][m]);
+      if (w + kDecWaves * i < NB)  // uniform
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          oacc[4 * i + m] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ctr[i][m], pb, oacc[4 * i + m], 0, 0, 0);
+    }
+  }
+  wait_vm<0>();  // the ring's loads past the split's sub-tiles
+
+  // ---- the wave's channels of head n: lane (n, g) holds O^T[16 m + 4 g + j][n]
+  // of each block; l and e summed over the head's four lane groups
+  float l_w = l_part + shfl_xor_f32(l_part, 16);
+  l_w += shfl_xor_f32(l_w, 32);
+  float e_w = e_part + shfl_xor_f32(e_part, 16);
+  e_w += shfl_xor_f32(e_w, 32);
+  const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
+  const float lse2 = e_w > 0.f ? m_run + __log2f(e_w) : -INFINITY;  // log2 domain
+  if (ns <= 1) {
+    uint16_t* op = static_cast<uint16_t*>(a.o_lat) + r * a.o_rs + n * a.o_hs + 4 * g;
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int c = w + kDecWaves * i;
+      if (c < NB)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          uint2 pk;
+          pk.x = pack_bf16x2(oacc[4 * i + m][0] * inv, oacc[4 * i + m][1] * inv);
+          pk.y = pack_bf16x2(oacc[4 * i + m][2] * inv, oacc[4 * i + m][3] * inv);
+          *reinterpret_cast<uint2*>(op + 64 * c + 16 * m) = pk;
+        }
+    }
+    if (a.lse_out && w == 0 && g == 0) a.lse_out[static_cast<int64_t>(r) * kH + n] = lse2 * kLn2;
+    return;
+  }
+  const int64_t pidx = (static_cast<int64_t>(r) * a.n_splits + split) * kH + n;
+  float* op = a.o_part + pidx * RP + 4 * g;
+#pragma unroll
+  for (int i = 0; i < NBW; ++i) {
+    const int c = w + kDecWaves * i;
+    if (c < NB)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        __builtin_nontemporal_store(f32x4_t{oacc[4 * i + m][0] * inv, oacc[4 * i + m][1] * inv,
+                                            oacc[4 * i + m][2] * inv, oacc[4 * i + m][3] * inv},
+                                    reinterpret_cast<f32x4_t*>(op + 64 * c + 16 * m));
+  }
+  if (w == 0 && g == 0) __builtin_nontemporal_store(lse2 * kLn2, a.lse_part + pidx);
+}
+
+// ===========================================================================
 // Measurement kernels (no reference counterpart; used by bench.py's ceiling
 // legs, never by the module).
 // ===========================================================================
@@ -834,8 +1156,27 @@ const void* decode_kernel(int c_dt, bool fuse, int hg) {
 
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
+  if (dt == 1 && c_dt == 1 && padded_rank(a.R) > 64 * kMaxNB) {
+    // bf16 ranks above 512: the channel-split MFMA kernel (no fused append, 16 heads)
+    if (a.fa.kv_in != nullptr || a.H != kH) return -1;
+    const dim3 grid = a.balance > 0 ? dim3(a.balance, 1) : dim3(a.n_splits, a.n_rows);
+    const int rc = with_nb_wide(a.R, [&](auto nb) {
+      constexpr int NB = decltype(nb)::value;
+      if constexpr (NB <= kMaxNB) {
+        return -1;
+      } else {
+        void* args[] = {const_cast<DecodeArgs*>(&a)};
+        return hipLaunchKernel(reinterpret_cast<const void*>(&mla_decode_wide<NB>), grid, dim3(kDecWaves * 64),
+                               args, 0, s) == hipSuccess
+                   ? 0
+                   : -2;
+      }
+    });
+    if (rc != 0) return rc;
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+  }
   if (dt == 0 || padded_rank(a.R) > 64 * kMaxNB) {
-    // the VALU kernel: fp32 models, and ranks above the MFMA kernel's
+    // the VALU kernel: fp32 models, and e4m3 caches above the MFMA kernels' 512
     if (a.fa.kv_in != nullptr || a.H != kH) return -1;
     return launch_decode_vec(a, dt, c_dt, s);
   }
@@ -872,6 +1213,11 @@ int launch_stream_probe(const DecodeArgs& a, int c_dt, uint32_t* sink, hipStream
 // Workgroups of a decode launch one CU holds at once: the MFMA kernel takes a
 // whole CU (its LDS ring), the fp32 kernel's own count.
 int decode_blocks_per_cu(int dt, int c_dt, int R, bool fuse, int* blocks) {
+  if (dt == 1 && c_dt == 1 && padded_rank(R) > 64 * kMaxNB) {
+    if (fuse) return -1;
+    *blocks = 1;  // the wide kernel's ring takes a CU
+    return 0;
+  }
   if (dt == 0 || padded_rank(R) > 64 * kMaxNB) return fuse ? -1 : decode_vec_blocks_per_cu(dt, c_dt, R, blocks);
   if (dt != 1) return -1;
   return with_nb(R, [&](auto nb) {
