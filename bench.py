@@ -99,6 +99,10 @@ def parse():
                    help="only time the prompt pass: MLA.forward over T tokens per sequence at start_pos 0 "
                         "(its own JSON line; the profiling workload for the prefill-side products)")
     p.add_argument("--prefill-batch", type=int, default=4)
+    p.add_argument("--rank-sweep", type=str, default="", metavar="R1,R2,...",
+                   help="only time the drop-in decode step at config 2's shape (batch, ctx, dim, heads) for "
+                        "each kv_lora_rank listed, graph-replayed over --layers layers (one JSON line per rank; "
+                        "the profiling workload for ranks above 512)")
     args = p.parse_args()
     preset = CONFIGS[args.config]
     for k, v in preset.items():
@@ -222,6 +226,83 @@ def build_layers(args, dev, torch):
         layers.append(m)
     torch.cuda.synchronize()
     return layers
+
+
+def run_rank_sweep(args, dev, torch) -> int:
+    """The drop-in decode step at config 2's shape for each listed
+    kv_lora_rank: every sequence prefilled to ctx through the append path,
+    one step of MLA.forward over the layers captured as a HIP graph, K timed
+    replays (median of the repetitions).  Ranks above 512 take the unfused
+    step (ATen query projection, append, channel-split decode attention,
+    merge, ATen W_uv and wo).  `attention_bytes` is the decode launch's
+    algorithmic bytes at the mean timed length."""
+    from swamla_amd import MLA, MLAConfig
+
+    ranks = [int(x) for x in args.rank_sweep.split(",") if x]
+    nl = min(args.layers, 4)
+    for rank in ranks:
+        cfg = MLAConfig(n_embd=args.dim, n_head=args.heads, kv_lora_rank=rank, max_batch_size=args.batch,
+                        max_seq_len=(args.ctx + args.steps + args.warmup + 63) // 64 * 64)
+        g = torch.Generator(device=dev).manual_seed(1234)
+        layers = []
+        for i in range(nl):
+            m = MLA(cfg)
+            init_linear_weights(m, 100 + i, torch)
+            m.eval().to(torch.bfloat16).to(dev)
+            m.set_inference_mode(True)
+            m.split_plan = "static"
+            with torch.no_grad():
+                m.prefill_cache(torch.randn(args.batch, args.ctx, args.dim, generator=g, device=dev,
+                                            dtype=torch.bfloat16), 0)
+            layers.append(m)
+        xs = [torch.randn(args.batch, 1, args.dim, generator=g, device=dev, dtype=torch.bfloat16) for _ in layers]
+        sp0 = torch.full((args.batch,), args.ctx, dtype=torch.int32, device=dev)
+        sp = sp0.clone()
+        layers[-1].advance_positions = True
+        outs = [None] * nl
+
+        def stack_step():
+            for i, m in enumerate(layers):
+                outs[i] = m(xs[i], sp)
+
+        with torch.no_grad():
+            side = torch.cuda.Stream(dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                stack_step()
+            torch.cuda.current_stream(dev).wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                stack_step()
+            sp.copy_(sp0)
+            for _ in range(args.warmup):
+                graph.replay()
+            reps = []
+            for _ in range(TIMING_REPS):
+                sp.copy_(sp0)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(args.steps):
+                    graph.replay()
+                torch.cuda.synchronize()
+                reps.append(time.perf_counter() - t0)
+        for m in layers:
+            m.check_cache_errors()
+        us = median(reps) / (args.steps * nl) * 1e6
+        mid = args.ctx + (args.steps + 1) // 2
+        rp = (rank + 63) // 64 * 64
+        abytes = args.batch * mid * (rp * 2 + P * 2) + args.batch * args.heads * (2 * rp + P) * 2
+        print(json.dumps({
+            "metric": "MLA decode layer-step time at config 2's shape, by kv_lora_rank",
+            "kv_lora_rank": rank, "us_per_layer_step": us, "value": args.batch / (us * 1e-6), "unit": "tok/s",
+            "layers_rotated": nl, "steps": args.steps, "timed_reps": TIMING_REPS,
+            "attention_bytes": abytes, "finite": all(bool(torch.isfinite(o).all()) for o in outs),
+            "config": {"batch": args.batch, "ctx": args.ctx, "n_embd": args.dim, "heads": args.heads,
+                       "cache": "bf16"},
+        }), flush=True)
+        del layers, graph, outs
+        torch.cuda.empty_cache()
+    return 0
 
 
 def time_decode_kernel(layers, xs, lens, args, dev, torch):
@@ -580,6 +661,8 @@ def main() -> int:
         return 0
     if args.prefill:
         return run_prefill(args, dev, torch)
+    if args.rank_sweep:
+        return run_rank_sweep(args, dev, torch)
     fp8 = args.cache == "fp8"
     log(f"building {args.layers} layers, batch {args.batch}, prefill {args.ctx} ({args.cache} cache)")
     layers = build_layers(args, dev, torch)
