@@ -23,7 +23,8 @@
  * kv_lora_rank 1 <= R <= 1024 (the real model scales the rank per layer,
  * models/swa_mla_model.py:216-247, up to twice its base).  mla_append,
  * mla_merge, mla_decode_attn and mla_decode_attn_noalloc take every such
- * rank (decode attention above 512 runs a VALU kernel);
+ * rank (decode attention above 512 runs a channel-split MFMA kernel for a
+ * bf16 model and cache, a VALU kernel for fp32 models and e4m3 caches);
  * mla_decode_attn_append, mla_merge_project and the measurement probes take
  * R <= 512, mla_prefill_attn R <= 256.
  * mla_decode_attn, mla_decode_attn_append, mla_merge and mla_merge_project
