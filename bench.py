@@ -246,7 +246,7 @@ def run_rank_sweep(args, dev, torch) -> int:
         g = torch.Generator(device=dev).manual_seed(1234)
         layers = []
         for i in range(nl):
-            m = MLA(cfg)
+            m = MLA(cfg, cache_dtype="fp8_e4m3" if args.cache == "fp8" else None)
             init_linear_weights(m, 100 + i, torch)
             m.eval().to(torch.bfloat16).to(dev)
             m.set_inference_mode(True)
@@ -291,14 +291,16 @@ def run_rank_sweep(args, dev, torch) -> int:
         us = median(reps) / (args.steps * nl) * 1e6
         mid = args.ctx + (args.steps + 1) // 2
         rp = (rank + 63) // 64 * 64
-        abytes = args.batch * mid * (rp * 2 + P * 2) + args.batch * args.heads * (2 * rp + P) * 2
+        fp8 = args.cache == "fp8"
+        abytes = (args.batch * mid * (rp * (1 if fp8 else 2) + P * 2 + (4 if fp8 else 0))
+                  + args.batch * args.heads * (2 * rp + P) * 2)
         print(json.dumps({
             "metric": "MLA decode layer-step time at config 2's shape, by kv_lora_rank",
             "kv_lora_rank": rank, "us_per_layer_step": us, "value": args.batch / (us * 1e-6), "unit": "tok/s",
             "layers_rotated": nl, "steps": args.steps, "timed_reps": TIMING_REPS,
             "attention_bytes": abytes, "finite": all(bool(torch.isfinite(o).all()) for o in outs),
             "config": {"batch": args.batch, "ctx": args.ctx, "n_embd": args.dim, "heads": args.heads,
-                       "cache": "bf16"},
+                       "cache": args.cache},
         }), flush=True)
         del layers, graph, outs
         torch.cuda.empty_cache()

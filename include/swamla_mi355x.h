@@ -24,7 +24,7 @@
  * models/swa_mla_model.py:216-247, up to twice its base).  mla_append,
  * mla_merge, mla_decode_attn and mla_decode_attn_noalloc take every such
  * rank (decode attention above 512 runs a channel-split MFMA kernel for a
- * bf16 model and cache, a VALU kernel for fp32 models and e4m3 caches);
+ * bf16 model, bf16 or e4m3 cache, and a VALU kernel for fp32 models);
  * mla_decode_attn_append, mla_merge_project and the measurement probes take
  * R <= 512, mla_prefill_attn R <= 256.
  * mla_decode_attn, mla_decode_attn_append, mla_merge and mla_merge_project

@@ -782,17 +782,20 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_dma(DecodeArgs a
 // weights in the product, o normalised by their sum, the LSE from the fp32
 // weights, per-op rounded q_pe RoPE, query channels >= R zeroed.
 namespace {
-template <int NB>
+template <int C_DT, int NB>
 struct WideGeo {
   static constexpr int RP = 64 * NB;
   static constexpr int NBW = (NB + kDecWaves - 1) / kDecWaves;  // channel blocks of the most loaded wave
-  static constexpr int kBlk = kSubTok * 128;                    // one 64-channel block of 16 rows
+  static constexpr int kBlk = kSubTok * 128;                    // one 64-channel block of 16 bf16 rows
+  static constexpr int kBlkC = C_DT == 2 ? kSubTok * 64 : kBlk;  // ring bytes of a block (e4m3: codes)
   static constexpr int kPe = 1024;                              // 16 rope slices of 32 B (+ 512 B re-read)
-  static constexpr int kSub = NBW * kBlk + kPe;                 // a wave's bytes of one sub-tile
-  static constexpr int kVm = 2 * NBW + 1;                       // DMA instructions per sub-tile
+  static constexpr int kSc = C_DT == 2 ? 256 : 0;               // e4m3: 4 copies of the 16 scales
+  static constexpr int kSub = NBW * kBlkC + kPe + kSc;          // a wave's ring bytes of one sub-tile
+  static constexpr int kVm = (C_DT == 2 ? NBW + 2 : 2 * NBW + 1);  // DMA instructions per sub-tile
+  static constexpr int kStage = C_DT == 2 ? NBW * kBlk : 0;     // e4m3: the wave's blocks decoded to bf16
   static constexpr int NBUF = 3, kFill = 2, kCap = 2;
   static constexpr int kXch = 2 * kDecWaves * 1024;             // two exchange buffers of 4 waves x 64 lanes x 16 B
-  static constexpr int kWave = NBUF * kSub;
+  static constexpr int kWave = NBUF * kSub + kStage;
   static constexpr int kLds = kDecWaves * kWave + kXch;
   static_assert(kLds <= kLdsMax, "LDS budget");
   static_assert((kFill + 1) * kVm < 64, "vmcnt range");
@@ -803,9 +806,9 @@ __device__ __forceinline__ void ds_write16(uint32_t addr, f32x4_t v) {
 }
 }  // namespace
 
-template <int NB>
+template <int C_DT, int NB>
 __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_wide(DecodeArgs a) {
-  using G = WideGeo<NB>;
+  using G = WideGeo<C_DT, NB>;
   constexpr int RP = G::RP, NBW = G::NBW, NBUF = G::NBUF;
   __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[G::kLds];
   lds_u8* const lds = (lds_u8*)(lds_raw);
@@ -886,14 +889,21 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_wide(DecodeArgs 
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
       const int c = min(w + kDecWaves * i, NB - 1);
+      if constexpr (C_DT == 2) {
+        // e4m3 codes as they lie: row lane / 4, bytes 16 (lane % 4) of the block's 64
+        const int tok = min(tb + (lane >> 2), t_last);
+        dma16(ckv + (row0 + tok) * RP + 64 * c + 16 * (lane & 3), dst + i * G::kBlkC);
+      } else {
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int tok = min(tb + lat_row[q], t_last);
-        dma16(ckv + (row0 + tok) * (2 * RP) + 128 * c + lat_col[q], dst + i * G::kBlk + 1024 * q);
+        for (int q = 0; q < 2; ++q) {
+          const int tok = min(tb + lat_row[q], t_last);
+          dma16(ckv + (row0 + tok) * (2 * RP) + 128 * c + lat_col[q], dst + i * G::kBlk + 1024 * q);
+        }
       }
     }
     const int tok = min(tb + pe_row, t_last);
-    dma16(kpe + (row0 + tok) * (2 * kP) + pe_col, dst + NBW * G::kBlk);
+    dma16(kpe + (row0 + tok) * (2 * kP) + pe_col, dst + NBW * G::kBlkC);
+    if constexpr (C_DT == 2) dma4(a.ckv_scale + row0 + min(tb + (lane & 15), t_last), dst + NBW * G::kBlkC + G::kPe);
   };
   issue(0);
 #pragma unroll
@@ -909,7 +919,9 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_wide(DecodeArgs 
   uint32_t pv_m[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) pv_m[m] = pv_row * 128 + 16 * ((2 * m + ((n & 3) >> 1)) ^ pv_sw) + 8 * (n & 1);
-  const uint32_t pe_rd = NBW * G::kBlk + n * 32 + 8 * g;
+  const uint32_t pe_rd = NBW * G::kBlkC + n * 32 + 8 * g;
+  lds_u8* const stage_p = wave_lds + NBUF * G::kSub;  // e4m3 only
+  const uint32_t stage = lds_off(stage_p);
   const uint32_t xw = lds_off(xch) + 1024 * w + 16 * lane;  // this wave's exchange slot (buffer 0)
   const uint32_t xr = lds_off(xch) + 16 * lane;             // wave v's slot: + 1024 v
 
@@ -951,11 +963,40 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_wide(DecodeArgs 
     wait_subtiles<G::kVm, NBUF>(max(G::kFill, min(n_sub, k + G::kCap + 1)) - (k + 1));
     const int tb = t0 + kSubTok * k;
     const uint32_t sb = lds_off(wave_lds + (k % NBUF) * G::kSub);
+    uint32_t lat = sb;  // the bf16 blocks the operand reads take
+    float4 scv = make_float4(1.f, 1.f, 1.f, 1.f);
+    if constexpr (C_DT == 2) {
+      // scales of the lane's tokens 4 g .. 4 g + 3, and the codes decoded into
+      // the staging tile in the bf16 ring layout (each lane: 8 codes -> one
+      // 16-byte chunk, two chunks per block)
+      u32x4v_t sc = ds_read16<0>(sb + NBW * G::kBlkC + G::kPe + 16 * g);
+      s16x4_t cv[NBW][2];
+      static_for<0, NBW>([&](auto iI) {
+        constexpr int I = decltype(iI)::value;
+        cv[I][0] = ds_read8<I * G::kBlkC>(sb + 8 * lane);
+        cv[I][1] = ds_read8<I * G::kBlkC + 512>(sb + 8 * lane);
+      });
+      lds_fence();
+      tie(sc);
+      scv = make_float4(u2f(sc.x), u2f(sc.y), u2f(sc.z), u2f(sc.w));
+#pragma unroll
+      for (int i = 0; i < NBW; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          tie(cv[i][q]);
+          const uint2 raw = __builtin_bit_cast(uint2, cv[i][q]);
+          const int o = 512 * q + 8 * lane;  // code offset in the block: row o / 64, chunk (o % 64) / 8
+          const int tt = o >> 6, c0 = (o & 63) >> 3;
+          const uint2 d0 = e4m3x4_to_bf16x4_hw(raw.x), d1 = e4m3x4_to_bf16x4_hw(raw.y);
+          lds_st16(stage_p + i * G::kBlk + tt * 128 + 16 * (c0 ^ swz<1>(tt)), make_uint4(d0.x, d0.y, d1.x, d1.y));
+        }
+      lat = stage;
+    }
     u32x4v_t kr[NBW][2];
     static_for<0, NBW>([&](auto iI) {
       constexpr int I = decltype(iI)::value;
-      kr[I][0] = ds_read16<I * G::kBlk>(sb + qk_b[0]);
-      kr[I][1] = ds_read16<I * G::kBlk>(sb + qk_b[1]);
+      kr[I][0] = ds_read16<I * G::kBlk>(lat + qk_b[0]);
+      kr[I][1] = ds_read16<I * G::kBlk>(lat + qk_b[1]);
     });
     s16x4_t kp = ds_read8<0>(sb + pe_rd);
     lds_fence();
@@ -970,7 +1011,7 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_wide(DecodeArgs 
       constexpr int I = decltype(iI)::value;
       static_for<0, 4>([&](auto mI) {
         constexpr int M = decltype(mI)::value;
-        ctr[I][M] = ds_read_tr16<I * G::kBlk>(sb + pv_m[M]);
+        ctr[I][M] = ds_read_tr16<I * G::kBlk>(lat + pv_m[M]);
       });
     });
 
@@ -989,7 +1030,9 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_wide(DecodeArgs 
     // lost); the VALU adds also keep the inline-asm store below off a
     // matrix-core result.
     const f32x4_t spe = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kp, qpe, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    const f32x4_t stot = f32x4_t{sp[0] + spe[0], sp[1] + spe[1], sp[2] + spe[2], sp[3] + spe[3]};
+    // (e4m3: the token's scale multiplies the latent part, as in mla_decode_dma)
+    const f32x4_t stot = f32x4_t{scv.x * sp[0] + spe[0], scv.y * sp[1] + spe[1], scv.z * sp[2] + spe[2],
+                                 scv.w * sp[3] + spe[3]};
     const uint32_t xo = 4096 * (k & 1);
     ds_write16(xw + xo, stot);
     lds_fence();  // the partial (and the C^T reads) are in LDS
@@ -1025,7 +1068,12 @@ __global__ __launch_bounds__(kDecWaves * 64, 1) void mla_decode_wide(DecodeArgs 
     const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
     l_part += (u2f(w01 << 16) + u2f(w01 & 0xFFFF0000u)) + (u2f(w23 << 16) + u2f(w23 & 0xFFFF0000u));
     e_part += (p[0] + p[1]) + (p[2] + p[3]);
-    const s16x4_t pb = __builtin_bit_cast(s16x4_t, make_uint2(w01, w23));
+    uint2 pw = make_uint2(w01, w23);
+    if constexpr (C_DT == 2) {
+      pw.x = pack_bf16x2(u2f(w01 << 16) * scv.x, u2f(w01 & 0xFFFF0000u) * scv.y);
+      pw.y = pack_bf16x2(u2f(w23 << 16) * scv.z, u2f(w23 & 0xFFFF0000u) * scv.w);
+    }
+    const s16x4_t pb = __builtin_bit_cast(s16x4_t, pw);
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
 #pragma unroll
@@ -1156,8 +1204,8 @@ const void* decode_kernel(int c_dt, bool fuse, int hg) {
 
 int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
   if (a.n_rows == 0) return 0;
-  if (dt == 1 && c_dt == 1 && padded_rank(a.R) > 64 * kMaxNB) {
-    // bf16 ranks above 512: the channel-split MFMA kernel (no fused append, 16 heads)
+  if (dt == 1 && (c_dt == 1 || c_dt == 2) && padded_rank(a.R) > 64 * kMaxNB) {
+    // bf16 models above rank 512: the channel-split MFMA kernel (no fused append, 16 heads)
     if (a.fa.kv_in != nullptr || a.H != kH) return -1;
     const dim3 grid = a.balance > 0 ? dim3(a.balance, 1) : dim3(a.n_splits, a.n_rows);
     const int rc = with_nb_wide(a.R, [&](auto nb) {
@@ -1166,8 +1214,9 @@ int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
         return -1;
       } else {
         void* args[] = {const_cast<DecodeArgs*>(&a)};
-        return hipLaunchKernel(reinterpret_cast<const void*>(&mla_decode_wide<NB>), grid, dim3(kDecWaves * 64),
-                               args, 0, s) == hipSuccess
+        const void* fn = c_dt == 2 ? reinterpret_cast<const void*>(&mla_decode_wide<2, NB>)
+                                   : reinterpret_cast<const void*>(&mla_decode_wide<1, NB>);
+        return hipLaunchKernel(fn, grid, dim3(kDecWaves * 64), args, 0, s) == hipSuccess
                    ? 0
                    : -2;
       }
@@ -1176,7 +1225,7 @@ int launch_decode(const DecodeArgs& a, int dt, int c_dt, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? 0 : -2;
   }
   if (dt == 0 || padded_rank(a.R) > 64 * kMaxNB) {
-    // the VALU kernel: fp32 models, and e4m3 caches above the MFMA kernels' 512
+    // the VALU kernel: fp32 models
     if (a.fa.kv_in != nullptr || a.H != kH) return -1;
     return launch_decode_vec(a, dt, c_dt, s);
   }
@@ -1213,7 +1262,7 @@ int launch_stream_probe(const DecodeArgs& a, int c_dt, uint32_t* sink, hipStream
 // Workgroups of a decode launch one CU holds at once: the MFMA kernel takes a
 // whole CU (its LDS ring), the fp32 kernel's own count.
 int decode_blocks_per_cu(int dt, int c_dt, int R, bool fuse, int* blocks) {
-  if (dt == 1 && c_dt == 1 && padded_rank(R) > 64 * kMaxNB) {
+  if (dt == 1 && (c_dt == 1 || c_dt == 2) && padded_rank(R) > 64 * kMaxNB) {
     if (fuse) return -1;
     *blocks = 1;  // the wide kernel's ring takes a CU
     return 0;

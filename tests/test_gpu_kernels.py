@@ -224,24 +224,26 @@ def test_decode_any_rank(gpu, dtype, fp8, rank):
     """kv_lora_rank other than 256: one split, split-KV with the merge, and
     the balanced plan; the query padding is ignored and the output padding 0.
     Ranks above 512 run the four-chunk merge, and attention on the
-    channel-split MFMA kernel (bf16 cache) or the VALU kernel (e4m3 cache,
-    fp32 models)."""
+    channel-split MFMA kernel (bf16 model) or the VALU kernel (fp32
+    models)."""
     tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else {}
     _decode_case(gpu, dtype, fp8, [1, 70, 300], 1, 256, seed=rank, rank=rank, **tol)
     _decode_case(gpu, dtype, fp8, [1000, 1, 513, 2100], 8, 64, seed=rank + 1, rank=rank, **tol)
     _decode_case(gpu, dtype, fp8, [1000, 0, 513, 2100], 16, 64, seed=rank + 2, rank=rank, balance=256, **tol)
 
 
+@pytest.mark.parametrize("fp8", [False, True])
 @pytest.mark.parametrize("rank", [576, 640, 768, 960, 1024])
-def test_decode_wide_rank_long(gpu, rank):
-    """Ranks above 512 on the channel-split MFMA kernel at the headline's
-    length (the four waves own 64-channel blocks w, w + 4, ...: spare blocks
-    at NB = 9, 10, 15, none at 12 and 16), with the graph plan's splits,
-    peaked and flat scores, against the fp64 oracle with the LSE."""
+def test_decode_wide_rank_long(gpu, rank, fp8):
+    """Ranks above 512 on the channel-split MFMA kernel (bf16 and e4m3
+    caches) at the headline's length (the four waves own 64-channel blocks
+    w, w + 4, ...: spare blocks at NB = 9, 10, 15, none at 12 and 16), with
+    the graph plan's splits, peaked and flat scores, against the fp64 oracle
+    with the LSE."""
     lens = [4097] * 8
     n_splits, mc = kernels.plan_splits(8, 4097)
-    _decode_case(gpu, torch.bfloat16, False, lens, n_splits, mc, seed=rank, rank=rank, q_scale=0.5)
-    _decode_case(gpu, torch.bfloat16, False, [4097, 17, 1, 2000], 1, 64, seed=rank + 1, rank=rank, q_scale=3.0,
+    _decode_case(gpu, torch.bfloat16, fp8, lens, n_splits, mc, seed=rank, rank=rank, q_scale=0.5)
+    _decode_case(gpu, torch.bfloat16, fp8, [4097, 17, 1, 2000], 1, 64, seed=rank + 1, rank=rank, q_scale=3.0,
                  rope_pos=[3000, 7, 0, 1999])
 
 
