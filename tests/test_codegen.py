@@ -66,6 +66,7 @@ def test_device_code_has_no_packed_fp32_or_scalar_stores(tmp_path):
 SCRATCH_BUDGET = {
     "mla_linear_packed_kernel": 0,
     "mla_decode_dma": 0,
+    "mla_decode_wide": 0,
     "mla_merge_project_kernel": 0,
     "mla_merge_kernel": 0,
     "mla_append_g16_kernel": 0,
